@@ -1,0 +1,264 @@
+/* pmoe.h -- C ABI of the MI355X routed-expert MoE hot path (libpmoe.so).
+ *
+ * Plain pointers and sizes only.  Device pointers are HBM addresses (from
+ * hipMalloc, a torch tensor's data_ptr(), or the slab), streams are
+ * hipStream_t passed as void* (NULL = the default stream).  Every entry point
+ * returns 0 on success and a negative PMOE_E* code on error; the message of
+ * the calling thread's last error is pmoe_last_error().  Nothing crosses the
+ * ABI as an exception.  Compute entry points allocate nothing: scratch comes
+ * in through a caller-provided workspace whose size the *_workspace() query
+ * returns.  Calls on one stream are ordered by that stream; calls on
+ * different streams that share a workspace race.
+ *
+ * The reference (noahclark556/paged-moe) has no C ABI for this path: its
+ * arithmetic runs inside mlx (gather_qmm / quantized_matmul) called from
+ * Python.  Each declaration below names the reference interface it replaces.
+ */
+#ifndef PMOE_H
+#define PMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PMOE_ABI_VERSION 1
+
+enum {
+  PMOE_OK = 0,
+  PMOE_EINVAL = -1,  /* bad argument or unsupported shape */
+  PMOE_EHIP = -2,    /* HIP runtime error */
+  PMOE_ENOMEM = -3,  /* allocation failed (create/alloc calls only) */
+  PMOE_ESTATE = -4,  /* object in the wrong state */
+  PMOE_ESPACE = -5   /* workspace too small */
+};
+
+enum { PMOE_SCORE_SOFTMAX = 0, PMOE_SCORE_SIGMOID = 1 };
+
+/* Component order inside one slab slot (names as slab.py:90-126 keys). */
+enum {
+  PMOE_GATE_W = 0, PMOE_GATE_S, PMOE_GATE_B,
+  PMOE_UP_W, PMOE_UP_S, PMOE_UP_B,
+  PMOE_DOWN_W, PMOE_DOWN_S, PMOE_DOWN_B,
+  PMOE_NCOMP
+};
+
+/* Geometry of one quantized SwiGLU expert and its byte layout in a slab
+ * slot.  gate/up weight u32 [inter, hidden*bits/32], scales/biases bf16
+ * [inter, hidden/group]; down weight u32 [hidden, inter*bits/32],
+ * scales/biases bf16 [hidden, inter/group] (safetensors_index.py:8-25,
+ * bench/slab_probe.py:82).  off[c] is the byte offset of component c inside a
+ * slot, expert_bytes the slot stride. */
+typedef struct {
+  int32_t hidden;
+  int32_t inter;
+  int32_t bits;   /* 4 or 6 */
+  int32_t group;  /* 64 */
+  int64_t expert_bytes;
+  int64_t off[PMOE_NCOMP];
+  int64_t nbytes[PMOE_NCOMP];
+} pmoe_geom;
+
+/* Routing configuration of one MoE block. */
+typedef struct {
+  int32_t scoring;        /* PMOE_SCORE_* */
+  int32_t n_experts;      /* E (routed) */
+  int32_t top_k;          /* K */
+  int32_t norm_topk_prob; /* renormalise the K weights */
+  int32_t n_group;        /* sigmoid: expert groups (1 = none) */
+  int32_t topk_group;     /* sigmoid: groups kept */
+  float routed_scale;     /* sigmoid: routed_scaling_factor */
+} pmoe_route_cfg;
+
+/* ---- library ---------------------------------------------------------- */
+
+/* ABI version of the loaded library (PMOE_ABI_VERSION). No reference
+ * counterpart (the reference's native module reports API_VERSION 3,
+ * _native_read.c:693, for its read pool only). */
+int pmoe_abi_version(void);
+
+/* Last error message of the calling thread ("" if none). */
+const char* pmoe_last_error(void);
+
+/* Fill g for an expert of the given shape; the slot layout is
+ * component-contiguous in PMOE_* order, each component 256-byte aligned.
+ * Replaces SlabStore's per-component specs (slab.py:90-126). */
+int pmoe_geom_init(pmoe_geom* g, int hidden, int inter, int bits, int group);
+
+/* ---- routing (replaces mlx-lm's router: gate(x) then softmax/argpartition,
+ *      restated tests/test_stream.py:191-196, or deepseek_v3.MoEGate,
+ *      consumed streaming.py:2424-2442) ----------------------------------- */
+
+/* logits[n, e] = x[n, :] . w[e, :] (+ logit_bias[e]); x bf16 [n, d], w bf16
+ * [e, d], fp32 out, fixed summation order (bit-exact with the CPU oracle).
+ * d must be a multiple of 8. */
+int pmoe_router_logits(const void* x, const void* w, const float* logit_bias,
+                       int n, int d, int e, float* logits, void* stream);
+
+/* Top-k of a softmax router: inds[n, k] (descending weight, ties to the lower
+ * expert id) and weights[n, k] fp32. */
+int pmoe_route_softmax_topk(const float* logits, int n, int e, int k,
+                            int norm_topk_prob, int32_t* inds, float* weights,
+                            void* stream);
+
+/* DeepSeek-V3 noaux_tc: sigmoid + bias, grouped top-k, routed scaling. */
+int pmoe_route_sigmoid_group_topk(const float* logits, const float* bias,
+                                  int n, int e, int n_group, int topk_group,
+                                  int k, int norm_topk_prob, float routed_scale,
+                                  int32_t* inds, float* weights, void* stream);
+
+/* ---- dispatch (replaces np.argsort(kind="stable") + searchsorted,
+ *      streaming.py:789-808, and the unsort inv, :833-836) ---------------- */
+
+size_t pmoe_dispatch_workspace(int rows, int n_experts);
+
+/* Stable grouping of the rows flat positions of inds (int32 [rows]) by
+ * expert: order[rows], counts[E], offsets[E+1], inv[rows] (inv[order[i]] =
+ * i), active[E] (ascending ids with counts > 0) and *n_active (device). */
+int pmoe_dispatch(const int32_t* inds, int rows, int n_experts, int32_t* order,
+                  int32_t* counts, int32_t* offsets, int32_t* inv,
+                  int32_t* active, int32_t* n_active, void* ws,
+                  size_t ws_bytes, void* stream);
+
+/* ---- quantization format (replaces mx.quantize / mx.dequantize semantics
+ *      used by QuantizedSwitchLinear; format safetensors_index.py:8-25) ---- */
+
+/* w fp32 [rows, cols] -> q u32 [rows, cols*bits/32], scales/biases bf16
+ * [rows, cols/group]; min/max affine, bit-exact with the oracle quantizer. */
+int pmoe_quantize(const float* w, int rows, int cols, int bits, int group,
+                  uint32_t* q, uint16_t* scales, uint16_t* biases,
+                  void* stream);
+
+/* Dequantize to bf16: out = bf16(s*q + b). */
+int pmoe_dequant(const uint32_t* q, const uint16_t* scales,
+                 const uint16_t* biases, int rows, int cols, int bits,
+                 int group, uint16_t* out, void* stream);
+
+/* ---- expert compute --------------------------------------------------- */
+
+/* Workspace bytes for pmoe_switch_glu / pmoe_moe_experts / pmoe_moe_block at
+ * n tokens, k routed slots (+ shared: 0 or 1), E experts. */
+size_t pmoe_moe_workspace(const pmoe_geom* g, int n, int k, int shared,
+                          int n_experts);
+
+/* The seam: y[n, k, :] = FFN_{inds[n,k]}(x[n, :]) as bf16 [n, k, hidden],
+ * uncombined, in (token, k) order.  Expert e lives in slab slot table[e]
+ * (slab base + slot * expert_bytes).  Replaces
+ * StreamedSwitchGLU.__call__(x, indices) (streaming.py:946-1401:
+ * _run_slab :587-631 -> three mx.gather_qmm, _gather_proj :504-536). */
+int pmoe_switch_glu(const pmoe_geom* g, const void* slab, const int32_t* table,
+                    int n_experts, const void* x, const int32_t* inds, int n,
+                    int k, void* y, void* ws, size_t ws_bytes, void* stream);
+
+/* Experts + weighted combine given routing: out[n] = sum_k w[n,k] *
+ * FFN_{inds[n,k]}(x[n]) (+ shared expert in slot shared_slot, weight 1 or
+ * sigmoid(x . shared_gate) when shared_gate != NULL), fp32 accumulation in
+ * fixed k order, bf16 out.  shared_slot < 0: no shared expert.  Replaces
+ * switch_mlp(x, inds) followed by the block's (y*scores[...,None]).sum(-2)
+ * (tests/test_stream.py:198) and the shared-expert add. */
+int pmoe_moe_experts(const pmoe_geom* g, const void* slab, const int32_t* table,
+                     int n_experts, const void* x, const int32_t* inds,
+                     const float* weights, int n, int k, int shared_slot,
+                     const void* shared_gate, void* out, void* ws,
+                     size_t ws_bytes, void* stream);
+
+/* Whole MoE block: router -> top-k -> dispatch -> experts -> combine.
+ * gate_w bf16 [E, hidden]; score_bias fp32 [E] (sigmoid scoring; NULL
+ * otherwise); logit_bias fp32 [E] or NULL.  inds_out/weights_out (device,
+ * [n, k]) receive the routing.  Replaces the mlx-lm MoE block call around
+ * StreamedSwitchGLU (SURVEY call stack B). */
+int pmoe_moe_block(const pmoe_geom* g, const pmoe_route_cfg* rc,
+                   const void* slab, const int32_t* table, const void* gate_w,
+                   const float* score_bias, const float* logit_bias,
+                   const void* x, int n, int shared_slot,
+                   const void* shared_gate, void* out, int32_t* inds_out,
+                   float* weights_out, void* ws, size_t ws_bytes,
+                   void* stream);
+
+/* ---- slab slot table (replaces ExpertCache's slot policy, cache.py:410:
+ *      _alloc_slot :1118-1159, _begin :2327-2453, _finish :2455-2523,
+ *      _evict_to_budget :2236-2291, stitch :717-787, flow table :791-859) -- */
+
+typedef struct pmoe_slab pmoe_slab;
+
+typedef struct {
+  int64_t hits, misses, evictions, starved, installs, resident, slots,
+      budget, reserve, stitched, bytes_copied;
+} pmoe_slab_stats;
+
+/* Slot policy + device table [n_layers, n_experts] int32 (-1 = absent).
+ * The slab memory itself is caller-owned. */
+int pmoe_slab_create(pmoe_slab** out, int slots, int n_layers, int n_experts,
+                     float reserve_frac, int lfru, int lfru_scan);
+int pmoe_slab_destroy(pmoe_slab* s);
+
+/* Device pointer of layer's expert->slot row (n_experts int32). */
+const int32_t* pmoe_slab_device_table(pmoe_slab* s, int layer);
+
+/* Host copy of layer's expert->slot row. */
+int pmoe_slab_host_table(pmoe_slab* s, int layer, int32_t* out);
+
+/* One layer fetch: ids (host, any order, duplicates allowed) are classified
+ * hit/miss, misses get slots (evicting LRU unpinned entries), and are
+ * installed in ascending id order with the LFRU second-chance trim.  Writes
+ * the misses that got a slot to miss_ids/miss_slots (capacity n_ids) and
+ * their count to *n_miss.  Does not touch the GPU. */
+int pmoe_slab_request(pmoe_slab* s, int layer, const int32_t* ids, int n_ids,
+                      int32_t* miss_ids, int32_t* miss_slots, int* n_miss);
+
+/* Fill every (layer, expert) into fixed slots slot = layer*E + e when they
+ * all fit; returns 1 if stitched, 0 if declined. */
+int pmoe_slab_stitch(pmoe_slab* s);
+
+/* Enqueue on stream the upload of layer's host table row to the device
+ * table. */
+int pmoe_slab_publish(pmoe_slab* s, int layer, void* stream);
+
+int pmoe_slab_stats_get(pmoe_slab* s, pmoe_slab_stats* out);
+
+/* ---- copy engine (replaces the native pread pool, _native_read.c:38-698:
+ *      urgent/normal queues, split pieces, promote, first-error latch) ----- */
+
+typedef struct pmoe_copy_engine pmoe_copy_engine;
+
+/* Pinned host memory (hipHostMalloc) for the host expert store. */
+int pmoe_host_alloc(void** out, size_t bytes);
+int pmoe_host_free(void* p);
+
+/* Engine with its own copy streams (default priority) on the current
+ * device; copies are split into pieces of at most split_bytes. */
+int pmoe_copy_engine_create(pmoe_copy_engine** out, size_t split_bytes,
+                            int n_streams);
+int pmoe_copy_engine_destroy(pmoe_copy_engine* ce);
+
+/* Queue a host->device copy; urgent jobs are issued before queued normal
+ * ones at the next pmoe_copy_flush. */
+int pmoe_copy_submit(pmoe_copy_engine* ce, void* dst, const void* src,
+                     size_t bytes, int urgent);
+
+/* Issue every queued job (urgent first) and make stream wait for all of
+ * them (event wait, no host block). */
+int pmoe_copy_flush(pmoe_copy_engine* ce, void* stream);
+
+/* Block until every issued copy has finished; returns the first error. */
+int pmoe_copy_sync(pmoe_copy_engine* ce);
+
+/* Bytes issued so far. */
+int64_t pmoe_copy_bytes(pmoe_copy_engine* ce);
+
+/* One decode-layer fetch through slab + engine: request(ids), copy each miss
+ * from host_store + (layer*n_experts + e)*g->expert_bytes into
+ * slab + slot*g->expert_bytes, publish the table on stream and make stream
+ * wait for the copies.  *n_miss receives the number of misses copied.
+ * Replaces ExpertCache.fetch (cache.py:2525) on the slab path. */
+int pmoe_slab_fetch(pmoe_slab* s, pmoe_copy_engine* ce, const pmoe_geom* g,
+                    void* slab, const void* host_store, int layer,
+                    const int32_t* ids, int n_ids, int* n_miss, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PMOE_H */

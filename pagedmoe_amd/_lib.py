@@ -1,0 +1,137 @@
+"""ctypes binding of libpmoe.so (the C ABI declared in include/pmoe.h).
+
+The library is built in-tree (``__graft_entry__.build()`` or ``make -C
+pagedmoe_amd/csrc``).  There is no fallback: if the library is missing every
+entry point raises ``PmoeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libpmoe.so"
+
+PMOE_OK = 0
+PMOE_NCOMP = 9
+COMPONENTS = (
+    "gate_proj.weight", "gate_proj.scales", "gate_proj.biases",
+    "up_proj.weight", "up_proj.scales", "up_proj.biases",
+    "down_proj.weight", "down_proj.scales", "down_proj.biases",
+)
+SCORE_SOFTMAX = 0
+SCORE_SIGMOID = 1
+
+
+class PmoeError(RuntimeError):
+    """An entry point of libpmoe returned an error (or the library is absent)."""
+
+
+class Geom(ctypes.Structure):
+    _fields_ = [
+        ("hidden", ctypes.c_int32),
+        ("inter", ctypes.c_int32),
+        ("bits", ctypes.c_int32),
+        ("group", ctypes.c_int32),
+        ("expert_bytes", ctypes.c_int64),
+        ("off", ctypes.c_int64 * PMOE_NCOMP),
+        ("nbytes", ctypes.c_int64 * PMOE_NCOMP),
+    ]
+
+
+class RouteCfg(ctypes.Structure):
+    _fields_ = [
+        ("scoring", ctypes.c_int32),
+        ("n_experts", ctypes.c_int32),
+        ("top_k", ctypes.c_int32),
+        ("norm_topk_prob", ctypes.c_int32),
+        ("n_group", ctypes.c_int32),
+        ("topk_group", ctypes.c_int32),
+        ("routed_scale", ctypes.c_float),
+    ]
+
+
+class SlabStats(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int64) for n in (
+        "hits", "misses", "evictions", "starved", "installs", "resident", "slots",
+        "budget", "reserve", "stitched", "bytes_copied")]
+
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+_I32P = ctypes.POINTER(ctypes.c_int32)
+
+# name -> (restype, argtypes); every symbol include/pmoe.h declares.
+SIGNATURES = {
+    "pmoe_abi_version": (_I, []),
+    "pmoe_last_error": (ctypes.c_char_p, []),
+    "pmoe_geom_init": (_I, [ctypes.POINTER(Geom), _I, _I, _I, _I]),
+    "pmoe_router_logits": (_I, [_P, _P, _P, _I, _I, _I, _P, _P]),
+    "pmoe_route_softmax_topk": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
+    "pmoe_route_sigmoid_group_topk": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P]),
+    "pmoe_dispatch_workspace": (_SZ, [_I, _I]),
+    "pmoe_dispatch": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "pmoe_quantize": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P]),
+    "pmoe_dequant": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _P]),
+    "pmoe_moe_workspace": (_SZ, [ctypes.POINTER(Geom), _I, _I, _I, _I]),
+    "pmoe_switch_glu": (_I, [ctypes.POINTER(Geom), _P, _P, _I, _P, _P, _I, _I, _P, _P, _SZ, _P]),
+    "pmoe_moe_experts": (_I, [ctypes.POINTER(Geom), _P, _P, _I, _P, _P, _P, _I, _I, _I, _P,
+                              _P, _P, _SZ, _P]),
+    "pmoe_moe_block": (_I, [ctypes.POINTER(Geom), ctypes.POINTER(RouteCfg), _P, _P, _P, _P, _P,
+                            _P, _I, _I, _P, _P, _P, _P, _P, _SZ, _P]),
+    "pmoe_slab_create": (_I, [ctypes.POINTER(_P), _I, _I, _I, _F, _I, _I]),
+    "pmoe_slab_destroy": (_I, [_P]),
+    "pmoe_slab_device_table": (_P, [_P, _I]),
+    "pmoe_slab_host_table": (_I, [_P, _I, _I32P]),
+    "pmoe_slab_request": (_I, [_P, _I, _I32P, _I, _I32P, _I32P, ctypes.POINTER(_I)]),
+    "pmoe_slab_stitch": (_I, [_P]),
+    "pmoe_slab_publish": (_I, [_P, _I, _P]),
+    "pmoe_slab_stats_get": (_I, [_P, ctypes.POINTER(SlabStats)]),
+    "pmoe_host_alloc": (_I, [ctypes.POINTER(_P), _SZ]),
+    "pmoe_host_free": (_I, [_P]),
+    "pmoe_copy_engine_create": (_I, [ctypes.POINTER(_P), _SZ, _I]),
+    "pmoe_copy_engine_destroy": (_I, [_P]),
+    "pmoe_copy_submit": (_I, [_P, _P, _P, _SZ, _I]),
+    "pmoe_copy_flush": (_I, [_P, _P]),
+    "pmoe_copy_sync": (_I, [_P]),
+    "pmoe_copy_bytes": (ctypes.c_int64, [_P]),
+    "pmoe_slab_fetch": (_I, [_P, _P, ctypes.POINTER(Geom), _P, _P, _I, _I32P, _I,
+                             ctypes.POINTER(_I), _P]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises PmoeError when it has not been built."""
+    global _lib
+    if _lib is None:
+        path = Path(os.environ.get("PMOE_LIB", LIB_PATH))
+        if not path.exists():
+            raise PmoeError(
+                f"libpmoe.so not found at {path}: build it with "
+                "`python -c 'import __graft_entry__ as g; g.build()'` or "
+                "`make -C pagedmoe_amd/csrc`")
+        handle = ctypes.CDLL(str(path))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str = "") -> None:
+    """Raise PmoeError with the library's message for a nonzero status."""
+    if rc != PMOE_OK:
+        msg = lib().pmoe_last_error().decode(errors="replace")
+        raise PmoeError(f"{what or 'pmoe'} failed ({rc}): {msg}")
+
+
+def geom(hidden: int, inter: int, bits: int, group: int = 64) -> Geom:
+    g = Geom()
+    check(lib().pmoe_geom_init(ctypes.byref(g), hidden, inter, bits, group), "pmoe_geom_init")
+    return g

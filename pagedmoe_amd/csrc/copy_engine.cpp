@@ -1,0 +1,153 @@
+// Host -> HBM copy engine for slab misses.
+//
+// Counterpart of the reference's native read pool (_native_read.c:38-698):
+// jobs wait in an urgent and a normal queue (urgent = a layer is blocked on
+// it, :260-269), are cut into pieces of at most split_bytes so several copy
+// streams / SDMA engines share one expert (:213-241), and the first error of
+// a batch is the one reported (:131-156, :293-302).  Instead of pread into
+// unified memory, a piece is one hipMemcpyAsync from pinned host memory into
+// its slab slot.  Ordering with compute uses events only: at flush the copy
+// streams wait for everything already queued on the compute stream (so no
+// slot is overwritten while an earlier kernel may still read it), and the
+// compute stream waits for the copies.  All streams have default priority.
+#include <hip/hip_runtime.h>
+
+#include <deque>
+#include <mutex>
+#include <vector>
+
+#include "pmoe_internal.h"
+
+struct pmoe_copy_engine {
+  struct Job {
+    void* dst;
+    const void* src;
+    size_t bytes;
+  };
+  size_t split = 4u << 20;
+  std::vector<hipStream_t> streams;
+  std::vector<hipEvent_t> done;
+  hipEvent_t start = nullptr;
+  std::deque<Job> urgent, normal;
+  int64_t bytes = 0;
+  int next_stream = 0;
+  std::mutex mu;
+};
+
+extern "C" int pmoe_host_alloc(void** out, size_t bytes) {
+  pmoe::clear_error();
+  if (!out) return pmoe::fail(PMOE_EINVAL, "host_alloc: null out");
+  *out = nullptr;
+  if (bytes == 0) return PMOE_OK;
+  hipError_t e = hipHostMalloc(out, bytes, hipHostMallocDefault);
+  if (e != hipSuccess) {
+    *out = nullptr;
+    return pmoe::fail(PMOE_ENOMEM, std::string("host_alloc: ") + hipGetErrorString(e));
+  }
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_host_free(void* p) {
+  pmoe::clear_error();
+  if (p) PMOE_HIP(hipHostFree(p));
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_copy_engine_create(pmoe_copy_engine** out, size_t split_bytes,
+                                       int n_streams) {
+  pmoe::clear_error();
+  if (!out) return pmoe::fail(PMOE_EINVAL, "copy_engine_create: null out");
+  *out = nullptr;
+  if (n_streams <= 0 || n_streams > 8)
+    return pmoe::fail(PMOE_EINVAL, "copy_engine_create: n_streams must be 1..8");
+  auto* ce = new (std::nothrow) pmoe_copy_engine();
+  if (!ce) return pmoe::fail(PMOE_ENOMEM, "copy_engine_create: out of host memory");
+  if (split_bytes > 0) ce->split = split_bytes;
+  hipError_t e = hipEventCreateWithFlags(&ce->start, hipEventDisableTiming);
+  for (int i = 0; i < n_streams && e == hipSuccess; ++i) {
+    hipStream_t s = nullptr;
+    hipEvent_t ev = nullptr;
+    e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e == hipSuccess) ce->streams.push_back(s);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e == hipSuccess) ce->done.push_back(ev);
+  }
+  if (e != hipSuccess) {
+    pmoe_copy_engine_destroy(ce);
+    return pmoe::hip_fail(e, "copy_engine_create");
+  }
+  *out = ce;
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_copy_engine_destroy(pmoe_copy_engine* ce) {
+  pmoe::clear_error();
+  if (!ce) return PMOE_OK;
+  for (hipStream_t s : ce->streams) {
+    (void)hipStreamSynchronize(s);
+    (void)hipStreamDestroy(s);
+  }
+  for (hipEvent_t ev : ce->done) (void)hipEventDestroy(ev);
+  if (ce->start) (void)hipEventDestroy(ce->start);
+  delete ce;
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_copy_submit(pmoe_copy_engine* ce, void* dst, const void* src, size_t bytes,
+                                int urgent) {
+  pmoe::clear_error();
+  if (!ce || (bytes && (!dst || !src))) return pmoe::fail(PMOE_EINVAL, "copy_submit: bad argument");
+  if (!bytes) return PMOE_OK;
+  std::lock_guard<std::mutex> lk(ce->mu);
+  (urgent ? ce->urgent : ce->normal).push_back({dst, src, bytes});
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_copy_flush(pmoe_copy_engine* ce, void* stream) {
+  pmoe::clear_error();
+  if (!ce) return pmoe::fail(PMOE_EINVAL, "copy_flush: null engine");
+  hipStream_t compute = static_cast<hipStream_t>(stream);
+  std::lock_guard<std::mutex> lk(ce->mu);
+  if (ce->urgent.empty() && ce->normal.empty()) return PMOE_OK;
+  PMOE_HIP(hipEventRecord(ce->start, compute));
+  for (hipStream_t s : ce->streams) PMOE_HIP(hipStreamWaitEvent(s, ce->start, 0));
+  int first_err = PMOE_OK;
+  auto issue = [&](std::deque<pmoe_copy_engine::Job>& q) {
+    while (!q.empty()) {
+      const auto job = q.front();
+      q.pop_front();
+      for (size_t off = 0; off < job.bytes; off += ce->split) {
+        const size_t len = std::min(ce->split, job.bytes - off);
+        hipStream_t s = ce->streams[ce->next_stream];
+        ce->next_stream = (ce->next_stream + 1) % int(ce->streams.size());
+        hipError_t e = hipMemcpyAsync(static_cast<uint8_t*>(job.dst) + off,
+                                      static_cast<const uint8_t*>(job.src) + off, len,
+                                      hipMemcpyHostToDevice, s);
+        if (e != hipSuccess && first_err == PMOE_OK)
+          first_err = pmoe::hip_fail(e, "copy_flush: hipMemcpyAsync");
+        else if (e == hipSuccess)
+          ce->bytes += int64_t(len);
+      }
+    }
+  };
+  issue(ce->urgent);
+  issue(ce->normal);
+  for (size_t i = 0; i < ce->streams.size(); ++i) {
+    PMOE_HIP(hipEventRecord(ce->done[i], ce->streams[i]));
+    PMOE_HIP(hipStreamWaitEvent(compute, ce->done[i], 0));
+  }
+  return first_err;
+}
+
+extern "C" int pmoe_copy_sync(pmoe_copy_engine* ce) {
+  pmoe::clear_error();
+  if (!ce) return pmoe::fail(PMOE_EINVAL, "copy_sync: null engine");
+  int first_err = PMOE_OK;
+  for (hipStream_t s : ce->streams) {
+    hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess && first_err == PMOE_OK) first_err = pmoe::hip_fail(e, "copy_sync");
+  }
+  return first_err;
+}
+
+extern "C" int64_t pmoe_copy_bytes(pmoe_copy_engine* ce) { return ce ? ce->bytes : 0; }

@@ -1,0 +1,259 @@
+// Token -> expert dispatch: histogram, exclusive scan, stable scatter.
+//
+// Replaces the reference's host-side dispatch: order = np.argsort(flat,
+// kind="stable"), rows = order // K, per-expert searchsorted
+// (streaming.py:789-808) and the unsort inv[order] = arange (:833-836).
+// Integer work, HBM/latency bound; no float anywhere, so every output is
+// bit-exact.
+//
+// Stability: the position of flat row r inside expert e's segment is the
+// number of earlier rows with the same expert.  Rows are cut into blocks of
+// kChunk; a row's rank inside its block comes from a broadcast LDS scan of the
+// earlier rows of the block, and the block's base per expert from an
+// exclusive scan over blocks (block-major within each expert).
+#include "pmoe_internal.h"
+#include "pmoe_kernels.h"
+
+namespace pmoe {
+
+namespace {
+
+constexpr int kChunk = 256;        // rows per block in the multi-block path
+constexpr int kSmallRows = 1024;   // single-kernel path up to this many rows
+constexpr int kMaxExperts = 1024;
+
+// Source of flat row ids: row r = n*kk + c reads inds[n*k_routed + c] for
+// c < k_routed (valid in [0, n_routed)) and the shared pseudo-id n_routed for
+// the extra column.  Returns -1 for an id out of range.
+struct IdSrc {
+  const int32_t* inds;
+  int k_routed, kk, n_routed;
+};
+
+__device__ __forceinline__ int load_id(const IdSrc& src, int r) {
+  const int n = r / src.kk;
+  const int c = r - n * src.kk;
+  if (c >= src.k_routed) return src.n_routed;
+  const int e = src.inds[size_t(n) * src.k_routed + c];
+  return (e >= 0 && e < src.n_routed) ? e : -1;
+}
+
+// Exclusive scan of one int per thread over a block of NT threads.  s_tmp
+// holds NT/64 ints.  Returns the exclusive prefix; *total gets the sum.
+template <int NT>
+__device__ __forceinline__ int block_excl_scan(int v, int* s_tmp, int* total) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off, kWave);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) s_tmp[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    int wvv = lane < NT / 64 ? s_tmp[lane] : 0;
+    int wi = wvv;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(wi, off, kWave);
+      if (lane >= off) wi += o;
+    }
+    if (lane < NT / 64) s_tmp[lane] = wi;  // inclusive wave totals
+  }
+  __syncthreads();
+  const int base = wave > 0 ? s_tmp[wave - 1] : 0;
+  const int t = s_tmp[NT / 64 - 1];
+  __syncthreads();
+  if (total) *total = t;
+  return base + incl - v;
+}
+
+// Per-expert totals -> counts, offsets, active list, n_active and (when
+// tile_m > 0) the (expert, first row) list of tile_m-row tiles.  Run by a
+// block of 1024 threads; cnt[] is in LDS, one entry per expert.
+__device__ void finish_scan(const int* cnt, int n_experts, int32_t* counts, int32_t* offsets,
+                            int32_t* active, int32_t* n_active, int tile_m, int2* tiles,
+                            int32_t* n_tiles, int* s_off, int* s_tmp) {
+  const int e = threadIdx.x;
+  const int c = e < n_experts ? cnt[e] : 0;
+  int total = 0;
+  const int off = block_excl_scan<1024>(c, s_tmp, &total);
+  int act_total = 0;
+  const int act = block_excl_scan<1024>(c > 0 ? 1 : 0, s_tmp, &act_total);
+  int tiles_total = 0;
+  const int nt = tile_m > 0 ? (c + tile_m - 1) / tile_m : 0;
+  const int toff = block_excl_scan<1024>(nt, s_tmp, &tiles_total);
+  if (e < n_experts) {
+    s_off[e] = off;
+    counts[e] = c;
+    offsets[e] = off;
+    if (c > 0) active[act] = e;
+    for (int t = 0; t < nt; ++t) tiles[toff + t] = make_int2(e, t * tile_m);
+  }
+  if (e == 0) {
+    offsets[n_experts] = total;
+    *n_active = act_total;
+    if (tile_m > 0) *n_tiles = tiles_total;
+  }
+  __syncthreads();
+}
+
+// Whole dispatch in one block (rows <= kSmallRows).
+__global__ __launch_bounds__(1024) void dispatch_small_kernel(
+    const IdSrc src, int rows, int n_experts, int32_t* __restrict__ order,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ inv,
+    int32_t* __restrict__ active, int32_t* __restrict__ n_active, int tile_m,
+    int2* __restrict__ tiles, int32_t* __restrict__ n_tiles) {
+  __shared__ int s_e[kSmallRows];
+  __shared__ int s_cnt[kMaxExperts];
+  __shared__ int s_off[kMaxExperts];
+  __shared__ int s_tmp[16];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < n_experts; e += 1024) s_cnt[e] = 0;
+  int my_e = -1;
+  if (tid < rows) {
+    my_e = load_id(src, tid);
+    s_e[tid] = my_e;
+  }
+  __syncthreads();
+  int rank = 0;
+  if (my_e >= 0) {
+    atomicAdd(&s_cnt[my_e], 1);
+    for (int j = 0; j < tid; ++j) rank += (s_e[j] == my_e);
+  }
+  __syncthreads();
+  finish_scan(s_cnt, n_experts, counts, offsets, active, n_active, tile_m, tiles, n_tiles, s_off,
+              s_tmp);
+  if (my_e >= 0) {
+    const int pos = s_off[my_e] + rank;
+    order[pos] = tid;
+    inv[tid] = pos;
+  } else if (tid < rows) {
+    inv[tid] = -1;
+  }
+}
+
+// Multi-block path, phase 1: per-block histogram and in-block ranks.
+__global__ __launch_bounds__(kChunk) void dispatch_count_kernel(
+    const IdSrc src, int rows, int n_experts, int32_t* __restrict__ hist,
+    int32_t* __restrict__ rank_out) {
+  __shared__ int s_e[kChunk];
+  __shared__ int s_h[kMaxExperts];
+  const int tid = threadIdx.x;
+  const int row = blockIdx.x * kChunk + tid;
+  for (int e = tid; e < n_experts; e += kChunk) s_h[e] = 0;
+  int my_e = -1;
+  if (row < rows) my_e = load_id(src, row);
+  s_e[tid] = my_e;
+  __syncthreads();
+  if (my_e >= 0) {
+    atomicAdd(&s_h[my_e], 1);
+    int rank = 0;
+    for (int j = 0; j < tid; ++j) rank += (s_e[j] == my_e);
+    rank_out[row] = rank;
+  }
+  __syncthreads();
+  for (int e = tid; e < n_experts; e += kChunk) hist[size_t(blockIdx.x) * n_experts + e] = s_h[e];
+}
+
+// Phase 2 (one block): turn hist[b][e] into each block's base position per
+// expert and produce counts/offsets/active/tiles.
+__global__ __launch_bounds__(1024) void dispatch_scan_kernel(
+    int32_t* __restrict__ hist, int n_blocks, int n_experts, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ active, int32_t* __restrict__ n_active,
+    int tile_m, int2* __restrict__ tiles, int32_t* __restrict__ n_tiles) {
+  __shared__ int s_cnt[kMaxExperts];
+  __shared__ int s_off[kMaxExperts];
+  __shared__ int s_tmp[16];
+  const int e = threadIdx.x;
+  if (e < n_experts) {
+    int run = 0;
+    for (int b = 0; b < n_blocks; ++b) {
+      const size_t i = size_t(b) * n_experts + e;
+      const int h = hist[i];
+      hist[i] = run;
+      run += h;
+    }
+    s_cnt[e] = run;
+  }
+  __syncthreads();
+  finish_scan(s_cnt, n_experts, counts, offsets, active, n_active, tile_m, tiles, n_tiles, s_off,
+              s_tmp);
+  if (e < n_experts) {
+    const int base = s_off[e];
+    for (int b = 0; b < n_blocks; ++b) hist[size_t(b) * n_experts + e] += base;
+  }
+}
+
+// Phase 3: scatter rows to their positions.
+__global__ __launch_bounds__(kChunk) void dispatch_scatter_kernel(
+    const IdSrc src, int rows, int n_experts, const int32_t* __restrict__ hist,
+    const int32_t* __restrict__ rank, int32_t* __restrict__ order, int32_t* __restrict__ inv) {
+  const int row = blockIdx.x * kChunk + threadIdx.x;
+  if (row >= rows) return;
+  const int e = load_id(src, row);
+  if (e < 0) {
+    inv[row] = -1;
+    return;
+  }
+  const int pos = hist[size_t(blockIdx.x) * n_experts + e] + rank[row];
+  order[pos] = row;
+  inv[row] = pos;
+}
+
+}  // namespace
+
+size_t dispatch_workspace(int rows, int n_experts) {
+  if (rows <= kSmallRows) return 256;
+  const size_t blocks = (rows + kChunk - 1) / kChunk;
+  return ((blocks * n_experts + rows) * sizeof(int32_t) + 255) / 256 * 256;
+}
+
+// Internal entry: also builds the prefill tile list when tile_m > 0.  Ids
+// outside their range are dropped: counted nowhere, inv = -1.
+int dispatch_ext(const int32_t* inds, int rows, int k_routed, int kk, int n_ids, int32_t* order,
+                 int32_t* counts, int32_t* offsets, int32_t* inv, int32_t* active,
+                 int32_t* n_active, int tile_m, int2* tiles, int32_t* n_tiles, void* ws,
+                 size_t ws_bytes, hipStream_t st) {
+  PMOE_REQUIRE(n_ids > 0 && n_ids <= kMaxExperts, "dispatch: experts must be 1..1024");
+  PMOE_REQUIRE(rows >= 0, "dispatch: negative rows");
+  PMOE_REQUIRE(k_routed >= 1 && kk >= k_routed && kk <= k_routed + 1, "dispatch: bad columns");
+  PMOE_REQUIRE(rows % kk == 0, "dispatch: rows must be a multiple of the columns");
+  const IdSrc src{inds, k_routed, kk, kk > k_routed ? n_ids - 1 : n_ids};
+  if (rows <= kSmallRows) {
+    dispatch_small_kernel<<<1, 1024, 0, st>>>(src, rows, n_ids, order, counts, offsets, inv,
+                                              active, n_active, tile_m, tiles, n_tiles);
+    PMOE_LAUNCH_CHECK("dispatch_small_kernel");
+    return PMOE_OK;
+  }
+  PMOE_REQUIRE(ws != nullptr && ws_bytes >= dispatch_workspace(rows, n_ids),
+               "dispatch: workspace too small");
+  const int blocks = (rows + kChunk - 1) / kChunk;
+  int32_t* hist = static_cast<int32_t*>(ws);
+  int32_t* rank = hist + size_t(blocks) * n_ids;
+  dispatch_count_kernel<<<blocks, kChunk, 0, st>>>(src, rows, n_ids, hist, rank);
+  PMOE_LAUNCH_CHECK("dispatch_count_kernel");
+  dispatch_scan_kernel<<<1, 1024, 0, st>>>(hist, blocks, n_ids, counts, offsets, active,
+                                           n_active, tile_m, tiles, n_tiles);
+  PMOE_LAUNCH_CHECK("dispatch_scan_kernel");
+  dispatch_scatter_kernel<<<blocks, kChunk, 0, st>>>(src, rows, n_ids, hist, rank, order, inv);
+  PMOE_LAUNCH_CHECK("dispatch_scatter_kernel");
+  return PMOE_OK;
+}
+
+}  // namespace pmoe
+
+extern "C" size_t pmoe_dispatch_workspace(int rows, int n_experts) {
+  return pmoe::dispatch_workspace(rows, n_experts);
+}
+
+extern "C" int pmoe_dispatch(const int32_t* inds, int rows, int n_experts, int32_t* order,
+                             int32_t* counts, int32_t* offsets, int32_t* inv, int32_t* active,
+                             int32_t* n_active, void* ws, size_t ws_bytes, void* stream) {
+  pmoe::clear_error();
+  return pmoe::dispatch_ext(inds, rows, 1, 1, n_experts, order, counts, offsets, inv, active,
+                            n_active, 0, nullptr, nullptr, ws, ws_bytes,
+                            static_cast<hipStream_t>(stream));
+}

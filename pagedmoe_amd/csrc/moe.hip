@@ -1,0 +1,305 @@
+// MoE layer orchestration: workspace layout, combine, and the public expert
+// entry points (seam, experts+combine, whole block).
+//
+// Replaces StreamedSwitchGLU's compute (streaming.py:587-641, :768-841) and the
+// parent block's combine `(y * scores[..., None]).sum(axis=-2)` plus the
+// shared-expert add (restated tests/test_stream.py:198).  The combine is a
+// fixed-order fp32 reduction: out[n] = fma over k = 0..K-1 of w[n,k]*y[n,k],
+// then the shared expert, so results do not depend on scheduling.
+#include "pmoe_internal.h"
+#include "pmoe_kernels.h"
+
+namespace pmoe {
+
+int prefill_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* table,
+                    int n_experts, int shared_slot, const uint16_t* x, int n, int kk,
+                    const int32_t* order, const int32_t* counts, const int32_t* offsets,
+                    const int2* tiles, const int32_t* n_tiles, int max_tiles, uint16_t* h,
+                    void* y, int y_f32, hipStream_t st);
+int prefill_tile_m();
+bool prefill_wanted(const pmoe_geom* g, int n, int kk, int n_ids);
+
+namespace {
+
+constexpr size_t kAlign = 256;
+
+struct MoeWs {
+  float* logits = nullptr;        // [n, E]
+  float* shared_logit = nullptr;  // [n]
+  int32_t* order = nullptr;       // [rows]
+  int32_t* inv = nullptr;         // [rows]
+  int32_t* counts = nullptr;      // [n_ids]
+  int32_t* offsets = nullptr;     // [n_ids + 1]
+  int32_t* active = nullptr;      // [n_ids]
+  int32_t* n_active = nullptr;    // [1]
+  int2* tiles = nullptr;          // [max_tiles]
+  int32_t* n_tiles = nullptr;     // [1]
+  uint16_t* h = nullptr;          // [rows, inter] bf16
+  float* y = nullptr;             // [rows, hidden] f32
+  void* dws = nullptr;            // dispatch scratch
+  size_t dws_bytes = 0;
+  int max_tiles = 0;
+};
+
+struct Carver {
+  uint8_t* base;
+  size_t off = 0;
+  template <class T>
+  T* take(size_t count) {
+    T* p = base ? reinterpret_cast<T*>(base + off) : nullptr;
+    off += (count * sizeof(T) + kAlign - 1) / kAlign * kAlign;
+    return p;
+  }
+};
+
+size_t carve(const pmoe_geom* g, int n, int k, int shared, int n_experts, void* base,
+             MoeWs* w) {
+  const int kk = k + (shared ? 1 : 0);
+  const size_t rows = size_t(n) * kk;
+  const int n_ids = n_experts + (shared ? 1 : 0);
+  Carver c{static_cast<uint8_t*>(base)};
+  MoeWs t;
+  t.logits = c.take<float>(size_t(n) * n_experts);
+  t.shared_logit = c.take<float>(size_t(n));
+  t.order = c.take<int32_t>(rows);
+  t.inv = c.take<int32_t>(rows);
+  t.counts = c.take<int32_t>(n_ids);
+  t.offsets = c.take<int32_t>(n_ids + 1);
+  t.active = c.take<int32_t>(n_ids);
+  t.n_active = c.take<int32_t>(1);
+  const int tm = prefill_tile_m();
+  t.max_tiles = int(rows / tm) + n_ids + 1;
+  t.tiles = c.take<int2>(t.max_tiles);
+  t.n_tiles = c.take<int32_t>(1);
+  t.h = c.take<uint16_t>(rows * g->inter);
+  t.y = c.take<float>(rows * g->hidden);
+  t.dws_bytes = dispatch_workspace(int(rows), n_ids);
+  t.dws = c.take<uint8_t>(t.dws_bytes);
+  if (w) *w = t;
+  return c.off;
+}
+
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y,
+                                                      const float* __restrict__ w,
+                                                      const int32_t* __restrict__ inv,
+                                                      const float* __restrict__ shared_logit,
+                                                      int has_shared, int k, int kk, int d,
+                                                      uint16_t* __restrict__ out) {
+  const int n = blockIdx.y;
+  const int d0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (d0 >= d) return;
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  for (int c = 0; c < kk; ++c) {
+    const size_t r = size_t(n) * kk + c;
+    if (inv[r] < 0) continue;  // dropped id: contributes nothing
+    float wt;
+    if (c < k)
+      wt = w[size_t(n) * k + c];
+    else
+      wt = shared_logit ? psigmoid(shared_logit[n]) : 1.0f;
+    const float4 v = *reinterpret_cast<const float4*>(y + r * d + d0);
+    a0 = __builtin_fmaf(wt, v.x, a0);
+    a1 = __builtin_fmaf(wt, v.y, a1);
+    a2 = __builtin_fmaf(wt, v.z, a2);
+    a3 = __builtin_fmaf(wt, v.w, a3);
+  }
+  uint2 o;
+  o.x = uint32_t(f2bf(a0)) | (uint32_t(f2bf(a1)) << 16);
+  o.y = uint32_t(f2bf(a2)) | (uint32_t(f2bf(a3)) << 16);
+  *reinterpret_cast<uint2*>(out + size_t(n) * d + d0) = o;
+}
+
+__global__ __launch_bounds__(256) void zero_dropped_rows_kernel(const int32_t* __restrict__ inv,
+                                                                int rows, int d,
+                                                                uint16_t* __restrict__ y) {
+  const int r = blockIdx.y;
+  if (r >= rows || inv[r] >= 0) return;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < d; i += gridDim.x * 256) y[size_t(r) * d + i] = 0;
+}
+
+int check_geom(const pmoe_geom* g) {
+  PMOE_REQUIRE(g != nullptr, "null geometry");
+  PMOE_REQUIRE(g->bits == 4 || g->bits == 6, "geometry: bits must be 4 or 6");
+  PMOE_REQUIRE(g->group == 64, "geometry: group must be 64");
+  PMOE_REQUIRE(g->hidden > 0 && g->hidden % 64 == 0 && g->inter > 0 && g->inter % 64 == 0,
+               "geometry: hidden and inter must be multiples of 64");
+  PMOE_REQUIRE(g->hidden <= 8192 && g->inter <= 8192, "geometry: dims above 8192");
+  return PMOE_OK;
+}
+
+// Dispatch + the three projections (+ SwiGLU) for rows = n*kk flat rows.
+// y receives [rows, hidden] (f32 when y_f32, else bf16).
+int run_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* table, int n_experts,
+                int shared_slot, const uint16_t* x, const int32_t* inds, int n, int k, int kk,
+                int max_rows_per_expert, const MoeWs& w, void* y, int y_f32, hipStream_t st) {
+  const int rows = n * kk;
+  const int n_ids = n_experts + (kk > k ? 1 : 0);
+  const bool prefill = prefill_wanted(g, n, kk, n_ids);
+  int rc = dispatch_ext(inds, rows, k, kk, n_ids, w.order, w.counts, w.offsets, w.inv, w.active,
+                        w.n_active, prefill ? prefill_tile_m() : 0, w.tiles, w.n_tiles, w.dws,
+                        w.dws_bytes, st);
+  if (rc) return rc;
+  if (prefill)
+    return prefill_experts(g, slab, table, n_experts, shared_slot, x, n, kk, w.order, w.counts,
+                           w.offsets, w.tiles, w.n_tiles, w.max_tiles, w.h, y, y_f32, st);
+  const int max_experts = rows < n_ids ? rows : n_ids;
+  GemvArgs a{};
+  a.slab = slab;
+  a.expert_bytes = g->expert_bytes;
+  a.table = table;
+  a.n_experts = n_experts;
+  a.shared_slot = shared_slot;
+  a.active = w.active;
+  a.n_active = w.n_active;
+  a.counts = w.counts;
+  a.offsets = w.offsets;
+  a.order = w.order;
+  a.kk = kk;
+  // gate + up -> h
+  a.p0 = {g->off[PMOE_GATE_W], g->off[PMOE_GATE_S], g->off[PMOE_GATE_B]};
+  a.p1 = {g->off[PMOE_UP_W], g->off[PMOE_UP_S], g->off[PMOE_UP_B]};
+  a.rows_out = g->inter;
+  a.cols = g->hidden;
+  a.act = x;
+  a.act_stride = g->hidden;
+  a.act_by_token = 1;
+  a.out = w.h;
+  a.out_stride = g->inter;
+  a.out_f32 = 0;
+  a.rows_per_block = qgemv_rows_per_block(g->hidden, g->inter, max_experts, 1024);
+  rc = qgemv(a, g->bits, true, max_experts, max_rows_per_expert, st);
+  if (rc) return rc;
+  // down -> y
+  a.p0 = {g->off[PMOE_DOWN_W], g->off[PMOE_DOWN_S], g->off[PMOE_DOWN_B]};
+  a.p1 = a.p0;
+  a.rows_out = g->hidden;
+  a.cols = g->inter;
+  a.act = w.h;
+  a.act_stride = g->inter;
+  a.act_by_token = 0;
+  a.out = y;
+  a.out_stride = g->hidden;
+  a.out_f32 = y_f32;
+  a.rows_per_block = qgemv_rows_per_block(g->inter, g->hidden, max_experts, 1024);
+  return qgemv(a, g->bits, false, max_experts, max_rows_per_expert, st);
+}
+
+int experts_and_combine(const pmoe_geom* g, const uint8_t* slab, const int32_t* table,
+                        int n_experts, const uint16_t* x, const int32_t* inds, const float* wts,
+                        int n, int k, int shared_slot, const uint16_t* shared_gate, int max_rpe,
+                        uint16_t* out, const MoeWs& w, hipStream_t st) {
+  const int shared = shared_slot >= 0 ? 1 : 0;
+  const int kk = k + shared;
+  int rc = run_experts(g, slab, table, n_experts, shared_slot, x, inds, n, k, kk, max_rpe, w,
+                       w.y, 1, st);
+  if (rc) return rc;
+  const float* sl = nullptr;
+  if (shared && shared_gate) {
+    rc = router_logits(x, shared_gate, nullptr, n, g->hidden, 1, w.shared_logit, st);
+    if (rc) return rc;
+    sl = w.shared_logit;
+  }
+  dim3 grid((g->hidden / 4 + 255) / 256, n);
+  combine_kernel<<<grid, 256, 0, st>>>(w.y, wts, w.inv, sl, shared, k, kk, g->hidden, out);
+  PMOE_LAUNCH_CHECK("combine_kernel");
+  return PMOE_OK;
+}
+
+}  // namespace
+
+}  // namespace pmoe
+
+using pmoe::MoeWs;
+
+extern "C" size_t pmoe_moe_workspace(const pmoe_geom* g, int n, int k, int shared,
+                                     int n_experts) {
+  if (!g || n < 0 || k <= 0 || n_experts <= 0) return 0;
+  return pmoe::carve(g, n, k, shared, n_experts, nullptr, nullptr);
+}
+
+extern "C" int pmoe_switch_glu(const pmoe_geom* g, const void* slab, const int32_t* table,
+                               int n_experts, const void* x, const int32_t* inds, int n, int k,
+                               void* y, void* ws, size_t ws_bytes, void* stream) {
+  pmoe::clear_error();
+  int rc = pmoe::check_geom(g);
+  if (rc) return rc;
+  PMOE_REQUIRE(slab && table && x && inds && y, "switch_glu: null pointer");
+  PMOE_REQUIRE(n >= 0 && k > 0 && n_experts > 0 && n_experts <= 1023, "switch_glu: bad shape");
+  if (n == 0) return PMOE_OK;
+  const size_t need = pmoe::carve(g, n, k, 0, n_experts, nullptr, nullptr);
+  if (!ws || ws_bytes < need) return pmoe::fail(PMOE_ESPACE, "switch_glu: workspace too small");
+  MoeWs w;
+  pmoe::carve(g, n, k, 0, n_experts, ws, &w);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = pmoe::run_experts(g, static_cast<const uint8_t*>(slab), table, n_experts, -1,
+                         static_cast<const uint16_t*>(x), inds, n, k, k, n * k, w, y, 0, st);
+  if (rc) return rc;
+  dim3 grid(1, n * k);
+  pmoe::zero_dropped_rows_kernel<<<grid, 256, 0, st>>>(w.inv, n * k, g->hidden,
+                                                       static_cast<uint16_t*>(y));
+  PMOE_LAUNCH_CHECK("zero_dropped_rows_kernel");
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_moe_experts(const pmoe_geom* g, const void* slab, const int32_t* table,
+                                int n_experts, const void* x, const int32_t* inds,
+                                const float* weights, int n, int k, int shared_slot,
+                                const void* shared_gate, void* out, void* ws, size_t ws_bytes,
+                                void* stream) {
+  pmoe::clear_error();
+  int rc = pmoe::check_geom(g);
+  if (rc) return rc;
+  PMOE_REQUIRE(slab && table && x && inds && weights && out, "moe_experts: null pointer");
+  PMOE_REQUIRE(n >= 0 && k > 0 && n_experts > 0 && n_experts <= 1023, "moe_experts: bad shape");
+  if (n == 0) return PMOE_OK;
+  const int shared = shared_slot >= 0 ? 1 : 0;
+  const size_t need = pmoe::carve(g, n, k, shared, n_experts, nullptr, nullptr);
+  if (!ws || ws_bytes < need) return pmoe::fail(PMOE_ESPACE, "moe_experts: workspace too small");
+  MoeWs w;
+  pmoe::carve(g, n, k, shared, n_experts, ws, &w);
+  return pmoe::experts_and_combine(
+      g, static_cast<const uint8_t*>(slab), table, n_experts, static_cast<const uint16_t*>(x),
+      inds, weights, n, k, shared_slot, static_cast<const uint16_t*>(shared_gate), n * (k + 1),
+      static_cast<uint16_t*>(out), w, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pmoe_moe_block(const pmoe_geom* g, const pmoe_route_cfg* rc_cfg, const void* slab,
+                              const int32_t* table, const void* gate_w, const float* score_bias,
+                              const float* logit_bias, const void* x, int n, int shared_slot,
+                              const void* shared_gate, void* out, int32_t* inds_out,
+                              float* weights_out, void* ws, size_t ws_bytes, void* stream) {
+  pmoe::clear_error();
+  int rc = pmoe::check_geom(g);
+  if (rc) return rc;
+  PMOE_REQUIRE(rc_cfg != nullptr, "moe_block: null routing config");
+  PMOE_REQUIRE(slab && table && gate_w && x && out && inds_out && weights_out,
+               "moe_block: null pointer");
+  const int e = rc_cfg->n_experts, k = rc_cfg->top_k;
+  PMOE_REQUIRE(n >= 0 && k > 0 && e > 0 && e <= 1023, "moe_block: bad shape");
+  if (n == 0) return PMOE_OK;
+  const int shared = shared_slot >= 0 ? 1 : 0;
+  const size_t need = pmoe::carve(g, n, k, shared, e, nullptr, nullptr);
+  if (!ws || ws_bytes < need) return pmoe::fail(PMOE_ESPACE, "moe_block: workspace too small");
+  MoeWs w;
+  pmoe::carve(g, n, k, shared, e, ws, &w);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint16_t* xb = static_cast<const uint16_t*>(x);
+  rc = pmoe::router_logits(xb, static_cast<const uint16_t*>(gate_w), logit_bias, n, g->hidden, e,
+                           w.logits, st);
+  if (rc) return rc;
+  if (rc_cfg->scoring == PMOE_SCORE_SOFTMAX) {
+    rc = pmoe::route_softmax(w.logits, n, e, k, rc_cfg->norm_topk_prob, inds_out, weights_out, st);
+  } else if (rc_cfg->scoring == PMOE_SCORE_SIGMOID) {
+    PMOE_REQUIRE(score_bias != nullptr, "moe_block: sigmoid scoring needs score_bias");
+    rc = pmoe::route_sigmoid(w.logits, score_bias, n, e, rc_cfg->n_group, rc_cfg->topk_group, k,
+                             rc_cfg->norm_topk_prob, rc_cfg->routed_scale, inds_out, weights_out,
+                             st);
+  } else {
+    return pmoe::fail(PMOE_EINVAL, "moe_block: unknown scoring");
+  }
+  if (rc) return rc;
+  return pmoe::experts_and_combine(g, static_cast<const uint8_t*>(slab), table, e, xb, inds_out,
+                                   weights_out, n, k, shared_slot,
+                                   static_cast<const uint16_t*>(shared_gate), n,
+                                   static_cast<uint16_t*>(out), w, st);
+}

@@ -1,0 +1,60 @@
+// Internal launch interfaces shared by the kernel files of libpmoe.
+#pragma once
+
+#include "pmoe_internal.h"
+
+namespace pmoe {
+
+// Component offsets of one projection inside a slab slot.
+struct QProj {
+  int64_t w, s, b;
+};
+
+// Arguments of one grouped dequant-GEMV launch (see decode.hip).
+struct GemvArgs {
+  const uint8_t* slab;
+  int64_t expert_bytes;
+  const int32_t* table;  // expert id -> slot (-1: absent)
+  int n_experts;         // id n_experts is the shared expert
+  int shared_slot;
+  QProj p0, p1;          // p1: second projection of a dual (gate/up) launch
+  int rows_out;          // output rows of the projection (O)
+  int cols;              // input dim
+  const uint16_t* act;   // activations, bf16
+  int act_stride;        // elements between activation rows
+  int act_by_token;      // 1: activation row = flat row / kk; 0: = flat row
+  int kk;                // flat columns per token
+  const int32_t* active;
+  const int32_t* n_active;
+  const int32_t* counts;
+  const int32_t* offsets;
+  const int32_t* order;
+  void* out;             // [flat rows, out_stride], f32 or bf16
+  int out_stride;
+  int out_f32;
+  int rows_per_block;
+};
+
+int qgemv(const GemvArgs& a, int bits, bool dual, int max_experts, int max_rows_per_expert,
+          hipStream_t st);
+int qgemv_rows_per_block(int cols, int rows_out, int max_experts, int target);
+
+// Routing (router.hip)
+int router_logits(const uint16_t* x, const uint16_t* w, const float* bias, int n, int d, int e,
+                  float* out, hipStream_t st);
+int route_softmax(const float* logits, int n, int e, int k, int norm, int32_t* inds,
+                  float* weights, hipStream_t st);
+int route_sigmoid(const float* logits, const float* bias, int n, int e, int n_group,
+                  int topk_group, int k, int norm, float scale, int32_t* inds, float* weights,
+                  hipStream_t st);
+
+// Dispatch (dispatch.hip).  Flat row r reads id inds[(r / kk) * k_routed +
+// r % kk] when r % kk < k_routed and the shared pseudo-id n_routed otherwise;
+// n_ids = n_routed + (kk > k_routed).
+size_t dispatch_workspace(int rows, int n_experts);
+int dispatch_ext(const int32_t* inds, int rows, int k_routed, int kk, int n_ids,
+                 int32_t* order, int32_t* counts, int32_t* offsets, int32_t* inv,
+                 int32_t* active, int32_t* n_active, int tile_m, int2* tiles, int32_t* n_tiles,
+                 void* ws, size_t ws_bytes, hipStream_t st);
+
+}  // namespace pmoe

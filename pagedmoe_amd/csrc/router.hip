@@ -1,0 +1,328 @@
+// Router: logits GEMV/GEMM in a fixed fp32 summation order, then top-k.
+//
+// Replaces the mlx-lm router the reference taps (streaming.py:167-193) and the
+// selection the block performs after it: softmax(precise) -> argpartition ->
+// take -> renorm (restated tests/test_stream.py:191-196) or DeepSeek-V3's
+// sigmoid + correction bias + grouped top-k + routed scaling (consumed
+// streaming.py:2424-2442).
+//
+// Summation order of a logit (shared with the CPU oracle, bit for bit):
+// element d = 512*t + 8*l + j is owned by lane l; each lane runs
+// acc = fma(x_d, w_d, acc) for t ascending, j ascending (one 16-byte load of
+// x and of w per t); the 64 lane partials are combined by an xor butterfly.
+#include "pmoe_internal.h"
+
+namespace pmoe {
+
+namespace {
+
+constexpr int kRouterWaves = 4;
+constexpr int kMaxEPL = 16;    // experts per lane in the select kernels (E <= 1024)
+constexpr int kMaxK = 16;
+
+__device__ __forceinline__ void fma8(float& acc, const uint4& a, const uint4& b) {
+  acc = __builtin_fmaf(bf16lo(a.x), bf16lo(b.x), acc);
+  acc = __builtin_fmaf(bf16hi(a.x), bf16hi(b.x), acc);
+  acc = __builtin_fmaf(bf16lo(a.y), bf16lo(b.y), acc);
+  acc = __builtin_fmaf(bf16hi(a.y), bf16hi(b.y), acc);
+  acc = __builtin_fmaf(bf16lo(a.z), bf16lo(b.z), acc);
+  acc = __builtin_fmaf(bf16hi(a.z), bf16hi(b.z), acc);
+  acc = __builtin_fmaf(bf16lo(a.w), bf16lo(b.w), acc);
+  acc = __builtin_fmaf(bf16hi(a.w), bf16hi(b.w), acc);
+}
+
+// One wave computes a TE x TN tile of logits (experts x tokens).
+template <int TE, int TN>
+__global__ __launch_bounds__(256) void router_logits_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    const float* __restrict__ bias, int n, int d, int e, float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int e0 = (blockIdx.x * kRouterWaves + wave) * TE;
+  const int n0 = blockIdx.y * TN;
+  if (e0 >= e) return;
+  float acc[TE][TN];
+#pragma unroll
+  for (int i = 0; i < TE; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = 0.0f;
+
+  const int passes = (d + 511) / 512;
+  for (int t = 0; t < passes; ++t) {
+    const int col = t * 512 + lane * 8;
+    if (col < d) {
+      uint4 wv[TE], xv[TN];
+#pragma unroll
+      for (int i = 0; i < TE; ++i) {
+        const int ei = min(e0 + i, e - 1);
+        wv[i] = *reinterpret_cast<const uint4*>(w + size_t(ei) * d + col);
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int nj = min(n0 + j, n - 1);
+        xv[j] = *reinterpret_cast<const uint4*>(x + size_t(nj) * d + col);
+      }
+#pragma unroll
+      for (int i = 0; i < TE; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fma8(acc[i][j], xv[j], wv[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TE; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const float s = wave_sum_bfly(acc[i][j]);
+      if (lane == ((i * TN + j) & 63) && e0 + i < e && n0 + j < n) {
+        const float b = bias ? bias[e0 + i] : 0.0f;
+        out[size_t(n0 + j) * e + e0 + i] = bias ? s + b : s;
+      }
+    }
+}
+
+// (value, index) order used by every top-k here: larger value first, lower
+// index first among equal values.  idx < 0 marks "nothing".
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  if (i < 0) return false;
+  if (bi < 0) return true;
+  return v > bv || (v == bv && i < bi);
+}
+
+__device__ __forceinline__ void wave_argmax(float& bv, int& bi) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, kWave);
+    const int oi = __shfl_xor(bi, off, kWave);
+    if (better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+}
+
+// K picks over the per-lane values v[i] (expert lane + 64*i); excluded bit i
+// of `skip` means v[i] is not a candidate.  Picks are written to sel_v/sel_i.
+__device__ __forceinline__ void wave_topk(const float (&v)[kMaxEPL], uint32_t skip, int epl,
+                                          int k, float* sel_v, int* sel_i) {
+  const int lane = threadIdx.x & 63;
+  uint32_t taken = skip;
+  for (int kk = 0; kk < k; ++kk) {
+    float bv = 0.0f;
+    int bi = -1;
+#pragma unroll
+    for (int i = 0; i < kMaxEPL; ++i) {
+      if (i < epl && !((taken >> i) & 1u)) {
+        const int ei = lane + 64 * i;
+        if (better(v[i], ei, bv, bi)) {
+          bv = v[i];
+          bi = ei;
+        }
+      }
+    }
+    wave_argmax(bv, bi);
+    if (bi >= 0 && (bi & 63) == lane) taken |= 1u << (bi >> 6);
+    sel_v[kk] = bv;
+    sel_i[kk] = bi;
+  }
+}
+
+__global__ __launch_bounds__(256) void route_softmax_kernel(
+    const float* __restrict__ logits, int n, int e, int k, int norm,
+    int32_t* __restrict__ inds, float* __restrict__ weights) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= n) return;
+  const int epl = (e + 63) / 64;
+  float v[kMaxEPL];
+  uint32_t skip = 0;
+#pragma unroll
+  for (int i = 0; i < kMaxEPL; ++i) {
+    const int ei = lane + 64 * i;
+    v[i] = (i < epl && ei < e) ? logits[size_t(row) * e + ei] : 0.0f;
+    if (i < epl && ei >= e) skip |= 1u << i;
+  }
+  float sv[kMaxK];
+  int si[kMaxK];
+  wave_topk(v, skip, epl, k, sv, si);
+  const float m = sv[0];
+  float s = 0.0f;
+  if (norm) {
+    for (int kk = 0; kk < k; ++kk) s = s + pexp(sv[kk] - m);
+  } else {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxEPL; ++i)
+      if (i < epl && lane + 64 * i < e) acc = acc + pexp(v[i] - m);
+    s = wave_sum_bfly(acc);
+  }
+  for (int kk = lane; kk < k; kk += 64) {
+    inds[size_t(row) * k + kk] = si[kk];
+    weights[size_t(row) * k + kk] = pexp(sv[kk] - m) / s;
+  }
+}
+
+__global__ __launch_bounds__(256) void route_sigmoid_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias, int n, int e,
+    int n_group, int topk_group, int k, int norm, float scale, int32_t* __restrict__ inds,
+    float* __restrict__ weights) {
+  __shared__ float s_c[4][1024];
+  __shared__ float s_sig[4][1024];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int row_raw = blockIdx.x * 4 + wv;
+  const bool valid = row_raw < n;
+  const int row = valid ? row_raw : n - 1;
+  const int epl = (e + 63) / 64;
+  float c[kMaxEPL];
+  uint32_t skip = 0;
+#pragma unroll
+  for (int i = 0; i < kMaxEPL; ++i) {
+    const int ei = lane + 64 * i;
+    c[i] = 0.0f;
+    if (i < epl && ei < e) {
+      const float sg = psigmoid(logits[size_t(row) * e + ei]);
+      c[i] = sg + bias[ei];
+      s_c[wv][ei] = c[i];
+      s_sig[wv][ei] = sg;
+    } else if (i < epl) {
+      skip |= 1u << i;
+    }
+  }
+  __syncthreads();
+  if (n_group > 1) {
+    const int gs = e / n_group;
+    float gv = 0.0f;
+    int gi = -1;
+    if (lane < n_group) {
+      float t1 = -__builtin_inff(), t2 = -__builtin_inff();
+      for (int j = 0; j < gs; ++j) {
+        const float xv = s_c[wv][lane * gs + j];
+        if (xv > t1) {
+          t2 = t1;
+          t1 = xv;
+        } else if (xv > t2) {
+          t2 = xv;
+        }
+      }
+      gv = t1 + t2;
+      gi = lane;
+    }
+    // topk_group picks among the group scores (one per lane < n_group).
+    uint64_t keep = 0;
+    bool mine_taken = false;
+    for (int kk = 0; kk < topk_group; ++kk) {
+      float bv = gv;
+      int bi = mine_taken ? -1 : gi;
+      wave_argmax(bv, bi);
+      if (bi >= 0) {
+        keep |= 1ull << bi;
+        if (bi == lane) mine_taken = true;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxEPL; ++i) {
+      const int ei = lane + 64 * i;
+      if (i < epl && ei < e && !((keep >> (ei / gs)) & 1ull)) c[i] = 0.0f;
+    }
+  }
+  float sv[kMaxK];
+  int si[kMaxK];
+  wave_topk(c, skip, epl, k, sv, si);
+  float wk[kMaxK];
+  float s = 0.0f;
+  for (int kk = 0; kk < k; ++kk) {
+    wk[kk] = s_sig[wv][si[kk]];
+    s = s + wk[kk];
+  }
+  if (!valid) return;
+  for (int kk = lane; kk < k; kk += 64) {
+    float wt = wk[kk];
+    if (norm) wt = wt / s;
+    wt = wt * scale;
+    inds[size_t(row) * k + kk] = si[kk];
+    weights[size_t(row) * k + kk] = wt;
+  }
+}
+
+}  // namespace
+
+int router_logits(const uint16_t* x, const uint16_t* w, const float* bias, int n, int d, int e,
+                  float* out, hipStream_t st) {
+  PMOE_REQUIRE(x && w && out, "router_logits: null pointer");
+  PMOE_REQUIRE(n >= 0 && d > 0 && e > 0, "router_logits: bad shape");
+  PMOE_REQUIRE(d % 8 == 0, "router_logits: hidden must be a multiple of 8");
+  if (n == 0) return PMOE_OK;
+  if (n >= 32) {
+    constexpr int TE = 4, TN = 8;
+    dim3 grid((e + kRouterWaves * TE - 1) / (kRouterWaves * TE), (n + TN - 1) / TN);
+    router_logits_kernel<TE, TN><<<grid, 256, 0, st>>>(x, w, bias, n, d, e, out);
+  } else if (n >= 4) {
+    constexpr int TE = 1, TN = 4;
+    dim3 grid((e + kRouterWaves * TE - 1) / (kRouterWaves * TE), (n + TN - 1) / TN);
+    router_logits_kernel<TE, TN><<<grid, 256, 0, st>>>(x, w, bias, n, d, e, out);
+  } else {
+    constexpr int TE = 1, TN = 1;
+    dim3 grid((e + kRouterWaves * TE - 1) / (kRouterWaves * TE), n);
+    router_logits_kernel<TE, TN><<<grid, 256, 0, st>>>(x, w, bias, n, d, e, out);
+  }
+  PMOE_LAUNCH_CHECK("router_logits_kernel");
+  return PMOE_OK;
+}
+
+int route_softmax(const float* logits, int n, int e, int k, int norm, int32_t* inds,
+                  float* weights, hipStream_t st) {
+  PMOE_REQUIRE(logits && inds && weights, "route_softmax_topk: null pointer");
+  PMOE_REQUIRE(e > 0 && e <= 64 * kMaxEPL, "route_softmax_topk: experts must be 1..1024");
+  PMOE_REQUIRE(k > 0 && k <= kMaxK && k <= e, "route_softmax_topk: k must be 1..min(16, E)");
+  if (n <= 0) return PMOE_OK;
+  route_softmax_kernel<<<(n + 3) / 4, 256, 0, st>>>(logits, n, e, k, norm, inds, weights);
+  PMOE_LAUNCH_CHECK("route_softmax_kernel");
+  return PMOE_OK;
+}
+
+int route_sigmoid(const float* logits, const float* bias, int n, int e, int n_group,
+                  int topk_group, int k, int norm, float scale, int32_t* inds, float* weights,
+                  hipStream_t st) {
+  PMOE_REQUIRE(logits && bias && inds && weights, "route_sigmoid_group_topk: null pointer");
+  PMOE_REQUIRE(e > 0 && e <= 64 * kMaxEPL, "route_sigmoid_group_topk: experts must be 1..1024");
+  PMOE_REQUIRE(k > 0 && k <= kMaxK && k <= e, "route_sigmoid_group_topk: k must be 1..min(16, E)");
+  PMOE_REQUIRE(n_group >= 1 && n_group <= 64 && e % n_group == 0,
+               "route_sigmoid_group_topk: n_group must divide E and be <= 64");
+  PMOE_REQUIRE(topk_group >= 1 && topk_group <= n_group,
+               "route_sigmoid_group_topk: topk_group must be 1..n_group");
+  PMOE_REQUIRE(n_group == 1 || e / n_group >= 2,
+               "route_sigmoid_group_topk: groups need at least 2 experts");
+  PMOE_REQUIRE(k <= (e / n_group) * topk_group,
+               "route_sigmoid_group_topk: k exceeds the experts of the kept groups");
+  if (n <= 0) return PMOE_OK;
+  route_sigmoid_kernel<<<(n + 3) / 4, 256, 0, st>>>(logits, bias, n, e, n_group, topk_group, k,
+                                                    norm, scale, inds, weights);
+  PMOE_LAUNCH_CHECK("route_sigmoid_kernel");
+  return PMOE_OK;
+}
+
+}  // namespace pmoe
+
+extern "C" int pmoe_router_logits(const void* x, const void* w, const float* logit_bias, int n,
+                                  int d, int e, float* logits, void* stream) {
+  pmoe::clear_error();
+  return pmoe::router_logits(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w),
+                             logit_bias, n, d, e, logits, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pmoe_route_softmax_topk(const float* logits, int n, int e, int k,
+                                       int norm_topk_prob, int32_t* inds, float* weights,
+                                       void* stream) {
+  pmoe::clear_error();
+  return pmoe::route_softmax(logits, n, e, k, norm_topk_prob, inds, weights,
+                             static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pmoe_route_sigmoid_group_topk(const float* logits, const float* bias, int n,
+                                             int e, int n_group, int topk_group, int k,
+                                             int norm_topk_prob, float routed_scale,
+                                             int32_t* inds, float* weights, void* stream) {
+  pmoe::clear_error();
+  return pmoe::route_sigmoid(logits, bias, n, e, n_group, topk_group, k, norm_topk_prob,
+                             routed_scale, inds, weights, static_cast<hipStream_t>(stream));
+}

@@ -1,0 +1,340 @@
+// Expert slab slot table: residency policy on the host, table on the device.
+//
+// Restates ExpertCache's slab policy (cache.py:410): free list popped LIFO so
+// the first allocation is slot 0 (:991, :1138-1139); a reserve of
+// max(4, int(slots*reserve_frac)) slots kept out of the resident budget
+// (:996-1002); per layer step: clear pins, classify ids (hit -> MRU,
+// freq = min(8, freq+1), pin), give each miss a free slot or evict the least
+// recent unpinned non-stitch entry (_alloc_slot :1118-1159), install misses
+// with the LFRU second-chance trim (_install :2293, _evict_to_budget
+// :2236-2291).  The reference installs in read-completion order
+// (:2482-2519); here installs run in ascending expert id so the table is a
+// deterministic function of the request sequence.  The device table
+// [layers, experts] int32 (-1 = absent) is the flow table (:791-859).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <mutex>
+#include <vector>
+
+#include "pmoe_internal.h"
+
+namespace {
+
+constexpr int kFreqMax = 8;
+constexpr int kPublishChunk = 512;
+
+struct TableChunk {
+  int32_t v[kPublishChunk];
+};
+
+__global__ void publish_kernel(const TableChunk chunk, int count, int32_t* __restrict__ dst) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < count) dst[i] = chunk.v[i];
+}
+
+}  // namespace
+
+struct pmoe_slab {
+  int slots = 0, n_layers = 0, n_experts = 0, reserve = 0, budget = 0;
+  int lfru = 1, lfru_scan = 8;
+  bool stitched = false;
+  std::vector<int> free_slots;            // stack; back() is popped first
+  // LRU over dense keys (layer*E + e): head = least recent, tail = most recent
+  std::vector<int> prev, next, slot_of, freq;
+  std::vector<char> in_lru, stitch_key;
+  int head = -1, tail = -1, lru_size = 0;
+  std::vector<char> pinned;               // per slot
+  std::vector<int> pinned_list;
+  std::vector<int32_t> table;             // host [layers*E]
+  int32_t* dtable = nullptr;              // device [layers*E]
+  pmoe_slab_stats st{};
+  std::mutex mu;
+
+  void lru_unlink(int k) {
+    const int p = prev[k], n = next[k];
+    if (p >= 0) next[p] = n; else head = n;
+    if (n >= 0) prev[n] = p; else tail = p;
+    prev[k] = next[k] = -1;
+    in_lru[k] = 0;
+    --lru_size;
+  }
+  void lru_push_back(int k) {
+    prev[k] = tail;
+    next[k] = -1;
+    if (tail >= 0) next[tail] = k; else head = k;
+    tail = k;
+    in_lru[k] = 1;
+    ++lru_size;
+  }
+  void move_to_end(int k) {
+    if (tail == k) return;
+    lru_unlink(k);
+    lru_push_back(k);
+  }
+  void pin(int slot) {
+    if (slot >= 0 && !pinned[slot]) {
+      pinned[slot] = 1;
+      pinned_list.push_back(slot);
+    }
+  }
+  void clear_pins() {
+    for (int s : pinned_list) pinned[s] = 0;
+    pinned_list.clear();
+  }
+  bool evictable(int k) const { return !stitch_key[k] && !pinned[slot_of[k]]; }
+  void evict(int k) {
+    lru_unlink(k);
+    freq[k] = 0;
+    const int s = slot_of[k];
+    slot_of[k] = -1;
+    table[k] = -1;
+    free_slots.push_back(s);
+    ++st.evictions;
+  }
+  int alloc(bool evict_ok) {
+    if (!free_slots.empty()) {
+      const int s = free_slots.back();
+      free_slots.pop_back();
+      return s;
+    }
+    if (!evict_ok) return -1;
+    for (int k = head; k >= 0; k = next[k]) {
+      if (!evictable(k)) continue;
+      evict(k);
+      const int s = free_slots.back();
+      free_slots.pop_back();
+      return s;
+    }
+    ++st.starved;
+    return -1;
+  }
+  void trim() {
+    const int scan = lfru ? lfru_scan : 0;
+    while (lru_size > budget && lru_size > 1) {
+      for (int i = 0; i < scan; ++i) {
+        if (lru_size <= 1) break;
+        const int k = head;
+        if (freq[k] <= 0) break;
+        freq[k] >>= 1;
+        move_to_end(k);
+      }
+      int victim = -1;
+      for (int k = head; k >= 0; k = next[k])
+        if (evictable(k)) {
+          victim = k;
+          break;
+        }
+      if (victim < 0) break;
+      evict(victim);
+    }
+  }
+};
+
+extern "C" int pmoe_slab_create(pmoe_slab** out, int slots, int n_layers, int n_experts,
+                                float reserve_frac, int lfru, int lfru_scan) {
+  pmoe::clear_error();
+  if (!out) return pmoe::fail(PMOE_EINVAL, "slab_create: null out");
+  *out = nullptr;
+  if (slots <= 0 || n_layers <= 0 || n_experts <= 0)
+    return pmoe::fail(PMOE_EINVAL, "slab_create: slots, layers and experts must be positive");
+  if (!(reserve_frac >= 0.0f && reserve_frac < 1.0f) || lfru_scan < 0)
+    return pmoe::fail(PMOE_EINVAL, "slab_create: bad reserve_frac or lfru_scan");
+  auto* s = new (std::nothrow) pmoe_slab();
+  if (!s) return pmoe::fail(PMOE_ENOMEM, "slab_create: out of host memory");
+  s->slots = slots;
+  s->n_layers = n_layers;
+  s->n_experts = n_experts;
+  s->lfru = lfru ? 1 : 0;
+  s->lfru_scan = lfru_scan;
+  s->reserve = std::max(4, int(float(slots) * reserve_frac));
+  s->budget = slots - s->reserve;
+  for (int i = slots - 1; i >= 0; --i) s->free_slots.push_back(i);
+  const size_t keys = size_t(n_layers) * n_experts;
+  s->prev.assign(keys, -1);
+  s->next.assign(keys, -1);
+  s->slot_of.assign(keys, -1);
+  s->freq.assign(keys, 0);
+  s->in_lru.assign(keys, 0);
+  s->stitch_key.assign(keys, 0);
+  s->pinned.assign(slots, 0);
+  s->table.assign(keys, -1);
+  s->st.slots = slots;
+  s->st.reserve = s->reserve;
+  s->st.budget = s->budget;
+  *out = s;
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_slab_destroy(pmoe_slab* s) {
+  pmoe::clear_error();
+  if (!s) return PMOE_OK;
+  if (s->dtable) (void)hipFree(s->dtable);
+  delete s;
+  return PMOE_OK;
+}
+
+// The device table is allocated on first use (the policy itself never needs
+// the GPU) and starts as a copy of the host table.
+static int ensure_device_table(pmoe_slab* s) {
+  if (s->dtable) return PMOE_OK;
+  const size_t bytes = s->table.size() * sizeof(int32_t);
+  PMOE_HIP(hipMalloc(reinterpret_cast<void**>(&s->dtable), bytes));
+  hipError_t e = hipMemcpy(s->dtable, s->table.data(), bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(s->dtable);
+    s->dtable = nullptr;
+    return pmoe::hip_fail(e, "slab: device table init");
+  }
+  return PMOE_OK;
+}
+
+extern "C" const int32_t* pmoe_slab_device_table(pmoe_slab* s, int layer) {
+  pmoe::clear_error();
+  if (!s || layer < 0 || layer >= s->n_layers) {
+    pmoe::set_error("slab_device_table: bad argument");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(s->mu);
+  if (ensure_device_table(s)) return nullptr;
+  return s->dtable + size_t(layer) * s->n_experts;
+}
+
+extern "C" int pmoe_slab_host_table(pmoe_slab* s, int layer, int32_t* out) {
+  pmoe::clear_error();
+  if (!s || !out || layer < 0 || layer >= s->n_layers)
+    return pmoe::fail(PMOE_EINVAL, "slab_host_table: bad argument");
+  std::lock_guard<std::mutex> lk(s->mu);
+  std::copy_n(s->table.begin() + size_t(layer) * s->n_experts, s->n_experts, out);
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_slab_request(pmoe_slab* s, int layer, const int32_t* ids, int n_ids,
+                                 int32_t* miss_ids, int32_t* miss_slots, int* n_miss) {
+  pmoe::clear_error();
+  if (!s || (n_ids > 0 && !ids) || !n_miss || layer < 0 || layer >= s->n_layers || n_ids < 0)
+    return pmoe::fail(PMOE_EINVAL, "slab_request: bad argument");
+  std::vector<int> uniq(ids, ids + n_ids);
+  for (int e : uniq)
+    if (e < 0 || e >= s->n_experts) return pmoe::fail(PMOE_EINVAL, "slab_request: id out of range");
+  std::sort(uniq.begin(), uniq.end());
+  uniq.erase(std::unique(uniq.begin(), uniq.end()), uniq.end());
+  std::lock_guard<std::mutex> lk(s->mu);
+  s->clear_pins();
+  const int base = layer * s->n_experts;
+  std::vector<int> misses;
+  for (int e : uniq) {
+    const int k = base + e;
+    if (s->in_lru[k]) {
+      ++s->st.hits;
+      s->move_to_end(k);
+      s->freq[k] = std::min(kFreqMax, s->freq[k] + 1);
+      s->pin(s->slot_of[k]);
+    } else {
+      ++s->st.misses;
+      misses.push_back(e);
+    }
+  }
+  int placed = 0;
+  std::vector<std::pair<int, int>> got;
+  for (int e : misses) {
+    const int slot = s->alloc(true);
+    if (slot < 0) continue;
+    s->slot_of[base + e] = slot;
+    s->pin(slot);
+    got.emplace_back(e, slot);
+  }
+  for (auto& es : got) {
+    const int k = base + es.first;
+    s->lru_push_back(k);
+    s->table[k] = es.second;
+    ++s->st.installs;
+    s->trim();
+    if (miss_ids) miss_ids[placed] = es.first;
+    if (miss_slots) miss_slots[placed] = es.second;
+    ++placed;
+  }
+  *n_miss = placed;
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_slab_stitch(pmoe_slab* s) {
+  pmoe::clear_error();
+  if (!s) return pmoe::fail(PMOE_EINVAL, "slab_stitch: null slab");
+  std::lock_guard<std::mutex> lk(s->mu);
+  if (s->stitched) return 1;
+  const long total = long(s->n_layers) * s->n_experts;
+  if (total > s->slots) return 0;
+  for (int k = 0; k < total; ++k) {
+    if (s->in_lru[k]) continue;
+    const int slot = s->alloc(false);
+    if (slot < 0) return 0;
+    s->slot_of[k] = slot;
+    s->lru_push_back(k);
+    s->table[k] = slot;
+  }
+  for (int k = 0; k < total; ++k) s->stitch_key[k] = 1;
+  s->budget = s->slots;
+  s->st.budget = s->budget;
+  s->stitched = true;
+  return 1;
+}
+
+extern "C" int pmoe_slab_publish(pmoe_slab* s, int layer, void* stream) {
+  pmoe::clear_error();
+  if (!s || layer < 0 || layer >= s->n_layers)
+    return pmoe::fail(PMOE_EINVAL, "slab_publish: bad argument");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  std::lock_guard<std::mutex> lk(s->mu);
+  int rc = ensure_device_table(s);
+  if (rc) return rc;
+  const int32_t* row = s->table.data() + size_t(layer) * s->n_experts;
+  int32_t* dst = s->dtable + size_t(layer) * s->n_experts;
+  for (int off = 0; off < s->n_experts; off += kPublishChunk) {
+    TableChunk c;
+    const int cnt = std::min(kPublishChunk, s->n_experts - off);
+    std::copy_n(row + off, cnt, c.v);
+    publish_kernel<<<(cnt + 255) / 256, 256, 0, st>>>(c, cnt, dst + off);
+    PMOE_LAUNCH_CHECK("publish_kernel");
+  }
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_slab_stats_get(pmoe_slab* s, pmoe_slab_stats* out) {
+  pmoe::clear_error();
+  if (!s || !out) return pmoe::fail(PMOE_EINVAL, "slab_stats: bad argument");
+  std::lock_guard<std::mutex> lk(s->mu);
+  s->st.resident = s->lru_size;
+  s->st.stitched = s->stitched ? 1 : 0;
+  *out = s->st;
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_slab_fetch(pmoe_slab* s, pmoe_copy_engine* ce, const pmoe_geom* g,
+                               void* slab, const void* host_store, int layer, const int32_t* ids,
+                               int n_ids, int* n_miss, void* stream) {
+  pmoe::clear_error();
+  if (!s || !ce || !g || !slab || !host_store || !n_miss || n_ids < 0)
+    return pmoe::fail(PMOE_EINVAL, "slab_fetch: bad argument");
+  std::vector<int32_t> mid(size_t(n_ids) + 1), msl(size_t(n_ids) + 1);
+  int nm = 0;
+  int rc = pmoe_slab_request(s, layer, ids, n_ids, mid.data(), msl.data(), &nm);
+  if (rc) return rc;
+  const size_t eb = size_t(g->expert_bytes);
+  for (int i = 0; i < nm; ++i) {
+    const size_t src = (size_t(layer) * s->n_experts + size_t(mid[i])) * eb;
+    rc = pmoe_copy_submit(ce, static_cast<uint8_t*>(slab) + size_t(msl[i]) * eb,
+                          static_cast<const uint8_t*>(host_store) + src, eb, 1);
+    if (rc) return rc;
+  }
+  {
+    std::lock_guard<std::mutex> lk(s->mu);
+    s->st.bytes_copied += int64_t(nm) * int64_t(eb);
+  }
+  rc = pmoe_slab_publish(s, layer, stream);
+  if (rc) return rc;
+  rc = pmoe_copy_flush(ce, stream);
+  if (rc) return rc;
+  *n_miss = nm;
+  return PMOE_OK;
+}

@@ -1,0 +1,228 @@
+"""torch-tensor wrappers over the libpmoe C ABI (one function per entry point).
+
+Every function takes device tensors, checks dtype/shape/contiguity on the
+host, and enqueues the HIP kernels on torch's current stream.  Packed
+quantized words travel as ``torch.int32`` (same bits as the u32 of the
+format); bf16 data as ``torch.bfloat16``.  There is no CPU path: without the
+built library every call raises ``PmoeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import Geom, RouteCfg, check, lib
+
+_WS: dict = {}
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _need(t, dtype, name, ndim=None):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: must be a device tensor (got {t.device})")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: expected {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name}: expected {ndim} dims, got {tuple(t.shape)}")
+
+
+def workspace(nbytes: int, device) -> torch.Tensor:
+    """A cached uint8 scratch tensor of at least nbytes on device."""
+    key = (torch.device(device).index or 0)
+    buf = _WS.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        _WS[key] = buf
+    return buf
+
+
+# ---------------------------------------------------------------- routing
+
+def router_logits(x: torch.Tensor, w: torch.Tensor, logit_bias=None) -> torch.Tensor:
+    """fp32 logits [N, E] of x [N, D] bf16 against w [E, D] bf16."""
+    _need(x, torch.bfloat16, "x", 2)
+    _need(w, torch.bfloat16, "w", 2)
+    n, d = x.shape
+    e = w.shape[0]
+    if w.shape[1] != d:
+        raise ValueError("router weight hidden size mismatch")
+    if logit_bias is not None:
+        _need(logit_bias, torch.float32, "logit_bias", 1)
+    out = torch.empty((n, e), dtype=torch.float32, device=x.device)
+    check(lib().pmoe_router_logits(_ptr(x), _ptr(w), _ptr(logit_bias), n, d, e, _ptr(out),
+                                   _stream()), "pmoe_router_logits")
+    return out
+
+
+def route_softmax_topk(logits: torch.Tensor, k: int, norm_topk_prob: bool = True):
+    _need(logits, torch.float32, "logits", 2)
+    n, e = logits.shape
+    inds = torch.empty((n, k), dtype=torch.int32, device=logits.device)
+    wts = torch.empty((n, k), dtype=torch.float32, device=logits.device)
+    check(lib().pmoe_route_softmax_topk(_ptr(logits), n, e, k, int(bool(norm_topk_prob)),
+                                        _ptr(inds), _ptr(wts), _stream()),
+          "pmoe_route_softmax_topk")
+    return inds, wts
+
+
+def route_sigmoid_group_topk(logits, bias, n_group: int, topk_group: int, k: int,
+                             norm_topk_prob: bool = True, routed_scale: float = 1.0):
+    _need(logits, torch.float32, "logits", 2)
+    _need(bias, torch.float32, "bias", 1)
+    n, e = logits.shape
+    inds = torch.empty((n, k), dtype=torch.int32, device=logits.device)
+    wts = torch.empty((n, k), dtype=torch.float32, device=logits.device)
+    check(lib().pmoe_route_sigmoid_group_topk(
+        _ptr(logits), _ptr(bias), n, e, n_group, topk_group, k, int(bool(norm_topk_prob)),
+        float(routed_scale), _ptr(inds), _ptr(wts), _stream()), "pmoe_route_sigmoid_group_topk")
+    return inds, wts
+
+
+# ---------------------------------------------------------------- dispatch
+
+def dispatch(inds: torch.Tensor, n_experts: int) -> dict:
+    """Stable grouping of the flat ids by expert (see pmoe_dispatch)."""
+    _need(inds, torch.int32, "inds")
+    rows = inds.numel()
+    dev = inds.device
+    out = {
+        "order": torch.empty(rows, dtype=torch.int32, device=dev),
+        "counts": torch.empty(n_experts, dtype=torch.int32, device=dev),
+        "offsets": torch.empty(n_experts + 1, dtype=torch.int32, device=dev),
+        "inv": torch.empty(rows, dtype=torch.int32, device=dev),
+        "active": torch.empty(n_experts, dtype=torch.int32, device=dev),
+        "n_active": torch.empty(1, dtype=torch.int32, device=dev),
+    }
+    wsb = lib().pmoe_dispatch_workspace(rows, n_experts)
+    ws = workspace(wsb, dev)
+    check(lib().pmoe_dispatch(_ptr(inds), rows, n_experts, _ptr(out["order"]),
+                              _ptr(out["counts"]), _ptr(out["offsets"]), _ptr(out["inv"]),
+                              _ptr(out["active"]), _ptr(out["n_active"]), _ptr(ws), ws.numel(),
+                              _stream()), "pmoe_dispatch")
+    return out
+
+
+# ---------------------------------------------------------------- format
+
+def quantize(w: torch.Tensor, bits: int, group: int = 64):
+    """fp32 [R, C] -> (q int32 [R, C*bits/32], scales bf16, biases bf16)."""
+    _need(w, torch.float32, "w", 2)
+    r, c = w.shape
+    if c % group or (c * bits) % 32:
+        raise ValueError("columns must be a multiple of the group size")
+    q = torch.empty((r, c * bits // 32), dtype=torch.int32, device=w.device)
+    s = torch.empty((r, c // group), dtype=torch.bfloat16, device=w.device)
+    b = torch.empty((r, c // group), dtype=torch.bfloat16, device=w.device)
+    check(lib().pmoe_quantize(_ptr(w), r, c, bits, group, _ptr(q), _ptr(s), _ptr(b), _stream()),
+          "pmoe_quantize")
+    return q, s, b
+
+
+def dequant(q, scales, biases, bits: int, group: int = 64) -> torch.Tensor:
+    _need(q, torch.int32, "q", 2)
+    _need(scales, torch.bfloat16, "scales", 2)
+    _need(biases, torch.bfloat16, "biases", 2)
+    r = q.shape[0]
+    c = q.shape[1] * 32 // bits
+    out = torch.empty((r, c), dtype=torch.bfloat16, device=q.device)
+    check(lib().pmoe_dequant(_ptr(q), _ptr(scales), _ptr(biases), r, c, bits, group, _ptr(out),
+                             _stream()), "pmoe_dequant")
+    return out
+
+
+# ---------------------------------------------------------------- experts
+
+def moe_workspace(g: Geom, n: int, k: int, shared: int, n_experts: int, device) -> torch.Tensor:
+    nb = lib().pmoe_moe_workspace(ctypes.byref(g), n, k, shared, n_experts)
+    return workspace(nb, device)
+
+
+def _table_ptr(table):
+    if isinstance(table, torch.Tensor):
+        _need(table, torch.int32, "table", 1)
+        return _ptr(table)
+    return ctypes.c_void_p(int(table))
+
+
+def switch_glu(g: Geom, slab: torch.Tensor, table, n_experts: int, x: torch.Tensor,
+               inds: torch.Tensor) -> torch.Tensor:
+    """y [N, K, D] bf16: row (n, k) through the expert in slot table[inds[n, k]]."""
+    _need(x, torch.bfloat16, "x", 2)
+    _need(inds, torch.int32, "inds", 2)
+    n, k = inds.shape
+    if x.shape != (n, g.hidden):
+        raise ValueError(f"x must be [{n}, {g.hidden}], got {tuple(x.shape)}")
+    y = torch.empty((n, k, g.hidden), dtype=torch.bfloat16, device=x.device)
+    ws = moe_workspace(g, n, k, 0, n_experts, x.device)
+    check(lib().pmoe_switch_glu(ctypes.byref(g), _ptr(slab), _table_ptr(table), n_experts,
+                                _ptr(x), _ptr(inds), n, k, _ptr(y), _ptr(ws), ws.numel(),
+                                _stream()), "pmoe_switch_glu")
+    return y
+
+
+def moe_experts(g: Geom, slab, table, n_experts: int, x, inds, weights, shared_slot: int = -1,
+                shared_gate=None) -> torch.Tensor:
+    """out [N, D] bf16 = sum_k w[n,k] FFN_{inds[n,k]}(x[n]) (+ shared)."""
+    _need(x, torch.bfloat16, "x", 2)
+    _need(inds, torch.int32, "inds", 2)
+    _need(weights, torch.float32, "weights", 2)
+    n, k = inds.shape
+    out = torch.empty((n, g.hidden), dtype=torch.bfloat16, device=x.device)
+    ws = moe_workspace(g, n, k, int(shared_slot >= 0), n_experts, x.device)
+    check(lib().pmoe_moe_experts(ctypes.byref(g), _ptr(slab), _table_ptr(table), n_experts,
+                                 _ptr(x), _ptr(inds), _ptr(weights), n, k, int(shared_slot),
+                                 _ptr(shared_gate), _ptr(out), _ptr(ws), ws.numel(), _stream()),
+          "pmoe_moe_experts")
+    return out
+
+
+def route_cfg(scoring: str, n_experts: int, top_k: int, norm_topk_prob: bool = True,
+              n_group: int = 1, topk_group: int = 1, routed_scale: float = 1.0) -> RouteCfg:
+    rc = RouteCfg()
+    rc.scoring = _lib.SCORE_SOFTMAX if scoring == "softmax" else _lib.SCORE_SIGMOID
+    rc.n_experts = n_experts
+    rc.top_k = top_k
+    rc.norm_topk_prob = int(bool(norm_topk_prob))
+    rc.n_group = n_group
+    rc.topk_group = topk_group
+    rc.routed_scale = float(routed_scale)
+    return rc
+
+
+def moe_block(g: Geom, rc: RouteCfg, slab, table, gate_w, x, score_bias=None, logit_bias=None,
+              shared_slot: int = -1, shared_gate=None, out=None, inds=None, weights=None,
+              ws=None):
+    """Route -> dispatch -> experts -> combine in one call.  Returns
+    (out [N, D] bf16, inds [N, K] int32, weights [N, K] fp32)."""
+    _need(x, torch.bfloat16, "x", 2)
+    _need(gate_w, torch.bfloat16, "gate_w", 2)
+    n = x.shape[0]
+    k = rc.top_k
+    dev = x.device
+    if out is None:
+        out = torch.empty((n, g.hidden), dtype=torch.bfloat16, device=dev)
+    if inds is None:
+        inds = torch.empty((n, k), dtype=torch.int32, device=dev)
+    if weights is None:
+        weights = torch.empty((n, k), dtype=torch.float32, device=dev)
+    if ws is None:
+        ws = moe_workspace(g, n, k, int(shared_slot >= 0), rc.n_experts, dev)
+    check(lib().pmoe_moe_block(ctypes.byref(g), ctypes.byref(rc), _ptr(slab), _table_ptr(table),
+                               _ptr(gate_w), _ptr(score_bias), _ptr(logit_bias), _ptr(x), n,
+                               int(shared_slot), _ptr(shared_gate), _ptr(out), _ptr(inds),
+                               _ptr(weights), _ptr(ws), ws.numel(), _stream()), "pmoe_moe_block")
+    return out, inds, weights
