@@ -1,0 +1,307 @@
+#!/usr/bin/env python3
+"""MoE-layer throughput of the routed-expert hot path on one MI355X.
+
+One step = one MoE layer (router -> top-k -> dispatch -> quantized SwiGLU
+experts -> combine) over one batch of tokens.  Default workload: the
+Qwen3-235B-A22B-shaped decode layer (hidden 4096, 128 experts,
+moe_intermediate 1536, top-8 softmax+renorm, 4-bit affine g64, bf16 scales and
+biases, all experts resident in the HBM slab), batch 1 (batch 8 reported in
+"extra").  Weights are synthetic: N(0, 0.02) quantized on the GPU; activations
+N(0, 1) bf16; every step routes a fresh token.  Steps cycle over `--layers`
+distinct layers (default 8, ~11 GB of experts) so no step finds the previous
+step's experts in the 256 MB last-level cache.
+
+The timed loop replays a HIP graph of `--layers` x 4 consecutive layer steps
+(launch overhead excluded, as in the reference's one-graph-per-token decode);
+inputs are resident in HBM before timing starts.  A second, eager pass
+brackets every kernel with HIP events to give the dominant kernel's average
+duration, from which roofline.achieved = algorithmic expert-weight bytes per
+launch / that duration.
+
+Prints ONE JSON line.  `--gpus N` with N > 1 exits: this build runs on one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+WORKLOADS = {
+    "qwen3-235b-decode": dict(hidden=4096, experts=128, inter=1536, top_k=8, bits=4,
+                              scoring="softmax"),
+}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_layers(g, spec, n_layers, device, seed=0):
+    """Slab with n_layers * E slots (slot = layer*E + e), router weights and
+    the per-layer expert->slot tables."""
+    import torch
+
+    from pagedmoe_amd import kernels as K
+    from pagedmoe_amd.slab import SlabStore
+
+    E, D, I = spec["experts"], spec["hidden"], spec["inter"]
+    slab = SlabStore(g, n_layers * E, device, zero=False)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    for slot in range(n_layers * E):
+        comps = {}
+        for prefix, rows, cols in (("gate_proj", I, D), ("up_proj", I, D), ("down_proj", D, I)):
+            w = torch.randn((rows, cols), generator=gen, device=device) * 0.02
+            q, s, b = K.quantize(w, g.bits)
+            comps[prefix + ".weight"] = q
+            comps[prefix + ".scales"] = s
+            comps[prefix + ".biases"] = b
+        slab.write_expert(slot, comps)
+    gate = (torch.randn((n_layers, E, D), generator=gen, device=device) * 0.02).to(torch.bfloat16)
+    tables = (torch.arange(n_layers, device=device, dtype=torch.int32)[:, None] * E
+              + torch.arange(E, device=device, dtype=torch.int32)[None, :]).contiguous()
+    return slab, gate, tables
+
+
+def run_decode(args, g, spec, slab, gate, tables, batch, device):
+    import torch
+
+    from pagedmoe_amd import kernels as K
+    from pagedmoe_amd._lib import KernelTimer
+
+    E, D, k = spec["experts"], spec["hidden"], spec["top_k"]
+    L = args.layers
+    seq = L * 4                                   # layer steps per graph
+    rc = K.route_cfg(spec["scoring"], E, k)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(1000 + batch)
+    x = torch.randn((seq, batch, D), generator=gen, device=device).to(torch.bfloat16)
+    out = torch.empty((seq, batch, D), dtype=torch.bfloat16, device=device)
+    inds = torch.empty((seq, batch, k), dtype=torch.int32, device=device)
+    wts = torch.empty((seq, batch, k), dtype=torch.float32, device=device)
+    ws = K.moe_workspace(g, batch, k, 0, E, device)
+    ws = ws.clone()                               # private workspace for the graph
+
+    def step(i):
+        layer = i % L
+        K.moe_block(g, rc, slab.buf, tables[layer], gate[layer], x[i], out=out[i],
+                    inds=inds[i], weights=wts[i], ws=ws)
+
+    def run_seq():
+        for i in range(seq):
+            step(i)
+
+    # eager warmup (also validates the call path)
+    for _ in range(max(1, args.warmup // seq + 1)):
+        run_seq()
+    torch.cuda.synchronize()
+
+    # per-kernel durations: eager pass with event brackets
+    with KernelTimer() as kt:
+        for _ in range(max(1, args.steps // seq)):
+            run_seq()
+    torch.cuda.synchronize()
+    reps_timer = max(1, args.steps // seq)
+
+    # graph of `seq` layer steps
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run_seq()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        run_seq()
+    for _ in range(max(1, args.warmup // seq)):
+        graph.replay()
+    torch.cuda.synchronize()
+    reps = max(1, args.steps // seq)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        graph.replay()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    steps_timed = reps * seq
+    ms = (t1 - t0) * 1e3 / steps_timed
+
+    # eager wall time for transparency
+    torch.cuda.synchronize()
+    e0 = time.perf_counter()
+    run_seq()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - e0) * 1e3 / seq
+
+    # algorithmic bytes: distinct experts per step x per-expert bytes
+    ids = inds.cpu().numpy().reshape(seq, -1)
+    uniq = [len(set(r.tolist())) for r in ids]
+    mean_unique = sum(uniq) / len(uniq)
+    gateup_bytes = int(g.nbytes[0] + g.nbytes[1] + g.nbytes[2]) * 2
+    down_bytes = int(g.nbytes[6] + g.nbytes[7] + g.nbytes[8])
+    res = {
+        "batch": batch,
+        "ms_per_step": ms,
+        "tokens_per_s": batch / (ms / 1e3),
+        "steps_timed": steps_timed,
+        "eager_ms_per_step": eager_ms,
+        "mean_unique_experts": mean_unique,
+        "expert_bytes_per_step": mean_unique * int(g.expert_bytes),
+        "kernels": {},
+    }
+    for name, (tot, cnt) in kt.result.items():
+        res["kernels"][name] = {"avg_us": tot * 1e3 / cnt, "launches": cnt}
+    # kernel launches in the timer pass = reps_timer * seq; each processed the
+    # distinct experts of its step
+    step_bytes_gu = mean_unique * gateup_bytes
+    step_bytes_dn = mean_unique * down_bytes
+    ku = res["kernels"].get("qgemv_gateup")
+    kd = res["kernels"].get("qgemv_down")
+    if ku:
+        res["gateup_gbs"] = step_bytes_gu / (ku["avg_us"] * 1e-6) / 1e9
+    if kd:
+        res["down_gbs"] = step_bytes_dn / (kd["avg_us"] * 1e-6) / 1e9
+    res["layer_expert_gbs"] = res["expert_bytes_per_step"] / (ms * 1e-3) / 1e9
+    res["_gateup_step_bytes"] = step_bytes_gu
+    del reps_timer
+    return res
+
+
+def cpu_baseline(g, spec, slab, gate, seconds, device):
+    """The oracle's C restatement (OpenMP over all host cores) running the
+    same decode layer (layer 0's 128 experts, fresh tokens) for ~seconds."""
+    import numpy as np
+    import torch
+
+    from oracle import c_oracle as C
+    from oracle import pmoe_oracle as O
+
+    E = spec["experts"]
+
+    def qt(prefix, slot, cols):
+        w = slab.expert(prefix + ".weight", slot).cpu().numpy().view(np.uint32)
+        s = slab.expert(prefix + ".scales", slot).cpu().view(torch.int16).numpy().view(np.uint16)
+        b = slab.expert(prefix + ".biases", slot).cpu().view(torch.int16).numpy().view(np.uint16)
+        return O.QTensor(np.ascontiguousarray(w), np.ascontiguousarray(s),
+                         np.ascontiguousarray(b), g.bits, g.group, cols)
+
+    experts = [O.Expert(qt("gate_proj", e, g.hidden), qt("up_proj", e, g.hidden),
+                        qt("down_proj", e, g.inter)) for e in range(E)]
+    gw = gate[0].cpu().view(torch.int16).numpy().view(np.uint16)
+    layer = C.DecodeLayer(gw, experts, g.hidden, g.inter, spec["top_k"], g.bits)
+    rng = np.random.default_rng(7)
+    layer(O.bf16_round(rng.standard_normal((1, g.hidden), dtype=np.float32)))  # warm
+    tokens = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        layer(O.bf16_round(rng.standard_normal((1, g.hidden), dtype=np.float32)))
+        tokens += 1
+    dt = time.perf_counter() - t0
+    return {"value": tokens / dt, "unit": "tokens/s", "cores": C.threads(), "kind": "port",
+            "sample": f"{tokens} decode tokens (batch 1) through one Qwen3-235B-shaped MoE layer "
+                      f"(128 resident experts, 4-bit g64) in {dt:.1f} s; C restatement of the "
+                      f"oracle, OpenMP over {C.threads()} threads; the reference's mlx CPU path "
+                      f"is not installable here"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=640)
+    ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--workload", default="qwen3-235b-decode", choices=sorted(WORKLOADS))
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--layers", type=int, default=8)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the batch-8 line in extra")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus > 1 or world > 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE "
+              f"{world}); the expert-parallel split is a design note, not built here.",
+              file=sys.stderr, flush=True)
+        sys.exit(2)
+
+    import torch
+
+    from pagedmoe_amd._lib import geom
+
+    device = "cuda:0"
+    spec = WORKLOADS[args.workload]
+    g = geom(spec["hidden"], spec["inter"], spec["bits"])
+    log(f"building {args.layers} layers x {spec['experts']} experts "
+        f"({args.layers * spec['experts'] * g.expert_bytes / 1e9:.1f} GB)")
+    t0 = time.perf_counter()
+    slab, gate, tables = build_layers(g, spec, args.layers, device)
+    torch.cuda.synchronize()
+    log(f"built in {time.perf_counter() - t0:.1f} s")
+
+    main_res = run_decode(args, g, spec, slab, gate, tables, args.batch, device)
+    log(f"batch {args.batch}: {main_res['ms_per_step'] * 1e3:.1f} us/step, "
+        f"{main_res['tokens_per_s']:.0f} tok/s, kernels {main_res['kernels']}")
+    extra = {}
+    if not args.no_extra and args.batch != 8:
+        r8 = run_decode(args, g, spec, slab, gate, tables, 8, device)
+        log(f"batch 8: {r8['ms_per_step'] * 1e3:.1f} us/step, {r8['tokens_per_s']:.0f} tok/s")
+        r8.pop("_gateup_step_bytes", None)
+        extra["decode_batch8"] = r8
+
+    ku = main_res["kernels"]["qgemv_gateup"]
+    achieved = main_res["gateup_gbs"]
+    roofline = {"bound": "hbm", "kernel": "qgemv_kernel (gate+up, dual)",
+                "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                "avg_launch_us": ku["avg_us"],
+                "algorithmic_bytes_per_launch": main_res["_gateup_step_bytes"]}
+    traffic_file = ROOT / "profiles" / f"traffic_{args.workload}_b{args.batch}.json"
+    if traffic_file.exists():
+        try:
+            roofline["traffic"] = json.loads(traffic_file.read_text()).get("bytes_per_launch")
+        except (ValueError, OSError):
+            pass
+    main_res.pop("_gateup_step_bytes", None)
+
+    cpu = None
+    if not args.no_cpu:
+        log(f"cpu baseline: ~{args.cpu_seconds:.0f} s")
+        cpu = cpu_baseline(g, spec, slab, gate, args.cpu_seconds, device)
+        log(f"cpu baseline: {cpu['value']:.1f} tok/s on {cpu['cores']} threads")
+
+    line = {
+        "metric": "MoE-layer tokens/s + % HBM roofline (decode) / % MFMA peak (prefill)",
+        "value": main_res["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": main_res["steps_timed"],
+        "warmup": args.warmup,
+        "ms_per_step": main_res["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 activations, 4-bit affine g64 weights, fp32 accumulate",
+        "data": "synthetic: N(0,0.02) weights quantized on the GPU, N(0,1) bf16 tokens",
+        "config": {"workload": "Qwen3-235B-A22B-shaped MoE layer decode", "hidden": 4096,
+                   "experts": 128, "moe_intermediate": 1536, "top_k": 8,
+                   "routing": "softmax+renorm", "bits": 4, "group": 64,
+                   "batch": args.batch, "layers_cycled": args.layers,
+                   "timing": "HIP graph replay of layer steps"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": {"decode": main_res, **extra},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

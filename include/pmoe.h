@@ -257,6 +257,18 @@ int pmoe_slab_fetch(pmoe_slab* s, pmoe_copy_engine* ce, const pmoe_geom* g,
                     void* slab, const void* host_store, int layer,
                     const int32_t* ids, int n_ids, int* n_miss, void* stream);
 
+/* ---- kernel timing --------------------------------------------------------
+ * No reference counterpart (the reference splits a token's wall time with
+ * host-side wrappers, bench/decode_profile.py).  While a profile is open,
+ * every kernel launch of the library is bracketed by HIP events on its own
+ * stream; pmoe_profile_end synchronises them and accumulates per-kernel time.
+ * Kernel ids are 0..pmoe_profile_kernels()-1. */
+int pmoe_profile_begin(int capacity);
+int pmoe_profile_end(void);
+int pmoe_profile_kernels(void);
+const char* pmoe_profile_name(int kernel);
+int pmoe_profile_read(int kernel, double* total_ms, int64_t* launches);
+
 #ifdef __cplusplus
 }
 #endif

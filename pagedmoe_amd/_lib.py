@@ -100,6 +100,11 @@ SIGNATURES = {
     "pmoe_copy_bytes": (ctypes.c_int64, [_P]),
     "pmoe_slab_fetch": (_I, [_P, _P, ctypes.POINTER(Geom), _P, _P, _I, _I32P, _I,
                              ctypes.POINTER(_I), _P]),
+    "pmoe_profile_begin": (_I, [_I]),
+    "pmoe_profile_end": (_I, []),
+    "pmoe_profile_kernels": (_I, []),
+    "pmoe_profile_name": (ctypes.c_char_p, [_I]),
+    "pmoe_profile_read": (_I, [_I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]),
 }
 
 _lib = None
@@ -135,3 +140,28 @@ def geom(hidden: int, inter: int, bits: int, group: int = 64) -> Geom:
     g = Geom()
     check(lib().pmoe_geom_init(ctypes.byref(g), hidden, inter, bits, group), "pmoe_geom_init")
     return g
+
+
+class KernelTimer:
+    """Context manager: per-kernel HIP-event time of every libpmoe launch in
+    the block (pmoe_profile_*).  ``result`` maps kernel name ->
+    (total_ms, launches)."""
+
+    def __init__(self, capacity: int = 65536):
+        self.capacity = capacity
+        self.result: dict = {}
+
+    def __enter__(self):
+        check(lib().pmoe_profile_begin(self.capacity), "pmoe_profile_begin")
+        return self
+
+    def __exit__(self, *exc):
+        L = lib()
+        check(L.pmoe_profile_end(), "pmoe_profile_end")
+        for k in range(L.pmoe_profile_kernels()):
+            ms = ctypes.c_double()
+            cnt = ctypes.c_int64()
+            check(L.pmoe_profile_read(k, ctypes.byref(ms), ctypes.byref(cnt)), "pmoe_profile_read")
+            if cnt.value:
+                self.result[L.pmoe_profile_name(k).decode()] = (ms.value, cnt.value)
+        return False

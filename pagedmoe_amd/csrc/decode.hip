@@ -288,6 +288,7 @@ int qgemv(const GemvArgs& a, int bits, bool dual, int max_experts, int max_rows_
   PMOE_REQUIRE(a.rows_per_block % (4 * (64 / sh.lpr)) == 0, "qgemv: bad rows_per_block");
   if (max_experts <= 0 || a.rows_out <= 0) return PMOE_OK;
   dim3 grid((a.rows_out + a.rows_per_block - 1) / a.rows_per_block, max_experts);
+  ProfScope prof_scope(dual ? K_GATEUP : K_DOWN, st);
   if (bits == 4)
     return dual ? launch_shape<4, true>(a, sh, max_rows_per_expert, grid, st)
                 : launch_shape<4, false>(a, sh, max_rows_per_expert, grid, st);

@@ -222,6 +222,7 @@ int dispatch_ext(const int32_t* inds, int rows, int k_routed, int kk, int n_ids,
   PMOE_REQUIRE(k_routed >= 1 && kk >= k_routed && kk <= k_routed + 1, "dispatch: bad columns");
   PMOE_REQUIRE(rows % kk == 0, "dispatch: rows must be a multiple of the columns");
   const IdSrc src{inds, k_routed, kk, kk > k_routed ? n_ids - 1 : n_ids};
+  ProfScope prof_scope(K_DISPATCH, st);
   if (rows <= kSmallRows) {
     dispatch_small_kernel<<<1, 1024, 0, st>>>(src, rows, n_ids, order, counts, offsets, inv,
                                               active, n_active, tile_m, tiles, n_tiles);

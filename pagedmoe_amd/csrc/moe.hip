@@ -200,6 +200,7 @@ int experts_and_combine(const pmoe_geom* g, const uint8_t* slab, const int32_t* 
     sl = w.shared_logit;
   }
   dim3 grid((g->hidden / 4 + 255) / 256, n);
+  ProfScope prof_scope(K_COMBINE, st);
   combine_kernel<<<grid, 256, 0, st>>>(w.y, wts, w.inv, sl, shared, k, kk, g->hidden, out);
   PMOE_LAUNCH_CHECK("combine_kernel");
   return PMOE_OK;

@@ -5,6 +5,30 @@
 
 namespace pmoe {
 
+// Kernel ids of the timing hooks (pmoe_profile_*).
+enum KernelId {
+  K_ROUTER_LOGITS = 0,
+  K_ROUTE_SELECT,
+  K_DISPATCH,
+  K_GATEUP,
+  K_DOWN,
+  K_COMBINE,
+  K_PREFILL_GATEUP,
+  K_PREFILL_DOWN,
+  K_COUNT
+};
+
+// Brackets the launches in its scope with events when a profile is open.
+class ProfScope {
+ public:
+  ProfScope(int id, hipStream_t st);
+  ~ProfScope();
+
+ private:
+  int slot_;
+  hipStream_t st_;
+};
+
 // Component offsets of one projection inside a slab slot.
 struct QProj {
   int64_t w, s, b;

@@ -11,6 +11,7 @@
 // acc = fma(x_d, w_d, acc) for t ascending, j ascending (one 16-byte load of
 // x and of w per t); the 64 lane partials are combined by an xor butterfly.
 #include "pmoe_internal.h"
+#include "pmoe_kernels.h"
 
 namespace pmoe {
 
@@ -252,6 +253,7 @@ int router_logits(const uint16_t* x, const uint16_t* w, const float* bias, int n
   PMOE_REQUIRE(n >= 0 && d > 0 && e > 0, "router_logits: bad shape");
   PMOE_REQUIRE(d % 8 == 0, "router_logits: hidden must be a multiple of 8");
   if (n == 0) return PMOE_OK;
+  ProfScope prof_scope(K_ROUTER_LOGITS, st);
   if (n >= 32) {
     constexpr int TE = 4, TN = 8;
     dim3 grid((e + kRouterWaves * TE - 1) / (kRouterWaves * TE), (n + TN - 1) / TN);
@@ -275,6 +277,7 @@ int route_softmax(const float* logits, int n, int e, int k, int norm, int32_t* i
   PMOE_REQUIRE(e > 0 && e <= 64 * kMaxEPL, "route_softmax_topk: experts must be 1..1024");
   PMOE_REQUIRE(k > 0 && k <= kMaxK && k <= e, "route_softmax_topk: k must be 1..min(16, E)");
   if (n <= 0) return PMOE_OK;
+  ProfScope prof_scope(K_ROUTE_SELECT, st);
   route_softmax_kernel<<<(n + 3) / 4, 256, 0, st>>>(logits, n, e, k, norm, inds, weights);
   PMOE_LAUNCH_CHECK("route_softmax_kernel");
   return PMOE_OK;
@@ -295,6 +298,7 @@ int route_sigmoid(const float* logits, const float* bias, int n, int e, int n_gr
   PMOE_REQUIRE(k <= (e / n_group) * topk_group,
                "route_sigmoid_group_topk: k exceeds the experts of the kept groups");
   if (n <= 0) return PMOE_OK;
+  ProfScope prof_scope(K_ROUTE_SELECT, st);
   route_sigmoid_kernel<<<(n + 3) / 4, 256, 0, st>>>(logits, bias, n, e, n_group, topk_group, k,
                                                     norm, scale, inds, weights);
   PMOE_LAUNCH_CHECK("route_sigmoid_kernel");
