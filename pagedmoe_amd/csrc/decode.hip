@@ -123,9 +123,14 @@ __device__ __forceinline__ float group_term(float acc, float s, float b, float x
   return __builtin_fmaf(s, acc, __builtin_fmaf(b - 128.0f * s, xs, part));
 }
 
-template <int BITS, int LPR, int GPL, int MT, bool DUAL>
-__global__ __launch_bounds__(256) void qgemv_kernel(const GemvArgs a) {
-  constexpr int RPW = 64 / LPR;  // rows per wave step
+// Rows per wave step RPW = 64/LPR; a wave owns R consecutive steps.  All of
+// its packed weights (R steps x GPL groups x 1-2 projections) are requested
+// before anything else, so every wave has its whole share of HBM traffic in
+// flight while the activations are still arriving from L2.
+template <int BITS, int LPR, int GPL, int MT, int R, bool DUAL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void qgemv_kernel(
+    const GemvArgs a) {
+  constexpr int RPW = 64 / LPR;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int sub = lane % LPR;
@@ -138,17 +143,14 @@ __global__ __launch_bounds__(256) void qgemv_kernel(const GemvArgs a) {
   const int32_t* rlist = a.order + a.offsets[e];
   const int groups = a.cols / 64;
   const int wpr = a.cols * BITS / 32;
-
-  const int row0 = blockIdx.x * a.rows_per_block;
-  const int rows_per_wave = a.rows_per_block / 4;
-  const int wrow0 = row0 + wave * rows_per_wave;
-  const int steps = rows_per_wave / RPW;
+  const int row0 = blockIdx.x * (4 * R * RPW);
+  const int wrow0 = row0 + wave * (R * RPW);
 
   if (slot < 0) {
     // Not resident: this expert contributes exact zero rows.
     for (int m = 0; m < m_total; ++m) {
       const int r = rlist[m];
-      for (int i = threadIdx.x; i < a.rows_per_block; i += 256) {
+      for (int i = threadIdx.x; i < 4 * R * RPW; i += 256) {
         const int o = row0 + i;
         if (o >= a.rows_out) break;
         if (a.out_f32)
@@ -167,9 +169,11 @@ __global__ __launch_bounds__(256) void qgemv_kernel(const GemvArgs a) {
   const uint16_t* S1 = reinterpret_cast<const uint16_t*>(base + a.p1.s);
   const uint16_t* B1 = reinterpret_cast<const uint16_t*>(base + a.p1.b);
 
-  for (int m0 = 0; m0 < m_total; m0 += MT) {
-    GroupAct<BITS> act[MT][GPL];
-    int rr[MT];
+  // Activations first (L2 hits), then the weight burst: vector loads retire
+  // in order, so row 0 can start as soon as its own words have landed.
+  GroupAct<BITS> act[MT][GPL];
+  int rr[MT];
+  auto load_act = [&](int m0) {
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
       const int m = min(m0 + t, m_total - 1);
@@ -182,29 +186,59 @@ __global__ __launch_bounds__(256) void qgemv_kernel(const GemvArgs a) {
         load_group_act<BITS>(src + size_t(g) * 64, act[t][j]);
       }
     }
-    for (int st = 0; st < steps; ++st) {
+  };
+  load_act(0);
+  __builtin_amdgcn_sched_barrier(0);
+  GroupW<BITS> q0[R][GPL];
+  GroupW<BITS> q1[DUAL ? R : 1][DUAL ? GPL : 1];
+#pragma unroll
+  for (int st = 0; st < R; ++st) {
+    const int o = min(wrow0 + st * RPW + rsub, a.rows_out - 1);
+#pragma unroll
+    for (int j = 0; j < GPL; ++j) {
+      const int g = min(sub + LPR * j, groups - 1);
+      load_group_w<BITS>(W0 + size_t(o) * wpr, S0 + size_t(o) * groups, B0 + size_t(o) * groups,
+                         g, q0[st][j]);
+      if (DUAL)
+        load_group_w<BITS>(W1 + size_t(o) * wpr, S1 + size_t(o) * groups,
+                           B1 + size_t(o) * groups, g, q1[DUAL ? st : 0][DUAL ? j : 0]);
+    }
+  }
+
+  __builtin_amdgcn_sched_barrier(0);
+
+  for (int m0 = 0; m0 < m_total; m0 += MT) {
+    if (m0 > 0) {
+      load_act(m0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int st = 0; st < R; ++st) {
+      // Opaque to the optimiser: without this the unpacked pairs of every
+      // row are hoisted out of the token loop and spill.
+#pragma unroll
+      for (int j = 0; j < GPL; ++j) {
+#pragma unroll
+        for (int c = 0; c < GroupW<BITS>::kWords; ++c) {
+          asm volatile("" : "+v"(q0[st][j].w[c]));
+          if (DUAL) asm volatile("" : "+v"(q1[DUAL ? st : 0][DUAL ? j : 0].w[c]));
+        }
+      }
       const int o = wrow0 + st * RPW + rsub;
-      const bool row_ok = o < a.rows_out;
-      const int oc = row_ok ? o : a.rows_out - 1;
       float p0[MT], p1[MT];
 #pragma unroll
       for (int t = 0; t < MT; ++t) p0[t] = p1[t] = 0.0f;
 #pragma unroll
       for (int j = 0; j < GPL; ++j) {
-        const int g = sub + LPR * j;
-        if (g < groups) {
-          GroupW<BITS> q0, q1;
-          load_group_w<BITS>(W0 + size_t(oc) * wpr, S0 + size_t(oc) * groups,
-                             B0 + size_t(oc) * groups, g, q0);
-          if (DUAL)
-            load_group_w<BITS>(W1 + size_t(oc) * wpr, S1 + size_t(oc) * groups,
-                               B1 + size_t(oc) * groups, g, q1);
+        if (sub + LPR * j < groups) {
 #pragma unroll
           for (int t = 0; t < MT; ++t) {
-            p0[t] = group_term(group_dot<BITS>(q0, act[t][j]), q0.s, q0.b, act[t][j].sum, p0[t]);
-            if (DUAL)
-              p1[t] =
-                  group_term(group_dot<BITS>(q1, act[t][j]), q1.s, q1.b, act[t][j].sum, p1[t]);
+            p0[t] = group_term(group_dot<BITS>(q0[st][j], act[t][j]), q0[st][j].s, q0[st][j].b,
+                               act[t][j].sum, p0[t]);
+            if (DUAL) {
+              const GroupW<BITS>& w1 = q1[DUAL ? st : 0][DUAL ? j : 0];
+              p1[t] = group_term(group_dot<BITS>(w1, act[t][j]), w1.s, w1.b, act[t][j].sum, p1[t]);
+            }
           }
         }
       }
@@ -216,7 +250,7 @@ __global__ __launch_bounds__(256) void qgemv_kernel(const GemvArgs a) {
           const float u1 = group_sum<LPR>(p1[t]);
           v = silu_fast(g0) * u1;
         }
-        if (sub == t && row_ok && m0 + t < m_total) {
+        if (sub == t && o < a.rows_out && m0 + t < m_total) {
           const size_t idx = size_t(rr[t]) * a.out_stride + o;
           if (a.out_f32)
             static_cast<float*>(a.out)[idx] = v;
@@ -228,54 +262,204 @@ __global__ __launch_bounds__(256) void qgemv_kernel(const GemvArgs a) {
   }
 }
 
+// Down projection + weighted combine for the decode block path.
+//
+// Tile-major: block b owns output rows [b*T, b*T + T) of the hidden dim for
+// every active expert; wave w takes experts w, w+4, ...  Each (flat row r,
+// output o) value lands in LDS, and once all experts are done the block
+// forms out[n, o] = sum_c w[n, c] * y[n*kk + c, o] for c = 0..kk-1 in that
+// fixed order (shared expert last), so the combine needs no y buffer, no
+// separate launch and no cross-block synchronisation, and every block does
+// the same amount of work.
+template <int BITS, int LPR, int GPL, int R>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void
+down_combine_kernel(const GemvArgs a, const CombineArgs c) {
+  constexpr int RPW = 64 / LPR;
+  constexpr int T = R * RPW;
+  extern __shared__ float s_y[];  // [rows][T]
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int sub = lane % LPR;
+  const int rsub = lane / LPR;
+  const int row0 = blockIdx.x * T;
+  const int groups = a.cols / 64;
+  const int wpr = a.cols * BITS / 32;
+  const int n_act = *a.n_active;
+
+  for (int u = wave; u < n_act; u += 4) {
+    const int e = a.active[u];
+    const int slot = e < a.n_experts ? a.table[e] : a.shared_slot;
+    const int m_total = a.counts[e];
+    const int32_t* rlist = a.order + a.offsets[e];
+    if (slot < 0) {
+      for (int m = 0; m < m_total; ++m)
+        for (int t = lane; t < T; t += 64) s_y[rlist[m] * T + t] = 0.0f;
+      continue;
+    }
+    const uint8_t* base = a.slab + size_t(slot) * a.expert_bytes;
+    const uint32_t* W0 = reinterpret_cast<const uint32_t*>(base + a.p0.w);
+    const uint16_t* S0 = reinterpret_cast<const uint16_t*>(base + a.p0.s);
+    const uint16_t* B0 = reinterpret_cast<const uint16_t*>(base + a.p0.b);
+    GroupAct<BITS> act[GPL];
+    int r = rlist[0];
+#pragma unroll
+    for (int j = 0; j < GPL; ++j) {
+      const int g = min(sub + LPR * j, groups - 1);
+      load_group_act<BITS>(a.act + size_t(r) * a.act_stride + size_t(g) * 64, act[j]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    GroupW<BITS> q0[R][GPL];
+#pragma unroll
+    for (int st = 0; st < R; ++st) {
+      const int o = min(row0 + st * RPW + rsub, a.rows_out - 1);
+#pragma unroll
+      for (int j = 0; j < GPL; ++j) {
+        const int g = min(sub + LPR * j, groups - 1);
+        load_group_w<BITS>(W0 + size_t(o) * wpr, S0 + size_t(o) * groups,
+                           B0 + size_t(o) * groups, g, q0[st][j]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    for (int m = 0; m < m_total; ++m) {
+      if (m > 0) {
+        r = rlist[m];
+#pragma unroll
+        for (int j = 0; j < GPL; ++j) {
+          const int g = min(sub + LPR * j, groups - 1);
+          load_group_act<BITS>(a.act + size_t(r) * a.act_stride + size_t(g) * 64, act[j]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int st = 0; st < R; ++st) {
+#pragma unroll
+        for (int j = 0; j < GPL; ++j)
+#pragma unroll
+          for (int cw = 0; cw < GroupW<BITS>::kWords; ++cw) asm volatile("" : "+v"(q0[st][j].w[cw]));
+        float p0 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < GPL; ++j)
+          if (sub + LPR * j < groups)
+            p0 = group_term(group_dot<BITS>(q0[st][j], act[j]), q0[st][j].s, q0[st][j].b,
+                            act[j].sum, p0);
+        const float y = group_sum<LPR>(p0);
+        if (sub == 0) s_y[r * T + st * RPW + rsub] = y;
+      }
+    }
+  }
+  __syncthreads();
+  // fixed-order combine of this tile
+  for (int i = threadIdx.x; i < c.n * T; i += 256) {
+    const int n = i / T, t = i - n * T;
+    const int o = row0 + t;
+    if (o >= a.rows_out) continue;
+    float acc = 0.0f;
+    for (int col = 0; col < a.kk; ++col) {
+      float wt;
+      if (col < c.k)
+        wt = c.w[size_t(n) * c.k + col];
+      else
+        wt = c.shared_logit ? psigmoid(c.shared_logit[n]) : 1.0f;
+      acc = __builtin_fmaf(wt, s_y[(n * a.kk + col) * T + t], acc);
+    }
+    c.out[size_t(n) * a.rows_out + o] = f2bf(acc);
+  }
+}
+
 struct Shape {
   int lpr, gpl;
 };
 
-// Lanes per row (a power of two) and groups per lane for a row of `groups`
-// quant groups: a lane owns groups sub, sub+LPR, ... so x for its groups stays
-// in registers across every row the wave visits.
+// Lanes per row: the smallest power of two >= groups (max 64), so a lane
+// owns one quant group (two for rows of 65..128 groups) and keeps that
+// group's activations in registers for every row the wave visits.
 Shape pick_shape(int groups) {
-  if (groups == 8 || groups == 16 || groups == 32 || groups == 64) return {groups, 1};
-  if (groups % 8 == 0 && groups / 8 <= 4) return {8, groups / 8};
-  if (groups <= 64) return {64, 1};
-  if (groups <= 128) return {64, 2};
-  return {0, 0};
+  if (groups <= 0 || groups > 128) return {0, 0};
+  int lpr = 8;
+  while (lpr < groups && lpr < 64) lpr <<= 1;
+  return {lpr, (groups + lpr - 1) / lpr};
 }
 
-template <int BITS, int LPR, int GPL, bool DUAL>
-int launch_mt(const GemvArgs& a, int max_rows_per_expert, dim3 grid, hipStream_t st) {
-  // activation registers: MT tokens x GPL groups x 33 VGPRs, capped at 4 groups
-  constexpr int kCap = 4 / GPL;
-  if (max_rows_per_expert <= 1 || kCap == 1) {
-    qgemv_kernel<BITS, LPR, GPL, 1, DUAL><<<grid, 256, 0, st>>>(a);
-  } else if (max_rows_per_expert <= 2 || kCap == 2) {
-    qgemv_kernel<BITS, LPR, GPL, (kCap >= 2 ? 2 : 1), DUAL><<<grid, 256, 0, st>>>(a);
-  } else {
-    qgemv_kernel<BITS, LPR, GPL, (kCap >= 4 ? 4 : 1), DUAL><<<grid, 256, 0, st>>>(a);
-  }
+// Row steps per wave: as many as fit next to the activations in a
+// 3-waves-per-SIMD register budget (~150 VGPRs: MT*GPL*33 for activations,
+// ~30 for addresses and sums, the rest for packed weights), at most 4.
+template <int BITS, int GPL, int MT, bool DUAL>
+constexpr int rows_r() {
+  constexpr int per_step = GPL * (64 * BITS / 32 + 2) * (DUAL ? 2 : 1);
+  constexpr int budget = 150 - 30 - MT * GPL * 33;
+  constexpr int r = budget / per_step;
+  return r < 1 ? 1 : (r > 4 ? 4 : r);
+}
+
+template <int BITS, int LPR, int GPL, int MT, bool DUAL>
+int launch_one(const GemvArgs& a, int max_experts, hipStream_t st) {
+  constexpr int R = rows_r<BITS, GPL, MT, DUAL>();
+  const int rows_per_block = 4 * R * (64 / LPR);
+  dim3 grid((a.rows_out + rows_per_block - 1) / rows_per_block, max_experts);
+  qgemv_kernel<BITS, LPR, GPL, MT, R, DUAL><<<grid, 256, 0, st>>>(a);
   PMOE_LAUNCH_CHECK("qgemv_kernel");
   return PMOE_OK;
 }
 
+// One token per pass: the packed weights stay in registers across passes,
+// so an expert serving several rows re-reads only its activations.
+template <int BITS, int LPR, int GPL, bool DUAL>
+int launch_mt(const GemvArgs& a, int, int max_experts, hipStream_t st) {
+  return launch_one<BITS, LPR, GPL, 1, DUAL>(a, max_experts, st);
+}
+
 template <int BITS, bool DUAL>
-int launch_shape(const GemvArgs& a, Shape sh, int max_rows_per_expert, dim3 grid,
+int launch_shape(const GemvArgs& a, Shape sh, int max_rows_per_expert, int max_experts,
                  hipStream_t st) {
 #define PMOE_SHAPE(L, G) \
-  if (sh.lpr == L && sh.gpl == G) return launch_mt<BITS, L, G, DUAL>(a, max_rows_per_expert, grid, st);
+  if (sh.lpr == L && sh.gpl == G) \
+    return launch_mt<BITS, L, G, DUAL>(a, max_rows_per_expert, max_experts, st);
   PMOE_SHAPE(64, 1)
   PMOE_SHAPE(64, 2)
   PMOE_SHAPE(8, 1)
-  PMOE_SHAPE(8, 2)
-  PMOE_SHAPE(8, 3)
-  PMOE_SHAPE(8, 4)
   PMOE_SHAPE(16, 1)
   PMOE_SHAPE(32, 1)
 #undef PMOE_SHAPE
   return fail(PMOE_EINVAL, "qgemv: unsupported row shape");
 }
 
+template <int BITS, int LPR, int GPL>
+int launch_down_combine(const GemvArgs& a, const CombineArgs& c, hipStream_t st) {
+  constexpr int R = rows_r<BITS, GPL, 1, false>();
+  constexpr int T = R * (64 / LPR);
+  const size_t lds = size_t(c.n) * a.kk * T * sizeof(float);
+  if (lds > 64 * 1024) return fail(PMOE_EINVAL, "down_combine: too many rows for one tile");
+  dim3 grid((a.rows_out + T - 1) / T);
+  down_combine_kernel<BITS, LPR, GPL, R><<<grid, 256, lds, st>>>(a, c);
+  PMOE_LAUNCH_CHECK("down_combine_kernel");
+  return PMOE_OK;
+}
+
+template <int BITS>
+int down_combine_bits(const GemvArgs& a, const CombineArgs& c, Shape sh, hipStream_t st) {
+#define PMOE_SHAPE(L, G) \
+  if (sh.lpr == L && sh.gpl == G) return launch_down_combine<BITS, L, G>(a, c, st);
+  PMOE_SHAPE(64, 1)
+  PMOE_SHAPE(64, 2)
+  PMOE_SHAPE(8, 1)
+  PMOE_SHAPE(16, 1)
+  PMOE_SHAPE(32, 1)
+#undef PMOE_SHAPE
+  return fail(PMOE_EINVAL, "down_combine: unsupported row shape");
+}
+
 }  // namespace
+
+// Down projection of every active expert plus the fixed-order combine into
+// c.out [n, rows_out] (decode block path).
+int down_combine(const GemvArgs& a, const CombineArgs& c, int bits, hipStream_t st) {
+  const Shape sh = pick_shape(a.cols / 64);
+  PMOE_REQUIRE(a.cols % 64 == 0 && sh.lpr > 0, "down_combine: bad input dim");
+  ProfScope prof_scope(K_DOWN, st);
+  if (bits == 4) return down_combine_bits<4>(a, c, sh, st);
+  if (bits == 6) return down_combine_bits<6>(a, c, sh, st);
+  return fail(PMOE_EINVAL, "down_combine: bits must be 4 or 6");
+}
 
 // One grouped projection launch.  max_experts bounds the number of active
 // experts (grid.y); max_rows_per_expert bounds the rows any expert serves.
@@ -285,29 +469,15 @@ int qgemv(const GemvArgs& a, int bits, bool dual, int max_experts, int max_rows_
   PMOE_REQUIRE(a.cols % 64 == 0 && groups > 0, "qgemv: input dim must be a multiple of 64");
   const Shape sh = pick_shape(groups);
   PMOE_REQUIRE(sh.lpr > 0, "qgemv: input dim too large (max 8192)");
-  PMOE_REQUIRE(a.rows_per_block % (4 * (64 / sh.lpr)) == 0, "qgemv: bad rows_per_block");
   if (max_experts <= 0 || a.rows_out <= 0) return PMOE_OK;
-  dim3 grid((a.rows_out + a.rows_per_block - 1) / a.rows_per_block, max_experts);
   ProfScope prof_scope(dual ? K_GATEUP : K_DOWN, st);
   if (bits == 4)
-    return dual ? launch_shape<4, true>(a, sh, max_rows_per_expert, grid, st)
-                : launch_shape<4, false>(a, sh, max_rows_per_expert, grid, st);
+    return dual ? launch_shape<4, true>(a, sh, max_rows_per_expert, max_experts, st)
+                : launch_shape<4, false>(a, sh, max_rows_per_expert, max_experts, st);
   if (bits == 6)
-    return dual ? launch_shape<6, true>(a, sh, max_rows_per_expert, grid, st)
-                : launch_shape<6, false>(a, sh, max_rows_per_expert, grid, st);
+    return dual ? launch_shape<6, true>(a, sh, max_rows_per_expert, max_experts, st)
+                : launch_shape<6, false>(a, sh, max_rows_per_expert, max_experts, st);
   return fail(PMOE_EINVAL, "qgemv: bits must be 4 or 6");
-}
-
-// Rows per block: a multiple of 4 waves x rows-per-wave-step, sized so the
-// grid has about `target` blocks when every possible expert is active.
-int qgemv_rows_per_block(int cols, int rows_out, int max_experts, int target) {
-  const Shape sh = pick_shape(cols / 64);
-  const int unit = 4 * (64 / (sh.lpr > 0 ? sh.lpr : 64));
-  long want = (long(rows_out) * max_experts + target - 1) / target;
-  long r = (want + unit - 1) / unit * unit;
-  if (r < unit) r = unit;
-  if (r > 16L * unit) r = 16L * unit;
-  return int(r);
 }
 
 }  // namespace pmoe

@@ -131,13 +131,16 @@ int check_geom(const pmoe_geom* g) {
 // y receives [rows, hidden] (f32 when y_f32, else bf16).
 int run_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* table, int n_experts,
                 int shared_slot, const uint16_t* x, const int32_t* inds, int n, int k, int kk,
-                int max_rows_per_expert, const MoeWs& w, void* y, int y_f32, hipStream_t st) {
+                int max_rows_per_expert, const MoeWs& w, void* y, int y_f32, hipStream_t st,
+                bool dispatched = false) {
   const int rows = n * kk;
   const int n_ids = n_experts + (kk > k ? 1 : 0);
   const bool prefill = prefill_wanted(g, n, kk, n_ids);
-  int rc = dispatch_ext(inds, rows, k, kk, n_ids, w.order, w.counts, w.offsets, w.inv, w.active,
-                        w.n_active, prefill ? prefill_tile_m() : 0, w.tiles, w.n_tiles, w.dws,
-                        w.dws_bytes, st);
+  int rc = PMOE_OK;
+  if (!dispatched)
+    rc = dispatch_ext(inds, rows, k, kk, n_ids, w.order, w.counts, w.offsets, w.inv, w.active,
+                      w.n_active, prefill ? prefill_tile_m() : 0, w.tiles, w.n_tiles, w.dws,
+                      w.dws_bytes, st);
   if (rc) return rc;
   if (prefill)
     return prefill_experts(g, slab, table, n_experts, shared_slot, x, n, kk, w.order, w.counts,
@@ -166,7 +169,6 @@ int run_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* table, i
   a.out = w.h;
   a.out_stride = g->inter;
   a.out_f32 = 0;
-  a.rows_per_block = qgemv_rows_per_block(g->hidden, g->inter, max_experts, 1024);
   rc = qgemv(a, g->bits, true, max_experts, max_rows_per_expert, st);
   if (rc) return rc;
   // down -> y
@@ -180,18 +182,71 @@ int run_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* table, i
   a.out = y;
   a.out_stride = g->hidden;
   a.out_f32 = y_f32;
-  a.rows_per_block = qgemv_rows_per_block(g->inter, g->hidden, max_experts, 1024);
   return qgemv(a, g->bits, false, max_experts, max_rows_per_expert, st);
+}
+
+// Decode block path after route_dispatch_decode: gate/up (expert-major) then
+// the tile-major down projection with the combine fused in.
+int decode_experts_combine(const pmoe_geom* g, const uint8_t* slab, const int32_t* table,
+                           int n_experts, const uint16_t* x, const float* wts, int n, int k,
+                           int shared_slot, const uint16_t* shared_gate, uint16_t* out,
+                           const MoeWs& w, hipStream_t st) {
+  const int shared = shared_slot >= 0 ? 1 : 0;
+  const int kk = k + shared;
+  const int rows = n * kk;
+  const int n_ids = n_experts + shared;
+  const int max_experts = rows < n_ids ? rows : n_ids;
+  int rc = PMOE_OK;
+  const float* sl = nullptr;
+  if (shared && shared_gate) {
+    rc = router_logits(x, shared_gate, nullptr, n, g->hidden, 1, w.shared_logit, st);
+    if (rc) return rc;
+    sl = w.shared_logit;
+  }
+  GemvArgs a{};
+  a.slab = slab;
+  a.expert_bytes = g->expert_bytes;
+  a.table = table;
+  a.n_experts = n_experts;
+  a.shared_slot = shared_slot;
+  a.active = w.active;
+  a.n_active = w.n_active;
+  a.counts = w.counts;
+  a.offsets = w.offsets;
+  a.order = w.order;
+  a.kk = kk;
+  a.p0 = {g->off[PMOE_GATE_W], g->off[PMOE_GATE_S], g->off[PMOE_GATE_B]};
+  a.p1 = {g->off[PMOE_UP_W], g->off[PMOE_UP_S], g->off[PMOE_UP_B]};
+  a.rows_out = g->inter;
+  a.cols = g->hidden;
+  a.act = x;
+  a.act_stride = g->hidden;
+  a.act_by_token = 1;
+  a.out = w.h;
+  a.out_stride = g->inter;
+  a.out_f32 = 0;
+  rc = qgemv(a, g->bits, true, max_experts, n, st);
+  if (rc) return rc;
+  a.p0 = {g->off[PMOE_DOWN_W], g->off[PMOE_DOWN_S], g->off[PMOE_DOWN_B]};
+  a.p1 = a.p0;
+  a.rows_out = g->hidden;
+  a.cols = g->inter;
+  a.act = w.h;
+  a.act_stride = g->inter;
+  a.act_by_token = 0;
+  a.out = nullptr;
+  const CombineArgs c{wts, sl, n, k, out};
+  return down_combine(a, c, g->bits, st);
 }
 
 int experts_and_combine(const pmoe_geom* g, const uint8_t* slab, const int32_t* table,
                         int n_experts, const uint16_t* x, const int32_t* inds, const float* wts,
                         int n, int k, int shared_slot, const uint16_t* shared_gate, int max_rpe,
-                        uint16_t* out, const MoeWs& w, hipStream_t st) {
+                        uint16_t* out, const MoeWs& w, hipStream_t st, bool dispatched = false) {
   const int shared = shared_slot >= 0 ? 1 : 0;
   const int kk = k + shared;
   int rc = run_experts(g, slab, table, n_experts, shared_slot, x, inds, n, k, kk, max_rpe, w,
-                       w.y, 1, st);
+                       w.y, 1, st, dispatched);
   if (rc) return rc;
   const float* sl = nullptr;
   if (shared && shared_gate) {
@@ -288,6 +343,29 @@ extern "C" int pmoe_moe_block(const pmoe_geom* g, const pmoe_route_cfg* rc_cfg, 
   rc = pmoe::router_logits(xb, static_cast<const uint16_t*>(gate_w), logit_bias, n, g->hidden, e,
                            w.logits, st);
   if (rc) return rc;
+  const int kk = k + shared;
+  const bool decode = n <= 64 && n * kk <= 1024 && e + 1 <= 1024 && k <= 16 &&
+                      !pmoe::prefill_wanted(g, n, kk, e + shared) &&
+                      (rc_cfg->scoring == PMOE_SCORE_SOFTMAX || e <= 512);
+  if (decode) {
+    if (rc_cfg->scoring == PMOE_SCORE_SIGMOID)
+      PMOE_REQUIRE(score_bias != nullptr, "moe_block: sigmoid scoring needs score_bias");
+    rc = pmoe::route_dispatch_decode(w.logits, score_bias, rc_cfg->scoring, n, e, k, shared,
+                                     rc_cfg->norm_topk_prob, rc_cfg->n_group, rc_cfg->topk_group,
+                                     rc_cfg->routed_scale, inds_out, weights_out, w.order,
+                                     w.counts, w.offsets, w.inv, w.active, w.n_active, nullptr, 0,
+                                     st);
+    if (rc) return rc;
+    if (size_t(n) * kk * 64 <= 16384)  // down tile rows x kk rows fit in LDS
+      return pmoe::decode_experts_combine(g, static_cast<const uint8_t*>(slab), table, e, xb,
+                                          weights_out, n, k, shared_slot,
+                                          static_cast<const uint16_t*>(shared_gate),
+                                          static_cast<uint16_t*>(out), w, st);
+    return pmoe::experts_and_combine(g, static_cast<const uint8_t*>(slab), table, e, xb, inds_out,
+                                     weights_out, n, k, shared_slot,
+                                     static_cast<const uint16_t*>(shared_gate), n,
+                                     static_cast<uint16_t*>(out), w, st, true);
+  }
   if (rc_cfg->scoring == PMOE_SCORE_SOFTMAX) {
     rc = pmoe::route_softmax(w.logits, n, e, k, rc_cfg->norm_topk_prob, inds_out, weights_out, st);
   } else if (rc_cfg->scoring == PMOE_SCORE_SIGMOID) {

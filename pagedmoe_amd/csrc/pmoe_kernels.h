@@ -56,12 +56,19 @@ struct GemvArgs {
   void* out;             // [flat rows, out_stride], f32 or bf16
   int out_stride;
   int out_f32;
-  int rows_per_block;
+};
+
+// Weighted combine of the down projection (decode block path).
+struct CombineArgs {
+  const float* w;             // [n, k] routing weights
+  const float* shared_logit;  // [n] or null (shared weight 1)
+  int n, k;
+  uint16_t* out;              // [n, hidden] bf16
 };
 
 int qgemv(const GemvArgs& a, int bits, bool dual, int max_experts, int max_rows_per_expert,
           hipStream_t st);
-int qgemv_rows_per_block(int cols, int rows_out, int max_experts, int target);
+int down_combine(const GemvArgs& a, const CombineArgs& c, int bits, hipStream_t st);
 
 // Routing (router.hip)
 int router_logits(const uint16_t* x, const uint16_t* w, const float* bias, int n, int d, int e,
@@ -71,6 +78,13 @@ int route_softmax(const float* logits, int n, int e, int k, int norm, int32_t* i
 int route_sigmoid(const float* logits, const float* bias, int n, int e, int n_group,
                   int topk_group, int k, int norm, float scale, int32_t* inds, float* weights,
                   hipStream_t st);
+
+// Decode route + dispatch in one block (route_decode.hip).
+int route_dispatch_decode(const float* logits, const float* bias, int scoring, int n, int e, int k,
+                          int shared, int norm, int n_group, int topk_group, float scale,
+                          int32_t* inds, float* weights, int32_t* order, int32_t* counts,
+                          int32_t* offsets, int32_t* inv, int32_t* active, int32_t* n_active,
+                          int32_t* zero, int n_zero, hipStream_t st);
 
 // Dispatch (dispatch.hip).  Flat row r reads id inds[(r / kk) * k_routed +
 // r % kk] when r % kk < k_routed and the shared pseudo-id n_routed otherwise;
