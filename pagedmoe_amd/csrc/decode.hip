@@ -17,6 +17,19 @@
 // both projections of a row together and writes h = silu(g)*u as bf16.
 #include "pmoe_internal.h"
 #include "pmoe_kernels.h"
+#include "route_common.h"
+
+// Tuning knobs (compile-time): rows per wave step override (0 = sized from
+// the register budget), non-temporal weight loads, minimum waves per SIMD.
+#ifndef PMOE_FORCE_R
+#define PMOE_FORCE_R 0
+#endif
+#ifndef PMOE_NT_LOADS
+#define PMOE_NT_LOADS 1
+#endif
+#ifndef PMOE_MIN_WAVES
+#define PMOE_MIN_WAVES 3
+#endif
 
 namespace pmoe {
 
@@ -79,7 +92,11 @@ __device__ __forceinline__ void load_group_w(const uint32_t* wrow, const uint16_
   const u32x4* v = reinterpret_cast<const u32x4*>(wrow + size_t(g) * kWords);
 #pragma unroll
   for (int c = 0; c < kWords / 4; ++c) {
+#if PMOE_NT_LOADS
     const u32x4 d = __builtin_nontemporal_load(v + c);
+#else
+    const u32x4 d = v[c];
+#endif
     q.w[4 * c + 0] = d.x;
     q.w[4 * c + 1] = d.y;
     q.w[4 * c + 2] = d.z;
@@ -127,40 +144,25 @@ __device__ __forceinline__ float group_term(float acc, float s, float b, float x
 // its packed weights (R steps x GPL groups x 1-2 projections) are requested
 // before anything else, so every wave has its whole share of HBM traffic in
 // flight while the activations are still arriving from L2.
-template <int BITS, int LPR, int GPL, int MT, int R, bool DUAL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void qgemv_kernel(
-    const GemvArgs a) {
+// ---------------------------------------------------------------- GEMV core
+//
+// One wave computes rows o = wrow0 + st*RPW + rsub (st < R) of one expert's
+// projection(s) for the expert's rows rlist[0..m_total).  Activations of the
+// first row are requested first (L2 hits), then the whole weight burst of the
+// wave (R steps x GPL groups x 1-2 projections); vector loads retire in
+// order, so row 0 starts as soon as its own words have landed.  The weights
+// stay in registers across the expert's rows.  store(t_row, st, o, value)
+// receives each finished output (value is silu(g)*u for DUAL).
+template <int BITS, int LPR, int GPL, int R, bool DUAL, class Act, class Store>
+__device__ __forceinline__ void gemv_expert(const GemvArgs& a, int slot, int m_total,
+                                            const int32_t* rlist, int wrow0, Act act_row,
+                                            Store store) {
   constexpr int RPW = 64 / LPR;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
   const int sub = lane % LPR;
   const int rsub = lane / LPR;
-  const int u = blockIdx.y;
-  if (u >= *a.n_active) return;
-  const int e = a.active[u];
-  const int slot = e < a.n_experts ? a.table[e] : a.shared_slot;
-  const int m_total = a.counts[e];
-  const int32_t* rlist = a.order + a.offsets[e];
   const int groups = a.cols / 64;
   const int wpr = a.cols * BITS / 32;
-  const int row0 = blockIdx.x * (4 * R * RPW);
-  const int wrow0 = row0 + wave * (R * RPW);
-
-  if (slot < 0) {
-    // Not resident: this expert contributes exact zero rows.
-    for (int m = 0; m < m_total; ++m) {
-      const int r = rlist[m];
-      for (int i = threadIdx.x; i < 4 * R * RPW; i += 256) {
-        const int o = row0 + i;
-        if (o >= a.rows_out) break;
-        if (a.out_f32)
-          static_cast<float*>(a.out)[size_t(r) * a.out_stride + o] = 0.0f;
-        else
-          static_cast<uint16_t*>(a.out)[size_t(r) * a.out_stride + o] = 0;
-      }
-    }
-    return;
-  }
   const uint8_t* base = a.slab + size_t(slot) * a.expert_bytes;
   const uint32_t* W0 = reinterpret_cast<const uint32_t*>(base + a.p0.w);
   const uint16_t* S0 = reinterpret_cast<const uint16_t*>(base + a.p0.s);
@@ -169,22 +171,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
   const uint16_t* S1 = reinterpret_cast<const uint16_t*>(base + a.p1.s);
   const uint16_t* B1 = reinterpret_cast<const uint16_t*>(base + a.p1.b);
 
-  // Activations first (L2 hits), then the weight burst: vector loads retire
-  // in order, so row 0 can start as soon as its own words have landed.
-  GroupAct<BITS> act[MT][GPL];
-  int rr[MT];
-  auto load_act = [&](int m0) {
+  GroupAct<BITS> act[GPL];
+  int r = 0;
+  auto load_act = [&](int m) {
+    r = rlist[m];
+    const uint16_t* src = act_row(r);
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const int m = min(m0 + t, m_total - 1);
-      rr[t] = rlist[m];
-      const int arow = a.act_by_token ? rr[t] / a.kk : rr[t];
-      const uint16_t* src = a.act + size_t(arow) * a.act_stride;
-#pragma unroll
-      for (int j = 0; j < GPL; ++j) {
-        const int g = min(sub + LPR * j, groups - 1);
-        load_group_act<BITS>(src + size_t(g) * 64, act[t][j]);
-      }
+    for (int j = 0; j < GPL; ++j) {
+      const int g = min(sub + LPR * j, groups - 1);
+      load_group_act<BITS>(src + size_t(g) * 64, act[j]);
     }
   };
   load_act(0);
@@ -204,18 +199,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
                            B1 + size_t(o) * groups, g, q1[DUAL ? st : 0][DUAL ? j : 0]);
     }
   }
-
   __builtin_amdgcn_sched_barrier(0);
-
-  for (int m0 = 0; m0 < m_total; m0 += MT) {
-    if (m0 > 0) {
-      load_act(m0);
+  for (int m = 0; m < m_total; ++m) {
+    if (m > 0) {
+      load_act(m);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int st = 0; st < R; ++st) {
       // Opaque to the optimiser: without this the unpacked pairs of every
-      // row are hoisted out of the token loop and spill.
+      // row are hoisted out of the row loop and spill.
 #pragma unroll
       for (int j = 0; j < GPL; ++j) {
 #pragma unroll
@@ -224,145 +217,171 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
           if (DUAL) asm volatile("" : "+v"(q1[DUAL ? st : 0][DUAL ? j : 0].w[c]));
         }
       }
-      const int o = wrow0 + st * RPW + rsub;
-      float p0[MT], p1[MT];
-#pragma unroll
-      for (int t = 0; t < MT; ++t) p0[t] = p1[t] = 0.0f;
+      float p0 = 0.0f, p1 = 0.0f;
 #pragma unroll
       for (int j = 0; j < GPL; ++j) {
         if (sub + LPR * j < groups) {
-#pragma unroll
-          for (int t = 0; t < MT; ++t) {
-            p0[t] = group_term(group_dot<BITS>(q0[st][j], act[t][j]), q0[st][j].s, q0[st][j].b,
-                               act[t][j].sum, p0[t]);
-            if (DUAL) {
-              const GroupW<BITS>& w1 = q1[DUAL ? st : 0][DUAL ? j : 0];
-              p1[t] = group_term(group_dot<BITS>(w1, act[t][j]), w1.s, w1.b, act[t][j].sum, p1[t]);
-            }
+          p0 = group_term(group_dot<BITS>(q0[st][j], act[j]), q0[st][j].s, q0[st][j].b,
+                          act[j].sum, p0);
+          if (DUAL) {
+            const GroupW<BITS>& w1 = q1[DUAL ? st : 0][DUAL ? j : 0];
+            p1 = group_term(group_dot<BITS>(w1, act[j]), w1.s, w1.b, act[j].sum, p1);
           }
         }
       }
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const float g0 = group_sum<LPR>(p0[t]);
-        float v = g0;
-        if (DUAL) {
-          const float u1 = group_sum<LPR>(p1[t]);
-          v = silu_fast(g0) * u1;
-        }
-        if (sub == t && o < a.rows_out && m0 + t < m_total) {
-          const size_t idx = size_t(rr[t]) * a.out_stride + o;
-          if (a.out_f32)
-            static_cast<float*>(a.out)[idx] = v;
-          else
-            static_cast<uint16_t*>(a.out)[idx] = f2bf(v);
-        }
-      }
+      float v = group_sum<LPR>(p0);
+      if (DUAL) v = silu_fast(v) * group_sum<LPR>(p1);
+      const int o = wrow0 + st * RPW + rsub;
+      if (sub == 0 && o < a.rows_out) store(r, st, o, v);
     }
   }
 }
 
-// Down projection + weighted combine for the decode block path.
-//
-// Tile-major: block b owns output rows [b*T, b*T + T) of the hidden dim for
-// every active expert; wave w takes experts w, w+4, ...  Each (flat row r,
-// output o) value lands in LDS, and once all experts are done the block
-// forms out[n, o] = sum_c w[n, c] * y[n*kk + c, o] for c = 0..kk-1 in that
-// fixed order (shared expert last), so the combine needs no y buffer, no
-// separate launch and no cross-block synchronisation, and every block does
-// the same amount of work.
-template <int BITS, int LPR, int GPL, int R>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void
-down_combine_kernel(const GemvArgs a, const CombineArgs c) {
-  constexpr int RPW = 64 / LPR;
-  constexpr int T = R * RPW;
-  extern __shared__ float s_y[];  // [rows][T]
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int sub = lane % LPR;
-  const int rsub = lane / LPR;
-  const int row0 = blockIdx.x * T;
-  const int groups = a.cols / 64;
-  const int wpr = a.cols * BITS / 32;
-  const int n_act = *a.n_active;
-
-  for (int u = wave; u < n_act; u += 4) {
-    const int e = a.active[u];
-    const int slot = e < a.n_experts ? a.table[e] : a.shared_slot;
-    const int m_total = a.counts[e];
-    const int32_t* rlist = a.order + a.offsets[e];
-    if (slot < 0) {
-      for (int m = 0; m < m_total; ++m)
-        for (int t = lane; t < T; t += 64) s_y[rlist[m] * T + t] = 0.0f;
-      continue;
-    }
-    const uint8_t* base = a.slab + size_t(slot) * a.expert_bytes;
-    const uint32_t* W0 = reinterpret_cast<const uint32_t*>(base + a.p0.w);
-    const uint16_t* S0 = reinterpret_cast<const uint16_t*>(base + a.p0.s);
-    const uint16_t* B0 = reinterpret_cast<const uint16_t*>(base + a.p0.b);
-    GroupAct<BITS> act[GPL];
-    int r = rlist[0];
-#pragma unroll
-    for (int j = 0; j < GPL; ++j) {
-      const int g = min(sub + LPR * j, groups - 1);
-      load_group_act<BITS>(a.act + size_t(r) * a.act_stride + size_t(g) * 64, act[j]);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    GroupW<BITS> q0[R][GPL];
-#pragma unroll
-    for (int st = 0; st < R; ++st) {
-      const int o = min(row0 + st * RPW + rsub, a.rows_out - 1);
-#pragma unroll
-      for (int j = 0; j < GPL; ++j) {
-        const int g = min(sub + LPR * j, groups - 1);
-        load_group_w<BITS>(W0 + size_t(o) * wpr, S0 + size_t(o) * groups,
-                           B0 + size_t(o) * groups, g, q0[st][j]);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    for (int m = 0; m < m_total; ++m) {
-      if (m > 0) {
-        r = rlist[m];
-#pragma unroll
-        for (int j = 0; j < GPL; ++j) {
-          const int g = min(sub + LPR * j, groups - 1);
-          load_group_act<BITS>(a.act + size_t(r) * a.act_stride + size_t(g) * 64, act[j]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int st = 0; st < R; ++st) {
-#pragma unroll
-        for (int j = 0; j < GPL; ++j)
-#pragma unroll
-          for (int cw = 0; cw < GroupW<BITS>::kWords; ++cw) asm volatile("" : "+v"(q0[st][j].w[cw]));
-        float p0 = 0.0f;
-#pragma unroll
-        for (int j = 0; j < GPL; ++j)
-          if (sub + LPR * j < groups)
-            p0 = group_term(group_dot<BITS>(q0[st][j], act[j]), q0[st][j].s, q0[st][j].b,
-                            act[j].sum, p0);
-        const float y = group_sum<LPR>(p0);
-        if (sub == 0) s_y[r * T + st * RPW + rsub] = y;
-      }
+// Zero outputs of an expert whose table entry is -1 (not resident): it
+// contributes exact zero rows (streaming.py:715-719).
+__device__ __forceinline__ void store_zero_rows(const GemvArgs& a, int m_total,
+                                                const int32_t* rlist, int row0, int rows) {
+  for (int m = 0; m < m_total; ++m) {
+    const int r = rlist[m];
+    for (int i = threadIdx.x; i < rows; i += 256) {
+      const int o = row0 + i;
+      if (o >= a.rows_out) break;
+      if (a.out_f32)
+        static_cast<float*>(a.out)[size_t(r) * a.out_stride + o] = 0.0f;
+      else
+        static_cast<uint16_t*>(a.out)[size_t(r) * a.out_stride + o] = 0;
     }
   }
+}
+
+// ---------------------------------------------------------------- kernels
+
+// Expert-major grouped projection: blockIdx.y = active expert (from a
+// dispatch in global memory), blockIdx.x = tile of 4*R*RPW output rows.
+template <int BITS, int LPR, int GPL, int R, bool DUAL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PMOE_MIN_WAVES, 8))) void qgemv_kernel(
+    const GemvArgs a) {
+  constexpr int RPW = 64 / LPR;
+  const int u = blockIdx.y;
+  if (u >= *a.n_active) return;
+  const int e = a.active[u];
+  const int slot = e < a.n_experts ? a.table[e] : a.shared_slot;
+  const int m_total = a.counts[e];
+  const int32_t* rlist = a.order + a.offsets[e];
+  const int row0 = blockIdx.x * (4 * R * RPW);
+  if (slot < 0) {
+    store_zero_rows(a, m_total, rlist, row0, 4 * R * RPW);
+    return;
+  }
+  const int wrow0 = row0 + (threadIdx.x >> 6) * (R * RPW);
+  auto act_row = [&](int r) {
+    return a.act + size_t(a.act_by_token ? r / a.kk : r) * a.act_stride;
+  };
+  auto store = [&](int r, int, int o, float v) {
+    const size_t idx = size_t(r) * a.out_stride + o;
+    if (a.out_f32)
+      static_cast<float*>(a.out)[idx] = v;
+    else
+      static_cast<uint16_t*>(a.out)[idx] = f2bf(v);
+  };
+  gemv_expert<BITS, LPR, GPL, R, DUAL>(a, slot, m_total, rlist, wrow0, act_row, store);
+}
+
+// Decode gate/up with the routing computed in the block's prologue (see
+// route_common.h): blockIdx.y = u-th active expert in ascending id order.
+// Block (0, 0) also publishes the routing (inds_out, w_out).
+// PRE: the routing record was written by route_record_kernel (several
+// tokens); otherwise every block routes its one token itself and block (0, 0)
+// publishes the record.
+template <int BITS, int LPR, int GPL, int R, int EPL, bool PRE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PMOE_MIN_WAVES, 8))) void
+gateup_routed_kernel(const GemvArgs a, const RouteDev rt, int32_t* inds_out, float* w_out,
+                     RouteRecord* rec) {
+  constexpr int RPW = 64 / LPR;
+  __shared__ RouteLds L;
+  __shared__ WaveTmp W[PRE ? 1 : 4];
+  __shared__ int32_t s_rows[kRouteMaxRows];
+  __shared__ int s_m;
+  if (PRE) {
+    load_route(rec, rt.n * rt.kk, rt.e + (rt.kk > rt.k ? 1 : 0), L);
+  } else {
+    const bool publish = blockIdx.x == 0 && blockIdx.y == 0;
+    route_block<EPL, 4>(rt, L, W, publish ? inds_out : nullptr, w_out);
+    if (publish) publish_route(L, rt.n * rt.kk, rt.e + (rt.kk > rt.k ? 1 : 0), rec);
+  }
+  const int u = blockIdx.y;
+  if (u >= L.n_active) return;
+  const int e = L.active[u];
+  if (threadIdx.x < 64) {
+    const int m = wave_rows_of(L, rt.n * rt.kk, e, s_rows);
+    if (threadIdx.x == 0) s_m = m;
+  }
+  const int slot = e < a.n_experts ? a.table[e] : a.shared_slot;
   __syncthreads();
-  // fixed-order combine of this tile
-  for (int i = threadIdx.x; i < c.n * T; i += 256) {
+  const int row0 = blockIdx.x * (4 * R * RPW);
+  if (slot < 0) {
+    store_zero_rows(a, s_m, s_rows, row0, 4 * R * RPW);
+    return;
+  }
+  const int wrow0 = row0 + (threadIdx.x >> 6) * (R * RPW);
+  auto act_row = [&](int r) { return a.act + size_t(r / rt.kk) * a.act_stride; };
+  auto store = [&](int r, int, int o, float v) {
+    static_cast<uint16_t*>(a.out)[size_t(r) * a.out_stride + o] = f2bf(v);
+  };
+  gemv_expert<BITS, LPR, GPL, R, true>(a, slot, s_m, s_rows, wrow0, act_row, store);
+}
+
+// Routing of several tokens at once (one wave per token, 16 waves), written
+// to the record and the routing outputs.
+template <int EPL>
+__global__ __launch_bounds__(1024) void route_record_kernel(const RouteDev rt, int32_t* inds_out,
+                                                             float* w_out, RouteRecord* rec) {
+  __shared__ RouteLds L;
+  __shared__ WaveTmp W[16];
+  route_block<EPL, 16>(rt, L, W, inds_out, w_out);
+  publish_route(L, rt.n * rt.kk, rt.e + (rt.kk > rt.k ? 1 : 0), rec);
+}
+
+// Decode down projection + weighted combine, routing recomputed in the
+// prologue.  Tile-major: block b owns output rows [b*T, b*T + T) for every
+// active expert (wave w takes experts w, w+4, ...); each (flat row, output)
+// value lands in LDS and the block then forms
+//   out[n, o] = sum_c w[n, c] * y[n*kk + c, o],  c = 0..kk-1 in that order
+// (shared expert last) -- no y buffer, no extra launch, no cross-block sync.
+template <int BITS, int LPR, int GPL, int R, int EPL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PMOE_MIN_WAVES, 8))) void
+down_routed_kernel(const GemvArgs a, const RouteDev rt, uint16_t* out, const RouteRecord* rec) {
+  constexpr int RPW = 64 / LPR;
+  constexpr int T = R * RPW;
+  __shared__ RouteLds L;
+  __shared__ int32_t s_rows[4][kRouteMaxRows];
+  extern __shared__ float s_y[];  // [rows][T]
+  const int wave = threadIdx.x >> 6;
+  load_route(rec, rt.n * rt.kk, rt.e + (rt.kk > rt.k ? 1 : 0), L);
+  const int rows = rt.n * rt.kk;
+  const int row0 = blockIdx.x * T;
+  for (int u = wave; u < L.n_active; u += 4) {
+    const int e = L.active[u];
+    const int m_total = wave_rows_of(L, rows, e, s_rows[wave]);
+    const int slot = e < a.n_experts ? a.table[e] : a.shared_slot;
+    if (slot < 0) {
+      for (int m = 0; m < m_total; ++m)
+        for (int t = threadIdx.x & 63; t < T; t += 64) s_y[s_rows[wave][m] * T + t] = 0.0f;
+      continue;
+    }
+    auto act_row = [&](int r) { return a.act + size_t(r) * a.act_stride; };
+    auto store = [&](int r, int st, int o, float v) { s_y[r * T + (o - row0)] = v; };
+    gemv_expert<BITS, LPR, GPL, R, false>(a, slot, m_total, s_rows[wave], row0, act_row, store);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < rt.n * T; i += 256) {
     const int n = i / T, t = i - n * T;
     const int o = row0 + t;
     if (o >= a.rows_out) continue;
     float acc = 0.0f;
-    for (int col = 0; col < a.kk; ++col) {
-      float wt;
-      if (col < c.k)
-        wt = c.w[size_t(n) * c.k + col];
-      else
-        wt = c.shared_logit ? psigmoid(c.shared_logit[n]) : 1.0f;
-      acc = __builtin_fmaf(wt, s_y[(n * a.kk + col) * T + t], acc);
-    }
-    c.out[size_t(n) * a.rows_out + o] = f2bf(acc);
+    for (int col = 0; col < rt.kk; ++col)
+      acc = __builtin_fmaf(L.w[n * rt.kk + col], s_y[(n * rt.kk + col) * T + t], acc);
+    out[size_t(n) * a.rows_out + o] = f2bf(acc);
   }
 }
 
@@ -381,90 +400,103 @@ Shape pick_shape(int groups) {
 }
 
 // Row steps per wave: as many as fit next to the activations in a
-// 3-waves-per-SIMD register budget (~150 VGPRs: MT*GPL*33 for activations,
+// 3-waves-per-SIMD register budget (~150 VGPRs: GPL*33 for activations,
 // ~30 for addresses and sums, the rest for packed weights), at most 4.
-template <int BITS, int GPL, int MT, bool DUAL>
+template <int BITS, int GPL, bool DUAL>
 constexpr int rows_r() {
   constexpr int per_step = GPL * (64 * BITS / 32 + 2) * (DUAL ? 2 : 1);
-  constexpr int budget = 150 - 30 - MT * GPL * 33;
+  constexpr int budget = 150 - 30 - GPL * 33;
   constexpr int r = budget / per_step;
+  if (PMOE_FORCE_R > 0) return PMOE_FORCE_R;
   return r < 1 ? 1 : (r > 4 ? 4 : r);
 }
 
-template <int BITS, int LPR, int GPL, int MT, bool DUAL>
-int launch_one(const GemvArgs& a, int max_experts, hipStream_t st) {
-  constexpr int R = rows_r<BITS, GPL, MT, DUAL>();
-  const int rows_per_block = 4 * R * (64 / LPR);
-  dim3 grid((a.rows_out + rows_per_block - 1) / rows_per_block, max_experts);
-  qgemv_kernel<BITS, LPR, GPL, MT, R, DUAL><<<grid, 256, 0, st>>>(a);
-  PMOE_LAUNCH_CHECK("qgemv_kernel");
-  return PMOE_OK;
-}
-
-// One token per pass: the packed weights stay in registers across passes,
-// so an expert serving several rows re-reads only its activations.
-template <int BITS, int LPR, int GPL, bool DUAL>
-int launch_mt(const GemvArgs& a, int, int max_experts, hipStream_t st) {
-  return launch_one<BITS, LPR, GPL, 1, DUAL>(a, max_experts, st);
-}
+#define PMOE_FOR_SHAPES(X) X(64, 1) X(64, 2) X(8, 1) X(16, 1) X(32, 1)
 
 template <int BITS, bool DUAL>
-int launch_shape(const GemvArgs& a, Shape sh, int max_rows_per_expert, int max_experts,
-                 hipStream_t st) {
-#define PMOE_SHAPE(L, G) \
-  if (sh.lpr == L && sh.gpl == G) \
-    return launch_mt<BITS, L, G, DUAL>(a, max_rows_per_expert, max_experts, st);
-  PMOE_SHAPE(64, 1)
-  PMOE_SHAPE(64, 2)
-  PMOE_SHAPE(8, 1)
-  PMOE_SHAPE(16, 1)
-  PMOE_SHAPE(32, 1)
-#undef PMOE_SHAPE
+int launch_qgemv(const GemvArgs& a, Shape sh, int max_experts, hipStream_t st) {
+#define PMOE_CASE(L, G)                                                          \
+  if (sh.lpr == L && sh.gpl == G) {                                              \
+    constexpr int R = rows_r<BITS, G, DUAL>();                                   \
+    dim3 grid((a.rows_out + 4 * R * (64 / L) - 1) / (4 * R * (64 / L)), max_experts); \
+    qgemv_kernel<BITS, L, G, R, DUAL><<<grid, 256, 0, st>>>(a);                  \
+    PMOE_LAUNCH_CHECK("qgemv_kernel");                                           \
+    return PMOE_OK;                                                              \
+  }
+  PMOE_FOR_SHAPES(PMOE_CASE)
+#undef PMOE_CASE
   return fail(PMOE_EINVAL, "qgemv: unsupported row shape");
 }
 
-template <int BITS, int LPR, int GPL>
-int launch_down_combine(const GemvArgs& a, const CombineArgs& c, hipStream_t st) {
-  constexpr int R = rows_r<BITS, GPL, 1, false>();
-  constexpr int T = R * (64 / LPR);
-  const size_t lds = size_t(c.n) * a.kk * T * sizeof(float);
-  if (lds > 64 * 1024) return fail(PMOE_EINVAL, "down_combine: too many rows for one tile");
-  dim3 grid((a.rows_out + T - 1) / T);
-  down_combine_kernel<BITS, LPR, GPL, R><<<grid, 256, lds, st>>>(a, c);
-  PMOE_LAUNCH_CHECK("down_combine_kernel");
+template <int BITS, int EPL, int L, int G>
+int launch_gateup_routed(const GemvArgs& gu, const RouteDev& rt, int max_experts,
+                         int32_t* inds_out, float* w_out, RouteRecord* rec, hipStream_t st) {
+  constexpr int R = rows_r<BITS, G, true>();
+  constexpr int rows = 4 * R * (64 / L);
+  dim3 grid((gu.rows_out + rows - 1) / rows, max_experts);
+  if (rt.n == 1) {
+    gateup_routed_kernel<BITS, L, G, R, EPL, false><<<grid, 256, 0, st>>>(gu, rt, inds_out, w_out,
+                                                                          rec);
+  } else {
+    {
+      ProfScope prof_scope(K_ROUTE_SELECT, st);
+      route_record_kernel<EPL><<<1, 1024, 0, st>>>(rt, inds_out, w_out, rec);
+      PMOE_LAUNCH_CHECK("route_record_kernel");
+    }
+    gateup_routed_kernel<BITS, L, G, R, EPL, true><<<grid, 256, 0, st>>>(gu, rt, inds_out, w_out,
+                                                                         rec);
+  }
+  PMOE_LAUNCH_CHECK("gateup_routed_kernel");
   return PMOE_OK;
 }
 
-template <int BITS>
-int down_combine_bits(const GemvArgs& a, const CombineArgs& c, Shape sh, hipStream_t st) {
-#define PMOE_SHAPE(L, G) \
-  if (sh.lpr == L && sh.gpl == G) return launch_down_combine<BITS, L, G>(a, c, st);
-  PMOE_SHAPE(64, 1)
-  PMOE_SHAPE(64, 2)
-  PMOE_SHAPE(8, 1)
-  PMOE_SHAPE(16, 1)
-  PMOE_SHAPE(32, 1)
-#undef PMOE_SHAPE
-  return fail(PMOE_EINVAL, "down_combine: unsupported row shape");
+template <int BITS, int EPL, int L, int G>
+int launch_down_routed(const GemvArgs& dn, const RouteDev& rt, uint16_t* out,
+                       const RouteRecord* rec, hipStream_t st) {
+  constexpr int R = rows_r<BITS, G, false>();
+  constexpr int T = R * (64 / L);
+  const size_t lds = size_t(rt.n) * rt.kk * T * sizeof(float);
+  if (lds > 48 * 1024) return fail(PMOE_EINVAL, "decode: too many rows per tile");
+  dim3 grid((dn.rows_out + T - 1) / T);
+  down_routed_kernel<BITS, L, G, R, EPL><<<grid, 256, lds, st>>>(dn, rt, out, rec);
+  PMOE_LAUNCH_CHECK("down_routed_kernel");
+  return PMOE_OK;
+}
+
+template <int BITS, int EPL>
+int launch_routed(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int max_experts,
+                  int32_t* inds_out, float* w_out, uint16_t* out, RouteRecord* rec,
+                  hipStream_t st) {
+  const Shape s1 = pick_shape(gu.cols / 64), s2 = pick_shape(dn.cols / 64);
+  int rc = PMOE_EINVAL;
+  {
+    ProfScope prof_scope(K_GATEUP, st);
+#define PMOE_CASE(L, G) \
+  if (s1.lpr == L && s1.gpl == G) rc = launch_gateup_routed<BITS, EPL, L, G>(gu, rt, max_experts, inds_out, w_out, rec, st);
+    PMOE_FOR_SHAPES(PMOE_CASE)
+#undef PMOE_CASE
+  }
+  if (rc == PMOE_EINVAL) return fail(PMOE_EINVAL, "decode: unsupported gate/up row shape");
+  if (rc) return rc;
+  rc = PMOE_EINVAL;
+  {
+    ProfScope prof_scope(K_DOWN, st);
+#define PMOE_CASE(L, G) \
+  if (s2.lpr == L && s2.gpl == G) rc = launch_down_routed<BITS, EPL, L, G>(dn, rt, out, rec, st);
+    PMOE_FOR_SHAPES(PMOE_CASE)
+#undef PMOE_CASE
+  }
+  if (rc == PMOE_EINVAL && pmoe_last_error()[0] == 0)
+    return fail(PMOE_EINVAL, "decode: unsupported down row shape");
+  return rc;
 }
 
 }  // namespace
 
-// Down projection of every active expert plus the fixed-order combine into
-// c.out [n, rows_out] (decode block path).
-int down_combine(const GemvArgs& a, const CombineArgs& c, int bits, hipStream_t st) {
-  const Shape sh = pick_shape(a.cols / 64);
-  PMOE_REQUIRE(a.cols % 64 == 0 && sh.lpr > 0, "down_combine: bad input dim");
-  ProfScope prof_scope(K_DOWN, st);
-  if (bits == 4) return down_combine_bits<4>(a, c, sh, st);
-  if (bits == 6) return down_combine_bits<6>(a, c, sh, st);
-  return fail(PMOE_EINVAL, "down_combine: bits must be 4 or 6");
-}
+size_t decode_record_bytes() { return sizeof(RouteRecord); }
 
-// One grouped projection launch.  max_experts bounds the number of active
-// experts (grid.y); max_rows_per_expert bounds the rows any expert serves.
-int qgemv(const GemvArgs& a, int bits, bool dual, int max_experts, int max_rows_per_expert,
-          hipStream_t st) {
+// One grouped projection launch (expert-major, dispatch in global memory).
+int qgemv(const GemvArgs& a, int bits, bool dual, int max_experts, int, hipStream_t st) {
   const int groups = a.cols / 64;
   PMOE_REQUIRE(a.cols % 64 == 0 && groups > 0, "qgemv: input dim must be a multiple of 64");
   const Shape sh = pick_shape(groups);
@@ -472,12 +504,47 @@ int qgemv(const GemvArgs& a, int bits, bool dual, int max_experts, int max_rows_
   if (max_experts <= 0 || a.rows_out <= 0) return PMOE_OK;
   ProfScope prof_scope(dual ? K_GATEUP : K_DOWN, st);
   if (bits == 4)
-    return dual ? launch_shape<4, true>(a, sh, max_rows_per_expert, max_experts, st)
-                : launch_shape<4, false>(a, sh, max_rows_per_expert, max_experts, st);
+    return dual ? launch_qgemv<4, true>(a, sh, max_experts, st)
+                : launch_qgemv<4, false>(a, sh, max_experts, st);
   if (bits == 6)
-    return dual ? launch_shape<6, true>(a, sh, max_rows_per_expert, max_experts, st)
-                : launch_shape<6, false>(a, sh, max_rows_per_expert, max_experts, st);
+    return dual ? launch_qgemv<6, true>(a, sh, max_experts, st)
+                : launch_qgemv<6, false>(a, sh, max_experts, st);
   return fail(PMOE_EINVAL, "qgemv: bits must be 4 or 6");
+}
+
+// Decode MoE experts with routing fused into both projections: gate/up into
+// gu.out (h), then down + combine into out [n, hidden].
+int decode_routed(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int bits,
+                  int32_t* inds_out, float* w_out, uint16_t* out, void* record,
+                  hipStream_t st) {
+  PMOE_REQUIRE(record != nullptr, "decode: null routing record");
+  RouteRecord* rec = static_cast<RouteRecord*>(record);
+  PMOE_REQUIRE(rt.n >= 1 && rt.n * rt.kk <= kRouteMaxRows, "decode: too many rows");
+  PMOE_REQUIRE(rt.e + 1 <= kRouteMaxIds && rt.k <= kRouteMaxK && rt.k <= rt.e,
+               "decode: bad experts/top-k");
+  if (rt.scoring == PMOE_SCORE_SIGMOID)
+    PMOE_REQUIRE(rt.e <= kRouteMaxSigE && rt.bias != nullptr && rt.n_group >= 1 &&
+                     rt.n_group <= 64 && rt.e % rt.n_group == 0 && rt.topk_group >= 1 &&
+                     rt.topk_group <= rt.n_group && rt.topk_group <= 8 &&
+                     (rt.n_group == 1 || rt.e / rt.n_group >= 2) &&
+                     rt.k <= (rt.e / rt.n_group) * rt.topk_group,
+                 "decode: bad sigmoid group configuration");
+  const int rows = rt.n * rt.kk;
+  const int n_ids = rt.e + (rt.kk > rt.k ? 1 : 0);
+  const int max_experts = rows < n_ids ? rows : n_ids;
+  const int epl = (rt.e + 63) / 64;
+#define PMOE_EPL(EP)                                                                     \
+  if (epl <= EP) {                                                                       \
+    if (bits == 4) return launch_routed<4, EP>(gu, dn, rt, max_experts, inds_out, w_out, out, rec, st); \
+    if (bits == 6) return launch_routed<6, EP>(gu, dn, rt, max_experts, inds_out, w_out, out, rec, st); \
+    return fail(PMOE_EINVAL, "decode: bits must be 4 or 6");                            \
+  }
+  PMOE_EPL(2)
+  PMOE_EPL(4)
+  PMOE_EPL(8)
+  PMOE_EPL(16)
+#undef PMOE_EPL
+  return fail(PMOE_EINVAL, "decode: too many experts");
 }
 
 }  // namespace pmoe

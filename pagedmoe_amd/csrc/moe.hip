@@ -8,6 +8,7 @@
 // then the shared expert, so results do not depend on scheduling.
 #include "pmoe_internal.h"
 #include "pmoe_kernels.h"
+#include "route_common.h"
 
 namespace pmoe {
 
@@ -38,6 +39,7 @@ struct MoeWs {
   float* y = nullptr;             // [rows, hidden] f32
   void* dws = nullptr;            // dispatch scratch
   size_t dws_bytes = 0;
+  void* record = nullptr;         // decode routing record
   int max_tiles = 0;
 };
 
@@ -59,7 +61,7 @@ size_t carve(const pmoe_geom* g, int n, int k, int shared, int n_experts, void* 
   const int n_ids = n_experts + (shared ? 1 : 0);
   Carver c{static_cast<uint8_t*>(base)};
   MoeWs t;
-  t.logits = c.take<float>(size_t(n) * n_experts);
+  t.logits = c.take<float>(size_t(n) * (n_experts + 1));
   t.shared_logit = c.take<float>(size_t(n));
   t.order = c.take<int32_t>(rows);
   t.inv = c.take<int32_t>(rows);
@@ -75,6 +77,7 @@ size_t carve(const pmoe_geom* g, int n, int k, int shared, int n_experts, void* 
   t.y = c.take<float>(rows * g->hidden);
   t.dws_bytes = dispatch_workspace(int(rows), n_ids);
   t.dws = c.take<uint8_t>(t.dws_bytes);
+  t.record = c.take<uint8_t>(decode_record_bytes());
   if (w) *w = t;
   return c.off;
 }
@@ -185,58 +188,59 @@ int run_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* table, i
   return qgemv(a, g->bits, false, max_experts, max_rows_per_expert, st);
 }
 
-// Decode block path after route_dispatch_decode: gate/up (expert-major) then
-// the tile-major down projection with the combine fused in.
-int decode_experts_combine(const pmoe_geom* g, const uint8_t* slab, const int32_t* table,
-                           int n_experts, const uint16_t* x, const float* wts, int n, int k,
-                           int shared_slot, const uint16_t* shared_gate, uint16_t* out,
-                           const MoeWs& w, hipStream_t st) {
+// Decode block path: logits (+ shared gate column), then gate/up and
+// down+combine, each recomputing the routing in its prologue.
+int decode_block(const pmoe_geom* g, const pmoe_route_cfg* rc, const uint8_t* slab,
+                 const int32_t* table, const uint16_t* gate_w, const float* score_bias,
+                 const float* logit_bias, const uint16_t* x, int n, int shared_slot,
+                 const uint16_t* shared_gate, uint16_t* out, int32_t* inds_out, float* w_out,
+                 const MoeWs& w, hipStream_t st) {
+  const int e = rc->n_experts, k = rc->top_k;
   const int shared = shared_slot >= 0 ? 1 : 0;
   const int kk = k + shared;
-  const int rows = n * kk;
-  const int n_ids = n_experts + shared;
-  const int max_experts = rows < n_ids ? rows : n_ids;
-  int rc = PMOE_OK;
-  const float* sl = nullptr;
-  if (shared && shared_gate) {
-    rc = router_logits(x, shared_gate, nullptr, n, g->hidden, 1, w.shared_logit, st);
-    if (rc) return rc;
-    sl = w.shared_logit;
-  }
-  GemvArgs a{};
-  a.slab = slab;
-  a.expert_bytes = g->expert_bytes;
-  a.table = table;
-  a.n_experts = n_experts;
-  a.shared_slot = shared_slot;
-  a.active = w.active;
-  a.n_active = w.n_active;
-  a.counts = w.counts;
-  a.offsets = w.offsets;
-  a.order = w.order;
-  a.kk = kk;
-  a.p0 = {g->off[PMOE_GATE_W], g->off[PMOE_GATE_S], g->off[PMOE_GATE_B]};
-  a.p1 = {g->off[PMOE_UP_W], g->off[PMOE_UP_S], g->off[PMOE_UP_B]};
-  a.rows_out = g->inter;
-  a.cols = g->hidden;
-  a.act = x;
-  a.act_stride = g->hidden;
-  a.act_by_token = 1;
-  a.out = w.h;
-  a.out_stride = g->inter;
-  a.out_f32 = 0;
-  rc = qgemv(a, g->bits, true, max_experts, n, st);
-  if (rc) return rc;
-  a.p0 = {g->off[PMOE_DOWN_W], g->off[PMOE_DOWN_S], g->off[PMOE_DOWN_B]};
-  a.p1 = a.p0;
-  a.rows_out = g->hidden;
-  a.cols = g->inter;
-  a.act = w.h;
-  a.act_stride = g->inter;
-  a.act_by_token = 0;
-  a.out = nullptr;
-  const CombineArgs c{wts, sl, n, k, out};
-  return down_combine(a, c, g->bits, st);
+  const uint16_t* extra = (shared && shared_gate) ? shared_gate : nullptr;
+  int r = router_logits_ext(x, gate_w, extra, logit_bias, n, g->hidden, e, w.logits, st);
+  if (r) return r;
+  RouteDev rt{};
+  rt.logits = w.logits;
+  rt.ld = e + (extra ? 1 : 0);
+  rt.bias = score_bias;
+  rt.scoring = rc->scoring;
+  rt.n = n;
+  rt.e = e;
+  rt.k = k;
+  rt.kk = kk;
+  rt.norm = rc->norm_topk_prob;
+  rt.n_group = rc->n_group;
+  rt.topk_group = rc->topk_group;
+  rt.scale = rc->routed_scale;
+  rt.shared_gate = extra ? 1 : 0;
+  GemvArgs gu{};
+  gu.slab = slab;
+  gu.expert_bytes = g->expert_bytes;
+  gu.table = table;
+  gu.n_experts = e;
+  gu.shared_slot = shared_slot;
+  gu.kk = kk;
+  gu.p0 = {g->off[PMOE_GATE_W], g->off[PMOE_GATE_S], g->off[PMOE_GATE_B]};
+  gu.p1 = {g->off[PMOE_UP_W], g->off[PMOE_UP_S], g->off[PMOE_UP_B]};
+  gu.rows_out = g->inter;
+  gu.cols = g->hidden;
+  gu.act = x;
+  gu.act_stride = g->hidden;
+  gu.act_by_token = 1;
+  gu.out = w.h;
+  gu.out_stride = g->inter;
+  GemvArgs dn = gu;
+  dn.p0 = {g->off[PMOE_DOWN_W], g->off[PMOE_DOWN_S], g->off[PMOE_DOWN_B]};
+  dn.p1 = dn.p0;
+  dn.rows_out = g->hidden;
+  dn.cols = g->inter;
+  dn.act = w.h;
+  dn.act_stride = g->inter;
+  dn.act_by_token = 0;
+  dn.out = nullptr;
+  return decode_routed(gu, dn, rt, g->bits, inds_out, w_out, out, w.record, st);
 }
 
 int experts_and_combine(const pmoe_geom* g, const uint8_t* slab, const int32_t* table,
@@ -340,32 +344,22 @@ extern "C" int pmoe_moe_block(const pmoe_geom* g, const pmoe_route_cfg* rc_cfg, 
   pmoe::carve(g, n, k, shared, e, ws, &w);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* xb = static_cast<const uint16_t*>(x);
-  rc = pmoe::router_logits(xb, static_cast<const uint16_t*>(gate_w), logit_bias, n, g->hidden, e,
-                           w.logits, st);
-  if (rc) return rc;
   const int kk = k + shared;
-  const bool decode = n <= 64 && n * kk <= 1024 && e + 1 <= 1024 && k <= 16 &&
-                      !pmoe::prefill_wanted(g, n, kk, e + shared) &&
-                      (rc_cfg->scoring == PMOE_SCORE_SOFTMAX || e <= 512);
+  const bool decode = n * kk <= pmoe::kRouteMaxRows && e + 1 <= pmoe::kRouteMaxIds &&
+                      k <= pmoe::kRouteMaxK && !pmoe::prefill_wanted(g, n, kk, e + shared) &&
+                      (rc_cfg->scoring == PMOE_SCORE_SOFTMAX ||
+                       (e <= pmoe::kRouteMaxSigE && rc_cfg->topk_group <= 8));
   if (decode) {
     if (rc_cfg->scoring == PMOE_SCORE_SIGMOID)
       PMOE_REQUIRE(score_bias != nullptr, "moe_block: sigmoid scoring needs score_bias");
-    rc = pmoe::route_dispatch_decode(w.logits, score_bias, rc_cfg->scoring, n, e, k, shared,
-                                     rc_cfg->norm_topk_prob, rc_cfg->n_group, rc_cfg->topk_group,
-                                     rc_cfg->routed_scale, inds_out, weights_out, w.order,
-                                     w.counts, w.offsets, w.inv, w.active, w.n_active, nullptr, 0,
-                                     st);
-    if (rc) return rc;
-    if (size_t(n) * kk * 64 <= 16384)  // down tile rows x kk rows fit in LDS
-      return pmoe::decode_experts_combine(g, static_cast<const uint8_t*>(slab), table, e, xb,
-                                          weights_out, n, k, shared_slot,
-                                          static_cast<const uint16_t*>(shared_gate),
-                                          static_cast<uint16_t*>(out), w, st);
-    return pmoe::experts_and_combine(g, static_cast<const uint8_t*>(slab), table, e, xb, inds_out,
-                                     weights_out, n, k, shared_slot,
-                                     static_cast<const uint16_t*>(shared_gate), n,
-                                     static_cast<uint16_t*>(out), w, st, true);
+    return pmoe::decode_block(g, rc_cfg, static_cast<const uint8_t*>(slab), table,
+                              static_cast<const uint16_t*>(gate_w), score_bias, logit_bias, xb, n,
+                              shared_slot, static_cast<const uint16_t*>(shared_gate),
+                              static_cast<uint16_t*>(out), inds_out, weights_out, w, st);
   }
+  rc = pmoe::router_logits(xb, static_cast<const uint16_t*>(gate_w), logit_bias, n, g->hidden, e,
+                           w.logits, st);
+  if (rc) return rc;
   if (rc_cfg->scoring == PMOE_SCORE_SOFTMAX) {
     rc = pmoe::route_softmax(w.logits, n, e, k, rc_cfg->norm_topk_prob, inds_out, weights_out, st);
   } else if (rc_cfg->scoring == PMOE_SCORE_SIGMOID) {

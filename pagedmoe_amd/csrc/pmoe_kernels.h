@@ -58,33 +58,28 @@ struct GemvArgs {
   int out_f32;
 };
 
-// Weighted combine of the down projection (decode block path).
-struct CombineArgs {
-  const float* w;             // [n, k] routing weights
-  const float* shared_logit;  // [n] or null (shared weight 1)
-  int n, k;
-  uint16_t* out;              // [n, hidden] bf16
-};
+struct RouteDev;
 
 int qgemv(const GemvArgs& a, int bits, bool dual, int max_experts, int max_rows_per_expert,
           hipStream_t st);
-int down_combine(const GemvArgs& a, const CombineArgs& c, int bits, hipStream_t st);
+// Decode experts with routing recomputed per block (decode.hip).
+// record: scratch for the routing handed from gate/up to down
+// (decode_record_bytes()).
+int decode_routed(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int bits,
+                  int32_t* inds_out, float* w_out, uint16_t* out, void* record, hipStream_t st);
+size_t decode_record_bytes();
 
 // Routing (router.hip)
 int router_logits(const uint16_t* x, const uint16_t* w, const float* bias, int n, int d, int e,
                   float* out, hipStream_t st);
+// Logits [n, e+1]: columns < e from w (+ bias), column e from w_extra.
+int router_logits_ext(const uint16_t* x, const uint16_t* w, const uint16_t* w_extra,
+                      const float* bias, int n, int d, int e, float* out, hipStream_t st);
 int route_softmax(const float* logits, int n, int e, int k, int norm, int32_t* inds,
                   float* weights, hipStream_t st);
 int route_sigmoid(const float* logits, const float* bias, int n, int e, int n_group,
                   int topk_group, int k, int norm, float scale, int32_t* inds, float* weights,
                   hipStream_t st);
-
-// Decode route + dispatch in one block (route_decode.hip).
-int route_dispatch_decode(const float* logits, const float* bias, int scoring, int n, int e, int k,
-                          int shared, int norm, int n_group, int topk_group, float scale,
-                          int32_t* inds, float* weights, int32_t* order, int32_t* counts,
-                          int32_t* offsets, int32_t* inv, int32_t* active, int32_t* n_active,
-                          int32_t* zero, int n_zero, hipStream_t st);
 
 // Dispatch (dispatch.hip).  Flat row r reads id inds[(r / kk) * k_routed +
 // r % kk] when r % kk < k_routed and the shared pseudo-id n_routed otherwise;

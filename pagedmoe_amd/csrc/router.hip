@@ -33,10 +33,13 @@ __device__ __forceinline__ void fma8(float& acc, const uint4& a, const uint4& b)
 }
 
 // One wave computes a TE x TN tile of logits (experts x tokens).
+// Rows e < n_w come from w (+ bias), row n_w (if e > n_w) from w_extra;
+// out has ld = e columns.
 template <int TE, int TN>
 __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-    const float* __restrict__ bias, int n, int d, int e, float* __restrict__ out) {
+    const uint16_t* __restrict__ w_extra, const float* __restrict__ bias, int n, int d, int e,
+    int n_w, float* __restrict__ out) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int e0 = (blockIdx.x * kRouterWaves + wave) * TE;
@@ -49,6 +52,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
     for (int j = 0; j < TN; ++j) acc[i][j] = 0.0f;
 
   const int passes = (d + 511) / 512;
+#pragma unroll 4
   for (int t = 0; t < passes; ++t) {
     const int col = t * 512 + lane * 8;
     if (col < d) {
@@ -56,7 +60,8 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
 #pragma unroll
       for (int i = 0; i < TE; ++i) {
         const int ei = min(e0 + i, e - 1);
-        wv[i] = *reinterpret_cast<const uint4*>(w + size_t(ei) * d + col);
+        const uint16_t* src = ei < n_w ? w + size_t(ei) * d : w_extra;
+        wv[i] = *reinterpret_cast<const uint4*>(src + col);
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
@@ -75,8 +80,8 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
     for (int j = 0; j < TN; ++j) {
       const float s = wave_sum_bfly(acc[i][j]);
       if (lane == ((i * TN + j) & 63) && e0 + i < e && n0 + j < n) {
-        const float b = bias ? bias[e0 + i] : 0.0f;
-        out[size_t(n0 + j) * e + e0 + i] = bias ? s + b : s;
+        const bool biased = bias && e0 + i < n_w;
+        out[size_t(n0 + j) * e + e0 + i] = biased ? s + bias[e0 + i] : s;
       }
     }
 }
@@ -247,28 +252,34 @@ __global__ __launch_bounds__(256) void route_sigmoid_kernel(
 
 }  // namespace
 
-int router_logits(const uint16_t* x, const uint16_t* w, const float* bias, int n, int d, int e,
-                  float* out, hipStream_t st) {
+int router_logits_ext(const uint16_t* x, const uint16_t* w, const uint16_t* w_extra,
+                      const float* bias, int n, int d, int n_w, float* out, hipStream_t st) {
   PMOE_REQUIRE(x && w && out, "router_logits: null pointer");
-  PMOE_REQUIRE(n >= 0 && d > 0 && e > 0, "router_logits: bad shape");
+  PMOE_REQUIRE(n >= 0 && d > 0 && n_w > 0, "router_logits: bad shape");
   PMOE_REQUIRE(d % 8 == 0, "router_logits: hidden must be a multiple of 8");
   if (n == 0) return PMOE_OK;
+  const int e = n_w + (w_extra ? 1 : 0);
   ProfScope prof_scope(K_ROUTER_LOGITS, st);
   if (n >= 32) {
     constexpr int TE = 4, TN = 8;
     dim3 grid((e + kRouterWaves * TE - 1) / (kRouterWaves * TE), (n + TN - 1) / TN);
-    router_logits_kernel<TE, TN><<<grid, 256, 0, st>>>(x, w, bias, n, d, e, out);
+    router_logits_kernel<TE, TN><<<grid, 256, 0, st>>>(x, w, w_extra, bias, n, d, e, n_w, out);
   } else if (n >= 4) {
     constexpr int TE = 1, TN = 4;
     dim3 grid((e + kRouterWaves * TE - 1) / (kRouterWaves * TE), (n + TN - 1) / TN);
-    router_logits_kernel<TE, TN><<<grid, 256, 0, st>>>(x, w, bias, n, d, e, out);
+    router_logits_kernel<TE, TN><<<grid, 256, 0, st>>>(x, w, w_extra, bias, n, d, e, n_w, out);
   } else {
     constexpr int TE = 1, TN = 1;
     dim3 grid((e + kRouterWaves * TE - 1) / (kRouterWaves * TE), n);
-    router_logits_kernel<TE, TN><<<grid, 256, 0, st>>>(x, w, bias, n, d, e, out);
+    router_logits_kernel<TE, TN><<<grid, 256, 0, st>>>(x, w, w_extra, bias, n, d, e, n_w, out);
   }
   PMOE_LAUNCH_CHECK("router_logits_kernel");
   return PMOE_OK;
+}
+
+int router_logits(const uint16_t* x, const uint16_t* w, const float* bias, int n, int d, int e,
+                  float* out, hipStream_t st) {
+  return router_logits_ext(x, w, nullptr, bias, n, d, e, out, st);
 }
 
 int route_softmax(const float* logits, int n, int e, int k, int norm, int32_t* inds,
