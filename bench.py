@@ -51,7 +51,6 @@ def build_layers(g, spec, n_layers, device, seed=0):
     the per-layer expert->slot tables."""
     import torch
 
-    from pagedmoe_amd import kernels as K
     from pagedmoe_amd.slab import SlabStore
 
     E, D, I = spec["experts"], spec["hidden"], spec["inter"]
@@ -59,14 +58,9 @@ def build_layers(g, spec, n_layers, device, seed=0):
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
     for slot in range(n_layers * E):
-        comps = {}
         for prefix, rows, cols in (("gate_proj", I, D), ("up_proj", I, D), ("down_proj", D, I)):
             w = torch.randn((rows, cols), generator=gen, device=device) * 0.02
-            q, s, b = K.quantize(w, g.bits)
-            comps[prefix + ".weight"] = q
-            comps[prefix + ".scales"] = s
-            comps[prefix + ".biases"] = b
-        slab.write_expert(slot, comps)
+            slab.quantize_into(slot, prefix, w)
     gate = (torch.randn((n_layers, E, D), generator=gen, device=device) * 0.02).to(torch.bfloat16)
     tables = (torch.arange(n_layers, device=device, dtype=torch.int32)[:, None] * E
               + torch.arange(E, device=device, dtype=torch.int32)[None, :]).contiguous()
@@ -176,6 +170,40 @@ def run_decode(args, g, spec, slab, gate, tables, batch, device):
     return res
 
 
+def pmc_run(args, g, spec, slab, gate, tables, device):
+    """Eager layer steps for hardware-counter runs (one dispatch per kernel,
+    no graph), followed by a plain copy of known size for calibration."""
+    import torch
+
+    from pagedmoe_amd import kernels as K
+
+    E, D, k = spec["experts"], spec["hidden"], spec["top_k"]
+    rc = K.route_cfg(spec["scoring"], E, k)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(2000)
+    x = torch.randn((args.steps, args.batch, D), generator=gen, device=device).to(torch.bfloat16)
+    ws = K.moe_workspace(g, args.batch, k, 0, E, device).clone()
+    inds = torch.empty((args.steps, args.batch, k), dtype=torch.int32, device=device)
+    for i in range(args.steps):
+        layer = i % args.layers
+        K.moe_block(g, rc, slab.buf, tables[layer], gate[layer], x[i], inds=inds[i], ws=ws)
+    torch.cuda.synchronize()
+    # calibration: one elementwise kernel reading and writing 256 MiB
+    src = torch.ones(64 << 20, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    ids = inds.cpu().numpy().reshape(args.steps, -1)
+    uniq = sum(len(set(r.tolist())) for r in ids) / args.steps
+    print(json.dumps({"pmc_run": True, "steps": args.steps, "batch": args.batch,
+                      "mean_unique_experts": uniq, "copy_read_bytes": 256 << 20,
+                      "copy_write_bytes": 256 << 20,
+                      "gateup_bytes_per_step": uniq * 2 * int(g.nbytes[0] + g.nbytes[1] + g.nbytes[2]),
+                      "down_bytes_per_step": uniq * int(g.nbytes[6] + g.nbytes[7] + g.nbytes[8])}),
+          flush=True)
+
+
 def cpu_baseline(g, spec, slab, gate, seconds, device):
     """The oracle's C restatement (OpenMP over all host cores) running the
     same decode layer (layer 0's 128 experts, fresh tokens) for ~seconds."""
@@ -224,6 +252,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the batch-8 line in extra")
+    ap.add_argument("--pmc-run", action="store_true",
+                    help="counter-collection run: `--steps` eager layer steps at `--batch`, then "
+                         "one 256 MiB device-to-device copy as the counter calibration")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -246,6 +277,10 @@ def main():
     slab, gate, tables = build_layers(g, spec, args.layers, device)
     torch.cuda.synchronize()
     log(f"built in {time.perf_counter() - t0:.1f} s")
+
+    if args.pmc_run:
+        pmc_run(args, g, spec, slab, gate, tables, device)
+        return
 
     main_res = run_decode(args, g, spec, slab, gate, tables, args.batch, device)
     log(f"batch {args.batch}: {main_res['ms_per_step'] * 1e3:.1f} us/step, "

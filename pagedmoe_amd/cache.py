@@ -1,0 +1,234 @@
+"""Expert residency over one HBM slab: slot table, pinned host store, paging.
+
+Counterpart of the reference's ``ExpertCache`` slab path (cache.py:410).  The
+policy itself is native (libpmoe ``pmoe_slab_*``): LRU with the LFRU second
+chance, a reserve of free slots, pins for the experts of the current layer
+step, and a full "stitch" when every expert fits (cache.py:717-787).  Misses
+are copied from a pinned host expert store into their slots by the native copy
+engine on side streams; the compute stream waits on events, never the host.
+The reference's misses come from SSD preads; the host store stands in for the
+page cache / checkpoint (loading real checkpoints into it is the next step).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import config
+from ._lib import Geom, PmoeError, SlabStats, check, lib
+from .slab import SlabStore
+
+
+class HostExpertStore:
+    """Pinned host memory holding every (layer, expert) in slot layout:
+    expert e of layer l at ``((l * n_experts) + e) * expert_bytes``."""
+
+    def __init__(self, g: Geom, n_layers: int, n_experts: int):
+        self.geom = g
+        self.n_layers = n_layers
+        self.n_experts = n_experts
+        self.expert_bytes = int(g.expert_bytes)
+        self.nbytes = n_layers * n_experts * self.expert_bytes
+        self._ptr = ctypes.c_void_p()
+        check(lib().pmoe_host_alloc(ctypes.byref(self._ptr), self.nbytes), "pmoe_host_alloc")
+        buf = (ctypes.c_uint8 * self.nbytes).from_address(self._ptr.value)
+        self.bytes = np.frombuffer(buf, dtype=np.uint8)
+
+    @property
+    def address(self) -> int:
+        return self._ptr.value
+
+    def expert_view(self, layer: int, e: int) -> np.ndarray:
+        off = (layer * self.n_experts + e) * self.expert_bytes
+        return self.bytes[off:off + self.expert_bytes]
+
+    def write_from_slot(self, layer: int, e: int, slab: SlabStore, slot: int) -> None:
+        """Copy one slot's bytes (device) into the store entry (host)."""
+        host = torch.from_numpy(self.expert_view(layer, e))
+        host.copy_(slab.slot_bytes(slot), non_blocking=False)
+
+    def close(self) -> None:
+        if self._ptr.value:
+            self.bytes = None
+            lib().pmoe_host_free(self._ptr)
+            self._ptr = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class ExpertCache:
+    """Slot residency of the routed experts of ``layer_keys`` (E experts each)
+    in a slab of ``slots`` routed slots, plus one pinned slot per layer for a
+    shared expert when ``n_shared`` is 1."""
+
+    def __init__(self, g: Geom, slots: int, layer_keys, n_experts: int, *,
+                 host_store: HostExpertStore | None = None, n_shared: int = 0,
+                 reserve_frac: float | None = None, lfru: bool | None = None,
+                 lfru_scan: int | None = None, device="cuda"):
+        self.geom = g
+        self.layer_keys = list(layer_keys)
+        self._layer = {k: i for i, k in enumerate(self.layer_keys)}
+        self.n_experts = int(n_experts)
+        self.routed_slots = int(slots)
+        self.n_shared = int(n_shared)
+        self.slab = SlabStore(g, self.routed_slots + self.n_shared * len(self.layer_keys), device)
+        self.host_store = host_store
+        self._h = ctypes.c_void_p()
+        check(lib().pmoe_slab_create(
+            ctypes.byref(self._h), self.routed_slots, len(self.layer_keys), self.n_experts,
+            config.SLAB_RESERVE_FRAC if reserve_frac is None else reserve_frac,
+            int(config.LFRU if lfru is None else lfru),
+            config.LFRU_SCAN if lfru_scan is None else lfru_scan), "pmoe_slab_create")
+        self._ce = ctypes.c_void_p()
+        if host_store is not None:
+            check(lib().pmoe_copy_engine_create(ctypes.byref(self._ce), config.COPY_SPLIT_BYTES,
+                                                config.COPY_STREAMS), "pmoe_copy_engine_create")
+        self.stitched = False
+        self.h2d_wait_s = 0.0
+
+    # ------------------------------------------------------------- tables
+
+    def layer_index(self, layer_key) -> int:
+        return self._layer[layer_key]
+
+    def table_ptr(self, layer_key) -> int:
+        """Device address of the layer's expert->slot row (int32 [E])."""
+        p = lib().pmoe_slab_device_table(self._h, self.layer_index(layer_key))
+        if not p:
+            raise PmoeError(lib().pmoe_last_error().decode())
+        return p
+
+    def host_table(self, layer_key) -> np.ndarray:
+        out = (ctypes.c_int32 * self.n_experts)()
+        check(lib().pmoe_slab_host_table(self._h, self.layer_index(layer_key), out),
+              "pmoe_slab_host_table")
+        return np.array(out[:], np.int32)
+
+    def flow_table(self, layer_key):
+        """Device pointer of the expert->slot table (-1 = not resident);
+        the reference's flow table (cache.py:843)."""
+        return self.table_ptr(layer_key)
+
+    def stitch_table(self, layer_key):
+        return self.table_ptr(layer_key) if self.stitched else None
+
+    def shared_slot(self, layer_key) -> int:
+        if not self.n_shared:
+            return -1
+        return self.routed_slots + self.layer_index(layer_key)
+
+    def publish(self, layer_key) -> None:
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        check(lib().pmoe_slab_publish(self._h, self.layer_index(layer_key), stream),
+              "pmoe_slab_publish")
+
+    # ------------------------------------------------------------- fetch
+
+    def request(self, layer_key, expert_ids):
+        """Policy step only: [(expert, slot)] of the misses that got a slot."""
+        ids = [int(e) for e in expert_ids]
+        arr = (ctypes.c_int32 * max(1, len(ids)))(*ids)
+        mid = (ctypes.c_int32 * max(1, len(ids)))()
+        msl = (ctypes.c_int32 * max(1, len(ids)))()
+        nm = ctypes.c_int()
+        check(lib().pmoe_slab_request(self._h, self.layer_index(layer_key), arr, len(ids), mid, msl,
+                                      ctypes.byref(nm)), "pmoe_slab_request")
+        return [(mid[i], msl[i]) for i in range(nm.value)]
+
+    def fetch(self, layer_key, expert_ids) -> int:
+        """One decode-layer fetch (cache.py:2525 on the slab path): classify,
+        copy the misses from the host store into their slots, publish the
+        table, and make the current stream wait for the copies.  Returns the
+        number of misses copied."""
+        if self.host_store is None:
+            raise PmoeError("fetch needs a host expert store")
+        ids = [int(e) for e in expert_ids]
+        arr = (ctypes.c_int32 * max(1, len(ids)))(*ids)
+        nm = ctypes.c_int()
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        check(lib().pmoe_slab_fetch(self._h, self._ce, ctypes.byref(self.geom),
+                                    ctypes.c_void_p(self.slab.data_ptr),
+                                    ctypes.c_void_p(self.host_store.address),
+                                    self.layer_index(layer_key), arr, len(ids),
+                                    ctypes.byref(nm), stream), "pmoe_slab_fetch")
+        return nm.value
+
+    def sync_copies(self) -> None:
+        if self._ce.value:
+            check(lib().pmoe_copy_sync(self._ce), "pmoe_copy_sync")
+
+    def load_stitch(self) -> bool:
+        """Pin every expert of every layer in slot layer*E + e when they all
+        fit (cache.py:717-787); copies them from the host store."""
+        if not config.STITCH:
+            return False
+        r = lib().pmoe_slab_stitch(self._h)
+        if r < 0:
+            check(r, "pmoe_slab_stitch")
+        if r == 0:
+            return False
+        if self.host_store is not None:
+            for layer_key in self.layer_keys:
+                li = self.layer_index(layer_key)
+                table = self.host_table(layer_key)
+                for e in range(self.n_experts):
+                    src = torch.from_numpy(self.host_store.expert_view(li, e))
+                    self.slab.slot_bytes(int(table[e])).copy_(src, non_blocking=False)
+        for layer_key in self.layer_keys:
+            self.publish(layer_key)
+        torch.cuda.current_stream().synchronize()
+        self.stitched = True
+        return True
+
+    # ------------------------------------------------------------- stats
+
+    def raw_stats(self) -> SlabStats:
+        st = SlabStats()
+        check(lib().pmoe_slab_stats_get(self._h, ctypes.byref(st)), "pmoe_slab_stats_get")
+        return st
+
+    @property
+    def hits(self) -> int:
+        return self.raw_stats().hits
+
+    @property
+    def misses(self) -> int:
+        return self.raw_stats().misses
+
+    @property
+    def evictions(self) -> int:
+        return self.raw_stats().evictions
+
+    def stats(self) -> dict:
+        """Residency counters in the reference's names (cache.py:2967-3061)."""
+        st = self.raw_stats()
+        total = st.hits + st.misses
+        h2d = lib().pmoe_copy_bytes(self._ce) if self._ce.value else 0
+        return {
+            "hits": st.hits, "misses": st.misses, "hit_rate": st.hits / total if total else 0.0,
+            "evictions": st.evictions, "slot_starved": st.starved, "slab_slots": st.slots,
+            "slab_free": st.slots - st.resident, "resident": st.resident, "budget": st.budget,
+            "reserve": st.reserve, "stitched": bool(st.stitched),
+            "read_gb": st.bytes_copied / 1e9, "h2d_gb": h2d / 1e9,
+        }
+
+    def close(self) -> None:
+        if self._ce.value:
+            lib().pmoe_copy_engine_destroy(self._ce)
+            self._ce = ctypes.c_void_p()
+        if self._h.value:
+            lib().pmoe_slab_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

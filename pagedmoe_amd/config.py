@@ -1,0 +1,45 @@
+"""Hot-path knobs, read from the environment once at import.
+
+Names and defaults follow the reference's PAGED_MOE_* knobs that touch this
+path (config.py: SLAB_RESERVE_FRAC :718, LFRU/LFRU_SCAN :1477-1478, STITCH
+:1186); ``sync_from_environ()`` re-reads them (config.py:853).
+"""
+
+from __future__ import annotations
+
+import os
+
+
+def _env(name: str, default, cast):
+    raw = os.environ.get("PAGED_MOE_" + name)
+    if raw is None or raw == "":
+        return default
+    try:
+        return cast(raw)
+    except ValueError:
+        return default
+
+
+def _bool(v: str) -> bool:
+    return v.strip().lower() not in ("0", "false", "off", "no")
+
+
+SLAB_RESERVE_FRAC = 0.1   # slots held back from the resident budget
+LFRU = True               # second-chance eviction for reused experts
+LFRU_SCAN = 8             # entries scanned per eviction
+STITCH = True             # pin every expert in a fixed slot when the slab holds them all
+COPY_SPLIT_BYTES = 4 << 20  # H2D copy piece size
+COPY_STREAMS = 2          # copy streams of the engine
+
+
+def sync_from_environ() -> None:
+    global SLAB_RESERVE_FRAC, LFRU, LFRU_SCAN, STITCH, COPY_SPLIT_BYTES, COPY_STREAMS
+    SLAB_RESERVE_FRAC = _env("SLAB_RESERVE_FRAC", 0.1, float)
+    LFRU = _env("LFRU", True, _bool)
+    LFRU_SCAN = _env("LFRU_SCAN", 8, int)
+    STITCH = _env("STITCH", True, _bool)
+    COPY_SPLIT_BYTES = _env("COPY_SPLIT_KB", 4096, int) * 1024
+    COPY_STREAMS = _env("COPY_STREAMS", 2, int)
+
+
+sync_from_environ()

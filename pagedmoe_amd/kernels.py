@@ -118,15 +118,25 @@ def dispatch(inds: torch.Tensor, n_experts: int) -> dict:
 
 # ---------------------------------------------------------------- format
 
-def quantize(w: torch.Tensor, bits: int, group: int = 64):
-    """fp32 [R, C] -> (q int32 [R, C*bits/32], scales bf16, biases bf16)."""
+def quantize(w: torch.Tensor, bits: int, group: int = 64, out=None):
+    """fp32 [R, C] -> (q int32 [R, C*bits/32], scales bf16, biases bf16).
+    ``out`` = (q, s, b) contiguous tensors to write into (e.g. slab views)."""
     _need(w, torch.float32, "w", 2)
     r, c = w.shape
     if c % group or (c * bits) % 32:
         raise ValueError("columns must be a multiple of the group size")
-    q = torch.empty((r, c * bits // 32), dtype=torch.int32, device=w.device)
-    s = torch.empty((r, c // group), dtype=torch.bfloat16, device=w.device)
-    b = torch.empty((r, c // group), dtype=torch.bfloat16, device=w.device)
+    if out is None:
+        q = torch.empty((r, c * bits // 32), dtype=torch.int32, device=w.device)
+        s = torch.empty((r, c // group), dtype=torch.bfloat16, device=w.device)
+        b = torch.empty((r, c // group), dtype=torch.bfloat16, device=w.device)
+    else:
+        q, s, b = out
+        for t, dt, shape, name in ((q, torch.int32, (r, c * bits // 32), "q"),
+                                   (s, torch.bfloat16, (r, c // group), "scales"),
+                                   (b, torch.bfloat16, (r, c // group), "biases")):
+            _need(t, dt, name)
+            if tuple(t.shape) != shape:
+                raise ValueError(f"{name}: expected {shape}, got {tuple(t.shape)}")
     check(lib().pmoe_quantize(_ptr(w), r, c, bits, group, _ptr(q), _ptr(s), _ptr(b), _stream()),
           "pmoe_quantize")
     return q, s, b

@@ -114,3 +114,12 @@ class SlabStore:
             if src.dtype != dt:
                 src = src.view(dt)
             self.expert(name, slot).copy_(src, non_blocking=False)
+
+    def quantize_into(self, slot: int, proj: str, w: torch.Tensor) -> None:
+        """Quantize fp32 weights w ([out, in] of projection `proj`) straight
+        into slot's components (no staging copy)."""
+        from . import kernels
+        kernels.quantize(w, self.geom.bits, self.geom.group,
+                         out=(self.expert(proj + ".weight", slot),
+                              self.expert(proj + ".scales", slot),
+                              self.expert(proj + ".biases", slot)))

@@ -1,0 +1,300 @@
+"""The MoE seam and the blocks around it (torch modules over libpmoe).
+
+Mirrors the reference's drop-in surface (streaming.py):
+  * ``StreamedSwitchGLU.__call__(x, indices) -> [..., K, D]`` -- per-slot,
+    uncombined expert outputs in ``indices`` order, the contract of mlx-lm's
+    ``SwitchGLU`` that the reference replaces (streaming.py:946-1401);
+  * ``patch_model(model, cache)`` swaps every resident ``QuantizedSwitchGLU``
+    for a ``StreamedSwitchGLU`` backed by the expert cache
+    (streaming.py:2575-2688); ``find_switch_glus`` (:2512-2526);
+  * the MoE blocks that call it: softmax top-k (Qwen3-MoE / Qwen3-Next, with an
+    optional gated shared expert) and sigmoid grouped top-k (DeepSeek-V3 /
+    Kimi-K2, with a shared expert) -- router, top-k, experts and the fixed-order
+    combine run as HIP kernels (pmoe_moe_block).
+All compute is on the GPU; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from . import kernels as K
+from ._lib import geom as make_geom
+from .cache import ExpertCache
+from .slab import SlabStore
+
+PROJS = ("gate_proj", "up_proj", "down_proj")
+
+
+class QuantizedSwitchGLU(nn.Module):
+    """Resident stacked experts: E affine-quantized SwiGLU experts (plus an
+    optional shared expert in slot E) in one slab, expert e in slot e.  The
+    resident counterpart of mlx-lm's SwitchGLU over QuantizedSwitchLinear."""
+
+    def __init__(self, hidden: int, inter: int, n_experts: int, bits: int = 4, group: int = 64,
+                 n_shared: int = 0, device="cuda"):
+        super().__init__()
+        self.geom = make_geom(hidden, inter, bits, group)
+        self.hidden, self.inter, self.bits = hidden, inter, bits
+        self.n_experts = n_experts
+        self.n_shared = n_shared
+        self.slab = SlabStore(self.geom, n_experts + n_shared, device)
+        self.register_buffer("table", torch.arange(n_experts, dtype=torch.int32, device=device),
+                             persistent=False)
+
+    @property
+    def shared_slot(self) -> int:
+        return self.n_experts if self.n_shared else -1
+
+    def quantize_expert(self, e: int, gate_w, up_w, down_w) -> None:
+        """Quantize fp32 weights gate/up [I, D], down [D, I] into expert e's
+        slot (e == n_experts: the shared expert)."""
+        for proj, w in zip(PROJS, (gate_w, up_w, down_w)):
+            self.slab.quantize_into(e, proj, w.float().contiguous())
+
+    def load_expert(self, e: int, comps: dict) -> None:
+        """Copy already quantized components (name -> tensor/array) into slot e."""
+        self.slab.write_expert(e, comps)
+
+    def forward(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        lead = indices.shape
+        x2 = x.reshape(-1, self.hidden).to(torch.bfloat16).contiguous()
+        ind2 = indices.reshape(-1, lead[-1]).to(torch.int32).contiguous()
+        y = K.switch_glu(self.geom, self.slab.buf, self.table, self.n_experts, x2, ind2)
+        return y.reshape(*lead, self.hidden)
+
+
+class StreamedSwitchGLU(nn.Module):
+    """The seam: same call contract as QuantizedSwitchGLU, experts paged
+    into the cache's slab on demand.
+
+    With every expert stitched into a fixed slot the call never leaves the
+    GPU.  Otherwise the routed ids reach the host (the one sync per layer the
+    reference also pays, streaming.py:1103-1129), the cache copies the misses
+    from the pinned host store and publishes the expert->slot table, and the
+    expert kernels read the slab through that table."""
+
+    def __init__(self, layer_key, original: QuantizedSwitchGLU | None, cache: ExpertCache,
+                 ring=None, predictor=None):
+        super().__init__()
+        self.layer_key = layer_key
+        self.cache = cache
+        self.ring = ring
+        self.pred = predictor
+        g = cache.geom
+        self.hidden, self.inter, self.bits = g.hidden, g.inter, g.bits
+        self.n_experts = cache.n_experts
+        self.last_ids: list[int] = []
+
+    @property
+    def geom(self):
+        return self.cache.geom
+
+    def prepare(self, indices: torch.Tensor) -> int:
+        """Make this layer's routed experts resident; returns the table
+        pointer to compute with."""
+        if not self.cache.stitched:
+            ids = torch.unique(indices.reshape(-1)).tolist()
+            self.cache.fetch(self.layer_key, ids)
+            self.last_ids = ids
+        return self.cache.table_ptr(self.layer_key)
+
+    def forward(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        lead = indices.shape
+        x2 = x.reshape(-1, self.hidden).to(torch.bfloat16).contiguous()
+        ind2 = indices.reshape(-1, lead[-1]).to(torch.int32).contiguous()
+        table = self.prepare(ind2)
+        y = K.switch_glu(self.cache.geom, self.cache.slab.buf, table, self.n_experts, x2, ind2)
+        return y.reshape(*lead, self.hidden)
+
+
+def _experts_of(switch_mlp):
+    """(geom, slab tensor, table, n_experts, shared slot) of a resident or
+    streamed switch."""
+    if isinstance(switch_mlp, StreamedSwitchGLU):
+        c = switch_mlp.cache
+        return c.geom, c.slab.buf, None, c.n_experts, c.shared_slot(switch_mlp.layer_key)
+    return (switch_mlp.geom, switch_mlp.slab.buf, switch_mlp.table, switch_mlp.n_experts,
+            switch_mlp.shared_slot)
+
+
+class _MoEBlock(nn.Module):
+    scoring = "softmax"
+
+    def _route_cfg(self):
+        raise NotImplementedError
+
+    def _score_bias(self):
+        return None
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1]).to(torch.bfloat16).contiguous()
+        g, slab, table, n_exp, shared_slot = _experts_of(self.switch_mlp)
+        if not self.use_shared:
+            shared_slot = -1
+        rc = self._route_cfg()
+        sg = self.shared_expert_gate if self.use_shared else None
+        sm = self.switch_mlp
+        if isinstance(sm, StreamedSwitchGLU) and not sm.cache.stitched:
+            # route, then make the routed experts resident, then compute
+            logits = K.router_logits(x2, self.gate_weight, self.logit_bias)
+            if self.scoring == "softmax":
+                inds, w = K.route_softmax_topk(logits, self.top_k, self.norm_topk_prob)
+            else:
+                inds, w = K.route_sigmoid_group_topk(logits, self._score_bias(), self.n_group,
+                                                     self.topk_group, self.top_k,
+                                                     self.norm_topk_prob, self.routed_scale)
+            table = sm.prepare(inds)
+            out = K.moe_experts(g, slab, table, n_exp, x2, inds, w, shared_slot, sg)
+            self.last_routing = (inds, w)
+            return out.reshape(shape)
+        if table is None:
+            table = sm.cache.table_ptr(sm.layer_key)
+        out, inds, w = K.moe_block(g, rc, slab, table, self.gate_weight, x2,
+                                   score_bias=self._score_bias(), logit_bias=self.logit_bias,
+                                   shared_slot=shared_slot, shared_gate=sg)
+        self.last_routing = (inds, w)
+        return out.reshape(shape)
+
+
+class SoftmaxMoEBlock(_MoEBlock):
+    """Qwen3-MoE / Qwen3-Next sparse MoE block: softmax router, top-k,
+    optional renormalisation, optional shared expert scaled by
+    sigmoid(x . shared_expert_gate).  ``logit_bias`` ([E] fp32) is an additive
+    router-logit skew used by the uneven-load synthetic workloads."""
+
+    scoring = "softmax"
+
+    def __init__(self, gate_weight: torch.Tensor, switch_mlp, top_k: int,
+                 norm_topk_prob: bool = True, shared_expert_gate: torch.Tensor | None = None,
+                 use_shared: bool | None = None, logit_bias: torch.Tensor | None = None):
+        super().__init__()
+        self.gate_weight = gate_weight.to(torch.bfloat16).contiguous()
+        self.switch_mlp = switch_mlp
+        self.top_k = top_k
+        self.norm_topk_prob = norm_topk_prob
+        self.shared_expert_gate = (None if shared_expert_gate is None
+                                   else shared_expert_gate.to(torch.bfloat16).contiguous())
+        has_shared = _experts_of(switch_mlp)[4] >= 0
+        self.use_shared = has_shared if use_shared is None else use_shared
+        self.logit_bias = logit_bias
+
+    def _route_cfg(self):
+        return K.route_cfg("softmax", self.gate_weight.shape[0], self.top_k, self.norm_topk_prob)
+
+
+class SigmoidGroupMoEBlock(_MoEBlock):
+    """DeepSeek-V3 / Kimi-K2 MoE block: sigmoid scores plus
+    e_score_correction_bias, grouped top-k, routed scaling, and an always-on
+    shared expert (out = routed mixture + shared(x))."""
+
+    scoring = "sigmoid"
+
+    def __init__(self, gate_weight: torch.Tensor, e_score_correction_bias: torch.Tensor, switch_mlp,
+                 top_k: int, n_group: int, topk_group: int, routed_scaling_factor: float,
+                 norm_topk_prob: bool = True, use_shared: bool | None = None):
+        super().__init__()
+        self.gate_weight = gate_weight.to(torch.bfloat16).contiguous()
+        self.e_score_correction_bias = e_score_correction_bias.float().contiguous()
+        self.switch_mlp = switch_mlp
+        self.top_k = top_k
+        self.n_group = n_group
+        self.topk_group = topk_group
+        self.routed_scale = routed_scaling_factor
+        self.norm_topk_prob = norm_topk_prob
+        self.shared_expert_gate = None
+        has_shared = _experts_of(switch_mlp)[4] >= 0
+        self.use_shared = has_shared if use_shared is None else use_shared
+        self.logit_bias = None
+
+    def _score_bias(self):
+        return self.e_score_correction_bias
+
+    def _route_cfg(self):
+        return K.route_cfg("sigmoid", self.gate_weight.shape[0], self.top_k, self.norm_topk_prob,
+                           self.n_group, self.topk_group, self.routed_scale)
+
+
+# ---------------------------------------------------------------- model surgery
+
+def find_switch_glus(model: nn.Module):
+    """All QuantizedSwitchGLU modules with their tree paths, in layer order
+    (streaming.py:2512-2526)."""
+    found = [(p, m) for p, m in model.named_modules() if isinstance(m, QuantizedSwitchGLU)]
+
+    def layer_num(path):
+        for part in path.split("."):
+            if part.isdigit():
+                return int(part)
+        return 0
+
+    found.sort(key=lambda kv: layer_num(kv[0]))
+    return found
+
+
+def _resolve_parent(model, path: str):
+    parts = path.split(".")
+    obj = model
+    for p in parts[:-1]:
+        obj = obj[int(p)] if p.isdigit() else getattr(obj, p)
+    return obj, parts[-1]
+
+
+def build_cache_for(model: nn.Module, slots: int, **kw) -> ExpertCache:
+    """An ExpertCache (with a pinned host store holding every expert of every
+    QuantizedSwitchGLU of ``model``) for patch_model."""
+    from .cache import HostExpertStore
+
+    glus = find_switch_glus(model)
+    if not glus:
+        raise ValueError("no QuantizedSwitchGLU modules found")
+    first = glus[0][1]
+    n_shared = first.n_shared
+    g = first.geom
+    store = HostExpertStore(g, len(glus), first.n_experts)
+    for li, (_, m) in enumerate(glus):
+        if (m.hidden, m.inter, m.bits, m.n_experts, m.n_shared) != (
+                first.hidden, first.inter, first.bits, first.n_experts, n_shared):
+            raise ValueError("all MoE layers must share one expert shape")
+        for e in range(m.n_experts):
+            store.write_from_slot(li, e, m.slab, e)
+    cache = ExpertCache(g, slots, [p for p, _ in glus], first.n_experts, host_store=store,
+                        n_shared=n_shared, **kw)
+    for li, (p, m) in enumerate(glus):
+        if n_shared:
+            cache.slab.slot_bytes(cache.shared_slot(p)).copy_(m.slab.slot_bytes(m.n_experts))
+    return cache
+
+
+def patch_model(model: nn.Module, cache: ExpertCache, prefetch_depth: int = 0):
+    """Replace every QuantizedSwitchGLU with a StreamedSwitchGLU over
+    ``cache`` (streaming.py:2575-2688).  Returns the list of streamed layers
+    (the reference returns its PrefetchRing; speculative prefetch is not part
+    of this path).  The cache's layer keys must be the module paths."""
+    glus = find_switch_glus(model)
+    if not glus:
+        raise ValueError("no QuantizedSwitchGLU modules found - this model has no MoE layers")
+    streamed = []
+    for path, module in glus:
+        s = StreamedSwitchGLU(path, module, cache)
+        parent, attr = _resolve_parent(model, path)
+        if attr.isdigit():
+            parent[int(attr)] = s
+        else:
+            setattr(parent, attr, s)
+        streamed.append(s)
+    model._pagedmoe_cache = cache
+    model._pagedmoe_ring = streamed
+    if cache.n_experts * len(glus) <= cache.routed_slots:
+        cache.load_stitch()
+    return streamed
+
+
+def get_stats(model: nn.Module) -> dict:
+    """Residency counters of a patched model (loader.py:1003)."""
+    cache = getattr(model, "_pagedmoe_cache", None)
+    if cache is None:
+        return {}
+    return {"cache": cache.stats()}

@@ -75,17 +75,11 @@ def slot_to_expert(slab, slot) -> "O.Expert":
 def fill_slab_gpu(slab, slots, seed=0, std=0.02):
     """Random N(0, std) experts quantized on the GPU into the given slots."""
     import torch
-    from pagedmoe_amd import kernels as K
     g = slab.geom
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed)
     for slot in slots:
-        comps = {}
         for prefix, rows, cols in (("gate_proj", g.inter, g.hidden), ("up_proj", g.inter, g.hidden),
                                    ("down_proj", g.hidden, g.inter)):
             w = torch.randn((rows, cols), generator=gen, device="cuda", dtype=torch.float32) * std
-            q, s, b = K.quantize(w, g.bits, g.group)
-            comps[prefix + ".weight"] = q
-            comps[prefix + ".scales"] = s
-            comps[prefix + ".biases"] = b
-        slab.write_expert(slot, comps)
+            slab.quantize_into(slot, prefix, w)
