@@ -177,6 +177,17 @@ int pmoe_moe_block(const pmoe_geom* g, const pmoe_route_cfg* rc,
                    float* weights_out, void* ws, size_t ws_bytes,
                    void* stream);
 
+/* Weighted combine of per-slot outputs: out[n] = bf16(fma over k of
+ * weights[n,k] * y[n,k,:], then + s * shared_y[n,:]) with s = 1, or
+ * sigmoid(shared_logit[n]) when shared_logit != NULL.  y bf16 [n, k, hidden],
+ * shared_y bf16 [n, hidden] or NULL.  The block's
+ * (y * scores[..., None]).sum(axis=-2) + shared (tests/test_stream.py:198),
+ * used when a layer's experts ran in several fetch groups
+ * (cache.py:2535-2578, streaming.py:804-826). */
+int pmoe_combine(const void* y, const float* weights, int n, int k, int hidden,
+                 const void* shared_y, const float* shared_logit, void* out,
+                 void* stream);
+
 /* ---- slab slot table (replaces ExpertCache's slot policy, cache.py:410:
  *      _alloc_slot :1118-1159, _begin :2327-2453, _finish :2455-2523,
  *      _evict_to_budget :2236-2291, stitch :717-787, flow table :791-859) -- */

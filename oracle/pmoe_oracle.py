@@ -455,14 +455,20 @@ def combine_f64(y, w, shared=None) -> np.ndarray:
     return out
 
 
-def combine_f32(y_f32, w) -> np.ndarray:
+def combine_f32(y_f32, w, shared=None, shared_w=None) -> np.ndarray:
     """Fixed-order fp32 combine: acc = fma(w_k, y_k, acc) for k ascending,
-    then round to bf16.  This is the deterministic order of the HIP combine."""
+    then acc = fma(s, shared, acc) with s = shared_w[n] (1 when None), then
+    round to bf16 (bits).  This is the deterministic order of the HIP combine.
+    Each fma is formed exactly in float64 (a float32 product has at most 48
+    significant bits) and rounded once more to float32."""
     y = np.asarray(y_f32, np.float64)
     w = np.asarray(w, np.float64)
     acc = np.zeros((y.shape[0], y.shape[2]), np.float32)
     for j in range(y.shape[1]):
         acc = (acc.astype(np.float64) + w[:, j, None] * y[:, j, :]).astype(np.float32)
+    if shared is not None:
+        s = np.ones(y.shape[0]) if shared_w is None else np.asarray(shared_w, np.float64)
+        acc = (acc.astype(np.float64) + s[:, None] * np.asarray(shared, np.float64)).astype(np.float32)
     return bf16_round(acc)
 
 

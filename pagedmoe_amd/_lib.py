@@ -82,6 +82,7 @@ SIGNATURES = {
                               _P, _P, _SZ, _P]),
     "pmoe_moe_block": (_I, [ctypes.POINTER(Geom), ctypes.POINTER(RouteCfg), _P, _P, _P, _P, _P,
                             _P, _I, _I, _P, _P, _P, _P, _P, _SZ, _P]),
+    "pmoe_combine": (_I, [_P, _P, _I, _I, _I, _P, _P, _P, _P]),
     "pmoe_slab_create": (_I, [ctypes.POINTER(_P), _I, _I, _I, _F, _I, _I]),
     "pmoe_slab_destroy": (_I, [_P]),
     "pmoe_slab_device_table": (_P, [_P, _I]),

@@ -91,7 +91,7 @@ class ExpertCache:
             check(lib().pmoe_copy_engine_create(ctypes.byref(self._ce), config.COPY_SPLIT_BYTES,
                                                 config.COPY_STREAMS), "pmoe_copy_engine_create")
         self.stitched = False
-        self.h2d_wait_s = 0.0
+        self.group_passes = 0
 
     # ------------------------------------------------------------- tables
 
@@ -217,6 +217,7 @@ class ExpertCache:
             "slab_free": st.slots - st.resident, "resident": st.resident, "budget": st.budget,
             "reserve": st.reserve, "stitched": bool(st.stitched),
             "read_gb": st.bytes_copied / 1e9, "h2d_gb": h2d / 1e9,
+            "group_passes": self.group_passes,
         }
 
     def close(self) -> None:

@@ -112,6 +112,33 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   *reinterpret_cast<uint2*>(out + size_t(n) * d + d0) = o;
 }
 
+// Same reduction over bf16 per-slot outputs (the seam's [N, K, D]), for
+// callers that ran the experts in several passes.
+__global__ __launch_bounds__(256) void combine_bf16_kernel(const uint16_t* __restrict__ y,
+                                                           const float* __restrict__ w,
+                                                           const uint16_t* __restrict__ shared_y,
+                                                           const float* __restrict__ shared_logit,
+                                                           int k, int d,
+                                                           uint16_t* __restrict__ out) {
+  const int n = blockIdx.y;
+  const int d0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (d0 >= d) return;
+  float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto add = [&](float wt, const uint16_t* src) {
+    const uint2 v = *reinterpret_cast<const uint2*>(src + d0);
+    a[0] = __builtin_fmaf(wt, bf16lo(v.x), a[0]);
+    a[1] = __builtin_fmaf(wt, bf16hi(v.x), a[1]);
+    a[2] = __builtin_fmaf(wt, bf16lo(v.y), a[2]);
+    a[3] = __builtin_fmaf(wt, bf16hi(v.y), a[3]);
+  };
+  for (int c = 0; c < k; ++c) add(w[size_t(n) * k + c], y + (size_t(n) * k + c) * d);
+  if (shared_y) add(shared_logit ? psigmoid(shared_logit[n]) : 1.0f, shared_y + size_t(n) * d);
+  uint2 o;
+  o.x = uint32_t(f2bf(a[0])) | (uint32_t(f2bf(a[1])) << 16);
+  o.y = uint32_t(f2bf(a[2])) | (uint32_t(f2bf(a[3])) << 16);
+  *reinterpret_cast<uint2*>(out + size_t(n) * d + d0) = o;
+}
+
 __global__ __launch_bounds__(256) void zero_dropped_rows_kernel(const int32_t* __restrict__ inv,
                                                                 int rows, int d,
                                                                 uint16_t* __restrict__ y) {
@@ -375,4 +402,26 @@ extern "C" int pmoe_moe_block(const pmoe_geom* g, const pmoe_route_cfg* rc_cfg, 
                                    weights_out, n, k, shared_slot,
                                    static_cast<const uint16_t*>(shared_gate), n,
                                    static_cast<uint16_t*>(out), w, st);
+}
+
+extern "C" int pmoe_combine(const void* y, const float* weights, int n, int k, int hidden,
+                            const void* shared_y, const float* shared_logit, void* out,
+                            void* stream) {
+  pmoe::clear_error();
+  PMOE_REQUIRE(y && weights && out, "combine: null pointer");
+  PMOE_REQUIRE(n >= 0 && n <= 65535 && k > 0 && hidden > 0 && hidden % 4 == 0,
+               "combine: bad shape");
+  PMOE_REQUIRE(!shared_logit || shared_y, "combine: shared_logit without shared_y");
+  PMOE_REQUIRE((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(out) |
+                reinterpret_cast<uintptr_t>(shared_y)) % 8 == 0,
+               "combine: y/out/shared_y must be 8-byte aligned");
+  if (n == 0) return PMOE_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid((hidden / 4 + 255) / 256, n);
+  pmoe::ProfScope prof_scope(pmoe::K_COMBINE, st);
+  pmoe::combine_bf16_kernel<<<grid, 256, 0, st>>>(
+      static_cast<const uint16_t*>(y), weights, static_cast<const uint16_t*>(shared_y),
+      shared_logit, k, hidden, static_cast<uint16_t*>(out));
+  PMOE_LAUNCH_CHECK("combine_bf16_kernel");
+  return PMOE_OK;
 }

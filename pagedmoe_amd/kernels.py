@@ -200,6 +200,28 @@ def moe_experts(g: Geom, slab, table, n_experts: int, x, inds, weights, shared_s
     return out
 
 
+def combine(y: torch.Tensor, weights: torch.Tensor, shared_y=None, shared_logit=None):
+    """out [N, D] bf16 = sum_k weights[n,k] y[n,k] (+ s * shared_y[n]) with
+    fp32 accumulation in k order; s = 1 or sigmoid(shared_logit[n])."""
+    _need(y, torch.bfloat16, "y", 3)
+    _need(weights, torch.float32, "weights", 2)
+    n, k, d = y.shape
+    if tuple(weights.shape) != (n, k):
+        raise ValueError(f"weights must be [{n}, {k}], got {tuple(weights.shape)}")
+    if shared_y is not None:
+        _need(shared_y, torch.bfloat16, "shared_y", 2)
+        if tuple(shared_y.shape) != (n, d):
+            raise ValueError("shared_y must be [N, D]")
+    if shared_logit is not None:
+        _need(shared_logit, torch.float32, "shared_logit")
+        if shared_logit.numel() != n:
+            raise ValueError("shared_logit must hold N values")
+    out = torch.empty((n, d), dtype=torch.bfloat16, device=y.device)
+    check(lib().pmoe_combine(_ptr(y), _ptr(weights), n, k, d, _ptr(shared_y), _ptr(shared_logit),
+                             _ptr(out), _stream()), "pmoe_combine")
+    return out
+
+
 def route_cfg(scoring: str, n_experts: int, top_k: int, norm_topk_prob: bool = True,
               n_group: int = 1, topk_group: int = 1, routed_scale: float = 1.0) -> RouteCfg:
     rc = RouteCfg()

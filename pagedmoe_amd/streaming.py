@@ -91,20 +91,61 @@ class StreamedSwitchGLU(nn.Module):
     def geom(self):
         return self.cache.geom
 
+    def plan_groups(self, indices: torch.Tensor) -> list:
+        """The layer's distinct routed ids (one host sync) split into fetch
+        groups that each fit the slab's routed slots; already resident ids
+        go first so they are not evicted by their own layer.  A single
+        group is the normal case; several happen only when one layer routes
+        to more experts than the slab holds (long prefill chunks on a small
+        slab), the bounded-memory grouping of cache.py:2535-2578."""
+        ids = [e for e in torch.unique(indices.reshape(-1)).tolist() if 0 <= e < self.n_experts]
+        cap = self.cache.routed_slots
+        if len(ids) <= cap:
+            return [ids]
+        table = self.cache.host_table(self.layer_key)
+        ordered = [e for e in ids if table[e] >= 0] + [e for e in ids if table[e] < 0]
+        return [sorted(ordered[i:i + cap]) for i in range(0, len(ordered), cap)]
+
     def prepare(self, indices: torch.Tensor) -> int:
-        """Make this layer's routed experts resident; returns the table
-        pointer to compute with."""
+        """Make this layer's routed experts resident (they must fit in one
+        fetch group); returns the table pointer to compute with."""
         if not self.cache.stitched:
-            ids = torch.unique(indices.reshape(-1)).tolist()
-            self.cache.fetch(self.layer_key, ids)
-            self.last_ids = ids
+            groups = self.plan_groups(indices)
+            if len(groups) != 1:
+                raise RuntimeError("routed experts exceed the slab; use run_groups")
+            self.cache.fetch(self.layer_key, groups[0])
+            self.last_ids = groups[0]
         return self.cache.table_ptr(self.layer_key)
+
+    def run_groups(self, x2: torch.Tensor, ind2: torch.Tensor, groups: list) -> torch.Tensor:
+        """Per-slot outputs [N, K, D] computed one fetch group at a time:
+        each pass sees only its group's ids (others dropped to zero rows) and
+        its rows are merged by selection, so every row is bit-identical to a
+        single pass over a slab that holds all of them."""
+        c = self.cache
+        y = None
+        for grp in groups:
+            c.fetch(self.layer_key, grp)
+            member = torch.isin(ind2, torch.tensor(grp, dtype=torch.int32, device=ind2.device))
+            ind_g = torch.where(member, ind2, torch.full_like(ind2, -1))
+            y_g = K.switch_glu(c.geom, c.slab.buf, c.table_ptr(self.layer_key), self.n_experts,
+                               x2, ind_g)
+            y = y_g if y is None else torch.where(member[..., None], y_g, y)
+        c.group_passes += len(groups)
+        self.last_ids = [e for grp in groups for e in grp]
+        return y
 
     def forward(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         lead = indices.shape
         x2 = x.reshape(-1, self.hidden).to(torch.bfloat16).contiguous()
         ind2 = indices.reshape(-1, lead[-1]).to(torch.int32).contiguous()
-        table = self.prepare(ind2)
+        if not self.cache.stitched:
+            groups = self.plan_groups(ind2)
+            if len(groups) > 1:
+                return self.run_groups(x2, ind2, groups).reshape(*lead, self.hidden)
+            self.cache.fetch(self.layer_key, groups[0])
+            self.last_ids = groups[0]
+        table = self.cache.table_ptr(self.layer_key)
         y = K.switch_glu(self.cache.geom, self.cache.slab.buf, table, self.n_experts, x2, ind2)
         return y.reshape(*lead, self.hidden)
 
@@ -146,8 +187,21 @@ class _MoEBlock(nn.Module):
                 inds, w = K.route_sigmoid_group_topk(logits, self._score_bias(), self.n_group,
                                                      self.topk_group, self.top_k,
                                                      self.norm_topk_prob, self.routed_scale)
-            table = sm.prepare(inds)
-            out = K.moe_experts(g, slab, table, n_exp, x2, inds, w, shared_slot, sg)
+            groups = sm.plan_groups(inds)
+            if len(groups) == 1:
+                sm.cache.fetch(sm.layer_key, groups[0])
+                table = sm.cache.table_ptr(sm.layer_key)
+                out = K.moe_experts(g, slab, table, n_exp, x2, inds, w, shared_slot, sg)
+            else:
+                y = sm.run_groups(x2, inds, groups)
+                shared_y = shared_logit = None
+                if shared_slot >= 0:
+                    one = torch.full((1,), shared_slot, dtype=torch.int32, device=x2.device)
+                    zero = torch.zeros((x2.shape[0], 1), dtype=torch.int32, device=x2.device)
+                    shared_y = K.switch_glu(g, slab, one, 1, x2, zero).reshape(x2.shape)
+                    if sg is not None:
+                        shared_logit = K.router_logits(x2, sg.reshape(1, -1)).reshape(-1)
+                out = K.combine(y, w, shared_y, shared_logit)
             self.last_routing = (inds, w)
             return out.reshape(shape)
         if table is None:

@@ -1,0 +1,317 @@
+"""GPU: the drop-in surface (StreamedSwitchGLU, MoE blocks, patch_model,
+ExpertCache paging) and the committed golden fixtures through the HIP path.
+
+The streamed seam must give the same bytes as the resident module for the
+same experts (same kernels, the slot is the only difference), its residency
+counters must follow the oracle's slot policy, and the blocks must match the
+oracle's routing exactly and its float64 outputs within tests/util tolerance.
+"""
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from oracle import pmoe_oracle as O
+from tests.util import bits_to_bf16_tensor, check_close, expert_to_comps, slot_to_expert
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+G = Path(__file__).resolve().parent / "golden"
+
+
+def _mods():
+    from pagedmoe_amd import kernels, streaming
+    return kernels, streaming
+
+
+def _load(name):
+    return np.load(G / name, allow_pickle=False)
+
+
+# ---------------------------------------------------------------- golden fixtures
+
+def test_golden_tiny_layer_on_gpu():
+    K, S = _mods()
+    f = _load("tiny_layer.npz")
+    spec = O.LayerSpec(1024, 32, 512, 4)
+    gw, experts, _, _, _ = O.make_layer(spec, seed=0)
+    sw = S.QuantizedSwitchGLU(spec.hidden, spec.inter, spec.experts, spec.bits)
+    for e in range(spec.experts):
+        sw.load_expert(e, expert_to_comps(experts[e]))
+    blk = S.SoftmaxMoEBlock(bits_to_bf16_tensor(f["gate_bits"], DEV), sw, spec.top_k)
+    x = bits_to_bf16_tensor(f["x_bits"], DEV)
+    out = blk(x)
+    gi, gwt = blk.last_routing
+    assert np.array_equal(gi.cpu().numpy(), f["inds"])
+    assert np.array_equal(gwt.cpu().numpy(), f["weights"])
+    check_close(out.float().cpu().numpy(), f["out"].astype(np.float64), "golden tiny layer out")
+    logits = K.router_logits(x, bits_to_bf16_tensor(f["gate_bits"], DEV))
+    assert np.array_equal(logits.cpu().numpy(), f["logits"])
+    y = sw(x[:2], torch.from_numpy(f["inds"][:2]).to(DEV))
+    check_close(y.float().cpu().numpy(), f["y"].astype(np.float64), "golden per-slot y")
+
+
+def test_golden_routing_dispatch_quant_on_gpu():
+    K, _ = _mods()
+    f = _load("routing_sigmoid.npz")
+    gi, gw = K.route_sigmoid_group_topk(torch.from_numpy(f["logits"]).to(DEV),
+                                        torch.from_numpy(f["bias"]).to(DEV), 8, 4, 8, True, 2.5)
+    assert np.array_equal(gi.cpu().numpy(), f["inds"])
+    assert np.array_equal(gw.cpu().numpy(), f["weights"])
+    f = _load("routing_softmax.npz")
+    lg = torch.from_numpy(f["logits"]).to(DEV)
+    for norm, ki, kw in ((True, "inds", "weights"), (False, "inds_nonorm", "weights_nonorm")):
+        gi, gw = K.route_softmax_topk(lg, 10, norm)
+        assert np.array_equal(gi.cpu().numpy(), f[ki])
+        assert np.array_equal(gw.cpu().numpy(), f[kw])
+    f = _load("dispatch.npz")
+    d = K.dispatch(torch.from_numpy(f["ids"]).to(DEV), 128)
+    for key in ("order", "counts", "offsets", "inv", "active"):
+        assert np.array_equal(d[key].cpu().numpy(), f[key]), key
+    f = _load("quant_format.npz")
+    for bits in (4, 6):
+        q, s, b = K.quantize(torch.from_numpy(f["w"]).to(DEV), bits)
+        assert np.array_equal(q.cpu().numpy().view(np.uint32), f[f"q{bits}"])
+        assert np.array_equal(s.cpu().view(torch.int16).numpy().view(np.uint16), f[f"s{bits}"])
+        assert np.array_equal(b.cpu().view(torch.int16).numpy().view(np.uint16), f[f"b{bits}"])
+        deq = K.dequant(q, s, b, bits)
+        assert np.array_equal(deq.cpu().view(torch.int16).numpy().view(np.uint16), f[f"deq{bits}"])
+
+
+# ---------------------------------------------------------------- a toy model
+
+class _Layer(nn.Module):
+    def __init__(self, mlp):
+        super().__init__()
+        self.mlp = mlp
+
+
+class _Model(nn.Module):
+    def __init__(self, blocks):
+        super().__init__()
+        self.layers = nn.ModuleList([_Layer(b) for b in blocks])
+
+
+def _softmax_model(spec, n_layers, seed):
+    """n_layers Qwen3-style blocks over resident QuantizedSwitchGLUs, oracle
+    experts per layer (make_layer seeds seed+layer)."""
+    _, S = _mods()
+    blocks, oracle_layers = [], []
+    for li in range(n_layers):
+        gw, experts, _, sh, sg = O.make_layer(spec, seed=seed + li)
+        sw = S.QuantizedSwitchGLU(spec.hidden, spec.inter, spec.experts, spec.bits,
+                                  n_shared=spec.shared)
+        for e in range(spec.experts):
+            sw.load_expert(e, expert_to_comps(experts[e]))
+        if spec.shared:
+            sw.load_expert(spec.experts, expert_to_comps(sh[0]))
+        sgt = None if sg is None else bits_to_bf16_tensor(sg, DEV)
+        blocks.append(S.SoftmaxMoEBlock(bits_to_bf16_tensor(gw, DEV), sw, spec.top_k,
+                                        shared_expert_gate=sgt))
+        oracle_layers.append((gw, experts, sh, sg))
+    return _Model(blocks), oracle_layers
+
+
+def _resident_outputs(model, xs):
+    with torch.no_grad():
+        return [[layer.mlp.switch_mlp(x, i).clone() for x, i in step] for step, layer in
+                zip([xs] * len(model.layers), model.layers)]
+
+
+def test_find_switch_glus_order():
+    _, S = _mods()
+    spec = O.LayerSpec(1024, 8, 512, 2)
+    model, _ = _softmax_model(spec, 3, seed=40)
+    paths = [p for p, _ in S.find_switch_glus(model)]
+    assert paths == [f"layers.{i}.mlp.switch_mlp" for i in range(3)]
+
+
+def test_streamed_switch_paging_matches_resident_and_policy():
+    """16 routed slots (reserve 4, budget 12) for 3 layers x 32 experts: the
+    streamed seam pages experts in and out; every call's output equals the
+    resident module's, and hits/misses/evictions equal the oracle policy's."""
+    _, S = _mods()
+    spec = O.LayerSpec(1024, 32, 512, 4)
+    model, _ = _softmax_model(spec, 3, seed=50)
+    resident = [layer.mlp.switch_mlp for layer in model.layers]
+    cache = S.build_cache_for(model, slots=16)
+    streamed = S.patch_model(model, cache)
+    assert not cache.stitched
+    assert all(isinstance(layer.mlp.switch_mlp, S.StreamedSwitchGLU) for layer in model.layers)
+    pol = O.SlotPolicy(16)
+    rng = np.random.default_rng(51)
+    for step in range(12):
+        n = 1 + step % 3
+        for li, (res, st) in enumerate(zip(resident, streamed)):
+            x = bits_to_bf16_tensor(O.bf16_round(rng.standard_normal((n, spec.hidden),
+                                                                     dtype=np.float32)), DEV)
+            ids = np.stack([rng.choice(spec.experts, spec.top_k, replace=False) for _ in range(n)])
+            ids = ids.astype(np.int32)
+            ind = torch.from_numpy(ids).to(DEV)
+            got = st(x, ind)
+            ref = res(x, ind)
+            assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), (step, li)
+            pol.step(st.layer_key, ids.reshape(-1))
+            assert np.array_equal(cache.host_table(st.layer_key),
+                                  pol.table(st.layer_key, spec.experts)), (step, li)
+    s = cache.stats()
+    assert (s["hits"], s["misses"], s["evictions"]) == (pol.hits, pol.misses, pol.evictions)
+    assert s["evictions"] > 0 and s["hits"] > 0
+    assert S.get_stats(model)["cache"]["misses"] == pol.misses
+    cache.close()
+
+
+def test_streamed_switch_stitched_when_all_fit():
+    _, S = _mods()
+    spec = O.LayerSpec(1024, 8, 512, 2)
+    model, _ = _softmax_model(spec, 2, seed=60)
+    resident = [layer.mlp.switch_mlp for layer in model.layers]
+    cache = S.build_cache_for(model, slots=16)
+    streamed = S.patch_model(model, cache)
+    assert cache.stitched
+    rng = np.random.default_rng(61)
+    for res, st in zip(resident, streamed):
+        assert np.array_equal(cache.host_table(st.layer_key),
+                              np.arange(8, dtype=np.int32) + 8 * cache.layer_index(st.layer_key))
+        x = bits_to_bf16_tensor(O.bf16_round(rng.standard_normal((5, spec.hidden),
+                                                                 dtype=np.float32)), DEV)
+        ind = torch.from_numpy(rng.integers(0, 8, (5, 2)).astype(np.int32)).to(DEV)
+        assert torch.equal(st(x, ind).view(torch.int16), res(x, ind).view(torch.int16))
+    assert cache.stats()["misses"] == 0
+    cache.close()
+
+
+@pytest.mark.parametrize("n", [1, 3])
+def test_softmax_block_paged_vs_oracle(n):
+    """Patched Qwen3-style model, experts paged through a 16-slot slab: each
+    layer's routing is bit-exact and its output within tolerance of the
+    float64 oracle."""
+    _, S = _mods()
+    spec = O.LayerSpec(1024, 32, 512, 4)
+    model, ol = _softmax_model(spec, 2, seed=70)
+    cache = S.build_cache_for(model, slots=16)
+    S.patch_model(model, cache)
+    rng = np.random.default_rng(71 + n)
+    for step in range(3):
+        for li, layer in enumerate(model.layers):
+            xb = O.bf16_round(rng.standard_normal((n, spec.hidden), dtype=np.float32))
+            out = layer.mlp(bits_to_bf16_tensor(xb, DEV))
+            gw, experts, _, _ = ol[li]
+            ref_i, ref_w, _, ref = O.moe_layer_f64(spec, xb, gw, experts)
+            gi, gwt = layer.mlp.last_routing
+            assert np.array_equal(gi.cpu().numpy(), ref_i)
+            assert np.array_equal(gwt.cpu().numpy(), ref_w)
+            check_close(out.float().cpu().numpy(), ref, f"paged block step {step} layer {li}")
+    assert cache.stats()["misses"] > 0
+    cache.close()
+
+
+def test_sigmoid_shared_block_paged_and_resident_vs_oracle():
+    """DeepSeek-style routing with a shared expert: resident block (fused
+    path) and paged block (route -> fetch -> experts) both match the oracle."""
+    _, S = _mods()
+    spec = O.LayerSpec(1024, 64, 512, 6, scoring="sigmoid", n_group=8, topk_group=4,
+                       routed_scale=2.5, shared=1)
+    gw, experts, bias, sh, _ = O.make_layer(spec, seed=80)
+    sw = S.QuantizedSwitchGLU(spec.hidden, spec.inter, spec.experts, spec.bits, n_shared=1)
+    for e in range(spec.experts):
+        sw.load_expert(e, expert_to_comps(experts[e]))
+    sw.load_expert(spec.experts, expert_to_comps(sh[0]))
+    blk = S.SigmoidGroupMoEBlock(bits_to_bf16_tensor(gw, DEV), torch.from_numpy(bias).to(DEV), sw,
+                                 spec.top_k, spec.n_group, spec.topk_group, spec.routed_scale)
+    model = _Model([blk])
+    rng = np.random.default_rng(81)
+    xb = O.bf16_round(rng.standard_normal((3, spec.hidden), dtype=np.float32))
+    ref_i, ref_w, _, ref = O.moe_layer_f64(spec, xb, gw, experts, bias=bias, shared=sh)
+    out_res = blk(bits_to_bf16_tensor(xb, DEV))
+    gi, gwt = blk.last_routing
+    assert np.array_equal(gi.cpu().numpy(), ref_i)
+    assert np.array_equal(gwt.cpu().numpy(), ref_w)
+    check_close(out_res.float().cpu().numpy(), ref, "sigmoid shared resident")
+    cache = S.build_cache_for(model, slots=20)
+    S.patch_model(model, cache)
+    assert not cache.stitched
+    assert cache.shared_slot("layers.0.mlp.switch_mlp") == 20
+    ex_sh = slot_to_expert(cache.slab, 20)
+    assert np.array_equal(ex_sh.down.weight, sh[0].down.weight)
+    out_pg = model.layers[0].mlp(bits_to_bf16_tensor(xb, DEV))
+    gi, gwt = model.layers[0].mlp.last_routing
+    assert np.array_equal(gi.cpu().numpy(), ref_i)
+    check_close(out_pg.float().cpu().numpy(), ref, "sigmoid shared paged")
+    cache.close()
+
+
+def test_streamed_switch_fetch_groups_match_resident():
+    """8 routed slots, 8 tokens x top-4 over 32 experts: the layer's ids
+    exceed the slab, so the seam runs several fetch groups; rows stay
+    bit-identical to the resident module and nothing starves."""
+    _, S = _mods()
+    spec = O.LayerSpec(1024, 32, 512, 4)
+    model, _ = _softmax_model(spec, 2, seed=90)
+    resident = [layer.mlp.switch_mlp for layer in model.layers]
+    cache = S.build_cache_for(model, slots=8)
+    streamed = S.patch_model(model, cache)
+    rng = np.random.default_rng(91)
+    for step in range(2):
+        for res, st in zip(resident, streamed):
+            x = bits_to_bf16_tensor(O.bf16_round(rng.standard_normal((8, spec.hidden),
+                                                                     dtype=np.float32)), DEV)
+            ids = np.stack([rng.choice(spec.experts, 4, replace=False) for _ in range(8)])
+            ind = torch.from_numpy(ids.astype(np.int32)).to(DEV)
+            assert torch.equal(st(x, ind).view(torch.int16), res(x, ind).view(torch.int16))
+    s = cache.stats()
+    assert s["group_passes"] >= 8 and s["slot_starved"] == 0
+    cache.close()
+
+
+def test_block_fetch_groups_with_gated_shared_vs_oracle():
+    """Qwen3-Next-style block (softmax top-4 + sigmoid-gated shared expert)
+    on an 8-slot slab: routed experts run in fetch groups, the shared expert
+    from its own slot, and pmoe_combine merges them; routing bit-exact,
+    output within tolerance of the float64 oracle."""
+    _, S = _mods()
+    spec = O.LayerSpec(1024, 32, 512, 4, shared=1, shared_gate=True)
+    model, ol = _softmax_model(spec, 1, seed=95)
+    cache = S.build_cache_for(model, slots=8)
+    S.patch_model(model, cache)
+    rng = np.random.default_rng(96)
+    xb = O.bf16_round(rng.standard_normal((16, spec.hidden), dtype=np.float32))
+    blk = model.layers[0].mlp
+    out = blk(bits_to_bf16_tensor(xb, DEV))
+    gw, experts, sh, sg = ol[0]
+    ref_i, ref_w, _, ref = O.moe_layer_f64(spec, xb, gw, experts, shared=sh, shared_gate_bits=sg)
+    gi, gwt = blk.last_routing
+    assert np.array_equal(gi.cpu().numpy(), ref_i)
+    assert np.array_equal(gwt.cpu().numpy(), ref_w)
+    check_close(out.float().cpu().numpy(), ref, "grouped block + gated shared")
+    assert cache.stats()["group_passes"] >= 2
+    cache.close()
+
+
+@pytest.mark.parametrize("shared,gate", [(False, False), (True, False), (True, True)])
+def test_combine_entry_point_vs_oracle(shared, gate):
+    K, _ = _mods()
+    rng = np.random.default_rng(7 + shared + 2 * gate)
+    n, k, d = 5, 6, 1024
+    y = O.bf16_round(rng.standard_normal((n, k, d), dtype=np.float32))
+    w = rng.random((n, k), dtype=np.float32)
+    sy = O.bf16_round(rng.standard_normal((n, d), dtype=np.float32)) if shared else None
+    sl = rng.standard_normal(n, dtype=np.float32) if gate else None
+    got = K.combine(bits_to_bf16_tensor(y, DEV), torch.from_numpy(w).to(DEV),
+                    None if sy is None else bits_to_bf16_tensor(sy, DEV),
+                    None if sl is None else torch.from_numpy(sl).to(DEV))
+    yf = O.bf16_to_f32(y)
+    shf = None
+    if shared:
+        shf = O.bf16_to_f32(sy).astype(np.float64)
+        if gate:
+            shf = shf * (1.0 / (1.0 + np.exp(-sl.astype(np.float64))))[:, None]
+    ref = O.combine_f64(yf.astype(np.float64), w, shf)
+    check_close(got.float().cpu().numpy(), ref, "pmoe_combine")
+    ref32 = O.combine_f32(yf, w, None if sy is None else O.bf16_to_f32(sy),
+                          None if sl is None else O.psigmoid(sl))
+    assert np.array_equal(got.cpu().view(torch.int16).numpy().view(np.uint16), ref32)

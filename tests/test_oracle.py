@@ -367,6 +367,36 @@ def test_combine_closed_form():
         assert np.allclose(got[n], ref)
 
 
+def test_combine_f32_fixed_order_known_answers():
+    """The fp32 combine accumulates in k order, then the shared term:
+    1 + 2^-25 rounds back to 1 in float32, so [1, 2^-25, -1] sums to 0 in
+    that order (2^-25 in any order that adds the small term last)."""
+    y = np.zeros((2, 3, 64), np.float32)
+    y[0, :, 0] = [1.0, 2.0 ** -25, -1.0]
+    y[1, :, 0] = [2.0 ** -25, 1.0, -1.0]
+    w = np.ones((2, 3), np.float32)
+    got = O.bf16_to_f32(O.combine_f32(y, w))
+    assert got[0, 0] == 0.0 and got[1, 0] == 0.0
+    sh = np.zeros((2, 64), np.float32)
+    sh[:, 0] = 2.0 ** -25
+    got = O.bf16_to_f32(O.combine_f32(y, w, sh))
+    assert got[0, 0] == np.float32(2.0 ** -25)      # shared added after the routed sum
+    # exact power-of-two weights reproduce the closed form bit for bit
+    rng = np.random.default_rng(5)
+    yb = O.bf16_to_f32(O.bf16_round(rng.standard_normal((4, 2, 128), dtype=np.float32)))
+    w2 = np.array([[0.5, 0.25]] * 4, np.float32)
+    ref = O.bf16_round((yb[:, 0] * 0.5 + yb[:, 1] * 0.25).astype(np.float32))
+    assert np.array_equal(O.combine_f32(yb, w2), ref)
+    # and sigmoid-gated shared terms agree with the float64 closed form
+    yf = rng.standard_normal((3, 5, 256)).astype(np.float32)
+    wf = rng.random((3, 5), dtype=np.float32)
+    shf = rng.standard_normal((3, 256)).astype(np.float32)
+    sw = O.psigmoid(rng.standard_normal(3, dtype=np.float32))
+    got = O.bf16_to_f32(O.combine_f32(yf, wf, shf, sw))
+    ref = O.combine_f64(yf, wf, shf.astype(np.float64) * sw[:, None])
+    assert np.abs(got - ref).max() <= 2.0 ** -8 * np.abs(ref).max()
+
+
 def test_c_decode_layer_matches_oracle():
     spec = O.LayerSpec(1024, 16, 256, 4)
     gw, experts, _, _, _ = O.make_layer(spec, seed=2)
