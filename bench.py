@@ -294,7 +294,8 @@ def main():
 
     ku = main_res["kernels"]["qgemv_gateup"]
     achieved = main_res["gateup_gbs"]
-    roofline = {"bound": "hbm", "kernel": "qgemv_kernel (gate+up, dual)",
+    roofline = {"bound": "hbm",
+                "kernel": "gateup_routed_kernel (gate+up+SwiGLU of the routed experts)",
                 "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": achieved / HBM_PEAK_GBS, "traffic": None,
                 "avg_launch_us": ku["avg_us"],

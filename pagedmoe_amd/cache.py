@@ -93,6 +93,16 @@ class ExpertCache:
         self.stitched = False
         self.group_passes = 0
 
+    @classmethod
+    def from_budget(cls, budget_bytes: int, g: Geom, layer_keys, n_experts: int, **kw):
+        """Size the slab from a byte budget, as the reference's
+        ``ExpertCache(budget_bytes)`` + ``enable_slabs`` do (cache.py:421,
+        :914-1006): slots = budget // expert_bytes."""
+        slots = int(budget_bytes) // int(g.expert_bytes)
+        if slots < 1:
+            raise ValueError(f"budget {budget_bytes} B holds no {int(g.expert_bytes)} B expert")
+        return cls(g, slots, layer_keys, n_experts, **kw)
+
     # ------------------------------------------------------------- tables
 
     def layer_index(self, layer_key) -> int:

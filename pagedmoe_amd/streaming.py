@@ -322,11 +322,18 @@ def build_cache_for(model: nn.Module, slots: int, **kw) -> ExpertCache:
     return cache
 
 
-def patch_model(model: nn.Module, cache: ExpertCache, prefetch_depth: int = 0):
+def patch_model(model: nn.Module, cache: ExpertCache, tensor_index=None, prefetch_depth: int = 0,
+                predict_mode: str | None = None, model_path: str | None = None):
     """Replace every QuantizedSwitchGLU with a StreamedSwitchGLU over
-    ``cache`` (streaming.py:2575-2688).  Returns the list of streamed layers
-    (the reference returns its PrefetchRing; speculative prefetch is not part
-    of this path).  The cache's layer keys must be the module paths."""
+    ``cache`` (streaming.py:2575-2688, same arguments).  Returns the list of
+    streamed layers (the reference returns its PrefetchRing).  The cache's
+    layer keys must be the module paths.  ``tensor_index``/``model_path``
+    locate checkpoint bytes in the reference; here the cache's pinned host
+    store already holds them, so they are accepted and unused.  Speculative
+    prefetch is not part of this path: ``predict_mode`` "on" raises."""
+    if predict_mode not in (None, "off", "auto"):
+        raise NotImplementedError(f"predict_mode={predict_mode!r}: speculative prefetch is not built")
+    del tensor_index, model_path, prefetch_depth
     glus = find_switch_glus(model)
     if not glus:
         raise ValueError("no QuantizedSwitchGLU modules found - this model has no MoE layers")
