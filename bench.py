@@ -170,6 +170,76 @@ def run_decode(args, g, spec, slab, gate, tables, batch, device):
     return res
 
 
+def run_prefill(args, g, spec, slab, gate, tables, device, tokens=2048):
+    """The same layers at a `tokens`-token prefill chunk: router logits
+    skewed by a per-expert N(0,1) bias (uneven expert loads), expert-sorted
+    dispatch feeding the dequant -> bf16 MFMA GEMMs.  Timed as HIP-graph
+    replays of one layer step per layer; per-kernel averages from an
+    event-bracketed eager pass."""
+    import torch
+
+    from pagedmoe_amd import kernels as K
+    from pagedmoe_amd._lib import KernelTimer
+
+    E, D, I, k = spec["experts"], spec["hidden"], spec["inter"], spec["top_k"]
+    L = args.layers
+    rc = K.route_cfg(spec["scoring"], E, k)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(3000)
+    x = torch.randn((L, tokens, D), generator=gen, device=device).to(torch.bfloat16)
+    lb = torch.randn((L, E), generator=gen, device=device)
+    out = torch.empty((L, tokens, D), dtype=torch.bfloat16, device=device)
+    inds = torch.empty((L, tokens, k), dtype=torch.int32, device=device)
+    wts = torch.empty((L, tokens, k), dtype=torch.float32, device=device)
+    ws = K.moe_workspace(g, tokens, k, 0, E, device).clone()
+
+    def run_seq():
+        for i in range(L):
+            K.moe_block(g, rc, slab.buf, tables[i], gate[i], x[i], logit_bias=lb[i], out=out[i],
+                        inds=inds[i], weights=wts[i], ws=ws)
+
+    run_seq()
+    torch.cuda.synchronize()
+    with KernelTimer() as kt:
+        run_seq()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run_seq()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        run_seq()
+    graph.replay()
+    torch.cuda.synchronize()
+    reps = max(2, args.prefill_reps)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / (reps * L)
+    rows = tokens * k
+    flops_gu = 4.0 * D * I * rows
+    flops_dn = 2.0 * D * I * rows
+    res = {"tokens": tokens, "ms_per_step": ms, "tokens_per_s": tokens / (ms * 1e-3),
+           "expert_tflops": (flops_gu + flops_dn) / (ms * 1e-3) / 1e12,
+           "mfma_frac_layer": (flops_gu + flops_dn) / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+           "expert_flops_per_step": flops_gu + flops_dn,
+           "router_flops_per_step": 2.0 * tokens * D * E,
+           "max_expert_rows": int(torch.bincount(inds[0].reshape(-1).long(), minlength=E).max()),
+           "kernels": {}}
+    for name, (tot, cnt) in kt.result.items():
+        res["kernels"][name] = {"avg_us": tot * 1e3 / cnt, "launches": cnt}
+    for name, fl in (("prefill_gateup", flops_gu), ("prefill_down", flops_dn)):
+        kr = res["kernels"].get(name)
+        if kr:
+            kr["tflops"] = fl / (kr["avg_us"] * 1e-6) / 1e12
+            kr["mfma_frac"] = kr["tflops"] / MFMA_BF16_PEAK_TFLOPS
+    return res
+
+
 def pmc_run(args, g, spec, slab, gate, tables, device):
     """Eager layer steps for hardware-counter runs (one dispatch per kernel,
     no graph), followed by a plain copy of known size for calibration."""
@@ -251,7 +321,10 @@ def main():
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-extra", action="store_true", help="skip the batch-8 line in extra")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the batch-8 and prefill lines in extra")
+    ap.add_argument("--prefill-reps", type=int, default=5,
+                    help="graph replays (of --layers prefill layer steps) timed for the prefill line")
     ap.add_argument("--pmc-run", action="store_true",
                     help="counter-collection run: `--steps` eager layer steps at `--batch`, then "
                          "one 256 MiB device-to-device copy as the counter calibration")
@@ -291,6 +364,12 @@ def main():
         log(f"batch 8: {r8['ms_per_step'] * 1e3:.1f} us/step, {r8['tokens_per_s']:.0f} tok/s")
         r8.pop("_gateup_step_bytes", None)
         extra["decode_batch8"] = r8
+    if not args.no_extra:
+        rp = run_prefill(args, g, spec, slab, gate, tables, device)
+        log(f"prefill {rp['tokens']} tokens: {rp['ms_per_step']:.3f} ms/layer, "
+            f"{rp['tokens_per_s']:.0f} tok/s, {rp['expert_tflops']:.0f} TFLOP/s "
+            f"({100 * rp['mfma_frac_layer']:.1f}% of bf16 MFMA peak), kernels {rp['kernels']}")
+        extra["prefill_2048"] = rp
 
     ku = main_res["kernels"]["qgemv_gateup"]
     achieved = main_res["gateup_gbs"]

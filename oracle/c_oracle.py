@@ -100,3 +100,14 @@ class DecodeLayer:
 
 def threads() -> int:
     return int(lib().pmo_threads())
+
+
+def expert_ffn(ex, x_f32, hidden, inter, bits):
+    """down(silu(gate x) * (up x)) of one expert for one token, fp32 on the
+    host (pmo_expert_ffn); ex has .gate/.up/.down QTensors."""
+    arr = make_experts([ex])
+    x = np.ascontiguousarray(x_f32, np.float32).reshape(-1)
+    y = np.empty(hidden, np.float32)
+    scratch = np.empty(lib().pmo_scratch_floats(hidden, inter), np.float32)
+    lib().pmo_expert_ffn(arr, _p(x), hidden, inter, bits, _p(y), _p(scratch))
+    return y

@@ -397,6 +397,17 @@ def test_combine_f32_fixed_order_known_answers():
     assert np.abs(got - ref).max() <= 2.0 ** -8 * np.abs(ref).max()
 
 
+@pytest.mark.parametrize("bits", [4, 6])
+def test_c_expert_ffn_matches_oracle(bits):
+    spec = O.LayerSpec(1024, 2, 512, 1, bits=bits)
+    _, experts, _, _, _ = O.make_layer(spec, seed=4)
+    x = O.bf16_to_f32(O.bf16_round(np.random.default_rng(44).standard_normal((1, 1024),
+                                                                           dtype=np.float32)))
+    got = C.expert_ffn(experts[1], x[0], 1024, 512, bits)
+    ref = O.expert_ffn_f64(x, experts[1])[0]
+    assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
 def test_c_decode_layer_matches_oracle():
     spec = O.LayerSpec(1024, 16, 256, 4)
     gw, experts, _, _, _ = O.make_layer(spec, seed=2)
