@@ -254,9 +254,12 @@ def pmc_run(args, g, spec, slab, gate, tables, device):
     x = torch.randn((args.steps, args.batch, D), generator=gen, device=device).to(torch.bfloat16)
     ws = K.moe_workspace(g, args.batch, k, 0, E, device).clone()
     inds = torch.empty((args.steps, args.batch, k), dtype=torch.int32, device=device)
+    # prefill-sized batches get the skewed router of the prefill workload
+    lb = torch.randn((args.layers, E), generator=gen, device=device) if args.batch > 256 else None
     for i in range(args.steps):
         layer = i % args.layers
-        K.moe_block(g, rc, slab.buf, tables[layer], gate[layer], x[i], inds=inds[i], ws=ws)
+        K.moe_block(g, rc, slab.buf, tables[layer], gate[layer], x[i], inds=inds[i], ws=ws,
+                    logit_bias=None if lb is None else lb[layer])
     torch.cuda.synchronize()
     # calibration: one elementwise kernel reading and writing 256 MiB
     src = torch.ones(64 << 20, dtype=torch.float32, device=device)
