@@ -83,8 +83,7 @@ def run_decode(args, g, spec, slab, gate, tables, batch, device):
     out = torch.empty((seq, batch, D), dtype=torch.bfloat16, device=device)
     inds = torch.empty((seq, batch, k), dtype=torch.int32, device=device)
     wts = torch.empty((seq, batch, k), dtype=torch.float32, device=device)
-    ws = K.moe_workspace(g, batch, k, 0, E, device)
-    ws = ws.clone()                               # private workspace for the graph
+    ws = K.moe_workspace(g, batch, k, 0, E, device, fresh=True)  # private to the graph
 
     def step(i):
         layer = i % L
@@ -142,6 +141,7 @@ def run_decode(args, g, spec, slab, gate, tables, batch, device):
     mean_unique = sum(uniq) / len(uniq)
     gateup_bytes = int(g.nbytes[0] + g.nbytes[1] + g.nbytes[2]) * 2
     down_bytes = int(g.nbytes[6] + g.nbytes[7] + g.nbytes[8])
+    layer_bytes = mean_unique * (gateup_bytes + down_bytes)
     res = {
         "batch": batch,
         "ms_per_step": ms,
@@ -164,6 +164,10 @@ def run_decode(args, g, spec, slab, gate, tables, batch, device):
         res["gateup_gbs"] = step_bytes_gu / (ku["avg_us"] * 1e-6) / 1e9
     if kd:
         res["down_gbs"] = step_bytes_dn / (kd["avg_us"] * 1e-6) / 1e9
+    kf = res["kernels"].get("decode_fused")
+    if kf:
+        res["fused_gbs"] = layer_bytes / (kf["avg_us"] * 1e-6) / 1e9
+    res["_layer_bytes"] = layer_bytes
     res["layer_expert_gbs"] = res["expert_bytes_per_step"] / (ms * 1e-3) / 1e9
     res["_gateup_step_bytes"] = step_bytes_gu
     del reps_timer
@@ -191,7 +195,7 @@ def run_prefill(args, g, spec, slab, gate, tables, device, tokens=2048):
     out = torch.empty((L, tokens, D), dtype=torch.bfloat16, device=device)
     inds = torch.empty((L, tokens, k), dtype=torch.int32, device=device)
     wts = torch.empty((L, tokens, k), dtype=torch.float32, device=device)
-    ws = K.moe_workspace(g, tokens, k, 0, E, device).clone()
+    ws = K.moe_workspace(g, tokens, k, 0, E, device, fresh=True)
 
     def run_seq():
         for i in range(L):
@@ -252,7 +256,7 @@ def pmc_run(args, g, spec, slab, gate, tables, device):
     gen = torch.Generator(device=device)
     gen.manual_seed(2000)
     x = torch.randn((args.steps, args.batch, D), generator=gen, device=device).to(torch.bfloat16)
-    ws = K.moe_workspace(g, args.batch, k, 0, E, device).clone()
+    ws = K.moe_workspace(g, args.batch, k, 0, E, device, fresh=True)
     inds = torch.empty((args.steps, args.batch, k), dtype=torch.int32, device=device)
     # prefill-sized batches get the skewed router of the prefill workload
     lb = torch.randn((args.layers, E), generator=gen, device=device) if args.batch > 256 else None
@@ -366,6 +370,7 @@ def main():
         r8 = run_decode(args, g, spec, slab, gate, tables, 8, device)
         log(f"batch 8: {r8['ms_per_step'] * 1e3:.1f} us/step, {r8['tokens_per_s']:.0f} tok/s")
         r8.pop("_gateup_step_bytes", None)
+        r8.pop("_layer_bytes", None)
         extra["decode_batch8"] = r8
     if not args.no_extra:
         rp = run_prefill(args, g, spec, slab, gate, tables, device)
@@ -374,21 +379,34 @@ def main():
             f"({100 * rp['mfma_frac_layer']:.1f}% of bf16 MFMA peak), kernels {rp['kernels']}")
         extra["prefill_2048"] = rp
 
-    ku = main_res["kernels"]["qgemv_gateup"]
-    achieved = main_res["gateup_gbs"]
-    roofline = {"bound": "hbm",
-                "kernel": "gateup_routed_kernel (gate+up+SwiGLU of the routed experts)",
+    if "decode_fused" in main_res["kernels"]:
+        kname = "decode_fused_kernel"
+        ku = main_res["kernels"]["decode_fused"]
+        achieved = main_res["fused_gbs"]
+        alg = main_res["_layer_bytes"]
+        what = ("decode_fused_kernel (whole layer in one launch: router, top-k, gate+up+SwiGLU, "
+                "down, combine)")
+    else:
+        kname = "gateup_routed_kernel"
+        ku = main_res["kernels"]["qgemv_gateup"]
+        achieved = main_res["gateup_gbs"]
+        alg = main_res["_gateup_step_bytes"]
+        what = "gateup_routed_kernel (gate+up+SwiGLU of the routed experts)"
+    roofline = {"bound": "hbm", "kernel": what,
                 "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": achieved / HBM_PEAK_GBS, "traffic": None,
                 "avg_launch_us": ku["avg_us"],
-                "algorithmic_bytes_per_launch": main_res["_gateup_step_bytes"]}
+                "algorithmic_bytes_per_launch": alg}
     traffic_file = ROOT / "profiles" / f"traffic_{args.workload}_b{args.batch}.json"
     if traffic_file.exists():
         try:
-            roofline["traffic"] = json.loads(traffic_file.read_text()).get("bytes_per_launch")
+            tf = json.loads(traffic_file.read_text())
+            if tf.get("kernel") == kname:
+                roofline["traffic"] = tf.get("bytes_per_launch")
         except (ValueError, OSError):
             pass
     main_res.pop("_gateup_step_bytes", None)
+    main_res.pop("_layer_bytes", None)
 
     cpu = None
     if not args.no_cpu:

@@ -143,6 +143,21 @@ int pmoe_dequant(const uint32_t* q, const uint16_t* scales,
 size_t pmoe_moe_workspace(const pmoe_geom* g, int n, int k, int shared,
                           int n_experts);
 
+/* A MoE workspace starts with a 65,792-byte synchronisation header (grid
+ * barrier counters, launch epoch and per-block flags of the one-launch
+ * decode layer).  It must be zero before the first pmoe_moe_block call on
+ * that workspace and is kept consistent by every call after that, so it
+ * must not be overwritten between calls.  This enqueues the zeroing on
+ * stream (a kernel, so it may be captured in a graph).  No reference
+ * counterpart: the reference's decode runs as mlx graph ops with no
+ * workspace (streaming.py:587-641). */
+int pmoe_moe_workspace_init(void* ws, size_t ws_bytes, void* stream);
+
+/* Synchronising read of the header's sticky error word into *error: bit 0 =
+ * a grid barrier wait of the one-launch decode gave up after 0.5 s (results
+ * of that call are invalid).  Zeroed only by pmoe_moe_workspace_init. */
+int pmoe_moe_workspace_status(const void* ws, uint32_t* error, void* stream);
+
 /* The seam: y[n, k, :] = FFN_{inds[n,k]}(x[n, :]) as bf16 [n, k, hidden],
  * uncombined, in (token, k) order.  Expert e lives in slab slot table[e]
  * (slab base + slot * expert_bytes).  Replaces

@@ -35,7 +35,8 @@ Profiler& prof() {
 }
 
 const char* kNames[K_COUNT] = {"router_logits", "route_select", "dispatch",  "qgemv_gateup",
-                               "qgemv_down",    "combine",      "prefill_gateup", "prefill_down"};
+                               "qgemv_down",    "combine",      "prefill_gateup", "prefill_down",
+                               "decode_fused"};
 
 }  // namespace
 

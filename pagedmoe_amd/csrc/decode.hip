@@ -7,235 +7,18 @@
 // from the dispatch), blockIdx.x a tile of output rows, and each wave walks its
 // rows with every lane owning whole 64-value quant groups of the row.
 //
-// Per lane and group: the packed weight words arrive as 16-byte loads, each
-// 32-bit word is turned into bf16 pairs (128+q) with one and/or (4-bit) or a
-// funnel shift (6-bit), and v_dot2_f32_bf16 accumulates x*(128+q) in fp32.
-// With xs = sum of the group's x, the group's contribution is
-//   s*sum(x*q) + b*xs = s*acc + (b - 128*s)*xs,
-// so dequantised weights are never materialised.  Rows are reduced across
-// their LPR lanes with an xor butterfly.  The gate/up launch (DUAL) computes
-// both projections of a row together and writes h = silu(g)*u as bf16.
+// The per-lane arithmetic (128-bit packed loads, in-register (128+q) bf16
+// pairs, v_dot2_f32_bf16, xor-butterfly row sums) is in gemv_common.h.  The
+// gate/up launch (DUAL) computes both projections of a row together and
+// writes h = silu(g)*u as bf16.
+#include "gemv_common.h"
 #include "pmoe_internal.h"
 #include "pmoe_kernels.h"
 #include "route_common.h"
 
-// Tuning knobs (compile-time): rows per wave step override (0 = sized from
-// the register budget), non-temporal weight loads, minimum waves per SIMD.
-#ifndef PMOE_FORCE_R
-#define PMOE_FORCE_R 0
-#endif
-#ifndef PMOE_NT_LOADS
-#define PMOE_NT_LOADS 1
-#endif
-#ifndef PMOE_MIN_WAVES
-#define PMOE_MIN_WAVES 3
-#endif
-
 namespace pmoe {
 
 namespace {
-
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
-                                         __builtin_bit_cast(bf16x2, b), c, false);
-}
-
-// Activations of one 64-value group, pre-arranged as the bf16 pairs the
-// weight words of that group are unpacked into, plus the group sum.
-template <int BITS>
-struct GroupAct {
-  uint32_t p[32];
-  float sum;
-};
-
-// Load 64 bf16 starting at src (16-byte aligned) into pair order.
-template <int BITS>
-__device__ __forceinline__ void load_group_act(const uint16_t* src, GroupAct<BITS>& a) {
-  const uint4* v = reinterpret_cast<const uint4*>(src);
-  float s = 0.0f;
-#pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    const uint4 d = v[c];
-    s += bf16lo(d.x) + bf16hi(d.x) + bf16lo(d.y) + bf16hi(d.y) + bf16lo(d.z) + bf16hi(d.z) +
-         bf16lo(d.w) + bf16hi(d.w);
-    if (BITS == 4) {
-      // word c of the group holds values 8c..8c+7; pair i is (x_{8c+i}, x_{8c+i+4})
-      a.p[4 * c + 0] = __builtin_amdgcn_perm(d.z, d.x, 0x05040100u);
-      a.p[4 * c + 1] = __builtin_amdgcn_perm(d.z, d.x, 0x07060302u);
-      a.p[4 * c + 2] = __builtin_amdgcn_perm(d.w, d.y, 0x05040100u);
-      a.p[4 * c + 3] = __builtin_amdgcn_perm(d.w, d.y, 0x07060302u);
-    } else {
-      // pair p is (x_{2p}, x_{2p+1}): the natural bf16 pairs
-      a.p[4 * c + 0] = d.x;
-      a.p[4 * c + 1] = d.y;
-      a.p[4 * c + 2] = d.z;
-      a.p[4 * c + 3] = d.w;
-    }
-  }
-  a.sum = s;
-}
-
-template <int BITS>
-struct GroupW {
-  static constexpr int kWords = 64 * BITS / 32;
-  uint32_t w[kWords];
-  float s, b;
-};
-
-template <int BITS>
-__device__ __forceinline__ void load_group_w(const uint32_t* wrow, const uint16_t* srow,
-                                             const uint16_t* brow, int g, GroupW<BITS>& q) {
-  constexpr int kWords = GroupW<BITS>::kWords;
-  const u32x4* v = reinterpret_cast<const u32x4*>(wrow + size_t(g) * kWords);
-#pragma unroll
-  for (int c = 0; c < kWords / 4; ++c) {
-#if PMOE_NT_LOADS
-    const u32x4 d = __builtin_nontemporal_load(v + c);
-#else
-    const u32x4 d = v[c];
-#endif
-    q.w[4 * c + 0] = d.x;
-    q.w[4 * c + 1] = d.y;
-    q.w[4 * c + 2] = d.z;
-    q.w[4 * c + 3] = d.w;
-  }
-  q.s = bf16f(srow[g]);
-  q.b = bf16f(brow[g]);
-}
-
-// sum over the group of x*(128+q)
-template <int BITS>
-__device__ __forceinline__ float group_dot(const GroupW<BITS>& q, const GroupAct<BITS>& a) {
-  float acc = 0.0f;
-  if (BITS == 4) {
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const uint32_t w = q.w[c];
-      acc = dot2(a.p[4 * c + 0], (w & 0x000F000Fu) | 0x43004300u, acc);
-      acc = dot2(a.p[4 * c + 1], ((w >> 4) & 0x000F000Fu) | 0x43004300u, acc);
-      acc = dot2(a.p[4 * c + 2], ((w >> 8) & 0x000F000Fu) | 0x43004300u, acc);
-      acc = dot2(a.p[4 * c + 3], ((w >> 12) & 0x000F000Fu) | 0x43004300u, acc);
-    }
-  } else {
-#pragma unroll
-    for (int p = 0; p < 32; ++p) {
-      const int bit = 12 * p;
-      const int wi = bit >> 5, sh = bit & 31;
-      uint32_t f;
-      if (sh + 12 <= 32)
-        f = q.w[wi] >> sh;
-      else
-        f = __builtin_amdgcn_alignbit(q.w[wi + 1], q.w[wi], sh);
-      const uint32_t pr = (f & 0x3Fu) | ((f << 10) & 0x003F0000u) | 0x43004300u;
-      acc = dot2(a.p[p], pr, acc);
-    }
-  }
-  return acc;
-}
-
-__device__ __forceinline__ float group_term(float acc, float s, float b, float xs, float part) {
-  return __builtin_fmaf(s, acc, __builtin_fmaf(b - 128.0f * s, xs, part));
-}
-
-// Rows per wave step RPW = 64/LPR; a wave owns R consecutive steps.  All of
-// its packed weights (R steps x GPL groups x 1-2 projections) are requested
-// before anything else, so every wave has its whole share of HBM traffic in
-// flight while the activations are still arriving from L2.
-// ---------------------------------------------------------------- GEMV core
-//
-// One wave computes rows o = wrow0 + st*RPW + rsub (st < R) of one expert's
-// projection(s) for the expert's rows rlist[0..m_total).  Activations of the
-// first row are requested first (L2 hits), then the whole weight burst of the
-// wave (R steps x GPL groups x 1-2 projections); vector loads retire in
-// order, so row 0 starts as soon as its own words have landed.  The weights
-// stay in registers across the expert's rows.  store(t_row, st, o, value)
-// receives each finished output (value is silu(g)*u for DUAL).
-template <int BITS, int LPR, int GPL, int R, bool DUAL, class Act, class Store>
-__device__ __forceinline__ void gemv_expert(const GemvArgs& a, int slot, int m_total,
-                                            const int32_t* rlist, int wrow0, Act act_row,
-                                            Store store) {
-  constexpr int RPW = 64 / LPR;
-  const int lane = threadIdx.x & 63;
-  const int sub = lane % LPR;
-  const int rsub = lane / LPR;
-  const int groups = a.cols / 64;
-  const int wpr = a.cols * BITS / 32;
-  const uint8_t* base = a.slab + size_t(slot) * a.expert_bytes;
-  const uint32_t* W0 = reinterpret_cast<const uint32_t*>(base + a.p0.w);
-  const uint16_t* S0 = reinterpret_cast<const uint16_t*>(base + a.p0.s);
-  const uint16_t* B0 = reinterpret_cast<const uint16_t*>(base + a.p0.b);
-  const uint32_t* W1 = reinterpret_cast<const uint32_t*>(base + a.p1.w);
-  const uint16_t* S1 = reinterpret_cast<const uint16_t*>(base + a.p1.s);
-  const uint16_t* B1 = reinterpret_cast<const uint16_t*>(base + a.p1.b);
-
-  GroupAct<BITS> act[GPL];
-  int r = 0;
-  auto load_act = [&](int m) {
-    r = rlist[m];
-    const uint16_t* src = act_row(r);
-#pragma unroll
-    for (int j = 0; j < GPL; ++j) {
-      const int g = min(sub + LPR * j, groups - 1);
-      load_group_act<BITS>(src + size_t(g) * 64, act[j]);
-    }
-  };
-  load_act(0);
-  __builtin_amdgcn_sched_barrier(0);
-  GroupW<BITS> q0[R][GPL];
-  GroupW<BITS> q1[DUAL ? R : 1][DUAL ? GPL : 1];
-#pragma unroll
-  for (int st = 0; st < R; ++st) {
-    const int o = min(wrow0 + st * RPW + rsub, a.rows_out - 1);
-#pragma unroll
-    for (int j = 0; j < GPL; ++j) {
-      const int g = min(sub + LPR * j, groups - 1);
-      load_group_w<BITS>(W0 + size_t(o) * wpr, S0 + size_t(o) * groups, B0 + size_t(o) * groups,
-                         g, q0[st][j]);
-      if (DUAL)
-        load_group_w<BITS>(W1 + size_t(o) * wpr, S1 + size_t(o) * groups,
-                           B1 + size_t(o) * groups, g, q1[DUAL ? st : 0][DUAL ? j : 0]);
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  for (int m = 0; m < m_total; ++m) {
-    if (m > 0) {
-      load_act(m);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-#pragma unroll
-    for (int st = 0; st < R; ++st) {
-      // Opaque to the optimiser: without this the unpacked pairs of every
-      // row are hoisted out of the row loop and spill.
-#pragma unroll
-      for (int j = 0; j < GPL; ++j) {
-#pragma unroll
-        for (int c = 0; c < GroupW<BITS>::kWords; ++c) {
-          asm volatile("" : "+v"(q0[st][j].w[c]));
-          if (DUAL) asm volatile("" : "+v"(q1[DUAL ? st : 0][DUAL ? j : 0].w[c]));
-        }
-      }
-      float p0 = 0.0f, p1 = 0.0f;
-#pragma unroll
-      for (int j = 0; j < GPL; ++j) {
-        if (sub + LPR * j < groups) {
-          p0 = group_term(group_dot<BITS>(q0[st][j], act[j]), q0[st][j].s, q0[st][j].b,
-                          act[j].sum, p0);
-          if (DUAL) {
-            const GroupW<BITS>& w1 = q1[DUAL ? st : 0][DUAL ? j : 0];
-            p1 = group_term(group_dot<BITS>(w1, act[j]), w1.s, w1.b, act[j].sum, p1);
-          }
-        }
-      }
-      float v = group_sum<LPR>(p0);
-      if (DUAL) v = silu_fast(v) * group_sum<LPR>(p1);
-      const int o = wrow0 + st * RPW + rsub;
-      if (sub == 0 && o < a.rows_out) store(r, st, o, v);
-    }
-  }
-}
 
 // Zero outputs of an expert whose table entry is -1 (not resident): it
 // contributes exact zero rows (streaming.py:715-719).
@@ -383,20 +166,6 @@ down_routed_kernel(const GemvArgs a, const RouteDev rt, uint16_t* out, const Rou
       acc = __builtin_fmaf(L.w[n * rt.kk + col], s_y[(n * rt.kk + col) * T + t], acc);
     out[size_t(n) * a.rows_out + o] = f2bf(acc);
   }
-}
-
-struct Shape {
-  int lpr, gpl;
-};
-
-// Lanes per row: the smallest power of two >= groups (max 64), so a lane
-// owns one quant group (two for rows of 65..128 groups) and keeps that
-// group's activations in registers for every row the wave visits.
-Shape pick_shape(int groups) {
-  if (groups <= 0 || groups > 128) return {0, 0};
-  int lpr = 8;
-  while (lpr < groups && lpr < 64) lpr <<= 1;
-  return {lpr, (groups + lpr - 1) / lpr};
 }
 
 // Row steps per wave: as many as fit next to the activations in a

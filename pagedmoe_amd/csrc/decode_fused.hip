@@ -1,0 +1,458 @@
+// Fused decode layer: router logits -> routing -> gate/up + SwiGLU -> down +
+// combine in ONE persistent launch.
+//
+// Replaces, for decode-sized batches, the same reference path as the
+// three-launch decode in decode.hip: the router the reference taps
+// (streaming.py:167-193), the selection (tests/test_stream.py:191-196;
+// streaming.py:2424-2442), the slab path's three gather_qmm + SwiGLU
+// (_run_slab, streaming.py:587-641) and the block's combine
+// (tests/test_stream.py:198).
+//
+// The grid holds one 512-thread block per CU (all resident at once) and the
+// phases are separated by two grid barriers:
+//   A  router logits: one wave per logit row (expert), every token, in the
+//      fixed summation order of router_logits_kernel (router.hip);
+//      -> barrier 1
+//   B  every block routes the batch from the logits with route_block
+//      (route_common.h: bit-exact top-k, the same bits in every block);
+//      block 0 publishes the routing outputs;
+//   C  gate/up items (active expert, R rows) are dealt over all waves;
+//      h = silu(g)*u is written as bf16.  Each wave then issues the weight
+//      loads of its first down item;  -> barrier 2 (the down weights stream
+//      in while the last gate/up rows finish)
+//   D  block b owns hidden rows [b*T, b*T + T) of every active expert: its
+//      waves run the down rows into LDS and the block combines them in fixed
+//      k order (shared expert last), bf16 out.
+// The GEMV arithmetic is the one of gemv_common.h, so the outputs are bit
+// for bit those of the three-launch decode.
+//
+// Grid barrier protocol (DecodeSync: the first kDecodeSyncBytes of the
+// workspace, all zero before the first call):
+//   - every wave waits for its own memory operations (s_waitcnt 0), the
+//     block syncs and thread 0 adds 1 to arrive[i];
+//   - the block that brings the count to the grid size resets it to 0 and
+//     writes this launch's tag into every block's flag (one 128-byte line
+//     per block); the others poll their own line, so no address is hot
+//     while the weight stream saturates HBM;
+//   - tags are 2*epoch+1 and 2*epoch+2; the last block at barrier 2 stores
+//     epoch+1, so the next launch on the workspace waits for new tags
+//     (no memset between launches: graph-safe).
+// Data crossing a barrier (logits, h) is stored and loaded at device scope,
+// which writes through / reads past the XCDs' L2s, so no cache writeback or
+// invalidate is needed.  A poll that has waited 0.5 s (100 MHz realtime
+// clock) sets error bit 0 and gives up, so a launch always ends.
+#include "gemv_common.h"
+#include "pmoe_internal.h"
+#include "pmoe_kernels.h"
+#include "route_common.h"
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
+namespace pmoe {
+
+namespace {
+
+constexpr int kFWaves = 8;
+constexpr int kFThreads = 64 * kFWaves;
+constexpr int kFMaxLogits = 8 * 1025;  // n * (E + shared gate) staged in LDS
+constexpr uint64_t kSpinTicks = 50000000ull;  // 0.5 s at 100 MHz
+
+struct FusedArgs {
+  const uint16_t* x;           // [n, hidden]
+  const uint16_t* gate_w;      // [E, hidden]
+  const uint16_t* gate_extra;  // shared-expert gate row (logit column E) or null
+  const float* logit_bias;     // [E] or null
+  float* logits;               // [n, ld]
+  GemvArgs gu, dn;
+  uint16_t* out;               // [n, hidden]
+  int32_t* inds_out;
+  float* w_out;
+  DecodeSync* sync;
+  int n_blocks;
+  int tile;                    // hidden rows per block in phase D
+};
+
+// Data that crosses a grid barrier (logits, h) is stored and loaded at
+// device scope (sc1): stores write through the XCD's L2 and loads bypass
+// its stale lines, so the barrier needs no cache writeback or invalidate.
+constexpr bool kCoherentLoads = true;
+
+#ifdef PMOE_FUSED_TRACE
+// Debug builds: every block's thread 0 records realtime stamps per phase.
+__device__ uint64_t g_trace[1024 * 16];
+__device__ __forceinline__ void trace_mark(DecodeSync*, int i) {
+  if (threadIdx.x == 0) g_trace[blockIdx.x * 16 + i] = __builtin_amdgcn_s_memrealtime();
+}
+#else
+__device__ __forceinline__ void trace_mark(DecodeSync*, int) {}
+#endif
+
+template <class T>
+__device__ __forceinline__ void shared_store(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Block arrival + wait.  Every wave's stores (and loads) have completed
+// before the block arrives; the block that arrives last resets the counter
+// and writes `tag` into every block's flag line; each block's thread 0 polls
+// its own line (no shared hot spot while HBM is saturated).
+__device__ __forceinline__ void grid_barrier(DecodeSync* sy, int i, uint32_t tag,
+                                             uint32_t n_blocks, int mark = -1) {
+  __shared__ int s_last;
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's memory operations have completed
+  __syncthreads();
+  if (mark >= 0) trace_mark(nullptr, mark);
+  if (threadIdx.x == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(&sy->arrive[i], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == n_blocks - 1;
+  }
+  __syncthreads();
+  uint8_t* flags = reinterpret_cast<uint8_t*>(sy) + 256;
+  if (s_last) {
+    if (threadIdx.x == 0) {
+      __hip_atomic_store(&sy->arrive[i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (i == 1)  // every block has read the epoch by now
+        __hip_atomic_store(&sy->epoch, tag >> 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    for (uint32_t b = threadIdx.x; b < n_blocks; b += blockDim.x)
+      __hip_atomic_store(reinterpret_cast<uint32_t*>(flags + b * kDecodeFlagStride), tag,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else if (threadIdx.x == 0) {
+    const uint32_t* mine =
+        reinterpret_cast<const uint32_t*>(flags + blockIdx.x * kDecodeFlagStride);
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (__hip_atomic_load(mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != tag) {
+      __builtin_amdgcn_s_sleep(2);
+      if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) {
+        __hip_atomic_fetch_or(&sy->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ void fma8(float& acc, const uint4& a, const uint4& b) {
+  acc = __builtin_fmaf(bf16lo(a.x), bf16lo(b.x), acc);
+  acc = __builtin_fmaf(bf16hi(a.x), bf16hi(b.x), acc);
+  acc = __builtin_fmaf(bf16lo(a.y), bf16lo(b.y), acc);
+  acc = __builtin_fmaf(bf16hi(a.y), bf16hi(b.y), acc);
+  acc = __builtin_fmaf(bf16lo(a.z), bf16lo(b.z), acc);
+  acc = __builtin_fmaf(bf16hi(a.z), bf16hi(b.z), acc);
+  acc = __builtin_fmaf(bf16lo(a.w), bf16lo(b.w), acc);
+  acc = __builtin_fmaf(bf16hi(a.w), bf16hi(b.w), acc);
+}
+
+// Logit (token t, row e) in router_logits_kernel's order: lane l owns
+// d = 512p + 8l + j, fma over p then j, xor butterfly over the lanes; the
+// bias is added to routed rows only.  The loads of 8 passes are issued
+// together (one memory round trip for hidden <= 4096).
+__device__ void router_pair(const FusedArgs& a, const RouteDev& rt, int e, int t) {
+  const int lane = threadIdx.x & 63;
+  const int d = a.gu.cols;
+  const uint16_t* wrow = e < rt.e ? a.gate_w + size_t(e) * d : a.gate_extra;
+  const uint16_t* xrow = a.x + size_t(t) * d;
+  const int passes = (d + 511) / 512;
+  float acc = 0.0f;
+  for (int p0 = 0; p0 < passes; p0 += 8) {
+    uint4 wv[8], xv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int col = (p0 + j) * 512 + lane * 8;
+      if (p0 + j < passes && col < d) {
+        wv[j] = *reinterpret_cast<const uint4*>(wrow + col);
+        xv[j] = *reinterpret_cast<const uint4*>(xrow + col);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int col = (p0 + j) * 512 + lane * 8;
+      if (p0 + j < passes && col < d) fma8(acc, xv[j], wv[j]);
+    }
+  }
+  const float sum = wave_sum_bfly(acc);
+  if (lane == 0) {
+    const bool biased = a.logit_bias && e < rt.e;
+    shared_store(&a.logits[size_t(t) * rt.ld + e], biased ? sum + a.logit_bias[e] : sum);
+  }
+}
+
+template <int BITS, int LG, int GG, int RG, int LD, int GD, int RD, int EPL>
+__global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs a,
+                                                                 const RouteDev rt) {
+  __shared__ RouteLds L;
+  __shared__ WaveTmp W[kFWaves];
+  __shared__ int32_t s_rows[kFWaves][kRouteMaxRows];
+  __shared__ float s_logit[kFMaxLogits];
+  __shared__ int32_t s_slot[kRouteMaxRows];  // slot of active expert u
+  extern __shared__ float s_y[];             // [rows][tile]
+  const int wave = threadIdx.x >> 6;
+  const int gw = blockIdx.x * kFWaves + wave;
+  const int n_waves = a.n_blocks * kFWaves;
+  DecodeSync* sy = a.sync;
+
+  // this launch's barrier tags: 2*epoch + 1 and 2*epoch + 2 (never 0, the
+  // initial flag value; consecutive launches differ)
+  const uint32_t epoch = __hip_atomic_load(&sy->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t tag1 = 2u * epoch + 1u, tag2 = 2u * epoch + 2u;
+
+  // A: router logits
+  const int n_log = rt.e + (a.gate_extra ? 1 : 0);
+  trace_mark(sy, 0);
+  for (int p = gw; p < n_log * rt.n; p += n_waves) {
+    const int t = p / n_log;
+    router_pair(a, rt, p - t * n_log, t);
+  }
+  trace_mark(sy, 1);
+  grid_barrier(sy, 0, tag1, a.n_blocks);
+
+  // B: routing (every block, identical bits)
+  trace_mark(sy, 2);
+  // the logits come in at device scope (written by other blocks), once
+  for (int i = threadIdx.x; i < rt.n * rt.ld; i += kFThreads)
+    s_logit[i] = __hip_atomic_load(rt.logits + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  trace_mark(sy, 9);
+  RouteDev rl = rt;
+  rl.logits = s_logit;
+  route_block<EPL, kFWaves>(rl, L, W, blockIdx.x == 0 ? a.inds_out : nullptr, a.w_out);
+  trace_mark(sy, 3);
+  const int rows = rt.n * rt.kk;
+  const int n_act = L.n_active;
+  for (int u = threadIdx.x; u < n_act; u += kFThreads) {
+    const int e = L.active[u];
+    s_slot[u] = e < a.gu.n_experts ? a.gu.table[e] : a.gu.shared_slot;
+  }
+  __syncthreads();
+  trace_mark(sy, 10);
+
+  // C: gate/up + SwiGLU -> h
+  {
+    constexpr int kRows = RG * (64 / LG);
+    const int chunks = (a.gu.rows_out + kRows - 1) / kRows;
+    const int items = n_act * chunks;
+    int cur = -1, m = 0;
+    for (int it = gw; it < items; it += n_waves) {
+      const int u = it / chunks;
+      const int c = it - u * chunks;
+      const int e = L.active[u];
+      if (e != cur) {
+        m = wave_rows_of(L, rows, e, s_rows[wave]);
+        cur = e;
+      }
+      const int slot = s_slot[u];
+      if (slot < 0) continue;  // not resident: phase D writes its zero rows
+      auto act_row = [&](int r) { return a.gu.act + size_t(r / rt.kk) * a.gu.act_stride; };
+      auto store = [&](int r, int, int o, float v) {
+        shared_store(&static_cast<uint16_t*>(a.gu.out)[size_t(r) * a.gu.out_stride + o], f2bf(v));
+      };
+      gemv_expert<BITS, LG, GG, RG, true>(a.gu, slot, m, s_rows[wave], c * kRows, act_row,
+                                          store);
+    }
+  }
+
+  trace_mark(sy, 7);
+  // D prologue: weights of this wave's first down item (expert `wave`,
+  // first sub-tile) requested before the barrier.
+  constexpr int kSub = RD * (64 / LD);
+  const int tile = a.tile;
+  const int row0 = blockIdx.x * tile;
+  const bool has_down = row0 < a.dn.rows_out;
+  GemvRegs<BITS, LD, GD, RD, false> qd;
+#ifndef PMOE_NO_PREFETCH
+  if (has_down && wave < n_act) {
+#else
+  if (false) {
+#endif
+    const int slot = s_slot[wave];
+    if (slot >= 0) gemv_load<BITS, LD, GD, RD, false>(a.dn, slot, row0, qd);
+  }
+  trace_mark(sy, 4);
+  grid_barrier(sy, 1, tag2, a.n_blocks, 12);
+  trace_mark(sy, 5);
+
+  // D: down rows of the block's tile into LDS, then the fixed-order combine
+  if (has_down) {
+    const int groups = a.dn.cols / 64;
+    const int n_sub = tile / kSub;
+    for (int u = wave; u < n_act; u += kFWaves) {
+      const int e = L.active[u];
+      const int m = wave_rows_of(L, rows, e, s_rows[wave]);
+      const int slot = s_slot[u];
+      for (int s = 0; s < n_sub; ++s) {
+        const int wrow0 = row0 + s * kSub;
+        if (slot < 0) {  // exact zero rows (streaming.py:715-719)
+          for (int mi = 0; mi < m; ++mi)
+            for (int t = threadIdx.x & 63; t < kSub; t += 64)
+              s_y[s_rows[wave][mi] * tile + (wrow0 - row0) + t] = 0.0f;
+          continue;
+        }
+#ifndef PMOE_NO_PREFETCH
+        if (u != wave || s != 0)
+#endif
+          gemv_load<BITS, LD, GD, RD, false>(a.dn, slot, wrow0, qd);
+        GroupAct<BITS> act[GD];
+        for (int mi = 0; mi < m; ++mi) {
+          const int r = s_rows[wave][mi];
+          gemv_load_act<BITS, LD, GD, kCoherentLoads>(a.dn.act + size_t(r) * a.dn.act_stride,
+                                                      groups, act);
+          gemv_rows<BITS, LD, GD, RD, false>(a.dn, qd, act, wrow0, [&](int, int o, float v) {
+            s_y[r * tile + (o - row0)] = v;
+          });
+        }
+      }
+      if (u == wave) trace_mark(sy, 11);
+    }
+    __syncthreads();
+    trace_mark(sy, 8);
+    for (int i = threadIdx.x; i < rt.n * tile; i += kFThreads) {
+      const int n = i / tile, t = i - n * tile;
+      const int o = row0 + t;
+      if (o >= a.dn.rows_out) continue;
+      float acc = 0.0f;
+      for (int col = 0; col < rt.kk; ++col)
+        acc = __builtin_fmaf(L.w[n * rt.kk + col], s_y[(n * rt.kk + col) * tile + t], acc);
+      a.out[size_t(n) * a.dn.rows_out + o] = f2bf(acc);
+    }
+  }
+  trace_mark(sy, 6);
+}
+
+// ---------------------------------------------------------------- host side
+
+// Row steps per wave item: weights of one item stay in registers next to the
+// activations, within the 256 VGPRs of two waves per SIMD.
+template <int BITS, int GPL, bool DUAL>
+constexpr int fused_r(int cap) {
+  constexpr int per_step = GPL * (64 * BITS / 32 + 2) * (DUAL ? 2 : 1);
+  constexpr int budget = 170 - GPL * 33;
+  int r = budget / per_step;
+  return r < 1 ? 1 : (r > cap ? cap : r);
+}
+
+struct Variant {
+  int bits, lg, gg, ld, gd, epl;
+  bool operator<(const Variant& o) const {
+    return std::tie(bits, lg, gg, ld, gd, epl) < std::tie(o.bits, o.lg, o.gg, o.ld, o.gd, o.epl);
+  }
+};
+
+using FusedFn = void (*)(const FusedArgs, const RouteDev);
+
+struct Entry {
+  FusedFn fn;
+  int sub_rows;  // down rows per wave item
+};
+
+template <int BITS, int LG, int GG, int LD, int GD, int EPL>
+Entry make_entry() {
+  // down items of ~16 rows (8 when a step already covers 8 rows): the
+  // tile of a block is about hidden / CUs rows
+  constexpr int RPW_D = 64 / LD;
+  constexpr int RG = fused_r<BITS, GG, true>(6);
+  constexpr int RD = RPW_D >= 8 ? 1 : fused_r<BITS, GD, false>(16 / RPW_D);
+  return {&decode_fused_kernel<BITS, LG, GG, RG, LD, GD, RD, EPL>, RD * (64 / LD)};
+}
+
+// Supported (gate/up row shape, down row shape) pairs: hidden 1024/inter 512,
+// hidden 4096/inter 1536 (and 2048), hidden 7168/inter 2048, hidden
+// 2048/inter 512; experts up to 512.  Other shapes use the three-launch path.
+const std::map<Variant, Entry>& variants() {
+  static const std::map<Variant, Entry> m = [] {
+    std::map<Variant, Entry> v;
+#define PMOE_FV(B, LG, GG, LD, GD, E) v[{B, LG, GG, LD, GD, E}] = make_entry<B, LG, GG, LD, GD, E>();
+#define PMOE_FV_E(B, LG, GG, LD, GD) \
+  PMOE_FV(B, LG, GG, LD, GD, 2) PMOE_FV(B, LG, GG, LD, GD, 4) PMOE_FV(B, LG, GG, LD, GD, 8)
+#define PMOE_FV_S(B)            \
+  PMOE_FV_E(B, 16, 1, 8, 1)     \
+  PMOE_FV_E(B, 64, 1, 32, 1)    \
+  PMOE_FV_E(B, 64, 2, 32, 1)    \
+  PMOE_FV_E(B, 32, 1, 8, 1)
+    PMOE_FV_S(4)
+    PMOE_FV_S(6)
+#undef PMOE_FV_S
+#undef PMOE_FV_E
+#undef PMOE_FV
+    return v;
+  }();
+  return m;
+}
+
+// Blocks per launch: one per CU, provided the kernel fits one block per CU
+// with this LDS size (checked once per device, kernel and size).
+int fused_blocks(FusedFn fn, size_t lds) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, void*, size_t>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lk(mu);
+  const auto key = std::make_tuple(dev, reinterpret_cast<void*>(fn), lds);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int cus = 0, nb = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(fn),
+                                                   kFThreads, lds) != hipSuccess)
+    nb = 0;
+  const int blocks = nb >= 1 ? cus : 0;
+  cache[key] = blocks;
+  return blocks;
+}
+
+}  // namespace
+
+#ifdef PMOE_FUSED_TRACE
+extern "C" int pmoe_debug_trace(uint64_t* out, int n) {
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_trace), size_t(n) * sizeof(uint64_t)) == hipSuccess
+             ? 0 : -2;
+}
+#endif
+
+int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int bits,
+                 const uint16_t* x, const uint16_t* gate_w, const uint16_t* gate_extra,
+                 const float* logit_bias, int32_t* inds_out, float* w_out, uint16_t* out,
+                 DecodeSync* sync, hipStream_t st) {
+  if (!sync || rt.n * rt.ld > kFMaxLogits) return kDecodeFusedDeclined;
+  const Shape sg = pick_shape(gu.cols / 64), sd = pick_shape(dn.cols / 64);
+  const int epl = (rt.e + 63) / 64;
+  const int epl_t = epl <= 2 ? 2 : (epl <= 4 ? 4 : (epl <= 8 ? 8 : 0));
+  if (sg.lpr == 0 || sd.lpr == 0 || epl_t == 0) return kDecodeFusedDeclined;
+  const auto& vs = variants();
+  const auto it = vs.find({bits, sg.lpr, sg.gpl, sd.lpr, sd.gpl, epl_t});
+  if (it == vs.end()) return kDecodeFusedDeclined;
+  const Entry& en = it->second;
+  // tile = down rows per block, a whole number of wave items
+  int blocks = fused_blocks(en.fn, 0);
+  if (blocks <= 0) return kDecodeFusedDeclined;
+  const int per_block = (dn.rows_out + blocks - 1) / blocks;
+  const int tile = (per_block + en.sub_rows - 1) / en.sub_rows * en.sub_rows;
+  const size_t lds = size_t(rt.n) * rt.kk * tile * sizeof(float);
+  if (lds > 64 * 1024) return kDecodeFusedDeclined;
+  blocks = fused_blocks(en.fn, lds);
+  if (blocks <= 0 || blocks > kDecodeMaxBlocks || blocks * tile < dn.rows_out)
+    return kDecodeFusedDeclined;
+  FusedArgs a{};
+  a.x = x;
+  a.gate_w = gate_w;
+  a.gate_extra = gate_extra;
+  a.logit_bias = logit_bias;
+  a.logits = const_cast<float*>(rt.logits);
+  a.gu = gu;
+  a.dn = dn;
+  a.out = out;
+  a.inds_out = inds_out;
+  a.w_out = w_out;
+  a.sync = sync;
+  a.n_blocks = blocks;
+  a.tile = tile;
+  ProfScope prof_scope(K_DECODE_FUSED, st);
+  en.fn<<<blocks, kFThreads, lds, st>>>(a, rt);
+  PMOE_LAUNCH_CHECK("decode_fused_kernel");
+  return PMOE_OK;
+}
+
+}  // namespace pmoe

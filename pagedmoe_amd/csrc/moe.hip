@@ -23,8 +23,10 @@ bool prefill_wanted(const pmoe_geom* g, int n, int kk, int n_ids);
 namespace {
 
 constexpr size_t kAlign = 256;
+constexpr size_t kSyncBytes = kDecodeSyncBytes;  // DecodeSync header at workspace offset 0
 
 struct MoeWs {
+  DecodeSync* sync = nullptr;     // first kSyncBytes of the workspace
   float* logits = nullptr;        // [n, E]
   float* shared_logit = nullptr;  // [n]
   int32_t* order = nullptr;       // [rows]
@@ -61,6 +63,7 @@ size_t carve(const pmoe_geom* g, int n, int k, int shared, int n_experts, void* 
   const int n_ids = n_experts + (shared ? 1 : 0);
   Carver c{static_cast<uint8_t*>(base)};
   MoeWs t;
+  t.sync = reinterpret_cast<DecodeSync*>(c.take<uint8_t>(kSyncBytes));
   t.logits = c.take<float>(size_t(n) * (n_experts + 1));
   t.shared_logit = c.take<float>(size_t(n));
   t.order = c.take<int32_t>(rows);
@@ -215,7 +218,16 @@ int run_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* table, i
   return qgemv(a, g->bits, false, max_experts, max_rows_per_expert, st);
 }
 
-// Decode block path: logits (+ shared gate column), then gate/up and
+// PMOE_DECODE_FUSED=1 in the environment selects the one-launch decode
+// layer, 0 the three-launch one (read per call, so the paths can be
+// compared); the default is the three-launch decode.
+bool fused_enabled() {
+  const char* v = getenv("PMOE_DECODE_FUSED");
+  return v && v[0] == '1';
+}
+
+// Decode block path: the fused one-launch layer (decode_fused.hip) when it
+// covers the shape, else logits (+ shared gate column), then gate/up and
 // down+combine, each recomputing the routing in its prologue.
 int decode_block(const pmoe_geom* g, const pmoe_route_cfg* rc, const uint8_t* slab,
                  const int32_t* table, const uint16_t* gate_w, const float* score_bias,
@@ -226,8 +238,7 @@ int decode_block(const pmoe_geom* g, const pmoe_route_cfg* rc, const uint8_t* sl
   const int shared = shared_slot >= 0 ? 1 : 0;
   const int kk = k + shared;
   const uint16_t* extra = (shared && shared_gate) ? shared_gate : nullptr;
-  int r = router_logits_ext(x, gate_w, extra, logit_bias, n, g->hidden, e, w.logits, st);
-  if (r) return r;
+  int r = PMOE_OK;
   RouteDev rt{};
   rt.logits = w.logits;
   rt.ld = e + (extra ? 1 : 0);
@@ -267,6 +278,13 @@ int decode_block(const pmoe_geom* g, const pmoe_route_cfg* rc, const uint8_t* sl
   dn.act_stride = g->inter;
   dn.act_by_token = 0;
   dn.out = nullptr;
+  if (fused_enabled()) {
+    const int r2 = decode_fused(gu, dn, rt, g->bits, x, gate_w, extra, logit_bias, inds_out, w_out,
+                                out, w.sync, st);
+    if (r2 != kDecodeFusedDeclined) return r2;
+  }
+  r = router_logits_ext(x, gate_w, extra, logit_bias, n, g->hidden, e, w.logits, st);
+  if (r) return r;
   return decode_routed(gu, dn, rt, g->bits, inds_out, w_out, out, w.record, st);
 }
 
@@ -302,6 +320,31 @@ extern "C" size_t pmoe_moe_workspace(const pmoe_geom* g, int n, int k, int share
                                      int n_experts) {
   if (!g || n < 0 || k <= 0 || n_experts <= 0) return 0;
   return pmoe::carve(g, n, k, shared, n_experts, nullptr, nullptr);
+}
+
+__global__ void workspace_init_kernel(uint32_t* p, int words) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < words; i += gridDim.x * blockDim.x)
+    p[i] = 0;
+}
+
+extern "C" int pmoe_moe_workspace_init(void* ws, size_t ws_bytes, void* stream) {
+  pmoe::clear_error();
+  PMOE_REQUIRE(ws != nullptr, "moe_workspace_init: null workspace");
+  PMOE_REQUIRE(ws_bytes >= pmoe::kSyncBytes, "moe_workspace_init: workspace too small");
+  workspace_init_kernel<<<64, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<uint32_t*>(ws), int(pmoe::kSyncBytes / 4));
+  PMOE_LAUNCH_CHECK("workspace_init_kernel");
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_moe_workspace_status(const void* ws, uint32_t* error, void* stream) {
+  pmoe::clear_error();
+  PMOE_REQUIRE(ws != nullptr && error != nullptr, "moe_workspace_status: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const pmoe::DecodeSync* sy = static_cast<const pmoe::DecodeSync*>(ws);
+  PMOE_HIP(hipMemcpyAsync(error, &sy->error, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+  PMOE_HIP(hipStreamSynchronize(st));
+  return PMOE_OK;
 }
 
 extern "C" int pmoe_switch_glu(const pmoe_geom* g, const void* slab, const int32_t* table,

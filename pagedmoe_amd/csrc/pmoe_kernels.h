@@ -15,6 +15,7 @@ enum KernelId {
   K_COMBINE,
   K_PREFILL_GATEUP,
   K_PREFILL_DOWN,
+  K_DECODE_FUSED,
   K_COUNT
 };
 
@@ -68,6 +69,29 @@ int qgemv(const GemvArgs& a, int bits, bool dual, int max_experts, int max_rows_
 int decode_routed(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int bits,
                   int32_t* inds_out, float* w_out, uint16_t* out, void* record, hipStream_t st);
 size_t decode_record_bytes();
+
+// Grid-barrier state of the fused decode launch: the first kDecodeSyncBytes
+// of the MoE workspace, zero before the first call.  arrive[i] counts the
+// blocks at barrier i (the last one to arrive resets it); epoch counts
+// launches; flag line b (128 bytes apart) is where block b waits.
+struct DecodeSync {
+  uint32_t arrive[2];  // blocks arrived at barrier 1 / barrier 2
+  uint32_t epoch;      // launches completed on this workspace
+  uint32_t error;      // sticky: bit 0 = a barrier wait timed out
+};
+constexpr int kDecodeMaxBlocks = 512;
+constexpr size_t kDecodeFlagStride = 128;  // bytes between two blocks' flags
+constexpr size_t kDecodeSyncBytes = 256 + kDecodeMaxBlocks * kDecodeFlagStride;
+constexpr int kDecodeFusedDeclined = 1;  // shape not covered: use decode_routed
+
+// Whole decode layer in one persistent launch (decode_fused.hip): router
+// logits into rt.logits, routing, gate/up into gu.out (h), down + combine
+// into out.  Returns kDecodeFusedDeclined (nothing launched) for shapes it
+// does not cover.
+int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int bits,
+                 const uint16_t* x, const uint16_t* gate_w, const uint16_t* gate_extra,
+                 const float* logit_bias, int32_t* inds_out, float* w_out, uint16_t* out,
+                 DecodeSync* sync, hipStream_t st);
 
 // Routing (router.hip)
 int router_logits(const uint16_t* x, const uint16_t* w, const float* bias, int n, int d, int e,

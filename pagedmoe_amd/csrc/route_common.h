@@ -123,9 +123,17 @@ __device__ __forceinline__ void wave_topk_radix(const float (&v)[EPL], int n_val
   wave_lds_sync();
 }
 
+// Logit loads: COHERENT reads the logits at device scope (they were written
+// by other blocks of the same launch and may be stale in this XCD's L2).
+template <bool COHERENT>
+__device__ __forceinline__ float load_logit(const float* p) {
+  if (COHERENT) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return *p;
+}
+
 // Route token t with the calling wave: writes L.ids / L.w for its kk rows
 // and, when inds_out is set, the routing outputs [n, k].
-template <int EPL>
+template <int EPL, bool COHERENT = false>
 __device__ void route_token(const RouteDev& r, int t, RouteLds& L, WaveTmp& W, int32_t* inds_out,
                             float* w_out) {
   const int lane = threadIdx.x & 63;
@@ -135,7 +143,7 @@ __device__ void route_token(const RouteDev& r, int t, RouteLds& L, WaveTmp& W, i
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     const int ei = lane + 64 * i;
-    v[i] = ei < e ? row[ei] : 0.0f;
+    v[i] = ei < e ? load_logit<COHERENT>(row + ei) : 0.0f;
     x[i] = 0.0f;
   }
   float wk = 0.0f;
@@ -220,20 +228,21 @@ __device__ void route_token(const RouteDev& r, int t, RouteLds& L, WaveTmp& W, i
   }
   if (r.kk > k && lane == 0) {
     L.ids[t * r.kk + k] = e;  // shared expert column
-    L.w[t * r.kk + k] = r.shared_gate ? psigmoid(row[e]) : 1.0f;
+    L.w[t * r.kk + k] = r.shared_gate ? psigmoid(load_logit<COHERENT>(row + e)) : 1.0f;
   }
 }
 
 // Route all tokens (waves take tokens round robin), then list the active
 // experts in ascending id order.  Ends with a block barrier.
-template <int EPL, int NW>
+template <int EPL, int NW, bool COHERENT = false>
 __device__ void route_block(const RouteDev& r, RouteLds& L, WaveTmp* W, int32_t* inds_out,
                             float* w_out) {
   const int tid = threadIdx.x;
   const int wv = tid >> 6;
   const int n_ids = r.e + (r.kk > r.k ? 1 : 0);
   for (int i = tid; i < kRouteMaxIds / 64; i += NW * 64) L.bits[i] = 0;
-  for (int t = wv; t < r.n; t += NW) route_token<EPL>(r, t, L, W[wv], inds_out, w_out);
+  for (int t = wv; t < r.n; t += NW)
+    route_token<EPL, COHERENT>(r, t, L, W[wv], inds_out, w_out);
   __syncthreads();
   const int rows = r.n * r.kk;
   for (int i = tid; i < rows; i += NW * 64) {

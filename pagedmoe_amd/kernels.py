@@ -17,6 +17,7 @@ from . import _lib
 from ._lib import Geom, RouteCfg, check, lib
 
 _WS: dict = {}
+_MOE_WS: dict = {}
 
 
 def _ptr(t):
@@ -156,9 +157,30 @@ def dequant(q, scales, biases, bits: int, group: int = 64) -> torch.Tensor:
 
 # ---------------------------------------------------------------- experts
 
-def moe_workspace(g: Geom, n: int, k: int, shared: int, n_experts: int, device) -> torch.Tensor:
-    nb = lib().pmoe_moe_workspace(ctypes.byref(g), n, k, shared, n_experts)
-    return workspace(nb, device)
+def moe_workspace(g: Geom, n: int, k: int, shared: int, n_experts: int, device,
+                  fresh: bool = False) -> torch.Tensor:
+    """Workspace of the expert entry points (pmoe_moe_workspace bytes).  Its
+    synchronisation header is zeroed on allocation (pmoe_moe_workspace_init);
+    the cached buffer is separate from the dispatch scratch so nothing else
+    ever writes the header.  fresh=True returns a new, private buffer."""
+    nb = max(int(lib().pmoe_moe_workspace(ctypes.byref(g), n, k, shared, n_experts)), 256)
+    key = (torch.device(device).index or 0)
+    buf = None if fresh else _MOE_WS.get(key)
+    if buf is None or buf.numel() < nb:
+        buf = torch.empty(nb, dtype=torch.uint8, device=device)
+        check(lib().pmoe_moe_workspace_init(_ptr(buf), buf.numel(), _stream()),
+              "pmoe_moe_workspace_init")
+        if not fresh:
+            _MOE_WS[key] = buf
+    return buf
+
+
+def workspace_error(ws: torch.Tensor) -> int:
+    """The sticky error word of a MoE workspace header (synchronises)."""
+    err = ctypes.c_uint32()
+    check(lib().pmoe_moe_workspace_status(_ptr(ws), ctypes.byref(err), _stream()),
+          "pmoe_moe_workspace_status")
+    return int(err.value)
 
 
 def _table_ptr(table):

@@ -1,0 +1,195 @@
+"""GPU: the one-launch decode layer (decode_fused.hip).
+
+The fused kernel runs the same GEMV arithmetic and combine order as the
+three-launch decode (router, gate/up, down+combine), so its outputs must be
+bit-identical to that path on the same inputs; routing must equal the oracle
+bit for bit.  The grid-barrier counters in the workspace header must be back
+at zero after every call and the launch epoch must count the calls (checked
+through repeated calls, batch-size changes and HIP-graph replays); the sticky
+error word must stay 0.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import pmoe_oracle as O
+from tests.util import bits_to_bf16_tensor, check_close, fill_slab_gpu, slot_to_expert
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True)
+def _fused_on(monkeypatch):
+    monkeypatch.setenv("PMOE_DECODE_FUSED", "1")
+
+
+def _k():
+    from pagedmoe_amd import kernels
+    return kernels
+
+
+class _Layer:
+    """Random resident layer of a given shape on the GPU."""
+
+    def __init__(self, hidden, experts, inter, top_k, bits=4, scoring="softmax", shared=False,
+                 shared_gate=False, seed=0, n_group=1, topk_group=1, scale=1.0):
+        from pagedmoe_amd._lib import geom
+        from pagedmoe_amd.slab import SlabStore
+        K = _k()
+        self.g = geom(hidden, inter, bits)
+        n_slots = experts + (1 if shared else 0)
+        self.slab = SlabStore(self.g, n_slots, DEV)
+        fill_slab_gpu(self.slab, range(n_slots), seed=seed)
+        rng = np.random.default_rng(seed)
+        self.gwb = O.bf16_round(rng.standard_normal((experts, hidden), dtype=np.float32)
+                                * np.float32(0.02))
+        self.gate = bits_to_bf16_tensor(self.gwb, DEV)
+        self.table = torch.arange(experts, dtype=torch.int32, device=DEV)
+        self.rc = K.route_cfg(scoring, experts, top_k, True, n_group, topk_group, scale)
+        self.bias = None
+        if scoring == "sigmoid":
+            b = (rng.standard_normal(experts, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+            self.bias = torch.from_numpy(b).to(DEV)
+        self.shared_slot = experts if shared else -1
+        self.sgate = None
+        if shared_gate:
+            sgb = O.bf16_round(rng.standard_normal((1, hidden), dtype=np.float32) * np.float32(0.02))
+            self.sgate = bits_to_bf16_tensor(sgb, DEV)
+        self.hidden = hidden
+        self.experts = experts
+
+    def x(self, n, seed):
+        rng = np.random.default_rng(seed)
+        return bits_to_bf16_tensor(O.bf16_round(rng.standard_normal((n, self.hidden),
+                                                                    dtype=np.float32)), DEV)
+
+    def run(self, x, ws=None, out=None, inds=None, weights=None):
+        return _k().moe_block(self.g, self.rc, self.slab.buf, self.table, self.gate, x,
+                              score_bias=self.bias, shared_slot=self.shared_slot,
+                              shared_gate=self.sgate, ws=ws, out=out, inds=inds, weights=weights)
+
+
+def _run_path(layer, x, fused, ws=None):
+    old = os.environ.get("PMOE_DECODE_FUSED")
+    os.environ["PMOE_DECODE_FUSED"] = "1" if fused else "0"
+    try:
+        out, inds, wts = layer.run(x, ws=ws)
+        torch.cuda.synchronize()
+    finally:
+        if old is None:
+            del os.environ["PMOE_DECODE_FUSED"]
+        else:
+            os.environ["PMOE_DECODE_FUSED"] = old
+    return out.clone(), inds.clone(), wts.clone()
+
+
+def _fused_launches(layer, x):
+    from pagedmoe_amd._lib import KernelTimer
+    with KernelTimer() as kt:
+        layer.run(x)
+    torch.cuda.synchronize()
+    return kt.result
+
+
+CASES = {
+    # hidden, experts, inter, top_k, bits, scoring, shared, shared_gate, n_group, topk_group, scale
+    "qwen3-235b": (4096, 128, 1536, 8, 4, "softmax", False, False, 1, 1, 1.0),
+    "deepseek-shapes": (7168, 64, 2048, 8, 4, "sigmoid", True, False, 8, 4, 2.5),
+    "qwen3-next-6bit": (2048, 512, 512, 10, 6, "softmax", True, True, 1, 1, 1.0),
+    "tiny": (1024, 32, 512, 4, 4, "softmax", False, False, 1, 1, 1.0),
+}
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+@pytest.mark.parametrize("n", [1, 8])
+def test_fused_matches_three_launch_bit_exact(name, n):
+    h, e, i, k, bits, sc, shared, sg, ng, tg, scale = CASES[name]
+    print(f"[fused] case {name} n={n}", flush=True)
+    layer = _Layer(h, e, i, k, bits, sc, shared, sg, seed=21, n_group=ng, topk_group=tg,
+                   scale=scale)
+    x = layer.x(n, seed=100 + n)
+    assert "decode_fused" in _fused_launches(layer, x), "fused path not taken"
+    a = _run_path(layer, x, fused=True)
+    b = _run_path(layer, x, fused=False)
+    assert torch.equal(a[1], b[1]), "routing indices differ"
+    assert torch.equal(a[2], b[2]), "routing weights differ"
+    assert torch.equal(a[0].view(torch.int16), b[0].view(torch.int16)), (
+        f"outputs differ: max |d| {(a[0].float() - b[0].float()).abs().max().item():.3e}")
+    ws = _k().moe_workspace(layer.g, n, k, int(shared), e, DEV)
+    assert _k().workspace_error(ws) == 0
+
+
+def test_fused_qwen3_235b_vs_oracle_and_reuse_across_batches():
+    """One workspace, batch sizes 1 -> 8 -> 3 -> 1: every call equals the
+    oracle routing and the float64 reference within tolerance."""
+    K = _k()
+    layer = _Layer(4096, 128, 1536, 8, seed=5)
+    ws = K.moe_workspace(layer.g, 8, 8, 0, 128, DEV, fresh=True)
+    for step, n in enumerate((1, 8, 3, 1)):
+        print(f"[fused] reuse step {step} n={n}", flush=True)
+        x = layer.x(n, seed=300 + step)
+        out, gi, gw = layer.run(x, ws=ws)
+        xb = x.cpu().view(torch.int16).numpy().view(np.uint16)
+        ref_i, ref_w = O.softmax_topk(O.router_logits(xb, layer.gwb), 8)
+        assert np.array_equal(gi.cpu().numpy(), ref_i)
+        assert np.array_equal(gw.cpu().numpy(), ref_w)
+        used = sorted(set(ref_i.reshape(-1).tolist()))
+        experts = {e: slot_to_expert(layer.slab, e) for e in used}
+        ref = O.combine_f64(O.switch_glu_f64(xb, ref_i, experts), ref_w)
+        check_close(out.float().cpu().numpy(), ref, f"fused reuse n={n}")
+    header = ws[:16].cpu().view(torch.int32).numpy()
+    assert header[0] == 0 and header[1] == 0, f"barrier counters not reset: {header}"
+    assert header[2] == 4, f"launch epoch {header[2]} after 4 calls"
+    assert header[3] == 0, "barrier timeout flagged"
+
+
+def test_fused_graph_replays_match_eager():
+    """A HIP graph of four layer steps (fused launches), replayed with fresh
+    inputs and eager work in between, equals eager runs bit for bit."""
+    K = _k()
+    layer = _Layer(4096, 128, 1536, 8, seed=7)
+    n, steps = 1, 4
+    ws = K.moe_workspace(layer.g, n, 8, 0, 128, DEV, fresh=True)
+    xs = torch.empty((steps, n, 4096), dtype=torch.bfloat16, device=DEV)
+    outs = torch.empty((steps, n, 4096), dtype=torch.bfloat16, device=DEV)
+    inds = torch.empty((steps, n, 8), dtype=torch.int32, device=DEV)
+    wts = torch.empty((steps, n, 8), dtype=torch.float32, device=DEV)
+
+    def seq():
+        for s in range(steps):
+            layer.run(xs[s], ws=ws, out=outs[s], inds=inds[s], weights=wts[s])
+
+    for s in range(steps):
+        xs[s].copy_(layer.x(n, seed=400 + s))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        seq()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        seq()
+    torch.cuda.synchronize()
+    for rep in range(4):
+        print(f"[fused] graph replay {rep}", flush=True)
+        for s in range(steps):
+            xs[s].copy_(layer.x(n, seed=500 + 10 * rep + s))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = outs.clone(), inds.clone(), wts.clone()
+        ref_ws = K.moe_workspace(layer.g, n, 8, 0, 128, DEV)
+        for s in range(steps):
+            eo, ei, ew = layer.run(xs[s].clone(), ws=ref_ws)
+            torch.cuda.synchronize()
+            assert torch.equal(ei, got[1][s]) and torch.equal(ew, got[2][s])
+            assert torch.equal(eo.view(torch.int16), got[0][s].view(torch.int16)), \
+                f"replay {rep} step {s} differs from eager"
+    assert K.workspace_error(ws) == 0
+    header = ws[:16].cpu().view(torch.int32).numpy()
+    assert header[0] == 0 and header[1] == 0, f"barrier counters not reset: {header}"
