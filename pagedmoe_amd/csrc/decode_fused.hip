@@ -49,6 +49,7 @@
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <type_traits>
 
 namespace pmoe {
 
@@ -229,13 +230,40 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
   __syncthreads();
   trace_mark(sy, 10);
 
-  // C: gate/up + SwiGLU -> h
+  // C: gate/up + SwiGLU -> h.  An item's weights are held as two halves
+  // (steps [0, RG/2) and [RG/2, RG)); on a wave's last item the weights of
+  // its first down item are requested as each half is consumed, so the down
+  // stream queues behind the gate/up stream instead of after it.
+  constexpr int kHG = RG / 2;                 // steps per gate/up half
+  constexpr int kRows = RG * (64 / LG);       // gate/up rows per item
+  constexpr int kHD = RD > 1 ? RD / 2 : 1;    // steps per down half
+  constexpr int kSub = RD * (64 / LD);        // down rows per item
+  const int tile = a.tile;
+  const int row0 = blockIdx.x * tile;
+  const bool has_down = row0 < a.dn.rows_out;
+  const int pre_slot = (has_down && wave < n_act) ? s_slot[wave] : -1;
+  GemvRegs<BITS, LD, GD, kHD, false> qd1, qd2;
+  // (scheduling fences keep the loads where they are: hoisted above the
+  // gate/up arithmetic they would hold both register sets at once)
+  auto prefetch_down = [&](int half) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (pre_slot >= 0) {
+      if (half == 0) gemv_load<BITS, LD, GD, kHD, false>(a.dn, pre_slot, row0, qd1);
+      if (half == 1 && RD > 1)
+        gemv_load<BITS, LD, GD, kHD, false>(a.dn, pre_slot, row0 + kHD * (64 / LD), qd2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
   {
-    constexpr int kRows = RG * (64 / LG);
+    const int groups = a.gu.cols / 64;
     const int chunks = (a.gu.rows_out + kRows - 1) / kRows;
     const int items = n_act * chunks;
     int cur = -1, m = 0;
-    for (int it = gw; it < items; it += n_waves) {
+    // item `it`; LAST: the wave's final item, which also issues the down
+    // prefetch (peeled out of the loop so the prefetch registers are not
+    // live across it)
+    auto item = [&](int it, auto last_tag) {
+      constexpr bool LAST = decltype(last_tag)::value;
       const int u = it / chunks;
       const int c = it - u * chunks;
       const int e = L.active[u];
@@ -244,32 +272,57 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
         cur = e;
       }
       const int slot = s_slot[u];
-      if (slot < 0) continue;  // not resident: phase D writes its zero rows
-      auto act_row = [&](int r) { return a.gu.act + size_t(r / rt.kk) * a.gu.act_stride; };
-      auto store = [&](int r, int, int o, float v) {
-        shared_store(&static_cast<uint16_t*>(a.gu.out)[size_t(r) * a.gu.out_stride + o], f2bf(v));
+      if (slot < 0) {  // not resident: phase D writes its zero rows
+        if (LAST) {
+          prefetch_down(0);
+          prefetch_down(1);
+        }
+        return;
+      }
+      const int wrow0 = c * kRows;
+      auto store = [&](int r) {
+        return [&a, r](int, int o, float v) {
+          shared_store(&static_cast<uint16_t*>(a.gu.out)[size_t(r) * a.gu.out_stride + o],
+                       f2bf(v));
+        };
       };
-      gemv_expert<BITS, LG, GG, RG, true>(a.gu, slot, m, s_rows[wave], c * kRows, act_row,
-                                          store);
+      GroupAct<BITS> act[GG];
+      int r = s_rows[wave][0];
+      gemv_load_act<BITS, LG, GG>(a.gu.act + size_t(r / rt.kk) * a.gu.act_stride, groups, act);
+      __builtin_amdgcn_sched_barrier(0);
+      GemvRegs<BITS, LG, GG, kHG, true> qa, qb;
+      gemv_load<BITS, LG, GG, kHG, true>(a.gu, slot, wrow0, qa);
+      gemv_load<BITS, LG, GG, kHG, true>(a.gu, slot, wrow0 + kHG * (64 / LG), qb);
+      __builtin_amdgcn_sched_barrier(0);
+      for (int mi = 0; mi < m; ++mi) {
+        if (mi > 0) {
+          r = s_rows[wave][mi];
+          gemv_load_act<BITS, LG, GG>(a.gu.act + size_t(r / rt.kk) * a.gu.act_stride, groups,
+                                      act);
+        }
+        gemv_rows<BITS, LG, GG, kHG, true>(a.gu, qa, act, wrow0, store(r));
+      }
+      if (LAST) prefetch_down(0);
+      for (int mi = 0; mi < m; ++mi) {
+        if (mi > 0 || m > 1) {
+          r = s_rows[wave][mi];
+          gemv_load_act<BITS, LG, GG>(a.gu.act + size_t(r / rt.kk) * a.gu.act_stride, groups,
+                                      act);
+        }
+        gemv_rows<BITS, LG, GG, kHG, true>(a.gu, qb, act, wrow0 + kHG * (64 / LG), store(r));
+      }
+      if (LAST) prefetch_down(1);
+    };
+    const int mine = gw < items ? (items - 1 - gw) / n_waves + 1 : 0;
+    for (int j = 0; j + 1 < mine; ++j) item(gw + j * n_waves, std::false_type{});
+    if (mine > 0) {
+      item(gw + (mine - 1) * n_waves, std::true_type{});
+    } else {
+      prefetch_down(0);
+      prefetch_down(1);
     }
   }
-
   trace_mark(sy, 7);
-  // D prologue: weights of this wave's first down item (expert `wave`,
-  // first sub-tile) requested before the barrier.
-  constexpr int kSub = RD * (64 / LD);
-  const int tile = a.tile;
-  const int row0 = blockIdx.x * tile;
-  const bool has_down = row0 < a.dn.rows_out;
-  GemvRegs<BITS, LD, GD, RD, false> qd;
-#ifndef PMOE_NO_PREFETCH
-  if (has_down && wave < n_act) {
-#else
-  if (false) {
-#endif
-    const int slot = s_slot[wave];
-    if (slot >= 0) gemv_load<BITS, LD, GD, RD, false>(a.dn, slot, row0, qd);
-  }
   trace_mark(sy, 4);
   grid_barrier(sy, 1, tag2, a.n_blocks, 12);
   trace_mark(sy, 5);
@@ -290,18 +343,19 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
               s_y[s_rows[wave][mi] * tile + (wrow0 - row0) + t] = 0.0f;
           continue;
         }
-#ifndef PMOE_NO_PREFETCH
-        if (u != wave || s != 0)
-#endif
-          gemv_load<BITS, LD, GD, RD, false>(a.dn, slot, wrow0, qd);
+        const int wrow1 = wrow0 + kHD * (64 / LD);
+        if (u != wave || s != 0) {  // else prefetched in phase C
+          gemv_load<BITS, LD, GD, kHD, false>(a.dn, slot, wrow0, qd1);
+          if (RD > 1) gemv_load<BITS, LD, GD, kHD, false>(a.dn, slot, wrow1, qd2);
+        }
         GroupAct<BITS> act[GD];
         for (int mi = 0; mi < m; ++mi) {
           const int r = s_rows[wave][mi];
           gemv_load_act<BITS, LD, GD, kCoherentLoads>(a.dn.act + size_t(r) * a.dn.act_stride,
                                                       groups, act);
-          gemv_rows<BITS, LD, GD, RD, false>(a.dn, qd, act, wrow0, [&](int, int o, float v) {
-            s_y[r * tile + (o - row0)] = v;
-          });
+          auto to_lds = [&](int, int o, float v) { s_y[r * tile + (o - row0)] = v; };
+          gemv_rows<BITS, LD, GD, kHD, false>(a.dn, qd1, act, wrow0, to_lds);
+          if (RD > 1) gemv_rows<BITS, LD, GD, kHD, false>(a.dn, qd2, act, wrow1, to_lds);
         }
       }
       if (u == wave) trace_mark(sy, 11);
@@ -352,8 +406,11 @@ Entry make_entry() {
   // down items of ~16 rows (8 when a step already covers 8 rows): the
   // tile of a block is about hidden / CUs rows
   constexpr int RPW_D = 64 / LD;
-  constexpr int RG = fused_r<BITS, GG, true>(6);
-  constexpr int RD = RPW_D >= 8 ? 1 : fused_r<BITS, GD, false>(16 / RPW_D);
+  // both item sizes split in two halves: even step counts (down: 1 when a
+  // step already covers 8 rows)
+  constexpr int RG = (fused_r<BITS, GG, true>(6) & ~1) < 2 ? 2 : (fused_r<BITS, GG, true>(6) & ~1);
+  constexpr int RD = RPW_D >= 8 ? 1 : ((fused_r<BITS, GD, false>(16 / RPW_D) & ~1) < 2
+                                           ? 2 : (fused_r<BITS, GD, false>(16 / RPW_D) & ~1));
   return {&decode_fused_kernel<BITS, LG, GG, RG, LD, GD, RD, EPL>, RD * (64 / LD)};
 }
 

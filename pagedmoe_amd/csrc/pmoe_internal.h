@@ -85,18 +85,52 @@ __device__ __forceinline__ float pexp(float x) {
 
 __device__ __forceinline__ float psigmoid(float x) { return 1.0f / (1.0f + pexp(-x)); }
 
+// Value of lane (lane ^ D) -- an exact xor exchange without a trip through
+// the LDS crossbar where the wave's cross-lane paths allow it: DPP quad
+// permutes for D = 1, 2; DPP row shifts (left for lanes whose bit D is
+// clear, right for the others) for D = 4, 8; ds_swizzle (xor mode) for 16;
+// ds_bpermute for 32.
+template <int D>
+__device__ __forceinline__ float xor_lane(float v) {
+  const int b = __float_as_int(v);
+  int r;
+  if constexpr (D == 1) {
+    r = __builtin_amdgcn_update_dpp(b, b, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  } else if constexpr (D == 2) {
+    r = __builtin_amdgcn_update_dpp(b, b, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else if constexpr (D == 4 || D == 8) {
+    const int up = __builtin_amdgcn_update_dpp(b, b, 0x100 + D, 0xF, 0xF, false);  // row_shl
+    const int dn = __builtin_amdgcn_update_dpp(b, b, 0x110 + D, 0xF, 0xF, false);  // row_shr
+    r = (threadIdx.x & D) ? dn : up;
+  } else if constexpr (D == 16) {
+    r = __builtin_amdgcn_ds_swizzle(b, 0x401F);  // and 0x1f, xor 0x10
+  } else {
+    static_assert(D == 32, "xor_lane: D must be a power of two <= 32");
+    r = __builtin_amdgcn_ds_bpermute(int((threadIdx.x & 63) ^ 32) << 2, b);
+  }
+  return __int_as_float(r);
+}
+
 // xor butterfly over the 64 lanes; every lane ends with the same bits.
 __device__ __forceinline__ float wave_sum_bfly(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = v + __shfl_xor(v, off, kWave);
+  v = v + xor_lane<32>(v);
+  v = v + xor_lane<16>(v);
+  v = v + xor_lane<8>(v);
+  v = v + xor_lane<4>(v);
+  v = v + xor_lane<2>(v);
+  v = v + xor_lane<1>(v);
   return v;
 }
 
 // xor butterfly within aligned groups of W lanes (W a power of two <= 64).
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int off = W / 2; off > 0; off >>= 1) v = v + __shfl_xor(v, off, kWave);
+  if constexpr (W >= 64) v = v + xor_lane<32>(v);
+  if constexpr (W >= 32) v = v + xor_lane<16>(v);
+  if constexpr (W >= 16) v = v + xor_lane<8>(v);
+  if constexpr (W >= 8) v = v + xor_lane<4>(v);
+  if constexpr (W >= 4) v = v + xor_lane<2>(v);
+  if constexpr (W >= 2) v = v + xor_lane<1>(v);
   return v;
 }
 

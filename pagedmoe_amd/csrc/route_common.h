@@ -56,6 +56,9 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
                                    __builtin_amdgcn_mbcnt_lo(uint32_t(mask), 0));
 }
 
+// Lanes of the wave where c holds (one compare into an SGPR pair).
+__device__ __forceinline__ uint64_t wave_ballot(bool c) { return __builtin_amdgcn_ballot_w64(c); }
+
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -78,26 +81,33 @@ __device__ __forceinline__ void wave_topk_radix(const float (&v)[EPL], int n_val
     valid[i] = lane + 64 * i < n_valid;
     key[i] = valid[i] ? order_key(v[i]) : 0u;
   }
+  // p = the k-th largest key: the largest value whose count of keys >= p is
+  // at least k, found two bits per step (three candidate thresholds).
+  // Invalid entries hold key 0, below every candidate (all are >= 1).
   uint32_t p = 0;
-  for (int b = 31; b >= 0; --b) {
-    const uint32_t cand = p | (1u << b);
-    int cnt = 0;
+  for (int b = 30; b >= 0; b -= 2) {
+    const uint32_t c1 = p | (1u << b), c2 = p | (2u << b), c3 = p | (3u << b);
+    int n1 = 0, n2 = 0, n3 = 0;
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) cnt += __popcll(__ballot(valid[i] && key[i] >= cand));
-    if (cnt >= k) p = cand;
+    for (int i = 0; i < EPL; ++i) {
+      n1 += __popcll(wave_ballot(key[i] >= c1));
+      n2 += __popcll(wave_ballot(key[i] >= c2));
+      n3 += __popcll(wave_ballot(key[i] >= c3));
+    }
+    p = n3 >= k ? c3 : (n2 >= k ? c2 : (n1 >= k ? c1 : p));
   }
   int gt = 0;
 #pragma unroll
-  for (int i = 0; i < EPL; ++i) gt += __popcll(__ballot(valid[i] && key[i] > p));
+  for (int i = 0; i < EPL; ++i) gt += __popcll(wave_ballot(key[i] > p));
   const int need = k - gt;
   int run_eq = 0, run_sel = 0;
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     const bool eq = valid[i] && key[i] == p;
-    const uint64_t eqm = __ballot(eq);
+    const uint64_t eqm = wave_ballot(eq);
     const bool sel = (valid[i] && key[i] > p) || (eq && run_eq + lanes_below(eqm) < need);
     run_eq += __popcll(eqm);
-    const uint64_t selm = __ballot(sel);
+    const uint64_t selm = wave_ballot(sel);
     if (sel) {
       const int pos = run_sel + lanes_below(selm);
       tmp_v[pos] = v[i];
@@ -110,12 +120,19 @@ __device__ __forceinline__ void wave_topk_radix(const float (&v)[EPL], int n_val
   if (lane < k) {
     const float mv = tmp_v[lane];
     const int mi = tmp_i[lane];
-    int rank = 0;
-    for (int j = 0; j < k; ++j) {
-      const float ov = tmp_v[j];
-      const int oi = tmp_i[j];
-      rank += (ov > mv || (ov == mv && oi < mi)) ? 1 : 0;
+    float ovs[kRouteMaxK];
+    int ois[kRouteMaxK];
+#pragma unroll
+    for (int j = 0; j < kRouteMaxK; ++j) {  // all loads in flight at once
+      if (j < k) {
+        ovs[j] = tmp_v[j];
+        ois[j] = tmp_i[j];
+      }
     }
+    int rank = 0;
+#pragma unroll
+    for (int j = 0; j < kRouteMaxK; ++j)
+      if (j < k) rank += (ovs[j] > mv || (ovs[j] == mv && ois[j] < mi)) ? 1 : 0;
     out_v[rank] = mv;
     out_i[rank] = mi;
     if (EXTRA) out_x[rank] = tmp_x[lane];
@@ -151,9 +168,11 @@ __device__ void route_token(const RouteDev& r, int t, RouteLds& L, WaveTmp& W, i
   if (r.scoring == PMOE_SCORE_SOFTMAX) {
     wave_topk_radix<false, EPL>(v, e, k, W.ov, W.oi, x, nullptr, W.tv, W.ti, W.tx);
     const float m = W.ov[0];
+    // lane j < k holds exp(v_j - m); the sum runs in pick order j = 0..k-1
+    const float ej = lane < k ? pexp(W.ov[lane] - m) : 0.0f;
     float s = 0.0f;
     if (r.norm) {
-      for (int j = 0; j < k; ++j) s = s + pexp(W.ov[j] - m);
+      for (int j = 0; j < k; ++j) s = s + __shfl(ej, j, kWave);
     } else {
       float acc = 0.0f;
 #pragma unroll
@@ -163,7 +182,7 @@ __device__ void route_token(const RouteDev& r, int t, RouteLds& L, WaveTmp& W, i
     }
     if (lane < k) {
       ik = W.oi[lane];
-      wk = pexp(W.ov[lane] - m) / s;
+      wk = ej / s;
     }
   } else {
     float c[EPL];
@@ -301,7 +320,7 @@ __device__ __forceinline__ int wave_rows_of(const RouteLds& L, int rows, int id,
   for (int base = 0; base < rows; base += 64) {
     const int r = base + lane;
     const bool hit = r < rows && L.ids[r] == id;
-    const uint64_t mask = __ballot(hit);
+    const uint64_t mask = wave_ballot(hit);
     if (hit) out[m + lanes_below(mask)] = r;
     m += __popcll(mask);
   }
