@@ -244,6 +244,222 @@ def run_prefill(args, g, spec, slab, gate, tables, device, tokens=2048):
     return res
 
 
+def run_paging(args, device, tokens=256, warm=96):
+    """DeepSeek-V3/Kimi-K2-shaped layer decode with paging: hidden 7168, 384
+    routed experts + 1 shared, moe_intermediate 2048, 4-bit g64, batch 1.
+    The HBM slab holds 96 routed slots (+ the shared expert's pinned slot);
+    every expert lives in a pinned host store and misses are copied in by the
+    copy engine (side streams, event hand-off).  Expert ids follow a seeded
+    Zipf(1.1) popularity (ranks through a fixed permutation; 8 distinct ids
+    per token, sigmoid-style weights summing to 2.5).  Reports tokens/s, hit
+    rate, H2D bytes and rate, and the stall (wall time not spent in kernels)."""
+    import numpy as np
+    import torch
+
+    from pagedmoe_amd import kernels as K
+    from pagedmoe_amd._lib import KernelTimer, geom
+    from pagedmoe_amd.cache import ExpertCache, HostExpertStore
+    from pagedmoe_amd.slab import SlabStore
+
+    D, E, I, k, slots = 7168, 384, 2048, 8, 96
+    g = geom(D, I, 4)
+    t0 = time.perf_counter()
+    store = HostExpertStore(g, 1, E)
+    tmp = SlabStore(g, 1, device, zero=False)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(4)
+
+    def synth(slab, slot):
+        for prefix, rows, cols in (("gate_proj", I, D), ("up_proj", I, D), ("down_proj", D, I)):
+            slab.quantize_into(slot, prefix, torch.randn((rows, cols), generator=gen,
+                                                         device=device) * 0.02)
+
+    for e in range(E):
+        synth(tmp, 0)
+        store.write_from_slot(0, e, tmp, 0)
+    tmp.release()
+    cache = ExpertCache(g, slots, [0], E, host_store=store, n_shared=1, device=device)
+    synth(cache.slab, cache.shared_slot(0))
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t0
+
+    rng = np.random.default_rng(0)
+    perm = rng.permutation(E)
+    pop = 1.0 / np.arange(1, E + 1) ** 1.1
+    pop = pop / pop.sum()
+    n_tok = warm + tokens
+    ids = np.stack([perm[rng.choice(E, k, replace=False, p=pop)] for _ in range(n_tok)])
+    w = rng.random((n_tok, k)).astype(np.float32) + 0.1
+    w = w / w.sum(1, keepdims=True) * 2.5
+    inds = torch.from_numpy(ids.astype(np.int32)).to(device)
+    wts = torch.from_numpy(w).to(device)
+    x = torch.randn((n_tok, 1, D), generator=gen, device=device).to(torch.bfloat16)
+    out = torch.empty((n_tok, 1, D), dtype=torch.bfloat16, device=device)
+    table = cache.table_ptr(0)
+    shared = cache.shared_slot(0)
+
+    def step(i):
+        cache.fetch(0, ids[i].tolist())
+        out[i] = K.moe_experts(g, cache.slab.buf, table, E, x[i], inds[i:i + 1],
+                               wts[i:i + 1], shared_slot=shared)
+
+    for i in range(warm):
+        step(i)
+    torch.cuda.synchronize()
+    st0 = cache.stats()
+    with KernelTimer() as kt:
+        c0 = time.perf_counter()
+        for i in range(warm, n_tok):
+            step(i)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - c0
+    st1 = cache.stats()
+    hits = st1["hits"] - st0["hits"]
+    misses = st1["misses"] - st0["misses"]
+    h2d = (st1["h2d_gb"] - st0["h2d_gb"]) * 1e9
+    kern_s = sum(tot for tot, _ in kt.result.values()) / 1e3
+    stall = max(0.0, wall - kern_s)
+    expert_bytes = int(g.expert_bytes)
+    res = {
+        "workload": "DeepSeek-V3/Kimi-K2-shaped layer decode with paging",
+        "hidden": D, "experts": E, "shared_experts": 1, "moe_intermediate": I, "top_k": k,
+        "bits": 4, "slab_slots": slots, "popularity": "Zipf(1.1), seed 0", "batch": 1,
+        "tokens_timed": tokens, "warmup_tokens": warm,
+        "tokens_per_s": tokens / wall, "ms_per_token": wall * 1e3 / tokens,
+        "hit_rate": hits / max(1, hits + misses), "misses_per_token": misses / tokens,
+        "h2d_gb": h2d / 1e9, "h2d_gbs": h2d / stall / 1e9 if stall > 0 else None,
+        "stall_ms_per_token": stall * 1e3 / tokens,
+        "kernel_ms_per_token": kern_s * 1e3 / tokens,
+        "hbm_expert_bytes_per_token": (k + 1) * expert_bytes,
+        "kernel_hbm_gbs": (k + 1) * expert_bytes * tokens / kern_s / 1e9 if kern_s else None,
+        "setup_s": setup_s,
+        "note": "stall = wall time - sum of kernel times (the compute stream waiting on host "
+                "copies); h2d_gbs = copied bytes / stall; no speculative prefetch",
+    }
+    cache.close()
+    store.close()
+    return res
+
+
+def run_qwen3_next(args, device, layers=2):
+    """Qwen3-Next-shaped layer (hidden 2048, 512 experts + 1 gated shared
+    expert, moe_intermediate 512, top-10 softmax+renorm, 6-bit g64, all
+    resident): the 8-token speculative-verify step and a 1024-token prefill,
+    each timed as HIP-graph replays over `layers` distinct layers."""
+    import torch
+
+    from pagedmoe_amd import kernels as K
+    from pagedmoe_amd._lib import KernelTimer, geom
+    from pagedmoe_amd.slab import SlabStore
+
+    D, E, I, k = 2048, 512, 512, 10
+    g = geom(D, I, 6)
+    slots = layers * (E + 1)
+    slab = SlabStore(g, slots, device, zero=False)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(5)
+    for slot in range(slots):
+        for prefix, rows, cols in (("gate_proj", I, D), ("up_proj", I, D), ("down_proj", D, I)):
+            slab.quantize_into(slot, prefix, torch.randn((rows, cols), generator=gen,
+                                                         device=device) * 0.02)
+    gate = (torch.randn((layers, E, D), generator=gen, device=device) * 0.02).to(torch.bfloat16)
+    sgate = (torch.randn((layers, 1, D), generator=gen, device=device) * 0.02).to(torch.bfloat16)
+    tables = (torch.arange(layers, device=device, dtype=torch.int32)[:, None] * (E + 1)
+              + torch.arange(E, device=device, dtype=torch.int32)[None, :]).contiguous()
+    rc = K.route_cfg("softmax", E, k)
+    expert_bytes = int(sum(int(g.nbytes[c]) for c in range(9)))
+    out = {}
+    for name, n in (("verify_8", 8), ("prefill_1024", 1024)):
+        x = torch.randn((layers, n, D), generator=gen, device=device).to(torch.bfloat16)
+        y = torch.empty((layers, n, D), dtype=torch.bfloat16, device=device)
+        inds = torch.empty((layers, n, k), dtype=torch.int32, device=device)
+        wts = torch.empty((layers, n, k), dtype=torch.float32, device=device)
+        ws = K.moe_workspace(g, n, k, 1, E, device, fresh=True)
+
+        def seq():
+            for l in range(layers):
+                K.moe_block(g, rc, slab.buf, tables[l], gate[l], x[l], shared_slot=l * (E + 1) + E,
+                            shared_gate=sgate[l], out=y[l], inds=inds[l], weights=wts[l], ws=ws)
+
+        seq()
+        torch.cuda.synchronize()
+        with KernelTimer() as kt:
+            seq()
+        torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            seq()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            seq()
+        graph.replay()
+        torch.cuda.synchronize()
+        reps = 20 if n <= 8 else 5
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            graph.replay()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / (reps * layers)
+        uniq = sum(len(set(inds[l].reshape(-1).tolist())) for l in range(layers)) / layers
+        layer_bytes = (uniq + 1) * expert_bytes
+        rows = n * (k + 1)
+        flops = 2.0 * 3 * D * I * rows
+        r = {"tokens": n, "ms_per_step": ms, "tokens_per_s": n / (ms * 1e-3),
+             "mean_unique_experts": uniq, "expert_bytes_per_step": layer_bytes,
+             "hbm_gbs": layer_bytes / (ms * 1e-3) / 1e9,
+             "hbm_frac": layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+             "expert_tflops": flops / (ms * 1e-3) / 1e12,
+             "mfma_frac": flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+             "kernels": {nm: {"avg_us": tot * 1e3 / cnt, "launches": cnt}
+                         for nm, (tot, cnt) in kt.result.items()}}
+        out[name] = r
+    slab.release()
+    out["config"] = {"workload": "Qwen3-Next-shaped MoE layer", "hidden": D, "experts": E,
+                     "shared_experts": 1, "shared_gate": True, "moe_intermediate": I,
+                     "top_k": k, "bits": 6, "group": 64, "layers_cycled": layers}
+    return out
+
+
+def measured_ceilings(device):
+    """What this box sustains, to put the spec peaks in context: HBM read
+    bandwidth of a 2 GiB device-to-device copy (read + write bytes / time)
+    and the bf16 dense GEMM rate of torch.matmul (hipBLASLt) at the prefill
+    gate/up shape (16384 x 4096 x 3072, the same 412 GFLOP)."""
+    import torch
+
+    res = {}
+    src = torch.empty(1 << 30, dtype=torch.int16, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / 10
+    res["hbm_copy_gbs"] = 2 * src.numel() * 2 / dt / 1e9
+    del src, dst
+    m, k, n = 16384, 4096, 3072
+    a = torch.randn(m, k, device=device, dtype=torch.bfloat16)
+    b = torch.randn(n, k, device=device, dtype=torch.bfloat16)
+    for _ in range(3):
+        c = a @ b.t()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(10):
+        c = a @ b.t()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / 10
+    res["dense_bf16_gemm_tflops"] = 2.0 * m * k * n / dt / 1e12
+    res["dense_bf16_gemm_shape"] = [m, k, n]
+    del a, b, c
+    return res
+
+
 def pmc_run(args, g, spec, slab, gate, tables, device):
     """Eager layer steps for hardware-counter runs (one dispatch per kernel,
     no graph), followed by a plain copy of known size for calibration."""
@@ -330,6 +546,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the batch-8 and prefill lines in extra")
+    ap.add_argument("--no-paging", action="store_true",
+                    help="skip the DeepSeek-shaped paging leg in extra")
+    ap.add_argument("--no-next", action="store_true",
+                    help="skip the Qwen3-Next-shaped (6-bit) leg in extra")
     ap.add_argument("--prefill-reps", type=int, default=5,
                     help="graph replays (of --layers prefill layer steps) timed for the prefill line")
     ap.add_argument("--pmc-run", action="store_true",
@@ -378,6 +598,31 @@ def main():
             f"{rp['tokens_per_s']:.0f} tok/s, {rp['expert_tflops']:.0f} TFLOP/s "
             f"({100 * rp['mfma_frac_layer']:.1f}% of bf16 MFMA peak), kernels {rp['kernels']}")
         extra["prefill_2048"] = rp
+    if not args.no_extra:
+        ceil = measured_ceilings(device)
+        log(f"measured ceilings: HBM copy {ceil['hbm_copy_gbs']:.0f} GB/s, dense bf16 GEMM "
+            f"{ceil['dense_bf16_gemm_tflops']:.0f} TFLOP/s")
+        extra["measured_ceilings"] = ceil
+        if "prefill_2048" in extra:
+            rp = extra["prefill_2048"]
+            rp["mfma_frac_of_dense_gemm"] = rp["expert_tflops"] / ceil["dense_bf16_gemm_tflops"]
+            for nm in ("prefill_gateup", "prefill_down"):
+                kr = rp["kernels"].get(nm)
+                if kr and "tflops" in kr:
+                    kr["frac_of_dense_gemm"] = kr["tflops"] / ceil["dense_bf16_gemm_tflops"]
+    if not args.no_extra and not args.no_next:
+        rn = run_qwen3_next(args, device)
+        log(f"qwen3-next 6-bit: verify-8 {rn['verify_8']['ms_per_step'] * 1e3:.1f} us/step "
+            f"({100 * rn['verify_8']['hbm_frac']:.1f}% HBM), prefill-1024 "
+            f"{rn['prefill_1024']['ms_per_step']:.3f} ms/layer "
+            f"({100 * rn['prefill_1024']['hbm_frac']:.1f}% HBM, "
+            f"{100 * rn['prefill_1024']['mfma_frac']:.1f}% MFMA)")
+        extra["qwen3_next_6bit"] = rn
+    if not args.no_extra and not args.no_paging:
+        rg = run_paging(args, device)
+        log(f"deepseek paging: {rg['tokens_per_s']:.0f} tok/s, hit rate {rg['hit_rate']:.3f}, "
+            f"stall {rg['stall_ms_per_token']:.3f} ms/token, H2D {rg['h2d_gbs'] or 0:.1f} GB/s")
+        extra["deepseek_paging"] = rg
 
     if "decode_fused" in main_res["kernels"]:
         kname = "decode_fused_kernel"
@@ -414,6 +659,8 @@ def main():
         cpu = cpu_baseline(g, spec, slab, gate, args.cpu_seconds, device)
         log(f"cpu baseline: {cpu['value']:.1f} tok/s on {cpu['cores']} threads")
 
+    if "measured_ceilings" in extra:
+        roofline["frac_of_measured_hbm_copy"] = achieved / extra["measured_ceilings"]["hbm_copy_gbs"]
     line = {
         "metric": "MoE-layer tokens/s + % HBM roofline (decode) / % MFMA peak (prefill)",
         "value": main_res["tokens_per_s"],

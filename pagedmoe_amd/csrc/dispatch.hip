@@ -167,14 +167,17 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(
   __shared__ int s_cnt[kMaxExperts];
   __shared__ int s_off[kMaxExperts];
   __shared__ int s_tmp[16];
+  constexpr int kBatch = 16;  // block histograms read per round, all in flight
   const int e = threadIdx.x;
   if (e < n_experts) {
     int run = 0;
-    for (int b = 0; b < n_blocks; ++b) {
-      const size_t i = size_t(b) * n_experts + e;
-      const int h = hist[i];
-      hist[i] = run;
-      run += h;
+    for (int b0 = 0; b0 < n_blocks; b0 += kBatch) {
+      int h[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j)
+        h[j] = b0 + j < n_blocks ? hist[size_t(b0 + j) * n_experts + e] : 0;
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) run += h[j];
     }
     s_cnt[e] = run;
   }
@@ -182,8 +185,19 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(
   finish_scan(s_cnt, n_experts, counts, offsets, active, n_active, tile_m, tiles, n_tiles, s_off,
               s_tmp);
   if (e < n_experts) {
-    const int base = s_off[e];
-    for (int b = 0; b < n_blocks; ++b) hist[size_t(b) * n_experts + e] += base;
+    // each block's base position per expert: expert offset + earlier blocks
+    int run = s_off[e];
+    for (int b0 = 0; b0 < n_blocks; b0 += kBatch) {
+      int h[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j)
+        h[j] = b0 + j < n_blocks ? hist[size_t(b0 + j) * n_experts + e] : 0;
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        if (b0 + j < n_blocks) hist[size_t(b0 + j) * n_experts + e] = run;
+        run += h[j];
+      }
+    }
   }
 }
 

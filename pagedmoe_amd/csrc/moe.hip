@@ -38,7 +38,7 @@ struct MoeWs {
   int2* tiles = nullptr;          // [max_tiles]
   int32_t* n_tiles = nullptr;     // [1]
   uint16_t* h = nullptr;          // [rows, inter] bf16
-  float* y = nullptr;             // [rows, hidden] f32
+  float* y = nullptr;             // [rows, hidden] (bf16 or f32 per-slot outputs)
   void* dws = nullptr;            // dispatch scratch
   size_t dws_bytes = 0;
   void* record = nullptr;         // decode routing record
@@ -85,16 +85,18 @@ size_t carve(const pmoe_geom* g, int n, int k, int shared, int n_experts, void* 
   return c.off;
 }
 
-__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y,
+// y: the per-slot expert outputs [n*kk, d] in bf16, as the reference's
+// gather_qmm returns them; 8 outputs per thread.
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y,
                                                       const float* __restrict__ w,
                                                       const int32_t* __restrict__ inv,
                                                       const float* __restrict__ shared_logit,
                                                       int has_shared, int k, int kk, int d,
                                                       uint16_t* __restrict__ out) {
   const int n = blockIdx.y;
-  const int d0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+  const int d0 = (blockIdx.x * 256 + threadIdx.x) * 8;
   if (d0 >= d) return;
-  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  float a[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
   for (int c = 0; c < kk; ++c) {
     const size_t r = size_t(n) * kk + c;
     if (inv[r] < 0) continue;  // dropped id: contributes nothing
@@ -103,16 +105,20 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
       wt = w[size_t(n) * k + c];
     else
       wt = shared_logit ? psigmoid(shared_logit[n]) : 1.0f;
-    const float4 v = *reinterpret_cast<const float4*>(y + r * d + d0);
-    a0 = __builtin_fmaf(wt, v.x, a0);
-    a1 = __builtin_fmaf(wt, v.y, a1);
-    a2 = __builtin_fmaf(wt, v.z, a2);
-    a3 = __builtin_fmaf(wt, v.w, a3);
+    const uint4 v = *reinterpret_cast<const uint4*>(y + r * d + d0);
+    const uint32_t p[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[2 * i] = __builtin_fmaf(wt, bf16lo(p[i]), a[2 * i]);
+      a[2 * i + 1] = __builtin_fmaf(wt, bf16hi(p[i]), a[2 * i + 1]);
+    }
   }
-  uint2 o;
-  o.x = uint32_t(f2bf(a0)) | (uint32_t(f2bf(a1)) << 16);
-  o.y = uint32_t(f2bf(a2)) | (uint32_t(f2bf(a3)) << 16);
-  *reinterpret_cast<uint2*>(out + size_t(n) * d + d0) = o;
+  uint4 o;
+  o.x = uint32_t(f2bf(a[0])) | (uint32_t(f2bf(a[1])) << 16);
+  o.y = uint32_t(f2bf(a[2])) | (uint32_t(f2bf(a[3])) << 16);
+  o.z = uint32_t(f2bf(a[4])) | (uint32_t(f2bf(a[5])) << 16);
+  o.w = uint32_t(f2bf(a[6])) | (uint32_t(f2bf(a[7])) << 16);
+  *reinterpret_cast<uint4*>(out + size_t(n) * d + d0) = o;
 }
 
 // Same reduction over bf16 per-slot outputs (the seam's [N, K, D]), for
@@ -295,7 +301,7 @@ int experts_and_combine(const pmoe_geom* g, const uint8_t* slab, const int32_t* 
   const int shared = shared_slot >= 0 ? 1 : 0;
   const int kk = k + shared;
   int rc = run_experts(g, slab, table, n_experts, shared_slot, x, inds, n, k, kk, max_rpe, w,
-                       w.y, 1, st, dispatched);
+                       w.y, 0, st, dispatched);
   if (rc) return rc;
   const float* sl = nullptr;
   if (shared && shared_gate) {
@@ -303,9 +309,10 @@ int experts_and_combine(const pmoe_geom* g, const uint8_t* slab, const int32_t* 
     if (rc) return rc;
     sl = w.shared_logit;
   }
-  dim3 grid((g->hidden / 4 + 255) / 256, n);
+  dim3 grid((g->hidden / 8 + 255) / 256, n);
   ProfScope prof_scope(K_COMBINE, st);
-  combine_kernel<<<grid, 256, 0, st>>>(w.y, wts, w.inv, sl, shared, k, kk, g->hidden, out);
+  combine_kernel<<<grid, 256, 0, st>>>(reinterpret_cast<const uint16_t*>(w.y), wts, w.inv, sl,
+                                       shared, k, kk, g->hidden, out);
   PMOE_LAUNCH_CHECK("combine_kernel");
   return PMOE_OK;
 }
