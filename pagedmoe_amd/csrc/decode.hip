@@ -5,7 +5,8 @@
 // SwiGLU between them (streaming.py:640).  One launch computes a projection
 // for every active expert at once: blockIdx.y picks the expert (ascending id,
 // from the dispatch), blockIdx.x a tile of output rows, and each wave walks its
-// rows with every lane owning whole 64-value quant groups of the row.
+// rows, each lane owning units of the row (16-byte chunks for 4-bit, whole
+// 64-value quant groups for 6-bit; gemv_common.h).
 //
 // The per-lane arithmetic (128-bit packed loads, in-register (128+q) bf16
 // pairs, v_dot2_f32_bf16, xor-butterfly row sums) is in gemv_common.h.  The
@@ -15,6 +16,9 @@
 #include "pmoe_internal.h"
 #include "pmoe_kernels.h"
 #include "route_common.h"
+
+#include <map>
+#include <mutex>
 
 namespace pmoe {
 
@@ -41,7 +45,7 @@ __device__ __forceinline__ void store_zero_rows(const GemvArgs& a, int m_total,
 
 // Expert-major grouped projection: blockIdx.y = active expert (from a
 // dispatch in global memory), blockIdx.x = tile of 4*R*RPW output rows.
-template <int BITS, int LPR, int GPL, int R, bool DUAL>
+template <int UB, int LPR, int GPL, int R, bool DUAL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PMOE_MIN_WAVES, 8))) void qgemv_kernel(
     const GemvArgs a) {
   constexpr int RPW = 64 / LPR;
@@ -67,7 +71,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PMOE_MIN_WA
     else
       static_cast<uint16_t*>(a.out)[idx] = f2bf(v);
   };
-  gemv_expert<BITS, LPR, GPL, R, DUAL>(a, slot, m_total, rlist, wrow0, act_row, store);
+  gemv_expert<UB, LPR, GPL, R, DUAL>(a, slot, m_total, rlist, wrow0, act_row, store);
 }
 
 // Decode gate/up with the routing computed in the block's prologue (see
@@ -76,7 +80,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PMOE_MIN_WA
 // PRE: the routing record was written by route_record_kernel (several
 // tokens); otherwise every block routes its one token itself and block (0, 0)
 // publishes the record.
-template <int BITS, int LPR, int GPL, int R, int EPL, bool PRE>
+template <int UB, int LPR, int GPL, int R, int EPL, bool PRE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PMOE_MIN_WAVES, 8))) void
 gateup_routed_kernel(const GemvArgs a, const RouteDev rt, int32_t* inds_out, float* w_out,
                      RouteRecord* rec) {
@@ -111,7 +115,7 @@ gateup_routed_kernel(const GemvArgs a, const RouteDev rt, int32_t* inds_out, flo
   auto store = [&](int r, int, int o, float v) {
     static_cast<uint16_t*>(a.out)[size_t(r) * a.out_stride + o] = f2bf(v);
   };
-  gemv_expert<BITS, LPR, GPL, R, true>(a, slot, s_m, s_rows, wrow0, act_row, store);
+  gemv_expert<UB, LPR, GPL, R, true>(a, slot, s_m, s_rows, wrow0, act_row, store);
 }
 
 // Routing of several tokens at once (one wave per token, 16 waves), written
@@ -131,7 +135,7 @@ __global__ __launch_bounds__(1024) void route_record_kernel(const RouteDev rt, i
 // value lands in LDS and the block then forms
 //   out[n, o] = sum_c w[n, c] * y[n*kk + c, o],  c = 0..kk-1 in that order
 // (shared expert last) -- no y buffer, no extra launch, no cross-block sync.
-template <int BITS, int LPR, int GPL, int R, int EPL>
+template <int UB, int LPR, int GPL, int R, int EPL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PMOE_MIN_WAVES, 8))) void
 down_routed_kernel(const GemvArgs a, const RouteDev rt, uint16_t* out, const RouteRecord* rec) {
   constexpr int RPW = 64 / LPR;
@@ -154,7 +158,7 @@ down_routed_kernel(const GemvArgs a, const RouteDev rt, uint16_t* out, const Rou
     }
     auto act_row = [&](int r) { return a.act + size_t(r) * a.act_stride; };
     auto store = [&](int r, int st, int o, float v) { s_y[r * T + (o - row0)] = v; };
-    gemv_expert<BITS, LPR, GPL, R, false>(a, slot, m_total, s_rows[wave], row0, act_row, store);
+    gemv_expert<UB, LPR, GPL, R, false>(a, slot, m_total, s_rows[wave], row0, act_row, store);
   }
   __syncthreads();
   for (int i = threadIdx.x; i < rt.n * T; i += 256) {
@@ -169,65 +173,78 @@ down_routed_kernel(const GemvArgs a, const RouteDev rt, uint16_t* out, const Rou
 }
 
 // Row steps per wave: as many as fit next to the activations in a
-// 3-waves-per-SIMD register budget (~150 VGPRs: GPL*33 for activations,
-// ~30 for addresses and sums, the rest for packed weights), at most 4.
-template <int BITS, int GPL, bool DUAL>
+// 3-waves-per-SIMD register budget (~150 VGPRs: GPL units of activation
+// pairs, ~30 for addresses and sums, ~8 per unit of unpacked pairs in flight
+// once a lane has 3 or more units, the rest for packed weights), at most 4.
+template <int UB, int GPL, bool DUAL>
 constexpr int rows_r() {
-  constexpr int per_step = GPL * (64 * BITS / 32 + 2) * (DUAL ? 2 : 1);
-  constexpr int budget = 150 - 30 - GPL * 33;
+  constexpr int per_step = GPL * (Unit<UB>::kWords + 2) * (DUAL ? 2 : 1);
+  constexpr int budget =
+      150 - 30 - GPL * (Unit<UB>::kVals / 2 + 1) - (GPL >= 3 ? 8 * GPL : 0);
   constexpr int r = budget / per_step;
   if (PMOE_FORCE_R > 0) return PMOE_FORCE_R;
   return r < 1 ? 1 : (r > 4 ? 4 : r);
 }
 
-#define PMOE_FOR_SHAPES(X) X(64, 1) X(64, 2) X(8, 1) X(16, 1) X(32, 1)
+// Every (unit bytes, lanes per row, units per lane) pick_shape returns for
+// rows of up to 8192 values.
+#define PMOE_FOR_SHAPES_4(X)                                                     \
+  X(32, 64, 1) X(32, 64, 2) X(16, 8, 1) X(16, 16, 1) X(16, 32, 1) X(16, 64, 1)   \
+  X(16, 64, 2) X(16, 64, 3) X(16, 64, 4) X(16, 8, 3) X(16, 16, 3) X(16, 32, 3)
+#define PMOE_FOR_SHAPES_6(X) X(48, 64, 1) X(48, 64, 2) X(48, 8, 1) X(48, 16, 1) X(48, 32, 1)
+#define PMOE_FOR_SHAPES(BITS, X) \
+  if constexpr (BITS == 4) {     \
+    PMOE_FOR_SHAPES_4(X)         \
+  } else {                       \
+    PMOE_FOR_SHAPES_6(X)         \
+  }
 
 template <int BITS, bool DUAL>
 int launch_qgemv(const GemvArgs& a, Shape sh, int max_experts, hipStream_t st) {
-#define PMOE_CASE(L, G)                                                          \
-  if (sh.lpr == L && sh.gpl == G) {                                              \
-    constexpr int R = rows_r<BITS, G, DUAL>();                                   \
+#define PMOE_CASE(U, L, G)                                                       \
+  if (sh.ub == U && sh.lpr == L && sh.gpl == G) {                                \
+    constexpr int R = rows_r<U, G, DUAL>();                                      \
     dim3 grid((a.rows_out + 4 * R * (64 / L) - 1) / (4 * R * (64 / L)), max_experts); \
-    qgemv_kernel<BITS, L, G, R, DUAL><<<grid, 256, 0, st>>>(a);                  \
+    qgemv_kernel<U, L, G, R, DUAL><<<grid, 256, 0, st>>>(a);                     \
     PMOE_LAUNCH_CHECK("qgemv_kernel");                                           \
     return PMOE_OK;                                                              \
   }
-  PMOE_FOR_SHAPES(PMOE_CASE)
+  PMOE_FOR_SHAPES(BITS, PMOE_CASE)
 #undef PMOE_CASE
   return fail(PMOE_EINVAL, "qgemv: unsupported row shape");
 }
 
-template <int BITS, int EPL, int L, int G>
+template <int UB, int EPL, int L, int G>
 int launch_gateup_routed(const GemvArgs& gu, const RouteDev& rt, int max_experts,
                          int32_t* inds_out, float* w_out, RouteRecord* rec, hipStream_t st) {
-  constexpr int R = rows_r<BITS, G, true>();
+  constexpr int R = rows_r<UB, G, true>();
   constexpr int rows = 4 * R * (64 / L);
   dim3 grid((gu.rows_out + rows - 1) / rows, max_experts);
   if (rt.n == 1) {
-    gateup_routed_kernel<BITS, L, G, R, EPL, false><<<grid, 256, 0, st>>>(gu, rt, inds_out, w_out,
-                                                                          rec);
+    gateup_routed_kernel<UB, L, G, R, EPL, false><<<grid, 256, 0, st>>>(gu, rt, inds_out, w_out,
+                                                                        rec);
   } else {
     {
       ProfScope prof_scope(K_ROUTE_SELECT, st);
       route_record_kernel<EPL><<<1, 1024, 0, st>>>(rt, inds_out, w_out, rec);
       PMOE_LAUNCH_CHECK("route_record_kernel");
     }
-    gateup_routed_kernel<BITS, L, G, R, EPL, true><<<grid, 256, 0, st>>>(gu, rt, inds_out, w_out,
-                                                                         rec);
+    gateup_routed_kernel<UB, L, G, R, EPL, true><<<grid, 256, 0, st>>>(gu, rt, inds_out, w_out,
+                                                                       rec);
   }
   PMOE_LAUNCH_CHECK("gateup_routed_kernel");
   return PMOE_OK;
 }
 
-template <int BITS, int EPL, int L, int G>
+template <int UB, int EPL, int L, int G>
 int launch_down_routed(const GemvArgs& dn, const RouteDev& rt, uint16_t* out,
                        const RouteRecord* rec, hipStream_t st) {
-  constexpr int R = rows_r<BITS, G, false>();
+  constexpr int R = rows_r<UB, G, false>();
   constexpr int T = R * (64 / L);
   const size_t lds = size_t(rt.n) * rt.kk * T * sizeof(float);
   if (lds > 48 * 1024) return fail(PMOE_EINVAL, "decode: too many rows per tile");
   dim3 grid((dn.rows_out + T - 1) / T);
-  down_routed_kernel<BITS, L, G, R, EPL><<<grid, 256, lds, st>>>(dn, rt, out, rec);
+  down_routed_kernel<UB, L, G, R, EPL><<<grid, 256, lds, st>>>(dn, rt, out, rec);
   PMOE_LAUNCH_CHECK("down_routed_kernel");
   return PMOE_OK;
 }
@@ -236,13 +253,14 @@ template <int BITS, int EPL>
 int launch_routed(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int max_experts,
                   int32_t* inds_out, float* w_out, uint16_t* out, RouteRecord* rec,
                   hipStream_t st) {
-  const Shape s1 = pick_shape(gu.cols / 64), s2 = pick_shape(dn.cols / 64);
+  const Shape s1 = gateup_shape(BITS, gu, max_experts), s2 = pick_shape(BITS, dn.cols);
   int rc = PMOE_EINVAL;
   {
     ProfScope prof_scope(K_GATEUP, st);
-#define PMOE_CASE(L, G) \
-  if (s1.lpr == L && s1.gpl == G) rc = launch_gateup_routed<BITS, EPL, L, G>(gu, rt, max_experts, inds_out, w_out, rec, st);
-    PMOE_FOR_SHAPES(PMOE_CASE)
+#define PMOE_CASE(U, L, G)                                     \
+  if (s1.ub == U && s1.lpr == L && s1.gpl == G)                 \
+    rc = launch_gateup_routed<U, EPL, L, G>(gu, rt, max_experts, inds_out, w_out, rec, st);
+    PMOE_FOR_SHAPES(BITS, PMOE_CASE)
 #undef PMOE_CASE
   }
   if (rc == PMOE_EINVAL) return fail(PMOE_EINVAL, "decode: unsupported gate/up row shape");
@@ -250,9 +268,10 @@ int launch_routed(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, in
   rc = PMOE_EINVAL;
   {
     ProfScope prof_scope(K_DOWN, st);
-#define PMOE_CASE(L, G) \
-  if (s2.lpr == L && s2.gpl == G) rc = launch_down_routed<BITS, EPL, L, G>(dn, rt, out, rec, st);
-    PMOE_FOR_SHAPES(PMOE_CASE)
+#define PMOE_CASE(U, L, G)                     \
+  if (s2.ub == U && s2.lpr == L && s2.gpl == G) \
+    rc = launch_down_routed<U, EPL, L, G>(dn, rt, out, rec, st);
+    PMOE_FOR_SHAPES(BITS, PMOE_CASE)
 #undef PMOE_CASE
   }
   if (rc == PMOE_EINVAL && pmoe_last_error()[0] == 0)
@@ -262,13 +281,36 @@ int launch_routed(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, in
 
 }  // namespace
 
+// Waves the device holds at once at 3 waves per SIMD (cached per device).
+static int resident_waves() {
+  static std::mutex mu;
+  static std::map<int, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 0;
+  return cache[dev] = cus * 4 * 3;
+}
+
+Shape gateup_shape(int bits, const GemvArgs& gu, int max_experts) {
+  const Shape whole = pick_shape(bits, gu.cols);
+  if (whole.ub != 32) return whole;
+  const int rows_per_block = 4 * (64 / whole.lpr) * (whole.gpl == 1 ? rows_r<32, 1, true>()
+                                                                    : rows_r<32, 2, true>());
+  const long waves = 4L * max_experts * ((gu.rows_out + rows_per_block - 1) / rows_per_block);
+  return waves > resident_waves() ? pick_shape(bits, gu.cols, true) : whole;
+}
+
 size_t decode_record_bytes() { return sizeof(RouteRecord); }
 
 // One grouped projection launch (expert-major, dispatch in global memory).
 int qgemv(const GemvArgs& a, int bits, bool dual, int max_experts, int, hipStream_t st) {
-  const int groups = a.cols / 64;
-  PMOE_REQUIRE(a.cols % 64 == 0 && groups > 0, "qgemv: input dim must be a multiple of 64");
-  const Shape sh = pick_shape(groups);
+  PMOE_REQUIRE(a.cols % 64 == 0 && a.cols > 0, "qgemv: input dim must be a multiple of 64");
+  const Shape sh = dual ? gateup_shape(bits, a, max_experts) : pick_shape(bits, a.cols);
   PMOE_REQUIRE(sh.lpr > 0, "qgemv: input dim too large (max 8192)");
   if (max_experts <= 0 || a.rows_out <= 0) return PMOE_OK;
   ProfScope prof_scope(dual ? K_GATEUP : K_DOWN, st);

@@ -181,7 +181,7 @@ __device__ void router_pair(const FusedArgs& a, const RouteDev& rt, int e, int t
   }
 }
 
-template <int BITS, int LG, int GG, int RG, int LD, int GD, int RD, int EPL>
+template <int UG, int LG, int GG, int RG, int UD, int LD, int GD, int RD, int EPL>
 __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs a,
                                                                  const RouteDev rt) {
   __shared__ RouteLds L;
@@ -242,20 +242,19 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
   const int row0 = blockIdx.x * tile;
   const bool has_down = row0 < a.dn.rows_out;
   const int pre_slot = (has_down && wave < n_act) ? s_slot[wave] : -1;
-  GemvRegs<BITS, LD, GD, kHD, false> qd1, qd2;
+  GemvRegs<UD, LD, GD, kHD, false> qd1, qd2;
   // (scheduling fences keep the loads where they are: hoisted above the
   // gate/up arithmetic they would hold both register sets at once)
   auto prefetch_down = [&](int half) {
     __builtin_amdgcn_sched_barrier(0);
     if (pre_slot >= 0) {
-      if (half == 0) gemv_load<BITS, LD, GD, kHD, false>(a.dn, pre_slot, row0, qd1);
+      if (half == 0) gemv_load<UD, LD, GD, kHD, false>(a.dn, pre_slot, row0, qd1);
       if (half == 1 && RD > 1)
-        gemv_load<BITS, LD, GD, kHD, false>(a.dn, pre_slot, row0 + kHD * (64 / LD), qd2);
+        gemv_load<UD, LD, GD, kHD, false>(a.dn, pre_slot, row0 + kHD * (64 / LD), qd2);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
   {
-    const int groups = a.gu.cols / 64;
     const int chunks = (a.gu.rows_out + kRows - 1) / kRows;
     const int items = n_act * chunks;
     int cur = -1, m = 0;
@@ -286,30 +285,30 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
                        f2bf(v));
         };
       };
-      GroupAct<BITS> act[GG];
+      GroupAct<UG> act[GG];
       int r = s_rows[wave][0];
-      gemv_load_act<BITS, LG, GG>(a.gu.act + size_t(r / rt.kk) * a.gu.act_stride, groups, act);
+      gemv_load_act<UG, LG, GG>(a.gu.act + size_t(r / rt.kk) * a.gu.act_stride, a.gu.cols, act);
       __builtin_amdgcn_sched_barrier(0);
-      GemvRegs<BITS, LG, GG, kHG, true> qa, qb;
-      gemv_load<BITS, LG, GG, kHG, true>(a.gu, slot, wrow0, qa);
-      gemv_load<BITS, LG, GG, kHG, true>(a.gu, slot, wrow0 + kHG * (64 / LG), qb);
+      GemvRegs<UG, LG, GG, kHG, true> qa, qb;
+      gemv_load<UG, LG, GG, kHG, true>(a.gu, slot, wrow0, qa);
+      gemv_load<UG, LG, GG, kHG, true>(a.gu, slot, wrow0 + kHG * (64 / LG), qb);
       __builtin_amdgcn_sched_barrier(0);
       for (int mi = 0; mi < m; ++mi) {
         if (mi > 0) {
           r = s_rows[wave][mi];
-          gemv_load_act<BITS, LG, GG>(a.gu.act + size_t(r / rt.kk) * a.gu.act_stride, groups,
+          gemv_load_act<UG, LG, GG>(a.gu.act + size_t(r / rt.kk) * a.gu.act_stride, a.gu.cols,
                                       act);
         }
-        gemv_rows<BITS, LG, GG, kHG, true>(a.gu, qa, act, wrow0, store(r));
+        gemv_rows<UG, LG, GG, kHG, true>(a.gu, qa, act, wrow0, store(r));
       }
       if (LAST) prefetch_down(0);
       for (int mi = 0; mi < m; ++mi) {
         if (mi > 0 || m > 1) {
           r = s_rows[wave][mi];
-          gemv_load_act<BITS, LG, GG>(a.gu.act + size_t(r / rt.kk) * a.gu.act_stride, groups,
+          gemv_load_act<UG, LG, GG>(a.gu.act + size_t(r / rt.kk) * a.gu.act_stride, a.gu.cols,
                                       act);
         }
-        gemv_rows<BITS, LG, GG, kHG, true>(a.gu, qb, act, wrow0 + kHG * (64 / LG), store(r));
+        gemv_rows<UG, LG, GG, kHG, true>(a.gu, qb, act, wrow0 + kHG * (64 / LG), store(r));
       }
       if (LAST) prefetch_down(1);
     };
@@ -329,7 +328,6 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
 
   // D: down rows of the block's tile into LDS, then the fixed-order combine
   if (has_down) {
-    const int groups = a.dn.cols / 64;
     const int n_sub = tile / kSub;
     for (int u = wave; u < n_act; u += kFWaves) {
       const int e = L.active[u];
@@ -345,17 +343,17 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
         }
         const int wrow1 = wrow0 + kHD * (64 / LD);
         if (u != wave || s != 0) {  // else prefetched in phase C
-          gemv_load<BITS, LD, GD, kHD, false>(a.dn, slot, wrow0, qd1);
-          if (RD > 1) gemv_load<BITS, LD, GD, kHD, false>(a.dn, slot, wrow1, qd2);
+          gemv_load<UD, LD, GD, kHD, false>(a.dn, slot, wrow0, qd1);
+          if (RD > 1) gemv_load<UD, LD, GD, kHD, false>(a.dn, slot, wrow1, qd2);
         }
-        GroupAct<BITS> act[GD];
+        GroupAct<UD> act[GD];
         for (int mi = 0; mi < m; ++mi) {
           const int r = s_rows[wave][mi];
-          gemv_load_act<BITS, LD, GD, kCoherentLoads>(a.dn.act + size_t(r) * a.dn.act_stride,
-                                                      groups, act);
+          gemv_load_act<UD, LD, GD, kCoherentLoads>(a.dn.act + size_t(r) * a.dn.act_stride,
+                                                      a.dn.cols, act);
           auto to_lds = [&](int, int o, float v) { s_y[r * tile + (o - row0)] = v; };
-          gemv_rows<BITS, LD, GD, kHD, false>(a.dn, qd1, act, wrow0, to_lds);
-          if (RD > 1) gemv_rows<BITS, LD, GD, kHD, false>(a.dn, qd2, act, wrow1, to_lds);
+          gemv_rows<UD, LD, GD, kHD, false>(a.dn, qd1, act, wrow0, to_lds);
+          if (RD > 1) gemv_rows<UD, LD, GD, kHD, false>(a.dn, qd2, act, wrow1, to_lds);
         }
       }
       if (u == wave) trace_mark(sy, 11);
@@ -379,18 +377,19 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
 
 // Row steps per wave item: weights of one item stay in registers next to the
 // activations, within the 256 VGPRs of two waves per SIMD.
-template <int BITS, int GPL, bool DUAL>
+template <int UB, int GPL, bool DUAL>
 constexpr int fused_r(int cap) {
-  constexpr int per_step = GPL * (64 * BITS / 32 + 2) * (DUAL ? 2 : 1);
-  constexpr int budget = 170 - GPL * 33;
+  constexpr int per_step = GPL * (Unit<UB>::kWords + 2) * (DUAL ? 2 : 1);
+  constexpr int budget = 170 - GPL * (Unit<UB>::kVals / 2 + 1);
   int r = budget / per_step;
   return r < 1 ? 1 : (r > cap ? cap : r);
 }
 
 struct Variant {
-  int bits, lg, gg, ld, gd, epl;
+  int bits, ug, lg, gg, ud, ld, gd, epl;
   bool operator<(const Variant& o) const {
-    return std::tie(bits, lg, gg, ld, gd, epl) < std::tie(o.bits, o.lg, o.gg, o.ld, o.gd, o.epl);
+    return std::tie(bits, ug, lg, gg, ud, ld, gd, epl) <
+           std::tie(o.bits, o.ug, o.lg, o.gg, o.ud, o.ld, o.gd, o.epl);
   }
 };
 
@@ -401,36 +400,45 @@ struct Entry {
   int sub_rows;  // down rows per wave item
 };
 
-template <int BITS, int LG, int GG, int LD, int GD, int EPL>
+template <int UG, int LG, int GG, int UD, int LD, int GD, int EPL>
 Entry make_entry() {
   // down items of ~16 rows (8 when a step already covers 8 rows): the
   // tile of a block is about hidden / CUs rows
   constexpr int RPW_D = 64 / LD;
   // both item sizes split in two halves: even step counts (down: 1 when a
   // step already covers 8 rows)
-  constexpr int RG = (fused_r<BITS, GG, true>(6) & ~1) < 2 ? 2 : (fused_r<BITS, GG, true>(6) & ~1);
-  constexpr int RD = RPW_D >= 8 ? 1 : ((fused_r<BITS, GD, false>(16 / RPW_D) & ~1) < 2
-                                           ? 2 : (fused_r<BITS, GD, false>(16 / RPW_D) & ~1));
-  return {&decode_fused_kernel<BITS, LG, GG, RG, LD, GD, RD, EPL>, RD * (64 / LD)};
+  constexpr int RG = (fused_r<UG, GG, true>(6) & ~1) < 2 ? 2 : (fused_r<UG, GG, true>(6) & ~1);
+  constexpr int RD = RPW_D >= 8 ? 1 : ((fused_r<UD, GD, false>(16 / RPW_D) & ~1) < 2
+                                           ? 2 : (fused_r<UD, GD, false>(16 / RPW_D) & ~1));
+  return {&decode_fused_kernel<UG, LG, GG, RG, UD, LD, GD, RD, EPL>, RD * (64 / LD)};
 }
 
-// Supported (gate/up row shape, down row shape) pairs: hidden 1024/inter 512,
-// hidden 4096/inter 1536 (and 2048), hidden 7168/inter 2048, hidden
-// 2048/inter 512; experts up to 512.  Other shapes use the three-launch path.
+// Supported (gate/up row shape, down row shape) pairs, from gateup_shape and
+// pick_shape (whole- or half-group gate/up units where both occur):
+// 4-bit hidden 1024/inter 512, 4096/1536, 4096/2048, 7168/2048, 2048/512,
+// 2048/768; 6-bit 1024/512, 4096/1536, 7168/2048, 2048/512; experts up to
+// 512.  Other shapes use the three-launch path.
 const std::map<Variant, Entry>& variants() {
   static const std::map<Variant, Entry> m = [] {
     std::map<Variant, Entry> v;
-#define PMOE_FV(B, LG, GG, LD, GD, E) v[{B, LG, GG, LD, GD, E}] = make_entry<B, LG, GG, LD, GD, E>();
-#define PMOE_FV_E(B, LG, GG, LD, GD) \
-  PMOE_FV(B, LG, GG, LD, GD, 2) PMOE_FV(B, LG, GG, LD, GD, 4) PMOE_FV(B, LG, GG, LD, GD, 8)
-#define PMOE_FV_S(B)            \
-  PMOE_FV_E(B, 16, 1, 8, 1)     \
-  PMOE_FV_E(B, 64, 1, 32, 1)    \
-  PMOE_FV_E(B, 64, 2, 32, 1)    \
-  PMOE_FV_E(B, 32, 1, 8, 1)
-    PMOE_FV_S(4)
-    PMOE_FV_S(6)
-#undef PMOE_FV_S
+#define PMOE_FV(B, UG, LG, GG, UD, LD, GD, E) \
+  v[{B, UG, LG, GG, UD, LD, GD, E}] = make_entry<UG, LG, GG, UD, LD, GD, E>();
+#define PMOE_FV_E(B, UG, LG, GG, UD, LD, GD)                                    \
+  PMOE_FV(B, UG, LG, GG, UD, LD, GD, 2) PMOE_FV(B, UG, LG, GG, UD, LD, GD, 4)   \
+  PMOE_FV(B, UG, LG, GG, UD, LD, GD, 8)
+    PMOE_FV_E(4, 16, 32, 1, 16, 16, 1)
+    PMOE_FV_E(4, 32, 64, 1, 16, 16, 3)
+    PMOE_FV_E(4, 32, 64, 1, 16, 64, 1)
+    PMOE_FV_E(4, 32, 64, 2, 16, 64, 1)
+    PMOE_FV_E(4, 16, 64, 2, 16, 16, 3)
+    PMOE_FV_E(4, 16, 64, 2, 16, 64, 1)
+    PMOE_FV_E(4, 16, 64, 4, 16, 64, 1)
+    PMOE_FV_E(4, 16, 64, 1, 16, 16, 1)
+    PMOE_FV_E(4, 16, 64, 1, 16, 8, 3)
+    PMOE_FV_E(6, 48, 16, 1, 48, 8, 1)
+    PMOE_FV_E(6, 48, 64, 1, 48, 32, 1)
+    PMOE_FV_E(6, 48, 64, 2, 48, 32, 1)
+    PMOE_FV_E(6, 48, 32, 1, 48, 8, 1)
 #undef PMOE_FV_E
 #undef PMOE_FV
     return v;
@@ -474,12 +482,14 @@ int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int
                  const float* logit_bias, int32_t* inds_out, float* w_out, uint16_t* out,
                  DecodeSync* sync, hipStream_t st) {
   if (!sync || rt.n * rt.ld > kFMaxLogits) return kDecodeFusedDeclined;
-  const Shape sg = pick_shape(gu.cols / 64), sd = pick_shape(dn.cols / 64);
+  const int n_ids = rt.e + (rt.kk > rt.k ? 1 : 0);
+  const int max_experts = rt.n * rt.kk < n_ids ? rt.n * rt.kk : n_ids;
+  const Shape sg = gateup_shape(bits, gu, max_experts), sd = pick_shape(bits, dn.cols);
   const int epl = (rt.e + 63) / 64;
   const int epl_t = epl <= 2 ? 2 : (epl <= 4 ? 4 : (epl <= 8 ? 8 : 0));
   if (sg.lpr == 0 || sd.lpr == 0 || epl_t == 0) return kDecodeFusedDeclined;
   const auto& vs = variants();
-  const auto it = vs.find({bits, sg.lpr, sg.gpl, sd.lpr, sd.gpl, epl_t});
+  const auto it = vs.find({bits, sg.ub, sg.lpr, sg.gpl, sd.ub, sd.lpr, sd.gpl, epl_t});
   if (it == vs.end()) return kDecodeFusedDeclined;
   const Entry& en = it->second;
   // tile = down rows per block, a whole number of wave items

@@ -1,10 +1,11 @@
 // Grouped dequant-GEMV primitives shared by the decode kernels (decode.hip,
 // decode_fused.hip).
 //
-// Per lane and group: the packed weight words arrive as 16-byte loads, each
-// 32-bit word is turned into bf16 pairs (128+q) with one and/or (4-bit) or a
-// funnel shift (6-bit), and v_dot2_f32_bf16 accumulates x*(128+q) in fp32.
-// With xs = sum of the group's x, the group's contribution is
+// Per lane and unit (a whole or half quantization group): the packed weight
+// words arrive as 16-byte loads, each 32-bit word is turned into bf16 pairs
+// (128+q) with one and/or (4-bit) or a funnel shift (6-bit), and
+// v_dot2_f32_bf16 accumulates x*(128+q) in fp32.  With xs = sum of the
+// unit's x and (s, b) its group's scale and bias, the unit's contribution is
 //   s*sum(x*q) + b*xs = s*acc + (b - 128*s)*xs,
 // so dequantised weights are never materialised.  Rows are reduced across
 // their LPR lanes with an xor butterfly.
@@ -35,11 +36,25 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
                                          __builtin_bit_cast(bf16x2, b), c, false);
 }
 
-// Activations of one 64-value group, pre-arranged as the bf16 pairs the
-// weight words of that group are unpacked into, plus the group sum.
-template <int BITS>
+// A lane's share of a weight row is made of units of UB packed bytes:
+//   UB = 32: a whole 4-bit quantization group (64 values);
+//   UB = 16: half of a 4-bit group (32 values).  Lane sub of a row owns
+//            units sub + LPR*j, so load instruction j covers the contiguous
+//            16*LPR bytes [16*LPR*j, 16*LPR*(j+1)) of the row;
+//   UB = 48: a whole 6-bit group (6-bit fields straddle 16-byte chunks).
+template <int UB>
+struct Unit {
+  static_assert(UB == 16 || UB == 32 || UB == 48, "unit of 16, 32 or 48 bytes");
+  static constexpr int kBits = UB == 48 ? 6 : 4;
+  static constexpr int kVals = UB * 8 / kBits;  // 32, 64, 64
+  static constexpr int kWords = UB / 4;         // 4, 8, 12
+};
+
+// Activations of one unit, pre-arranged as the bf16 pairs the weight words
+// of that unit are unpacked into, plus the unit's sum.
+template <int UB>
 struct GroupAct {
-  uint32_t p[32];
+  uint32_t p[Unit<UB>::kVals / 2];
   float sum;
 };
 
@@ -54,18 +69,19 @@ __device__ __forceinline__ uint4 load_act16(const uint4* p) {
   return make_uint4(uint32_t(lo), uint32_t(lo >> 32), uint32_t(hi), uint32_t(hi >> 32));
 }
 
-// Load 64 bf16 starting at src (16-byte aligned) into pair order.
-template <int BITS, bool COHERENT = false>
-__device__ __forceinline__ void load_group_act(const uint16_t* src, GroupAct<BITS>& a) {
+// Load one unit of activations starting at src (16-byte aligned) into pair
+// order.
+template <int UB, bool COHERENT = false>
+__device__ __forceinline__ void load_group_act(const uint16_t* src, GroupAct<UB>& a) {
   const uint4* v = reinterpret_cast<const uint4*>(src);
   float s = 0.0f;
 #pragma unroll
-  for (int c = 0; c < 8; ++c) {
+  for (int c = 0; c < Unit<UB>::kVals / 8; ++c) {
     const uint4 d = load_act16<COHERENT>(v + c);
     s += bf16lo(d.x) + bf16hi(d.x) + bf16lo(d.y) + bf16hi(d.y) + bf16lo(d.z) + bf16hi(d.z) +
          bf16lo(d.w) + bf16hi(d.w);
-    if (BITS == 4) {
-      // word c of the group holds values 8c..8c+7; pair i is (x_{8c+i}, x_{8c+i+4})
+    if (Unit<UB>::kBits == 4) {
+      // word c of the unit holds values 8c..8c+7; pair i is (x_{8c+i}, x_{8c+i+4})
       a.p[4 * c + 0] = __builtin_amdgcn_perm(d.z, d.x, 0x05040100u);
       a.p[4 * c + 1] = __builtin_amdgcn_perm(d.z, d.x, 0x07060302u);
       a.p[4 * c + 2] = __builtin_amdgcn_perm(d.w, d.y, 0x05040100u);
@@ -81,18 +97,19 @@ __device__ __forceinline__ void load_group_act(const uint16_t* src, GroupAct<BIT
   a.sum = s;
 }
 
-template <int BITS>
+template <int UB>
 struct GroupW {
-  static constexpr int kWords = 64 * BITS / 32;
+  static constexpr int kWords = Unit<UB>::kWords;
   uint32_t w[kWords];
   float s, b;
 };
 
-template <int BITS>
+// Unit u of a row: its packed words and its group's scale and bias.
+template <int UB>
 __device__ __forceinline__ void load_group_w(const uint32_t* wrow, const uint16_t* srow,
-                                             const uint16_t* brow, int g, GroupW<BITS>& q) {
-  constexpr int kWords = GroupW<BITS>::kWords;
-  const u32x4* v = reinterpret_cast<const u32x4*>(wrow + size_t(g) * kWords);
+                                             const uint16_t* brow, int u, GroupW<UB>& q) {
+  constexpr int kWords = GroupW<UB>::kWords;
+  const u32x4* v = reinterpret_cast<const u32x4*>(wrow + size_t(u) * kWords);
 #pragma unroll
   for (int c = 0; c < kWords / 4; ++c) {
 #if PMOE_NT_LOADS
@@ -105,17 +122,18 @@ __device__ __forceinline__ void load_group_w(const uint32_t* wrow, const uint16_
     q.w[4 * c + 2] = d.z;
     q.w[4 * c + 3] = d.w;
   }
+  const int g = u * Unit<UB>::kVals / 64;
   q.s = bf16f(srow[g]);
   q.b = bf16f(brow[g]);
 }
 
-// sum over the group of x*(128+q)
-template <int BITS>
-__device__ __forceinline__ float group_dot(const GroupW<BITS>& q, const GroupAct<BITS>& a) {
+// sum over the unit of x*(128+q)
+template <int UB>
+__device__ __forceinline__ float group_dot(const GroupW<UB>& q, const GroupAct<UB>& a) {
   float acc = 0.0f;
-  if (BITS == 4) {
+  if (Unit<UB>::kBits == 4) {
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
+    for (int c = 0; c < Unit<UB>::kWords; ++c) {
       const uint32_t w = q.w[c];
       acc = dot2(a.p[4 * c + 0], (w & 0x000F000Fu) | 0x43004300u, acc);
       acc = dot2(a.p[4 * c + 1], ((w >> 4) & 0x000F000Fu) | 0x43004300u, acc);
@@ -147,28 +165,30 @@ __device__ __forceinline__ float group_term(float acc, float s, float b, float x
 //
 // A wave computes rows o = wrow0 + st*RPW + rsub (st < R, RPW = 64/LPR rows
 // per step, lane = rsub*LPR + sub) of one expert's projection(s): each lane
-// owns groups sub + LPR*j (j < GPL) of its row.  The weights of all R steps
+// owns units sub + LPR*j (j < GPL) of its row (past the row's last unit a
+// lane re-loads that unit and leaves it out of the sum).  The weights of all R steps
 // (one or two projections) are held in registers (GemvRegs) and reused for
 // every activation row of the expert.
 
-template <int BITS, int LPR, int GPL, int R, bool DUAL>
+template <int UB, int LPR, int GPL, int R, bool DUAL>
 struct GemvRegs {
-  GroupW<BITS> q0[R][GPL];
-  GroupW<BITS> q1[DUAL ? R : 1][DUAL ? GPL : 1];
+  GroupW<UB> q0[R][GPL];
+  GroupW<UB> q1[DUAL ? R : 1][DUAL ? GPL : 1];
 };
 
-// Issue the whole weight burst of the wave (R steps x GPL groups x 1-2
+// Issue the whole weight burst of the wave (R steps x GPL units x 1-2
 // projections) for the expert in `slot`.  Rows past rows_out re-load the
 // last row (in bounds, never stored).
-template <int BITS, int LPR, int GPL, int R, bool DUAL>
+template <int UB, int LPR, int GPL, int R, bool DUAL>
 __device__ __forceinline__ void gemv_load(const GemvArgs& a, int slot, int wrow0,
-                                          GemvRegs<BITS, LPR, GPL, R, DUAL>& q) {
+                                          GemvRegs<UB, LPR, GPL, R, DUAL>& q) {
   constexpr int RPW = 64 / LPR;
   const int lane = threadIdx.x & 63;
   const int sub = lane % LPR;
   const int rsub = lane / LPR;
+  const int units = a.cols / Unit<UB>::kVals;
   const int groups = a.cols / 64;
-  const int wpr = a.cols * BITS / 32;
+  const int wpr = a.cols * Unit<UB>::kBits / 32;
   const uint8_t* base = a.slab + size_t(slot) * a.expert_bytes;
   const uint32_t* W0 = reinterpret_cast<const uint32_t*>(base + a.p0.w);
   const uint16_t* S0 = reinterpret_cast<const uint16_t*>(base + a.p0.s);
@@ -181,40 +201,41 @@ __device__ __forceinline__ void gemv_load(const GemvArgs& a, int slot, int wrow0
     const int o = min(wrow0 + st * RPW + rsub, a.rows_out - 1);
 #pragma unroll
     for (int j = 0; j < GPL; ++j) {
-      const int g = min(sub + LPR * j, groups - 1);
-      load_group_w<BITS>(W0 + size_t(o) * wpr, S0 + size_t(o) * groups, B0 + size_t(o) * groups,
-                         g, q.q0[st][j]);
+      const int u = min(sub + LPR * j, units - 1);
+      load_group_w<UB>(W0 + size_t(o) * wpr, S0 + size_t(o) * groups, B0 + size_t(o) * groups,
+                       u, q.q0[st][j]);
       if (DUAL)
-        load_group_w<BITS>(W1 + size_t(o) * wpr, S1 + size_t(o) * groups,
-                           B1 + size_t(o) * groups, g, q.q1[DUAL ? st : 0][DUAL ? j : 0]);
+        load_group_w<UB>(W1 + size_t(o) * wpr, S1 + size_t(o) * groups,
+                         B1 + size_t(o) * groups, u, q.q1[DUAL ? st : 0][DUAL ? j : 0]);
     }
   }
 }
 
-// The lane's activation groups of one activation row.
-template <int BITS, int LPR, int GPL, bool COHERENT = false>
-__device__ __forceinline__ void gemv_load_act(const uint16_t* src, int groups,
-                                              GroupAct<BITS> (&act)[GPL]) {
+// The lane's activation units of one activation row (cols values).
+template <int UB, int LPR, int GPL, bool COHERENT = false>
+__device__ __forceinline__ void gemv_load_act(const uint16_t* src, int cols,
+                                              GroupAct<UB> (&act)[GPL]) {
   const int sub = (threadIdx.x & 63) % LPR;
+  const int units = cols / Unit<UB>::kVals;
 #pragma unroll
   for (int j = 0; j < GPL; ++j) {
-    const int g = min(sub + LPR * j, groups - 1);
-    load_group_act<BITS, COHERENT>(src + size_t(g) * 64, act[j]);
+    const int u = min(sub + LPR * j, units - 1);
+    load_group_act<UB, COHERENT>(src + size_t(u) * Unit<UB>::kVals, act[j]);
   }
 }
 
 // Outputs of the R steps for the activation row held in act; store(st, o,
 // value) receives each finished row output (value = silu(g)*u for DUAL).
-template <int BITS, int LPR, int GPL, int R, bool DUAL, class Store>
+template <int UB, int LPR, int GPL, int R, bool DUAL, class Store>
 __device__ __forceinline__ void gemv_rows(const GemvArgs& a,
-                                          GemvRegs<BITS, LPR, GPL, R, DUAL>& q,
-                                          const GroupAct<BITS> (&act)[GPL], int wrow0,
+                                          GemvRegs<UB, LPR, GPL, R, DUAL>& q,
+                                          const GroupAct<UB> (&act)[GPL], int wrow0,
                                           Store store) {
   constexpr int RPW = 64 / LPR;
   const int lane = threadIdx.x & 63;
   const int sub = lane % LPR;
   const int rsub = lane / LPR;
-  const int groups = a.cols / 64;
+  const int units = a.cols / Unit<UB>::kVals;
 #pragma unroll
   for (int st = 0; st < R; ++st) {
     // Opaque to the optimiser: without this the unpacked pairs of every
@@ -222,7 +243,7 @@ __device__ __forceinline__ void gemv_rows(const GemvArgs& a,
 #pragma unroll
     for (int j = 0; j < GPL; ++j) {
 #pragma unroll
-      for (int c = 0; c < GroupW<BITS>::kWords; ++c) {
+      for (int c = 0; c < GroupW<UB>::kWords; ++c) {
         asm volatile("" : "+v"(q.q0[st][j].w[c]));
         if (DUAL) asm volatile("" : "+v"(q.q1[DUAL ? st : 0][DUAL ? j : 0].w[c]));
       }
@@ -230,12 +251,12 @@ __device__ __forceinline__ void gemv_rows(const GemvArgs& a,
     float p0 = 0.0f, p1 = 0.0f;
 #pragma unroll
     for (int j = 0; j < GPL; ++j) {
-      if (sub + LPR * j < groups) {
-        p0 = group_term(group_dot<BITS>(q.q0[st][j], act[j]), q.q0[st][j].s, q.q0[st][j].b,
+      if (sub + LPR * j < units) {
+        p0 = group_term(group_dot<UB>(q.q0[st][j], act[j]), q.q0[st][j].s, q.q0[st][j].b,
                         act[j].sum, p0);
         if (DUAL) {
-          const GroupW<BITS>& w1 = q.q1[DUAL ? st : 0][DUAL ? j : 0];
-          p1 = group_term(group_dot<BITS>(w1, act[j]), w1.s, w1.b, act[j].sum, p1);
+          const GroupW<UB>& w1 = q.q1[DUAL ? st : 0][DUAL ? j : 0];
+          p1 = group_term(group_dot<UB>(w1, act[j]), w1.s, w1.b, act[j].sum, p1);
         }
       }
     }
@@ -250,41 +271,64 @@ __device__ __forceinline__ void gemv_rows(const GemvArgs& a,
 // Activations of the first row are requested first (L2 hits), then the whole
 // weight burst of the wave; vector loads retire in order, so row 0 starts as
 // soon as its own words have landed.  store(t_row, st, o, value).
-template <int BITS, int LPR, int GPL, int R, bool DUAL, class Act, class Store>
+template <int UB, int LPR, int GPL, int R, bool DUAL, class Act, class Store>
 __device__ __forceinline__ void gemv_expert(const GemvArgs& a, int slot, int m_total,
                                             const int32_t* rlist, int wrow0, Act act_row,
                                             Store store) {
-  const int groups = a.cols / 64;
-  GroupAct<BITS> act[GPL];
+  GroupAct<UB> act[GPL];
   int r = rlist[0];
-  gemv_load_act<BITS, LPR, GPL>(act_row(r), groups, act);
+  gemv_load_act<UB, LPR, GPL>(act_row(r), a.cols, act);
   __builtin_amdgcn_sched_barrier(0);
-  GemvRegs<BITS, LPR, GPL, R, DUAL> q;
-  gemv_load<BITS, LPR, GPL, R, DUAL>(a, slot, wrow0, q);
+  GemvRegs<UB, LPR, GPL, R, DUAL> q;
+  gemv_load<UB, LPR, GPL, R, DUAL>(a, slot, wrow0, q);
   __builtin_amdgcn_sched_barrier(0);
   for (int m = 0; m < m_total; ++m) {
     if (m > 0) {
       r = rlist[m];
-      gemv_load_act<BITS, LPR, GPL>(act_row(r), groups, act);
+      gemv_load_act<UB, LPR, GPL>(act_row(r), a.cols, act);
       __builtin_amdgcn_sched_barrier(0);
     }
-    gemv_rows<BITS, LPR, GPL, R, DUAL>(a, q, act, wrow0,
+    gemv_rows<UB, LPR, GPL, R, DUAL>(a, q, act, wrow0,
                                        [&](int st, int o, float v) { store(r, st, o, v); });
   }
 }
 
 struct Shape {
-  int lpr, gpl;
+  int lpr, gpl, ub;  // lanes per row, units per lane, unit bytes
 };
 
-// Lanes per row: the smallest power of two >= groups (max 64), so a lane
-// owns one quant group (two for rows of 65..128 groups) and keeps that
-// group's activations in registers for every row the wave visits.
-inline Shape pick_shape(int groups) {
-  if (groups <= 0 || groups > 128) return {0, 0};
+// Row shape for rows of `cols` values.
+// 4-bit rows of >= 64 groups: whole groups (32-byte units) on 64 lanes, the
+// last step masked when the count is not a multiple of 64 -- the most bytes
+// in flight per register, for launches whose waves are all resident at once
+// -- or, with half_groups, 16-byte units on 64 lanes, each load instruction
+// covering a contiguous 1 KB of the row (the faster pattern once waves
+// queue behind each other).  Shorter 4-bit rows: half groups on the largest
+// power of two of lanes dividing the unit count when that leaves at most 3
+// units per lane, so every lane has work; else one unit per lane (64 lanes at
+// most), masked.
+// 6-bit (48-byte group units): the smallest power of two >= groups (8..64).
+inline Shape pick_shape(int bits, int cols, bool half_groups = false) {
+  if (cols <= 0 || cols % 64 || cols > 8192 || (bits != 4 && bits != 6)) return {0, 0, 0};
+  const int groups = cols / 64;
+  if (bits == 4 && groups >= 64)
+    return half_groups ? Shape{64, (2 * groups + 63) / 64, 16} : Shape{64, (groups + 63) / 64, 32};
+  const int units = bits == 4 ? 2 * groups : groups;
+  const int ub = bits == 4 ? 16 : 48;
+  if (bits == 4 && units % 8 == 0) {
+    int lpr = 64;
+    while (units % lpr) lpr >>= 1;
+    if (units / lpr <= 3) return {lpr, units / lpr, ub};
+  }
   int lpr = 8;
-  while (lpr < groups && lpr < 64) lpr <<= 1;
-  return {lpr, (groups + lpr - 1) / lpr};
+  while (lpr < units && lpr < 64) lpr <<= 1;
+  return {lpr, (units + lpr - 1) / lpr, ub};
 }
+
+// Gate/up row shape of the decode launches (both decode paths use it, so
+// they stay bit-identical): whole-group units while the three-launch gate/up
+// grid (max_experts blocks per row tile) fits the device in one round of
+// resident waves, half-group units once it does not (decode.hip).
+Shape gateup_shape(int bits, const GemvArgs& gu, int max_experts);
 
 }  // namespace pmoe
