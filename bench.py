@@ -426,7 +426,7 @@ def run_qwen3_next(args, device, layers=2):
 def measured_ceilings(device):
     """What this box sustains, to put the spec peaks in context: HBM
     bandwidth of a 2 GiB device-to-device copy (read + write bytes / time)
-    and of a 2 GiB reduction (torch.sum, read bytes / time), and the bf16
+    and of a 2 GiB fp32 reduction (torch.sum, read bytes / time), and the bf16
     dense GEMM rate of torch.matmul (hipBLASLt) at the prefill
     gate/up shape (16384 x 4096 x 3072, the same 412 GFLOP)."""
     import torch
@@ -444,15 +444,17 @@ def measured_ceilings(device):
     dt = (time.perf_counter() - t0) / 10
     res["hbm_copy_gbs"] = 2 * src.numel() * 2 / dt / 1e9
     del dst
+    srcf = src.view(torch.float32)  # fp32 reduction: torch's vectorised read path
     for _ in range(2):
-        src.sum()
+        srcf.sum()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(10):
-        src.sum()
+        srcf.sum()
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / 10
     res["hbm_read_gbs"] = src.numel() * 2 / dt / 1e9
+    del srcf
     del src
     m, k, n = 16384, 4096, 3072
     a = torch.randn(m, k, device=device, dtype=torch.bfloat16)

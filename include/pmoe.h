@@ -143,7 +143,7 @@ int pmoe_dequant(const uint32_t* q, const uint16_t* scales,
 size_t pmoe_moe_workspace(const pmoe_geom* g, int n, int k, int shared,
                           int n_experts);
 
-/* A MoE workspace starts with a 65,792-byte synchronisation header (grid
+/* A MoE workspace starts with a 73,984-byte synchronisation header (grid
  * barrier counters, launch epoch and per-block flags of the one-launch
  * decode layer).  It must be zero before the first pmoe_moe_block call on
  * that workspace and is kept consistent by every call after that, so it

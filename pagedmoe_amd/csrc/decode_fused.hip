@@ -29,8 +29,12 @@
 // Grid barrier protocol (DecodeSync: the first kDecodeSyncBytes of the
 // workspace, all zero before the first call):
 //   - every wave waits for its own memory operations (s_waitcnt 0), the
-//     block syncs and thread 0 adds 1 to arrive[i];
-//   - the block that brings the count to the grid size resets it to 0 and
+//     block syncs and thread 0 adds 1 to its group's counter (groups of
+//     kDecodeGroup blocks, one 128-byte line each); the group's last block
+//     resets that counter and adds 1 to arrive[i] -- device-scope atomics
+//     on one address are serialised, so a flat counter of 256 arrivals
+//     costs far more than two levels of 16;
+//   - the block that brings arrive[i] to the group count resets it to 0 and
 //     writes this launch's tag into every block's flag (one 128-byte line
 //     per block); the others poll their own line, so no address is hot
 //     while the weight stream saturates HBM;
@@ -59,6 +63,9 @@ constexpr int kFWaves = 8;
 constexpr int kFThreads = 64 * kFWaves;
 constexpr int kFMaxLogits = 8 * 1025;  // n * (E + shared gate) staged in LDS
 constexpr uint64_t kSpinTicks = 50000000ull;  // 0.5 s at 100 MHz
+#ifndef PMOE_POLL_SLEEP
+#define PMOE_POLL_SLEEP 2  // s_sleep units (64 clocks) between two flag polls
+#endif
 
 struct FusedArgs {
   const uint16_t* x;           // [n, hidden]
@@ -90,28 +97,55 @@ __device__ __forceinline__ void trace_mark(DecodeSync*, int i) {
 __device__ __forceinline__ void trace_mark(DecodeSync*, int) {}
 #endif
 
+// gemv_rows callback keeping step `sub`'s output in hv (each lane of a row
+// group keeps a different step).
+struct Collect {
+  float* hv;
+  int sub;
+  __device__ __forceinline__ void operator()(int st, int, float v) const {
+    if (sub == st) *hv = v;
+  }
+};
+__device__ __forceinline__ Collect collect_fn(float& hv, int sub) { return Collect{&hv, sub}; }
+
 template <class T>
 __device__ __forceinline__ void shared_store(T* p, T v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Block arrival + wait.  Every wave's stores (and loads) have completed
-// before the block arrives; the block that arrives last resets the counter
-// and writes `tag` into every block's flag line; each block's thread 0 polls
-// its own line (no shared hot spot while HBM is saturated).
+// before the block arrives.  Arrival is two-level, so no counter sees more
+// than kDecodeGroup (or group-count) device-scope atomics: the last block of
+// a group resets the group's counter and arrives at arrive[i]; the block
+// that completes arrive[i] resets it and writes `tag` into every block's
+// flag line; each block's thread 0 polls its own line (no shared hot spot
+// while HBM is saturated).
 __device__ __forceinline__ void grid_barrier(DecodeSync* sy, int i, uint32_t tag,
                                              uint32_t n_blocks, int mark = -1) {
   __shared__ int s_last;
   __builtin_amdgcn_s_waitcnt(0);  // this wave's memory operations have completed
   __syncthreads();
   if (mark >= 0) trace_mark(nullptr, mark);
+  uint8_t* base = reinterpret_cast<uint8_t*>(sy);
   if (threadIdx.x == 0) {
-    const uint32_t prev =
-        __hip_atomic_fetch_add(&sy->arrive[i], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == n_blocks - 1;
+    const uint32_t g = blockIdx.x / kDecodeGroup;
+    const uint32_t n_groups = (n_blocks + kDecodeGroup - 1) / kDecodeGroup;
+    const uint32_t in_group = min(uint32_t(kDecodeGroup), n_blocks - g * kDecodeGroup);
+    uint32_t* gc = reinterpret_cast<uint32_t*>(
+        base + kDecodeGroupOffset + (size_t(i) * kDecodeMaxGroups + g) * kDecodeFlagStride);
+    int last = 0;
+    if (__hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        in_group - 1) {
+      if (mark >= 0) trace_mark(nullptr, 13);
+      __hip_atomic_store(gc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = __hip_atomic_fetch_add(&sy->arrive[i], 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT) == n_groups - 1;
+      if (mark >= 0 && last) trace_mark(nullptr, 14);
+    }
+    s_last = last;
   }
   __syncthreads();
-  uint8_t* flags = reinterpret_cast<uint8_t*>(sy) + 256;
+  uint8_t* flags = base + 256;
   if (s_last) {
     if (threadIdx.x == 0) {
       __hip_atomic_store(&sy->arrive[i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -126,12 +160,13 @@ __device__ __forceinline__ void grid_barrier(DecodeSync* sy, int i, uint32_t tag
         reinterpret_cast<const uint32_t*>(flags + blockIdx.x * kDecodeFlagStride);
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     while (__hip_atomic_load(mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != tag) {
-      __builtin_amdgcn_s_sleep(2);
+      __builtin_amdgcn_s_sleep(PMOE_POLL_SLEEP);
       if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) {
         __hip_atomic_fetch_or(&sy->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
     }
+    if (mark >= 0) trace_mark(nullptr, 15);
   }
   __syncthreads();
 }
@@ -191,6 +226,7 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
   __shared__ int32_t s_slot[kRouteMaxRows];  // slot of active expert u
   extern __shared__ float s_y[];             // [rows][tile]
   const int wave = threadIdx.x >> 6;
+  const int lane_in_wave = threadIdx.x & 63;
   const int gw = blockIdx.x * kFWaves + wave;
   const int n_waves = a.n_blocks * kFWaves;
   DecodeSync* sy = a.sync;
@@ -279,11 +315,18 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
         return;
       }
       const int wrow0 = c * kRows;
-      auto store = [&](int r) {
-        return [&a, r](int, int o, float v) {
+      // h of one half (kHG steps) for activation row r: lane (rsub, sub)
+      // keeps step sub's value, then one store instruction writes the
+      // half's kHG * RPW consecutive bf16 (device-scope stores are written
+      // through one by one: one instruction, not kHG, per half)
+      const int g_sub = lane_in_wave % LG, g_rsub = lane_in_wave / LG;
+      auto run_half = [&](auto& q, const GroupAct<UG>(&xa)[GG], int r, int hrow0) {
+        float hv = 0.0f;
+        gemv_rows<UG, LG, GG, kHG, true, Collect, true>(a.gu, q, xa, hrow0, collect_fn(hv, g_sub));
+        const int o = hrow0 + g_sub * (64 / LG) + g_rsub;
+        if (g_sub < kHG && o < a.gu.rows_out)
           shared_store(&static_cast<uint16_t*>(a.gu.out)[size_t(r) * a.gu.out_stride + o],
-                       f2bf(v));
-        };
+                       f2bf(hv));
       };
       GroupAct<UG> act[GG];
       int r = s_rows[wave][0];
@@ -299,7 +342,7 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
           gemv_load_act<UG, LG, GG>(a.gu.act + size_t(r / rt.kk) * a.gu.act_stride, a.gu.cols,
                                       act);
         }
-        gemv_rows<UG, LG, GG, kHG, true>(a.gu, qa, act, wrow0, store(r));
+        run_half(qa, act, r, wrow0);
       }
       if (LAST) prefetch_down(0);
       for (int mi = 0; mi < m; ++mi) {
@@ -308,7 +351,7 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
           gemv_load_act<UG, LG, GG>(a.gu.act + size_t(r / rt.kk) * a.gu.act_stride, a.gu.cols,
                                       act);
         }
-        gemv_rows<UG, LG, GG, kHG, true>(a.gu, qb, act, wrow0 + kHG * (64 / LG), store(r));
+        run_half(qb, act, r, wrow0 + kHG * (64 / LG));
       }
       if (LAST) prefetch_down(1);
     };

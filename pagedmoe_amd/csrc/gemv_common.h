@@ -225,8 +225,10 @@ __device__ __forceinline__ void gemv_load_act(const uint16_t* src, int cols,
 }
 
 // Outputs of the R steps for the activation row held in act; store(st, o,
-// value) receives each finished row output (value = silu(g)*u for DUAL).
-template <int UB, int LPR, int GPL, int R, bool DUAL, class Store>
+// value) receives each finished row output (value = silu(g)*u for DUAL):
+// from the row group's first lane, for rows below rows_out, or (ALL) from
+// every lane of the row group, every row, unmasked.
+template <int UB, int LPR, int GPL, int R, bool DUAL, class Store, bool ALL = false>
 __device__ __forceinline__ void gemv_rows(const GemvArgs& a,
                                           GemvRegs<UB, LPR, GPL, R, DUAL>& q,
                                           const GroupAct<UB> (&act)[GPL], int wrow0,
@@ -263,7 +265,7 @@ __device__ __forceinline__ void gemv_rows(const GemvArgs& a,
     float v = group_sum<LPR>(p0);
     if (DUAL) v = silu_fast(v) * group_sum<LPR>(p1);
     const int o = wrow0 + st * RPW + rsub;
-    if (sub == 0 && o < a.rows_out) store(st, o, v);
+    if (ALL || (sub == 0 && o < a.rows_out)) store(st, o, v);
   }
 }
 

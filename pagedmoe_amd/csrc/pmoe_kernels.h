@@ -71,17 +71,24 @@ int decode_routed(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, in
 size_t decode_record_bytes();
 
 // Grid-barrier state of the fused decode launch: the first kDecodeSyncBytes
-// of the MoE workspace, zero before the first call.  arrive[i] counts the
-// blocks at barrier i (the last one to arrive resets it); epoch counts
-// launches; flag line b (128 bytes apart) is where block b waits.
+// of the MoE workspace, zero before the first call.  Blocks arrive in groups
+// of kDecodeGroup: group g's counter for barrier i (its own 128-byte line at
+// kDecodeGroupOffset + (i * kDecodeMaxGroups + g) * 128) counts the group's
+// blocks, and arrive[i] counts the groups that have fully arrived (each
+// last arriver resets the counter it completed); epoch counts launches;
+// flag line b (128 bytes apart from offset 256) is where block b waits.
 struct DecodeSync {
-  uint32_t arrive[2];  // blocks arrived at barrier 1 / barrier 2
+  uint32_t arrive[2];  // groups arrived at barrier 1 / barrier 2
   uint32_t epoch;      // launches completed on this workspace
   uint32_t error;      // sticky: bit 0 = a barrier wait timed out
 };
 constexpr int kDecodeMaxBlocks = 512;
+constexpr int kDecodeGroup = 16;  // blocks per arrival group
+constexpr int kDecodeMaxGroups = kDecodeMaxBlocks / kDecodeGroup;
 constexpr size_t kDecodeFlagStride = 128;  // bytes between two blocks' flags
-constexpr size_t kDecodeSyncBytes = 256 + kDecodeMaxBlocks * kDecodeFlagStride;
+constexpr size_t kDecodeGroupOffset = 256 + kDecodeMaxBlocks * kDecodeFlagStride;
+constexpr size_t kDecodeSyncBytes =
+    kDecodeGroupOffset + 2 * kDecodeMaxGroups * kDecodeFlagStride;
 constexpr int kDecodeFusedDeclined = 1;  // shape not covered: use decode_routed
 
 // Whole decode layer in one persistent launch (decode_fused.hip): router

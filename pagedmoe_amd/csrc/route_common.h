@@ -4,8 +4,8 @@
 // fp32 router logits (a few hundred floats) instead of waiting for a separate
 // routing launch.  The computation is deterministic and uses only separately
 // rounded float ops, so every block, and the CPU oracle, get identical bits:
-//   * top-k per token: radix select on order-preserving keys with wave
-//     ballots, ties to the lower expert id, picks sorted by (value desc, id
+//   * top-k per token: k rounds of a wave-wide maximum of order-preserving
+//     keys, ties to the lower expert id, picks sorted by (value desc, id
 //     asc) -- softmax(+renorm) or sigmoid+bias with grouped selection and
 //     routed scaling (tests/test_stream.py:191-196; streaming.py:2424-2442);
 //   * active experts: a bitmap of the used ids, listed in ascending order;
@@ -32,9 +32,7 @@ struct RouteDev {
 };
 
 struct WaveTmp {
-  float tv[kRouteMaxK], tx[kRouteMaxK], ov[kRouteMaxK], ox[kRouteMaxK];
-  int ti[kRouteMaxK], oi[kRouteMaxK];
-  float c[kRouteMaxSigE];
+  float c[kRouteMaxSigE];  // sigmoid scoring: biased scores, read across lanes
 };
 
 struct RouteLds {
@@ -65,79 +63,71 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Top-k of per-lane values v[i] (id lane + 64*i, valid when id < n_valid).
-// Writes the k picks sorted by (value desc, id asc) to out_v/out_i and, when
-// EXTRA, carries extra[i] along to out_x.  tmp_* hold k entries.
-template <bool EXTRA, int EPL>
-__device__ __forceinline__ void wave_topk_radix(const float (&v)[EPL], int n_valid, int k,
-                                                float* out_v, int* out_i,
-                                                const float (&extra)[EPL], float* out_x,
-                                                float* tmp_v, int* tmp_i, float* tmp_x) {
+// Maximum of an unsigned key over the wave, wave-uniform: xor exchanges
+// within each row of 16 lanes, then the four row maxima by readlane.
+__device__ __forceinline__ uint32_t wave_max_key(uint32_t v) {
+  v = max(v, __float_as_uint(xor_lane<1>(__uint_as_float(v))));
+  v = max(v, __float_as_uint(xor_lane<2>(__uint_as_float(v))));
+  v = max(v, __float_as_uint(xor_lane<4>(__uint_as_float(v))));
+  v = max(v, __float_as_uint(xor_lane<8>(__uint_as_float(v))));
+  const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+  return max(max(r0, r1), max(r2, r3));
+}
+
+// Pick j of a top-k, held by lane j.
+struct Pick {
+  float v;  // value
+  int i;    // id
+  float x;  // payload carried along
+};
+
+// Top-k of per-lane values v[i] (id lane + 64*i, valid when id < n_valid,
+// k <= n_valid): k rounds of a wave-wide maximum of order-preserving keys,
+// each taking the lowest id among the entries holding the maximum.  Lane j
+// (< k) returns pick j; picks come out sorted by (value desc, id asc), and
+// extra[i] of each pick is carried along.  Registers and scalar ops only.
+template <int EPL>
+__device__ __forceinline__ Pick wave_topk(const float (&v)[EPL], int n_valid, int k,
+                                          const float (&extra)[EPL]) {
   const int lane = threadIdx.x & 63;
   uint32_t key[EPL];
-  bool valid[EPL];
+  bool avail[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
-    valid[i] = lane + 64 * i < n_valid;
-    key[i] = valid[i] ? order_key(v[i]) : 0u;
+    avail[i] = lane + 64 * i < n_valid;
+    key[i] = order_key(v[i]);
   }
-  // p = the k-th largest key: the largest value whose count of keys >= p is
-  // at least k, found two bits per step (three candidate thresholds).
-  // Invalid entries hold key 0, below every candidate (all are >= 1).
-  uint32_t p = 0;
-  for (int b = 30; b >= 0; b -= 2) {
-    const uint32_t c1 = p | (1u << b), c2 = p | (2u << b), c3 = p | (3u << b);
-    int n1 = 0, n2 = 0, n3 = 0;
+  Pick pk{0.0f, 0, 0.0f};
+  for (int j = 0; j < k; ++j) {
+    uint32_t best = 0;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) best = avail[i] ? max(best, key[i]) : best;
+    const uint32_t top = wave_max_key(best);
+    int sel = -1;  // lowest id holding top: first i with a hit, lowest lane in it
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
-      n1 += __popcll(wave_ballot(key[i] >= c1));
-      n2 += __popcll(wave_ballot(key[i] >= c2));
-      n3 += __popcll(wave_ballot(key[i] >= c3));
+      const uint64_t hit = wave_ballot(avail[i] && key[i] == top);
+      if (sel < 0 && hit) sel = 64 * i + __builtin_ctzll(hit);
     }
-    p = n3 >= k ? c3 : (n2 >= k ? c2 : (n1 >= k ? c1 : p));
-  }
-  int gt = 0;
+    const int sl = sel & 63, si = sel >> 6;
+    float pv = 0.0f, px = 0.0f;
 #pragma unroll
-  for (int i = 0; i < EPL; ++i) gt += __popcll(wave_ballot(key[i] > p));
-  const int need = k - gt;
-  int run_eq = 0, run_sel = 0;
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    const bool eq = valid[i] && key[i] == p;
-    const uint64_t eqm = wave_ballot(eq);
-    const bool sel = (valid[i] && key[i] > p) || (eq && run_eq + lanes_below(eqm) < need);
-    run_eq += __popcll(eqm);
-    const uint64_t selm = wave_ballot(sel);
-    if (sel) {
-      const int pos = run_sel + lanes_below(selm);
-      tmp_v[pos] = v[i];
-      tmp_i[pos] = lane + 64 * i;
-      if (EXTRA) tmp_x[pos] = extra[i];
-    }
-    run_sel += __popcll(selm);
-  }
-  wave_lds_sync();
-  if (lane < k) {
-    const float mv = tmp_v[lane];
-    const int mi = tmp_i[lane];
-    float ovs[kRouteMaxK];
-    int ois[kRouteMaxK];
-#pragma unroll
-    for (int j = 0; j < kRouteMaxK; ++j) {  // all loads in flight at once
-      if (j < k) {
-        ovs[j] = tmp_v[j];
-        ois[j] = tmp_i[j];
+    for (int i = 0; i < EPL; ++i) {
+      if (i == si) {
+        pv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[i]), sl));
+        px = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(extra[i]), sl));
+        if (lane == sl) avail[i] = false;
       }
     }
-    int rank = 0;
-#pragma unroll
-    for (int j = 0; j < kRouteMaxK; ++j)
-      if (j < k) rank += (ovs[j] > mv || (ovs[j] == mv && ois[j] < mi)) ? 1 : 0;
-    out_v[rank] = mv;
-    out_i[rank] = mi;
-    if (EXTRA) out_x[rank] = tmp_x[lane];
+    if (lane == j) pk = Pick{pv, sel, px};
   }
-  wave_lds_sync();
+  return pk;
+}
+
+// Value of `v` in lane j (j wave-uniform).
+__device__ __forceinline__ float lane_value(float v, int j) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
 }
 
 // Logit loads: COHERENT reads the logits at device scope (they were written
@@ -166,13 +156,13 @@ __device__ void route_token(const RouteDev& r, int t, RouteLds& L, WaveTmp& W, i
   float wk = 0.0f;
   int ik = 0;
   if (r.scoring == PMOE_SCORE_SOFTMAX) {
-    wave_topk_radix<false, EPL>(v, e, k, W.ov, W.oi, x, nullptr, W.tv, W.ti, W.tx);
-    const float m = W.ov[0];
+    const Pick pk = wave_topk<EPL>(v, e, k, x);
+    const float m = lane_value(pk.v, 0);
     // lane j < k holds exp(v_j - m); the sum runs in pick order j = 0..k-1
-    const float ej = lane < k ? pexp(W.ov[lane] - m) : 0.0f;
+    const float ej = lane < k ? pexp(pk.v - m) : 0.0f;
     float s = 0.0f;
     if (r.norm) {
-      for (int j = 0; j < k; ++j) s = s + __shfl(ej, j, kWave);
+      for (int j = 0; j < k; ++j) s = s + lane_value(ej, j);
     } else {
       float acc = 0.0f;
 #pragma unroll
@@ -181,7 +171,7 @@ __device__ void route_token(const RouteDev& r, int t, RouteLds& L, WaveTmp& W, i
       s = wave_sum_bfly(acc);
     }
     if (lane < k) {
-      ik = W.oi[lane];
+      ik = pk.i;
       wk = ej / s;
     }
   } else {
@@ -216,25 +206,23 @@ __device__ void route_token(const RouteDev& r, int t, RouteLds& L, WaveTmp& W, i
         }
         gscore[0] = t1 + t2;
       }
-      // group picks land in the upper half of ov/oi (topk_group <= 8)
-      wave_topk_radix<false, EPL>(gscore, r.n_group, r.topk_group, W.ov + 8, W.oi + 8, x,
-                                  nullptr, W.tv, W.ti, W.tx);
+      const Pick gp = wave_topk<EPL>(gscore, r.n_group, r.topk_group, x);
       uint64_t keep = 0;
-      for (int j = 0; j < r.topk_group; ++j) keep |= 1ull << W.oi[8 + j];
+      for (int j = 0; j < r.topk_group; ++j) keep |= 1ull << __builtin_amdgcn_readlane(gp.i, j);
 #pragma unroll
       for (int i = 0; i < EPL; ++i) {
         const int ei = lane + 64 * i;
         if (ei < e && !((keep >> (ei / gs)) & 1ull)) c[i] = 0.0f;
       }
     }
-    wave_topk_radix<true, EPL>(c, e, k, W.ov, W.oi, x, W.ox, W.tv, W.ti, W.tx);
+    const Pick pk = wave_topk<EPL>(c, e, k, x);
     float s = 0.0f;
-    for (int j = 0; j < k; ++j) s = s + W.ox[j];
+    for (int j = 0; j < k; ++j) s = s + lane_value(pk.x, j);
     if (lane < k) {
-      float w = W.ox[lane];
+      float w = pk.x;
       if (r.norm) w = w / s;
       wk = w * r.scale;
-      ik = W.oi[lane];
+      ik = pk.i;
     }
   }
   if (lane < k) {

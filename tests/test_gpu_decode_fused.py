@@ -96,6 +96,17 @@ def _fused_launches(layer, x):
     return kt.result
 
 
+# Group arrival counters of the two grid barriers: 2 x 32 lines of 128 bytes
+# after the 256-byte header and the 512 per-block flag lines.
+GROUP_OFFSET = 256 + 512 * 128
+SYNC_BYTES = GROUP_OFFSET + 2 * 32 * 128
+
+
+def _assert_group_counters_reset(ws):
+    grp = ws[GROUP_OFFSET:SYNC_BYTES].cpu().view(torch.int32).numpy()
+    assert not grp.any(), f"group arrival counters not reset: {np.nonzero(grp)}"
+
+
 CASES = {
     # hidden, experts, inter, top_k, bits, scoring, shared, shared_gate, n_group, topk_group, scale
     "qwen3-235b": (4096, 128, 1536, 8, 4, "softmax", False, False, 1, 1, 1.0),
@@ -146,6 +157,7 @@ def test_fused_qwen3_235b_vs_oracle_and_reuse_across_batches():
     assert header[0] == 0 and header[1] == 0, f"barrier counters not reset: {header}"
     assert header[2] == 4, f"launch epoch {header[2]} after 4 calls"
     assert header[3] == 0, "barrier timeout flagged"
+    _assert_group_counters_reset(ws)
 
 
 def test_fused_graph_replays_match_eager():
@@ -193,3 +205,4 @@ def test_fused_graph_replays_match_eager():
     assert K.workspace_error(ws) == 0
     header = ws[:16].cpu().view(torch.int32).numpy()
     assert header[0] == 0 and header[1] == 0, f"barrier counters not reset: {header}"
+    _assert_group_counters_reset(ws)
