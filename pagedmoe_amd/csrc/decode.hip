@@ -17,9 +17,6 @@
 #include "pmoe_kernels.h"
 #include "route_common.h"
 
-#include <map>
-#include <mutex>
-
 namespace pmoe {
 
 namespace {
@@ -186,11 +183,11 @@ constexpr int rows_r() {
   return r < 1 ? 1 : (r > 4 ? 4 : r);
 }
 
-// Every (unit bytes, lanes per row, units per lane) pick_shape returns for
-// rows of up to 8192 values.
+// Every (unit bytes, lanes per row, units per lane) pick_shape and
+// gateup_shape return for rows of up to 8192 values.
 #define PMOE_FOR_SHAPES_4(X)                                                     \
   X(32, 64, 1) X(32, 64, 2) X(16, 8, 1) X(16, 16, 1) X(16, 32, 1) X(16, 64, 1)   \
-  X(16, 64, 2) X(16, 64, 3) X(16, 64, 4) X(16, 8, 3) X(16, 16, 3) X(16, 32, 3)
+  X(16, 64, 2) X(16, 8, 3) X(16, 16, 3) X(16, 32, 3)
 #define PMOE_FOR_SHAPES_6(X) X(48, 64, 1) X(48, 64, 2) X(48, 8, 1) X(48, 16, 1) X(48, 32, 1)
 #define PMOE_FOR_SHAPES(BITS, X) \
   if constexpr (BITS == 4) {     \
@@ -281,28 +278,9 @@ int launch_routed(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, in
 
 }  // namespace
 
-// Waves the device holds at once at 3 waves per SIMD (cached per device).
-static int resident_waves() {
-  static std::mutex mu;
-  static std::map<int, int> cache;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  std::lock_guard<std::mutex> lk(mu);
-  auto it = cache.find(dev);
-  if (it != cache.end()) return it->second;
-  int cus = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    cus = 0;
-  return cache[dev] = cus * 4 * 3;
-}
-
-Shape gateup_shape(int bits, const GemvArgs& gu, int max_experts) {
-  const Shape whole = pick_shape(bits, gu.cols);
-  if (whole.ub != 32) return whole;
-  const int rows_per_block = 4 * (64 / whole.lpr) * (whole.gpl == 1 ? rows_r<32, 1, true>()
-                                                                    : rows_r<32, 2, true>());
-  const long waves = 4L * max_experts * ((gu.rows_out + rows_per_block - 1) / rows_per_block);
-  return waves > resident_waves() ? pick_shape(bits, gu.cols, true) : whole;
+Shape gateup_shape(int bits, const GemvArgs& gu, int) {
+  const Shape half = pick_shape(bits, gu.cols, true);
+  return half.ub == 16 && half.gpl > 2 ? pick_shape(bits, gu.cols) : half;
 }
 
 size_t decode_record_bytes() { return sizeof(RouteRecord); }

@@ -423,7 +423,7 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
 template <int UB, int GPL, bool DUAL>
 constexpr int fused_r(int cap) {
   constexpr int per_step = GPL * (Unit<UB>::kWords + 2) * (DUAL ? 2 : 1);
-  constexpr int budget = 170 - GPL * (Unit<UB>::kVals / 2 + 1);
+  constexpr int budget = 180 - GPL * (Unit<UB>::kVals / 2 + 1);
   int r = budget / per_step;
   return r < 1 ? 1 : (r > cap ? cap : r);
 }
@@ -457,7 +457,7 @@ Entry make_entry() {
 }
 
 // Supported (gate/up row shape, down row shape) pairs, from gateup_shape and
-// pick_shape (whole- or half-group gate/up units where both occur):
+// pick_shape:
 // 4-bit hidden 1024/inter 512, 4096/1536, 4096/2048, 7168/2048, 2048/512,
 // 2048/768; 6-bit 1024/512, 4096/1536, 7168/2048, 2048/512; experts up to
 // 512.  Other shapes use the three-launch path.
@@ -470,12 +470,9 @@ const std::map<Variant, Entry>& variants() {
   PMOE_FV(B, UG, LG, GG, UD, LD, GD, 2) PMOE_FV(B, UG, LG, GG, UD, LD, GD, 4)   \
   PMOE_FV(B, UG, LG, GG, UD, LD, GD, 8)
     PMOE_FV_E(4, 16, 32, 1, 16, 16, 1)
-    PMOE_FV_E(4, 32, 64, 1, 16, 16, 3)
-    PMOE_FV_E(4, 32, 64, 1, 16, 64, 1)
     PMOE_FV_E(4, 32, 64, 2, 16, 64, 1)
     PMOE_FV_E(4, 16, 64, 2, 16, 16, 3)
     PMOE_FV_E(4, 16, 64, 2, 16, 64, 1)
-    PMOE_FV_E(4, 16, 64, 4, 16, 64, 1)
     PMOE_FV_E(4, 16, 64, 1, 16, 16, 1)
     PMOE_FV_E(4, 16, 64, 1, 16, 8, 3)
     PMOE_FV_E(6, 48, 16, 1, 48, 8, 1)

@@ -101,7 +101,9 @@ template <int UB>
 struct GroupW {
   static constexpr int kWords = Unit<UB>::kWords;
   uint32_t w[kWords];
-  float s, b;
+  uint32_t sb;  // the group's bf16 scale (low half) and bias (high half)
+  __device__ __forceinline__ float s() const { return __uint_as_float(sb << 16); }
+  __device__ __forceinline__ float b() const { return __uint_as_float(sb & 0xFFFF0000u); }
 };
 
 // Unit u of a row: its packed words and its group's scale and bias.
@@ -123,8 +125,7 @@ __device__ __forceinline__ void load_group_w(const uint32_t* wrow, const uint16_
     q.w[4 * c + 3] = d.w;
   }
   const int g = u * Unit<UB>::kVals / 64;
-  q.s = bf16f(srow[g]);
-  q.b = bf16f(brow[g]);
+  q.sb = uint32_t(srow[g]) | (uint32_t(brow[g]) << 16);
 }
 
 // sum over the unit of x*(128+q)
@@ -254,11 +255,11 @@ __device__ __forceinline__ void gemv_rows(const GemvArgs& a,
 #pragma unroll
     for (int j = 0; j < GPL; ++j) {
       if (sub + LPR * j < units) {
-        p0 = group_term(group_dot<UB>(q.q0[st][j], act[j]), q.q0[st][j].s, q.q0[st][j].b,
+        p0 = group_term(group_dot<UB>(q.q0[st][j], act[j]), q.q0[st][j].s(), q.q0[st][j].b(),
                         act[j].sum, p0);
         if (DUAL) {
           const GroupW<UB>& w1 = q.q1[DUAL ? st : 0][DUAL ? j : 0];
-          p1 = group_term(group_dot<UB>(w1, act[j]), w1.s, w1.b, act[j].sum, p1);
+          p1 = group_term(group_dot<UB>(w1, act[j]), w1.s(), w1.b(), act[j].sum, p1);
         }
       }
     }
@@ -328,9 +329,10 @@ inline Shape pick_shape(int bits, int cols, bool half_groups = false) {
 }
 
 // Gate/up row shape of the decode launches (both decode paths use it, so
-// they stay bit-identical): whole-group units while the three-launch gate/up
-// grid (max_experts blocks per row tile) fits the device in one round of
-// resident waves, half-group units once it does not (decode.hip).
+// they stay bit-identical): half-group units (each load instruction a
+// contiguous 1 KB of the row) for rows of up to 2 units per lane, whole
+// groups above that, where 4 half-group units per lane exceed the register
+// budget (decode.hip).
 Shape gateup_shape(int bits, const GemvArgs& gu, int max_experts);
 
 }  // namespace pmoe

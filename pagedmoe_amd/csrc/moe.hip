@@ -224,12 +224,16 @@ int run_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* table, i
   return qgemv(a, g->bits, false, max_experts, max_rows_per_expert, st);
 }
 
-// PMOE_DECODE_FUSED=1 in the environment selects the one-launch decode
-// layer, 0 the three-launch one (read per call, so the paths can be
-// compared); the default is the three-launch decode.
-bool fused_enabled() {
+// Decode path for n tokens: the one-launch layer for a single token (where
+// it is the faster one), the three-launch decode for more.  The environment
+// can pin either: PMOE_DECODE_FUSED=1 selects the one-launch layer for every
+// decode batch it covers, 0 never (read per call, so the paths can be
+// compared).
+bool fused_enabled(int n) {
   const char* v = getenv("PMOE_DECODE_FUSED");
-  return v && v[0] == '1';
+  if (v && v[0] == '1') return true;
+  if (v && v[0] == '0') return false;
+  return n == 1;
 }
 
 // Decode block path: the fused one-launch layer (decode_fused.hip) when it
@@ -284,7 +288,7 @@ int decode_block(const pmoe_geom* g, const pmoe_route_cfg* rc, const uint8_t* sl
   dn.act_stride = g->inter;
   dn.act_by_token = 0;
   dn.out = nullptr;
-  if (fused_enabled()) {
+  if (fused_enabled(n)) {
     const int r2 = decode_fused(gu, dn, rt, g->bits, x, gate_w, extra, logit_bias, inds_out, w_out,
                                 out, w.sync, st);
     if (r2 != kDecodeFusedDeclined) return r2;
