@@ -169,6 +169,60 @@ down_routed_kernel(const GemvArgs a, const RouteDev rt, uint16_t* out, const Rou
   }
 }
 
+// Decode down projection, expert-split (many active experts): blockIdx.y =
+// u-th active expert of the routing record, blockIdx.x = tile of 4*R*RPW
+// output rows; the expert's rows go to y[r, o] (fp32), combined afterwards
+// by combine_y_kernel.  The tile-major down_routed_kernel gives each wave
+// every fourth active expert, a serial chain that is latency-bound once
+// dozens of experts are active; here every (expert, tile) is its own block.
+// Per-row arithmetic and combine order are those of down_routed_kernel, so
+// the results are bit-identical.
+template <int UB, int LPR, int GPL, int R, int EPL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PMOE_MIN_WAVES, 8))) void
+down_split_kernel(const GemvArgs a, const RouteDev rt, float* y, const RouteRecord* rec) {
+  constexpr int RPW = 64 / LPR;
+  __shared__ RouteLds L;
+  __shared__ int32_t s_rows[kRouteMaxRows];
+  __shared__ int s_m;
+  const int rows = rt.n * rt.kk;
+  load_route(rec, rows, rt.e + (rt.kk > rt.k ? 1 : 0), L);
+  const int u = blockIdx.y;
+  if (u >= L.n_active) return;
+  const int e = L.active[u];
+  if (threadIdx.x < 64) {
+    const int m = wave_rows_of(L, rows, e, s_rows);
+    if (threadIdx.x == 0) s_m = m;
+  }
+  const int slot = e < a.n_experts ? a.table[e] : a.shared_slot;
+  __syncthreads();
+  const int row0 = blockIdx.x * (4 * R * RPW);
+  if (slot < 0) {  // exact zero rows (streaming.py:715-719)
+    for (int i = threadIdx.x; i < s_m * 4 * R * RPW; i += 256) {
+      const int o = row0 + i % (4 * R * RPW);
+      if (o < a.rows_out) y[size_t(s_rows[i / (4 * R * RPW)]) * a.rows_out + o] = 0.0f;
+    }
+    return;
+  }
+  const int wrow0 = row0 + (threadIdx.x >> 6) * (R * RPW);
+  auto act_row = [&](int r) { return a.act + size_t(r) * a.act_stride; };
+  auto store = [&](int r, int, int o, float v) { y[size_t(r) * a.rows_out + o] = v; };
+  gemv_expert<UB, LPR, GPL, R, false>(a, slot, s_m, s_rows, wrow0, act_row, store);
+}
+
+// out[n, o] = sum_c w[n, c] * y[n*kk + c, o] in c order (fma chain from 0,
+// as down_routed_kernel's combine).
+__global__ __launch_bounds__(256) void combine_y_kernel(const float* __restrict__ y,
+                                                        const RouteRecord* __restrict__ rec,
+                                                        int kk, int d, uint16_t* __restrict__ out) {
+  const int n = blockIdx.y;
+  const int o = blockIdx.x * 256 + threadIdx.x;
+  if (o >= d) return;
+  float acc = 0.0f;
+  for (int c = 0; c < kk; ++c)
+    acc = __builtin_fmaf(rec->w[n * kk + c], y[size_t(n * kk + c) * d + o], acc);
+  out[size_t(n) * d + o] = f2bf(acc);
+}
+
 // Row steps per wave: as many as fit next to the activations in a
 // 3-waves-per-SIMD register budget (~150 VGPRs: GPL units of activation
 // pairs, ~30 for addresses and sums, ~8 per unit of unpacked pairs in flight
@@ -233,10 +287,25 @@ int launch_gateup_routed(const GemvArgs& gu, const RouteDev& rt, int max_experts
   return PMOE_OK;
 }
 
+#ifndef PMOE_DOWN_SPLIT_MIN
+#define PMOE_DOWN_SPLIT_MIN 17  // active-expert bound from which the down runs expert-split
+#endif
+
 template <int UB, int EPL, int L, int G>
-int launch_down_routed(const GemvArgs& dn, const RouteDev& rt, uint16_t* out,
+int launch_down_routed(const GemvArgs& dn, const RouteDev& rt, int max_experts, uint16_t* out,
                        const RouteRecord* rec, hipStream_t st) {
   constexpr int R = rows_r<UB, G, false>();
+  if (dn.out && max_experts >= PMOE_DOWN_SPLIT_MIN) {
+    constexpr int rows = 4 * R * (64 / L);
+    dim3 grid((dn.rows_out + rows - 1) / rows, max_experts);
+    float* y = static_cast<float*>(dn.out);
+    down_split_kernel<UB, L, G, R, EPL><<<grid, 256, 0, st>>>(dn, rt, y, rec);
+    PMOE_LAUNCH_CHECK("down_split_kernel");
+    dim3 cgrid((dn.rows_out + 255) / 256, rt.n);
+    combine_y_kernel<<<cgrid, 256, 0, st>>>(y, rec, rt.kk, dn.rows_out, out);
+    PMOE_LAUNCH_CHECK("combine_y_kernel");
+    return PMOE_OK;
+  }
   constexpr int T = R * (64 / L);
   const size_t lds = size_t(rt.n) * rt.kk * T * sizeof(float);
   if (lds > 48 * 1024) return fail(PMOE_EINVAL, "decode: too many rows per tile");
@@ -267,7 +336,7 @@ int launch_routed(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, in
     ProfScope prof_scope(K_DOWN, st);
 #define PMOE_CASE(U, L, G)                     \
   if (s2.ub == U && s2.lpr == L && s2.gpl == G) \
-    rc = launch_down_routed<U, EPL, L, G>(dn, rt, out, rec, st);
+    rc = launch_down_routed<U, EPL, L, G>(dn, rt, max_experts, out, rec, st);
     PMOE_FOR_SHAPES(BITS, PMOE_CASE)
 #undef PMOE_CASE
   }

@@ -295,6 +295,7 @@ int decode_block(const pmoe_geom* g, const pmoe_route_cfg* rc, const uint8_t* sl
   }
   r = router_logits_ext(x, gate_w, extra, logit_bias, n, g->hidden, e, w.logits, st);
   if (r) return r;
+  dn.out = w.y;  // fp32 per-slot outputs when the down runs expert-split
   return decode_routed(gu, dn, rt, g->bits, inds_out, w_out, out, w.record, st);
 }
 

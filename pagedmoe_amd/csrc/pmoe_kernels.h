@@ -65,7 +65,9 @@ int qgemv(const GemvArgs& a, int bits, bool dual, int max_experts, int max_rows_
           hipStream_t st);
 // Decode experts with routing recomputed per block (decode.hip).
 // record: scratch for the routing handed from gate/up to down
-// (decode_record_bytes()).
+// (decode_record_bytes()).  dn.out: fp32 [n*kk, hidden] scratch for the
+// expert-split down (many active experts), or null for the tile-major down
+// only.
 int decode_routed(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int bits,
                   int32_t* inds_out, float* w_out, uint16_t* out, void* record, hipStream_t st);
 size_t decode_record_bytes();
