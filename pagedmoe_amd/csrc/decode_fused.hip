@@ -60,6 +60,8 @@ namespace pmoe {
 namespace {
 
 constexpr int kFWaves = 8;
+constexpr int kXcds = 8;        // MI355X: blocks are dealt round robin over 8 XCDs
+constexpr int kRouterXcds = 4;  // XCDs whose blocks compute the router logits
 constexpr int kFThreads = 64 * kFWaves;
 constexpr int kFMaxLogits = 8 * 1025;  // n * (E + shared gate) staged in LDS
 constexpr uint64_t kSpinTicks = 50000000ull;  // 0.5 s at 100 MHz
@@ -236,12 +238,27 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
   const uint32_t epoch = __hip_atomic_load(&sy->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const uint32_t tag1 = 2u * epoch + 1u, tag2 = 2u * epoch + 2u;
 
-  // A: router logits
+  // A: router logits on the blocks of the first kRouterXcds XCDs (block b
+  // runs on XCD b % kXcds; a launch reaches the XCDs in turn, the last ~3 us
+  // after the first), one (token, expert) pair per block before a block's
+  // next wave takes one, so each CU streams only a few router rows.
   const int n_log = rt.e + (a.gate_extra ? 1 : 0);
   trace_mark(sy, 0);
-  for (int p = gw; p < n_log * rt.n; p += n_waves) {
-    const int t = p / n_log;
-    router_pair(a, rt, p - t * n_log, t);
+  {
+    const int n_pairs = n_log * rt.n;
+    const int xcd = blockIdx.x % kXcds;
+    auto on_xcd = [&](int x) { return (a.n_blocks - x + kXcds - 1) / kXcds; };
+    int n_rblocks = 0, rank = -1;
+    for (int x = 0; x < kRouterXcds; ++x) {
+      if (x == xcd) rank = n_rblocks + int(blockIdx.x) / kXcds;
+      n_rblocks += on_xcd(x);
+    }
+    if (rank >= 0) {
+      for (int p = rank + n_rblocks * wave; p < n_pairs; p += n_rblocks * kFWaves) {
+        const int t = p / n_log;
+        router_pair(a, rt, p - t * n_log, t);
+      }
+    }
   }
   trace_mark(sy, 1);
   grid_barrier(sy, 0, tag1, a.n_blocks);
