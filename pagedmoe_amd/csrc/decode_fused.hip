@@ -65,6 +65,9 @@ constexpr int kRouterXcds = 4;  // XCDs whose blocks compute the router logits
 constexpr int kFThreads = 64 * kFWaves;
 constexpr int kFMaxLogits = 8 * 1025;  // n * (E + shared gate) staged in LDS
 constexpr uint64_t kSpinTicks = 50000000ull;  // 0.5 s at 100 MHz
+#ifndef PMOE_GU_PIPE
+#define PMOE_GU_PIPE 1  // single-row gate/up items: two row steps in flight
+#endif
 #ifndef PMOE_POLL_SLEEP
 #define PMOE_POLL_SLEEP 2  // s_sleep units (64 clocks) between two flag polls
 #endif
@@ -349,6 +352,34 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
       int r = s_rows[wave][0];
       gemv_load_act<UG, LG, GG>(a.gu.act + size_t(r / rt.kk) * a.gu.act_stride, a.gu.cols, act);
       __builtin_amdgcn_sched_barrier(0);
+      if (PMOE_GU_PIPE && m == 1) {
+        // One activation row: the item's RG row steps go through a window of
+        // two steps in flight, each step computed as soon as its words land.
+        // (Issued all at once, a wave's loads come back in issue order but
+        // are served in any order, so nearly every wave would receive its
+        // last words at the end of the stream and do all its arithmetic
+        // after it.)  Lane sub keeps step sub's value; one store writes the
+        // item's RG * RPW bf16.
+        constexpr int RPW = 64 / LG;
+        GemvRegs<UG, LG, GG, 1, true> q[2];
+        gemv_load<UG, LG, GG, 1, true>(a.gu, slot, wrow0, q[0]);
+        gemv_load<UG, LG, GG, 1, true>(a.gu, slot, wrow0 + RPW, q[1]);
+        float hv = 0.0f;
+#pragma unroll
+        for (int st = 0; st < RG; ++st) {
+          __builtin_amdgcn_sched_barrier(0);
+          gemv_rows<UG, LG, GG, 1, true, Collect, true>(a.gu, q[st & 1], act, wrow0 + st * RPW,
+                                                        collect_fn(hv, g_sub - st));
+          __builtin_amdgcn_sched_barrier(0);
+          if (st + 2 < RG) gemv_load<UG, LG, GG, 1, true>(a.gu, slot, wrow0 + (st + 2) * RPW, q[st & 1]);
+          if (LAST && st == kHG - 1) prefetch_down(0);
+        }
+        const int o = wrow0 + g_sub * RPW + g_rsub;
+        if (g_sub < RG && o < a.gu.rows_out)
+          shared_store(&static_cast<uint16_t*>(a.gu.out)[size_t(r) * a.gu.out_stride + o], f2bf(hv));
+        if (LAST) prefetch_down(1);
+        return;
+      }
       GemvRegs<UG, LG, GG, kHG, true> qa, qb;
       gemv_load<UG, LG, GG, kHG, true>(a.gu, slot, wrow0, qa);
       gemv_load<UG, LG, GG, kHG, true>(a.gu, slot, wrow0 + kHG * (64 / LG), qb);

@@ -25,6 +25,9 @@
 #ifndef PMOE_MIN_WAVES
 #define PMOE_MIN_WAVES 3
 #endif
+#ifndef PMOE_AND_OR
+#define PMOE_AND_OR 1
+#endif
 
 namespace pmoe {
 
@@ -128,18 +131,44 @@ __device__ __forceinline__ void load_group_w(const uint32_t* wrow, const uint16_
   q.sb = uint32_t(srow[g]) | (uint32_t(brow[g]) << 16);
 }
 
+// (v & mask) | bias in one v_and_or_b32.  A VOP3 instruction takes no
+// literal operand on this target, so written plainly the compiler emits a
+// separate and + or pair (two VOP2 with literals); here the mask comes from an
+// SGPR and the OR constant from a VGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t bias) {
+#if PMOE_AND_OR
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(mask), "v"(bias));
+  return r;
+#else
+  return (v & mask) | bias;
+#endif
+}
+
+// bf16 (128+q) pairs (q_i, q_{i+4}) of the 4-bit word w: pair k holds the
+// nibbles at bits 4k and 16+4k
+template <int K>
+__device__ __forceinline__ uint32_t nib_pair(uint32_t w, uint32_t k43) {
+  return and_or(K ? w >> (4 * K) : w, 0x000F000Fu, k43);
+}
+
 // sum over the unit of x*(128+q)
 template <int UB>
 __device__ __forceinline__ float group_dot(const GroupW<UB>& q, const GroupAct<UB>& a) {
   float acc = 0.0f;
   if (Unit<UB>::kBits == 4) {
+    // the OR constant, held in a VGPR for and_or
+    uint32_t k43 = 0x43004300u;
+#if PMOE_AND_OR
+    asm volatile("" : "+v"(k43));
+#endif
 #pragma unroll
     for (int c = 0; c < Unit<UB>::kWords; ++c) {
       const uint32_t w = q.w[c];
-      acc = dot2(a.p[4 * c + 0], (w & 0x000F000Fu) | 0x43004300u, acc);
-      acc = dot2(a.p[4 * c + 1], ((w >> 4) & 0x000F000Fu) | 0x43004300u, acc);
-      acc = dot2(a.p[4 * c + 2], ((w >> 8) & 0x000F000Fu) | 0x43004300u, acc);
-      acc = dot2(a.p[4 * c + 3], ((w >> 12) & 0x000F000Fu) | 0x43004300u, acc);
+      acc = dot2(a.p[4 * c + 0], nib_pair<0>(w, k43), acc);
+      acc = dot2(a.p[4 * c + 1], nib_pair<1>(w, k43), acc);
+      acc = dot2(a.p[4 * c + 2], nib_pair<2>(w, k43), acc);
+      acc = dot2(a.p[4 * c + 3], nib_pair<3>(w, k43), acc);
     }
   } else {
 #pragma unroll
