@@ -64,7 +64,11 @@ constexpr int kXcds = 8;        // MI355X: blocks are dealt round robin over 8 X
 constexpr int kRouterXcds = 4;  // XCDs whose blocks compute the router logits
 constexpr int kFThreads = 64 * kFWaves;
 constexpr int kFMaxLogits = 8 * 1025;  // n * (E + shared gate) staged in LDS
+constexpr int kFMaxTable = 1024;       // slot-table entries copied to LDS
 constexpr uint64_t kSpinTicks = 50000000ull;  // 0.5 s at 100 MHz
+#ifndef PMOE_RANK1
+#define PMOE_RANK1 1  // single-token routing by rank counts over the block
+#endif
 #ifndef PMOE_GU_PIPE
 #define PMOE_GU_PIPE 1  // single-row gate/up items: two row steps in flight
 #endif
@@ -227,8 +231,10 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
   __shared__ RouteLds L;
   __shared__ WaveTmp W[kFWaves];
   __shared__ int32_t s_rows[kFWaves][kRouteMaxRows];
-  __shared__ float s_logit[kFMaxLogits];
+  __shared__ __align__(16) float s_logit[kFMaxLogits];
   __shared__ int32_t s_slot[kRouteMaxRows];  // slot of active expert u
+  __shared__ int32_t s_table[kFMaxTable];     // expert id -> slot, read at launch start
+  __shared__ Rank1Lds R1;
   extern __shared__ float s_y[];             // [rows][tile]
   const int wave = threadIdx.x >> 6;
   const int lane_in_wave = threadIdx.x & 63;
@@ -240,6 +246,12 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
   // initial flag value; consecutive launches differ)
   const uint32_t epoch = __hip_atomic_load(&sy->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const uint32_t tag1 = 2u * epoch + 1u, tag2 = 2u * epoch + 2u;
+
+  // the slot table comes in while the router runs (it is an input, not a
+  // result of this launch), so the slots of the picked experts are LDS reads
+  const bool table_lds = a.gu.n_experts <= kFMaxTable;
+  if (table_lds)
+    for (int i = threadIdx.x; i < a.gu.n_experts; i += kFThreads) s_table[i] = a.gu.table[i];
 
   // A: router logits on the blocks of the first kRouterXcds XCDs (block b
   // runs on XCD b % kXcds; a launch reaches the XCDs in turn, the last ~3 us
@@ -275,13 +287,18 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
   trace_mark(sy, 9);
   RouteDev rl = rt;
   rl.logits = s_logit;
-  route_block<EPL, kFWaves>(rl, L, W, blockIdx.x == 0 ? a.inds_out : nullptr, a.w_out);
+  static_assert(kFThreads >= 512, "route_rank1_select counts with 512 threads");
+  const bool rank1 = PMOE_RANK1 && rank1_route_ok(rl);
+  if (rank1)  // the weights follow before barrier 2 (route_rank1_weights)
+    route_rank1_select(rl, s_logit, L, R1);
+  else
+    route_block<EPL, kFWaves>(rl, L, W, blockIdx.x == 0 ? a.inds_out : nullptr, a.w_out);
   trace_mark(sy, 3);
   const int rows = rt.n * rt.kk;
   const int n_act = L.n_active;
   for (int u = threadIdx.x; u < n_act; u += kFThreads) {
     const int e = L.active[u];
-    s_slot[u] = e < a.gu.n_experts ? a.gu.table[e] : a.gu.shared_slot;
+    s_slot[u] = e < a.gu.n_experts ? (table_lds ? s_table[e] : a.gu.table[e]) : a.gu.shared_slot;
   }
   __syncthreads();
   trace_mark(sy, 10);
@@ -413,6 +430,7 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
     }
   }
   trace_mark(sy, 7);
+  if (rank1) route_rank1_weights(rl, s_logit, L, blockIdx.x == 0 ? a.inds_out : nullptr, a.w_out);
   trace_mark(sy, 4);
   grid_barrier(sy, 1, tag2, a.n_blocks, 12);
   trace_mark(sy, 5);

@@ -271,6 +271,96 @@ __device__ void route_block(const RouteDev& r, RouteLds& L, WaveTmp* W, int32_t*
   __syncthreads();
 }
 
+// Top-k selection of ONE token over at most 128 routed experts (softmax +
+// renorm scoring), logits in LDS, with a block of at least 512 threads.
+// Expert i is picked at rank #{j : K_j > K_i}, K = order_key << 32 | ~id
+// (ties to the lower id), counted by 4 lanes over 32 experts each; picks
+// come out in rank order -- the order of wave_topk (value descending, lower
+// id first).  Wave 0 lists the picks (L.ids), the active experts in
+// ascending id order (L.active, shared expert last) and their count; the
+// weights are left to route_rank1_weights, so the selection the weight
+// stream waits for is all that comes first.  Results are bit-identical to
+// route_block's.
+struct Rank1Lds {
+  uint64_t key[128];
+  int32_t rank[128];
+};
+
+__device__ __forceinline__ bool rank1_route_ok(const RouteDev& r) {
+  return r.scoring == PMOE_SCORE_SOFTMAX && r.norm && r.n == 1 && r.e <= 128 && r.k <= r.e &&
+         r.k <= kRouteMaxK;
+}
+
+__device__ __forceinline__ void route_rank1_select(const RouteDev& r, const float* lg,
+                                                   RouteLds& L, Rank1Lds& R) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int e = r.e, k = r.k;
+  if (tid < 128)
+    R.key[tid] = tid < e ? (uint64_t(order_key(lg[tid])) << 32) | uint32_t(~tid) : 0ull;
+  __syncthreads();
+  if (tid < 512) {
+    const int i = tid >> 2, q = tid & 3;  // expert i, quarter q of the comparisons
+    const uint64_t ki = R.key[i];
+    const ulonglong2* kv = reinterpret_cast<const ulonglong2*>(R.key + 32 * q);
+    int cnt = 0;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const ulonglong2 kj = kv[c];
+      cnt += kj.x > ki ? 1 : 0;
+      cnt += kj.y > ki ? 1 : 0;
+    }
+    cnt += __float_as_int(xor_lane<1>(__int_as_float(cnt)));
+    cnt += __float_as_int(xor_lane<2>(__int_as_float(cnt)));
+    if (q == 0) R.rank[i] = i < e ? cnt : 0x7fffffff;
+  }
+  __syncthreads();
+  if (tid < 64) {
+    const int r0 = R.rank[lane], r1 = R.rank[lane + 64];
+    const bool sel0 = r0 < k, sel1 = r1 < k;
+    if (sel0) L.ids[r0] = lane;
+    if (sel1) L.ids[r1] = lane + 64;
+    const uint64_t b0 = wave_ballot(sel0), b1 = wave_ballot(sel1);
+    const int n0 = __popcll(b0);
+    if (sel0) L.active[lanes_below(b0)] = lane;
+    if (sel1) L.active[n0 + lanes_below(b1)] = lane + 64;
+    if (lane == 0) {
+      const int n_act = n0 + __popcll(b1);
+      if (r.kk > k) {  // shared expert column: id e, listed last
+        L.ids[k] = e;
+        L.active[n_act] = e;
+      }
+      L.n_active = n_act + (r.kk > k ? 1 : 0);
+    }
+  }
+  __syncthreads();
+}
+
+// The combine weights of route_rank1_select's picks, by wave 0, exactly as
+// route_token computes them: w_j = exp(v_j - v_0) / sum over picks in pick
+// order (shared expert: 1, or sigmoid of its gate logit).
+__device__ __forceinline__ void route_rank1_weights(const RouteDev& r, const float* lg,
+                                                    RouteLds& L, int32_t* inds_out,
+                                                    float* w_out) {
+  const int lane = threadIdx.x & 63;
+  if (threadIdx.x >= 64) return;
+  const int k = r.k;
+  const int ik = lane < k ? L.ids[lane] : 0;
+  const float pv = lane < k ? lg[ik] : 0.0f;
+  const float m = lane_value(pv, 0);
+  const float ej = lane < k ? pexp(pv - m) : 0.0f;
+  float s = 0.0f;
+  for (int j = 0; j < k; ++j) s = s + lane_value(ej, j);
+  if (lane < k) {
+    const float wk = ej / s;
+    L.w[lane] = wk;
+    if (inds_out) {
+      inds_out[lane] = ik;
+      w_out[lane] = wk;
+    }
+  }
+  if (r.kk > k && lane == 0) L.w[k] = r.shared_gate ? psigmoid(lg[r.e]) : 1.0f;
+}
+
 // Routing record in global memory: what block (0, 0) of the gate/up launch
 // publishes for the down launch (same layout as the LDS copy).
 struct RouteRecord {
