@@ -81,8 +81,9 @@ __device__ __forceinline__ void load_group_act(const uint16_t* src, GroupAct<UB>
 #pragma unroll
   for (int c = 0; c < Unit<UB>::kVals / 8; ++c) {
     const uint4 d = load_act16<COHERENT>(v + c);
-    s += bf16lo(d.x) + bf16hi(d.x) + bf16lo(d.y) + bf16hi(d.y) + bf16lo(d.z) + bf16hi(d.z) +
-         bf16lo(d.w) + bf16hi(d.w);
+    // the unit's sum as dot products of the bf16 pairs with (1, 1)
+    constexpr uint32_t kOnes = 0x3F803F80u;
+    s = dot2(d.w, kOnes, dot2(d.z, kOnes, dot2(d.y, kOnes, dot2(d.x, kOnes, s))));
     if (Unit<UB>::kBits == 4) {
       // word c of the unit holds values 8c..8c+7; pair i is (x_{8c+i}, x_{8c+i+4})
       a.p[4 * c + 0] = __builtin_amdgcn_perm(d.z, d.x, 0x05040100u);
