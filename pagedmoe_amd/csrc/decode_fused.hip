@@ -65,6 +65,10 @@ constexpr int kRouterXcds = 4;  // XCDs whose blocks compute the router logits
 constexpr int kFThreads = 64 * kFWaves;
 constexpr int kFMaxLogits = 8 * 1025;  // n * (E + shared gate) staged in LDS
 constexpr int kFMaxTable = 1024;       // slot-table entries copied to LDS
+constexpr int kFMaxH = 20480;          // bf16 h values staged in LDS in phase D
+#ifndef PMOE_H_LDS
+#define PMOE_H_LDS 1
+#endif
 constexpr uint64_t kSpinTicks = 50000000ull;  // 0.5 s at 100 MHz
 #ifndef PMOE_RANK1
 #define PMOE_RANK1 1  // single-token routing by rank counts over the block
@@ -235,6 +239,7 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
   __shared__ int32_t s_slot[kRouteMaxRows];  // slot of active expert u
   __shared__ int32_t s_table[kFMaxTable];     // expert id -> slot, read at launch start
   __shared__ Rank1Lds R1;
+  __shared__ uint4 s_h[kFMaxH / 8];           // phase D: h of the routed rows
   extern __shared__ float s_y[];             // [rows][tile]
   const int wave = threadIdx.x >> 6;
   const int lane_in_wave = threadIdx.x & 63;
@@ -438,6 +443,18 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
   // D: down rows of the block's tile into LDS, then the fixed-order combine
   if (has_down) {
     const int n_sub = tile / kSub;
+    // h of every routed row comes in once per block (device scope, 16 bytes
+    // a thread) when it fits, instead of once per row group of every wave
+    const int hc = a.dn.cols / 8;  // 16-byte chunks per h row
+    const bool h_lds = PMOE_H_LDS && rows * a.dn.cols <= kFMaxH;
+    if (h_lds) {
+      for (int i = threadIdx.x; i < rows * hc; i += kFThreads) {
+        const int r = i / hc, c = i - r * hc;
+        s_h[i] = load_act16<kCoherentLoads>(
+            reinterpret_cast<const uint4*>(a.dn.act + size_t(r) * a.dn.act_stride) + c);
+      }
+      __syncthreads();
+    }
     for (int u = wave; u < n_act; u += kFWaves) {
       const int e = L.active[u];
       const int m = wave_rows_of(L, rows, e, s_rows[wave]);
@@ -458,8 +475,12 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
         GroupAct<UD> act[GD];
         for (int mi = 0; mi < m; ++mi) {
           const int r = s_rows[wave][mi];
-          gemv_load_act<UD, LD, GD, kCoherentLoads>(a.dn.act + size_t(r) * a.dn.act_stride,
-                                                      a.dn.cols, act);
+          if (h_lds)
+            gemv_load_act<UD, LD, GD>(reinterpret_cast<const uint16_t*>(s_h) + size_t(r) * a.dn.cols,
+                                      a.dn.cols, act);
+          else
+            gemv_load_act<UD, LD, GD, kCoherentLoads>(a.dn.act + size_t(r) * a.dn.act_stride,
+                                                        a.dn.cols, act);
           auto to_lds = [&](int, int o, float v) { s_y[r * tile + (o - row0)] = v; };
           gemv_rows<UD, LD, GD, kHD, false>(a.dn, qd1, act, wrow0, to_lds);
           if (RD > 1) gemv_rows<UD, LD, GD, kHD, false>(a.dn, qd2, act, wrow1, to_lds);
