@@ -158,10 +158,13 @@ template <int UB>
 __device__ __forceinline__ float group_dot(const GroupW<UB>& q, const GroupAct<UB>& a) {
   float acc = 0.0f;
   if (Unit<UB>::kBits == 4) {
-    // the OR constant, held in a VGPR for and_or
-    uint32_t k43 = 0x43004300u;
+    // the OR constant, held in a VGPR for and_or (a pure asm: one register
+    // shared by every unit)
+    uint32_t k43;
 #if PMOE_AND_OR
-    asm volatile("" : "+v"(k43));
+    asm("v_mov_b32 %0, 0x43004300" : "=v"(k43));
+#else
+    k43 = 0x43004300u;
 #endif
 #pragma unroll
     for (int c = 0; c < Unit<UB>::kWords; ++c) {
@@ -172,6 +175,12 @@ __device__ __forceinline__ float group_dot(const GroupW<UB>& q, const GroupAct<U
       acc = dot2(a.p[4 * c + 3], nib_pair<3>(w, k43), acc);
     }
   } else {
+    uint32_t k43;
+#if PMOE_AND_OR
+    asm("v_mov_b32 %0, 0x43004300" : "=v"(k43));
+#else
+    k43 = 0x43004300u;
+#endif
 #pragma unroll
     for (int p = 0; p < 32; ++p) {
       const int bit = 12 * p;
@@ -181,7 +190,9 @@ __device__ __forceinline__ float group_dot(const GroupW<UB>& q, const GroupAct<U
         f = q.w[wi] >> sh;
       else
         f = __builtin_amdgcn_alignbit(q.w[wi + 1], q.w[wi], sh);
-      const uint32_t pr = (f & 0x3Fu) | ((f << 10) & 0x003F0000u) | 0x43004300u;
+      // (f & 0x3F) | ((f << 10) & 0x3F0000) | 0x43004300 as two and_or (the
+      // inner result has bits 0-5 clear)
+      const uint32_t pr = and_or(f, 0x3Fu, and_or(f << 10, 0x003F0000u, k43));
       acc = dot2(a.p[p], pr, acc);
     }
   }
