@@ -113,6 +113,8 @@ CASES = {
     "deepseek-shapes": (7168, 64, 2048, 8, 4, "sigmoid", True, False, 8, 4, 2.5),
     "qwen3-next-6bit": (2048, 512, 512, 10, 6, "softmax", True, True, 1, 1, 1.0),
     "tiny": (1024, 32, 512, 4, 4, "softmax", False, False, 1, 1, 1.0),
+    # single-token rank routing with the shared-expert column and its gate
+    "tiny-shared-gate": (1024, 96, 512, 6, 4, "softmax", True, True, 1, 1, 1.0),
 }
 
 
@@ -206,3 +208,35 @@ def test_fused_graph_replays_match_eager():
     header = ws[:16].cpu().view(torch.int32).numpy()
     assert header[0] == 0 and header[1] == 0, f"barrier counters not reset: {header}"
     _assert_group_counters_reset(ws)
+
+
+@pytest.mark.parametrize("n", [1, 2])
+def test_fused_routing_exact_ties_lower_id_first(n):
+    """Pairs of identical router rows give exactly tied logits: the one-launch
+    routing (rank counts for one token, the wave top-k for more) must pick
+    and order them as the three-launch routing and the oracle do -- value
+    descending, lower expert id first."""
+    h, e, i, k = 1024, 64, 512, 8
+    print(f"[fused] exact ties n={n}", flush=True)
+    layer = _Layer(h, e, i, k, seed=33)
+    layer.gwb[1::2] = layer.gwb[0::2]  # expert 2j+1 duplicates expert 2j
+    layer.gate = bits_to_bf16_tensor(layer.gwb, DEV)
+    x = layer.x(n, seed=7)
+    a = _run_path(layer, x, fused=True)
+    b = _run_path(layer, x, fused=False)
+    assert torch.equal(a[1], b[1]), "routing indices differ"
+    assert torch.equal(a[2], b[2]), "routing weights differ"
+    assert torch.equal(a[0].view(torch.int16), b[0].view(torch.int16)), "outputs differ"
+    xb = x.cpu().view(torch.int16).numpy().view(np.uint16)
+    lg = O.router_logits(xb, layer.gwb)
+    ref_i, ref_w = O.softmax_topk(lg, k)
+    inds = a[1].cpu().numpy()
+    assert np.array_equal(inds, ref_i), f"{inds} vs oracle {ref_i}"
+    assert np.array_equal(a[2].cpu().numpy(), ref_w)
+    tied = lg[:, 0::2] == lg[:, 1::2]
+    assert tied.all(), "duplicated router rows must give exactly tied logits"
+    # every picked odd id sits right after its even twin
+    for row in inds:
+        for j, v in enumerate(row):
+            if v % 2 == 1:
+                assert j > 0 and row[j - 1] == v - 1, f"tie order broken: {row}"
