@@ -86,21 +86,28 @@ gateup_routed_kernel(const GemvArgs a, const RouteDev rt, int32_t* inds_out, flo
   __shared__ WaveTmp W[PRE ? 1 : 4];
   __shared__ int32_t s_rows[kRouteMaxRows];
   __shared__ int s_m;
+  const int u = blockIdx.y;
+  int e, slot;
   if (PRE) {
-    load_route(rec, rt.n * rt.kk, rt.e + (rt.kk > rt.k ? 1 : 0), L);
+    __shared__ RouteOne one;
+    load_route_one(rec, rt.n * rt.kk, u, L, one);
+    if (u >= one.n_active) return;
+    e = one.e;
+    slot = one.slot;
   } else {
     const bool publish = blockIdx.x == 0 && blockIdx.y == 0;
     route_block<EPL, 4>(rt, L, W, publish ? inds_out : nullptr, w_out);
-    if (publish) publish_route(L, rt.n * rt.kk, rt.e + (rt.kk > rt.k ? 1 : 0), rec);
+    if (publish)
+      publish_route(L, rt.n * rt.kk, rt.e + (rt.kk > rt.k ? 1 : 0), rec, a.table, a.n_experts,
+                    a.shared_slot);
+    if (u >= L.n_active) return;
+    e = L.active[u];
+    slot = e < a.n_experts ? a.table[e] : a.shared_slot;
   }
-  const int u = blockIdx.y;
-  if (u >= L.n_active) return;
-  const int e = L.active[u];
   if (threadIdx.x < 64) {
     const int m = wave_rows_of(L, rt.n * rt.kk, e, s_rows);
     if (threadIdx.x == 0) s_m = m;
   }
-  const int slot = e < a.n_experts ? a.table[e] : a.shared_slot;
   __syncthreads();
   const int row0 = blockIdx.x * (4 * R * RPW);
   if (slot < 0) {
@@ -119,11 +126,14 @@ gateup_routed_kernel(const GemvArgs a, const RouteDev rt, int32_t* inds_out, flo
 // to the record and the routing outputs.
 template <int EPL>
 __global__ __launch_bounds__(1024) void route_record_kernel(const RouteDev rt, int32_t* inds_out,
-                                                             float* w_out, RouteRecord* rec) {
+                                                             float* w_out, RouteRecord* rec,
+                                                             const int32_t* table, int n_experts,
+                                                             int shared_slot) {
   __shared__ RouteLds L;
   __shared__ WaveTmp W[16];
   route_block<EPL, 16>(rt, L, W, inds_out, w_out);
-  publish_route(L, rt.n * rt.kk, rt.e + (rt.kk > rt.k ? 1 : 0), rec);
+  publish_route(L, rt.n * rt.kk, rt.e + (rt.kk > rt.k ? 1 : 0), rec, table, n_experts,
+                shared_slot);
 }
 
 // Decode down projection + weighted combine, routing recomputed in the
@@ -184,16 +194,17 @@ down_split_kernel(const GemvArgs a, const RouteDev rt, float* y, const RouteReco
   __shared__ RouteLds L;
   __shared__ int32_t s_rows[kRouteMaxRows];
   __shared__ int s_m;
+  __shared__ RouteOne one;
   const int rows = rt.n * rt.kk;
-  load_route(rec, rows, rt.e + (rt.kk > rt.k ? 1 : 0), L);
   const int u = blockIdx.y;
-  if (u >= L.n_active) return;
-  const int e = L.active[u];
+  load_route_one(rec, rows, u, L, one);
+  if (u >= one.n_active) return;
+  const int e = one.e;
   if (threadIdx.x < 64) {
     const int m = wave_rows_of(L, rows, e, s_rows);
     if (threadIdx.x == 0) s_m = m;
   }
-  const int slot = e < a.n_experts ? a.table[e] : a.shared_slot;
+  const int slot = one.slot;
   __syncthreads();
   const int row0 = blockIdx.x * (4 * R * RPW);
   if (slot < 0) {  // exact zero rows (streaming.py:715-719)
@@ -277,7 +288,8 @@ int launch_gateup_routed(const GemvArgs& gu, const RouteDev& rt, int max_experts
   } else {
     {
       ProfScope prof_scope(K_ROUTE_SELECT, st);
-      route_record_kernel<EPL><<<1, 1024, 0, st>>>(rt, inds_out, w_out, rec);
+      route_record_kernel<EPL><<<1, 1024, 0, st>>>(rt, inds_out, w_out, rec, gu.table,
+                                                   gu.n_experts, gu.shared_slot);
       PMOE_LAUNCH_CHECK("route_record_kernel");
     }
     gateup_routed_kernel<UB, L, G, R, EPL, true><<<grid, 256, 0, st>>>(gu, rt, inds_out, w_out,

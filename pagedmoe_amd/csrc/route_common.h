@@ -363,21 +363,49 @@ __device__ __forceinline__ void route_rank1_weights(const RouteDev& r, const flo
 
 // Routing record in global memory: what block (0, 0) of the gate/up launch
 // publishes for the down launch (same layout as the LDS copy).
+// It also holds the slab slot of every active expert (slot[u] for
+// active[u]), so a per-expert block of the later launches finds its weights
+// without a dependent slot-table read.
 struct RouteRecord {
   int32_t ids[kRouteMaxRows];
   float w[kRouteMaxRows];
   int32_t active[kRouteMaxIds];
+  int32_t slot[kRouteMaxIds];
   int32_t n_active;
 };
 
+// table: expert id -> slot (-1: absent); id n_experts is the shared expert.
 __device__ __forceinline__ void publish_route(const RouteLds& L, int rows, int n_ids,
-                                              RouteRecord* g) {
+                                              RouteRecord* g, const int32_t* table,
+                                              int n_experts, int shared_slot) {
   for (int i = threadIdx.x; i < rows; i += blockDim.x) {
     g->ids[i] = L.ids[i];
     g->w[i] = L.w[i];
   }
   for (int i = threadIdx.x; i < n_ids; i += blockDim.x) g->active[i] = L.active[i];
+  for (int u = threadIdx.x; u < L.n_active; u += blockDim.x) {
+    const int e = L.active[u];
+    g->slot[u] = e < n_experts ? table[e] : shared_slot;
+  }
   if (threadIdx.x == 0) g->n_active = L.n_active;
+}
+
+// What a block working on the u-th active expert needs from the record, in
+// one round of independent loads: the flat rows' ids (for wave_rows_of), the
+// expert's id and slot, and the active count.  Ends with a block barrier.
+struct RouteOne {
+  int n_active, e, slot;
+};
+
+__device__ __forceinline__ void load_route_one(const RouteRecord* g, int rows, int u,
+                                               RouteLds& L, RouteOne& o) {
+  for (int i = threadIdx.x; i < rows; i += blockDim.x) L.ids[i] = g->ids[i];
+  if (threadIdx.x == 0) {
+    o.n_active = g->n_active;
+    o.e = g->active[u];
+    o.slot = g->slot[u];
+  }
+  __syncthreads();
 }
 
 __device__ __forceinline__ void load_route(const RouteRecord* g, int rows, int n_ids, RouteLds& L) {
