@@ -118,11 +118,16 @@ __device__ __forceinline__ void load_group_w(const uint32_t* wrow, const uint16_
   const u32x4* v = reinterpret_cast<const u32x4*>(wrow + size_t(u) * kWords);
 #pragma unroll
   for (int c = 0; c < kWords / 4; ++c) {
-#if PMOE_NT_LOADS
-    const u32x4 d = __builtin_nontemporal_load(v + c);
-#else
-    const u32x4 d = v[c];
-#endif
+    // Non-temporal only for 16-byte units, where one load instruction covers
+    // whole contiguous lines of the row.  With 32- or 48-byte units two or
+    // three instructions share each line, and a normal load keeps the line
+    // in L2 for the next one (6-bit Qwen3-Next-shaped verify step: 119 ->
+    // 108 us).
+    u32x4 d;
+    if (PMOE_NT_LOADS && UB == 16)
+      d = __builtin_nontemporal_load(v + c);
+    else
+      d = v[c];
     q.w[4 * c + 0] = d.x;
     q.w[4 * c + 1] = d.y;
     q.w[4 * c + 2] = d.z;
