@@ -28,7 +28,7 @@ SLAB_RESERVE_FRAC = 0.1   # slots held back from the resident budget
 LFRU = True               # second-chance eviction for reused experts
 LFRU_SCAN = 8             # entries scanned per eviction
 STITCH = True             # pin every expert in a fixed slot when the slab holds them all
-COPY_SPLIT_BYTES = 4 << 20  # H2D copy piece size
+COPY_SPLIT_BYTES = 64 << 20  # H2D copy piece size (an expert of up to 64 MiB is one copy)
 COPY_STREAMS = 2          # copy streams of the engine
 
 
@@ -38,7 +38,7 @@ def sync_from_environ() -> None:
     LFRU = _env("LFRU", True, _bool)
     LFRU_SCAN = _env("LFRU_SCAN", 8, int)
     STITCH = _env("STITCH", True, _bool)
-    COPY_SPLIT_BYTES = _env("COPY_SPLIT_KB", 4096, int) * 1024
+    COPY_SPLIT_BYTES = _env("COPY_SPLIT_KB", 65536, int) * 1024
     COPY_STREAMS = _env("COPY_STREAMS", 2, int)
 
 

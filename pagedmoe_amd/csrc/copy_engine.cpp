@@ -24,7 +24,7 @@ struct pmoe_copy_engine {
     const void* src;
     size_t bytes;
   };
-  size_t split = 4u << 20;
+  size_t split = size_t(64) << 20;  // whole experts: larger pieces copy faster
   std::vector<hipStream_t> streams;
   std::vector<hipEvent_t> done;
   hipEvent_t start = nullptr;
