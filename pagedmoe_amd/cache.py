@@ -37,6 +37,31 @@ class HostExpertStore:
         buf = (ctypes.c_uint8 * self.nbytes).from_address(self._ptr.value)
         self.bytes = np.frombuffer(buf, dtype=np.uint8)
 
+    @classmethod
+    def from_checkpoint(cls, model_dir, layers=None, group: int = 64) -> "HostExpertStore":
+        """A store holding every expert of the MoE layers of a quantized
+        safetensors checkpoint (stacked or per-expert layout), read straight
+        from the files into slot layout (checkpoint.py).  ``layers`` keeps
+        only those layer numbers; ``layer_numbers`` lists the store's layers
+        in order."""
+        from . import checkpoint as ck
+        from ._lib import geom
+
+        index = ck.read_headers(model_dir)
+        found = ck.find_moe_layers(index)
+        if layers is not None:
+            keep = set(int(n) for n in layers)
+            found = [f for f in found if f[0] in keep]
+        if not found:
+            raise PmoeError(f"{model_dir}: no quantized MoE expert tensors found")
+        layouts = [ck.layer_layout(path, index) for _, path in found]
+        hidden, inter, bits = layouts[0].geometry(group)
+        g = geom(hidden, inter, bits, group)
+        store = cls(g, len(layouts), layouts[0].n_experts)
+        ck.fill_host_store(store, layouts, g)
+        store.layer_numbers = [n for n, _ in found]
+        return store
+
     @property
     def address(self) -> int:
         return self._ptr.value

@@ -296,9 +296,13 @@ def _resolve_parent(model, path: str):
     return obj, parts[-1]
 
 
-def build_cache_for(model: nn.Module, slots: int, **kw) -> ExpertCache:
+def build_cache_for(model: nn.Module, slots: int, model_path=None, **kw) -> ExpertCache:
     """An ExpertCache (with a pinned host store holding every expert of every
-    QuantizedSwitchGLU of ``model``) for patch_model."""
+    QuantizedSwitchGLU of ``model``) for patch_model.  With ``model_path``
+    the store is read from that quantized safetensors checkpoint (its MoE
+    layers in layer order, one per module; checkpoint.py) instead of from the
+    modules' own slabs -- the reference pages experts from the checkpoint
+    files (safetensors_index.py)."""
     from .cache import HostExpertStore
 
     glus = find_switch_glus(model)
@@ -307,13 +311,25 @@ def build_cache_for(model: nn.Module, slots: int, **kw) -> ExpertCache:
     first = glus[0][1]
     n_shared = first.n_shared
     g = first.geom
-    store = HostExpertStore(g, len(glus), first.n_experts)
-    for li, (_, m) in enumerate(glus):
+    for _, m in glus:
         if (m.hidden, m.inter, m.bits, m.n_experts, m.n_shared) != (
                 first.hidden, first.inter, first.bits, first.n_experts, n_shared):
             raise ValueError("all MoE layers must share one expert shape")
-        for e in range(m.n_experts):
-            store.write_from_slot(li, e, m.slab, e)
+    if model_path is not None:
+        store = HostExpertStore.from_checkpoint(model_path)
+        sg = store.geom
+        if (store.n_layers, store.n_experts, sg.hidden, sg.inter, sg.bits) != (
+                len(glus), first.n_experts, first.hidden, first.inter, first.bits):
+            store.close()
+            raise ValueError(f"{model_path}: {store.n_layers} MoE layers of {store.n_experts} "
+                             f"experts ({sg.hidden}/{sg.inter}/{sg.bits}-bit) do not match the "
+                             f"model's {len(glus)} layers of {first.n_experts} "
+                             f"({first.hidden}/{first.inter}/{first.bits}-bit)")
+    else:
+        store = HostExpertStore(g, len(glus), first.n_experts)
+        for li, (_, m) in enumerate(glus):
+            for e in range(m.n_experts):
+                store.write_from_slot(li, e, m.slab, e)
     cache = ExpertCache(g, slots, [p for p, _ in glus], first.n_experts, host_store=store,
                         n_shared=n_shared, **kw)
     for li, (p, m) in enumerate(glus):

@@ -315,3 +315,45 @@ def test_combine_entry_point_vs_oracle(shared, gate):
     ref32 = O.combine_f32(yf, w, None if sy is None else O.bf16_to_f32(sy),
                           None if sl is None else O.psigmoid(sl))
     assert np.array_equal(got.cpu().view(torch.int16).numpy().view(np.uint16), ref32)
+
+
+def test_paged_block_reads_experts_from_a_safetensors_checkpoint(tmp_path):
+    """Experts paged from a quantized safetensors checkpoint
+    (build_cache_for(model_path=...) -> HostExpertStore.from_checkpoint):
+    the modules' own slabs are zeroed first, so every routed expert the
+    layers use comes from the files; routing bit-exact and outputs within
+    tolerance of the float64 oracle."""
+    from safetensors.torch import save_file
+
+    _, S = _mods()
+    spec = O.LayerSpec(1024, 32, 512, 4)
+    model, ol = _softmax_model(spec, 2, seed=90)
+    tensors = {}
+    for li, (_, experts, _, _) in enumerate(ol):
+        for proj in ("gate", "up", "down"):
+            qts = [getattr(experts[e], proj) for e in range(spec.experts)]
+            pre = f"model.layers.{li}.mlp.switch_mlp.{proj}_proj"
+            tensors[pre + ".weight"] = torch.from_numpy(
+                np.stack([q.weight for q in qts]).astype(np.uint32).view(np.int32))
+            for comp in ("scales", "biases"):
+                a = np.stack([getattr(q, comp) for q in qts]).view(np.int16)
+                tensors[f"{pre}.{comp}"] = torch.from_numpy(a).view(torch.bfloat16)
+    save_file(tensors, str(tmp_path / "model.safetensors"))
+    for _, m in S.find_switch_glus(model):
+        m.slab.buf.zero_()
+    cache = S.build_cache_for(model, slots=16, model_path=tmp_path)
+    S.patch_model(model, cache)
+    rng = np.random.default_rng(91)
+    print("[checkpoint] paged block from safetensors", flush=True)
+    for step in range(2):
+        for li, layer in enumerate(model.layers):
+            xb = O.bf16_round(rng.standard_normal((2, spec.hidden), dtype=np.float32))
+            out = layer.mlp(bits_to_bf16_tensor(xb, DEV))
+            gw, experts, _, _ = ol[li]
+            ref_i, ref_w, _, ref = O.moe_layer_f64(spec, xb, gw, experts)
+            gi, gwt = layer.mlp.last_routing
+            assert np.array_equal(gi.cpu().numpy(), ref_i)
+            assert np.array_equal(gwt.cpu().numpy(), ref_w)
+            check_close(out.float().cpu().numpy(), ref, f"checkpoint paging step {step} layer {li}")
+    assert cache.stats()["misses"] > 0
+    cache.close()
