@@ -245,7 +245,11 @@ constexpr int rows_r() {
       150 - 30 - GPL * (Unit<UB>::kVals / 2 + 1) - (GPL >= 3 ? 8 * GPL : 0);
   constexpr int r = budget / per_step;
   if (PMOE_FORCE_R > 0) return PMOE_FORCE_R;
-  return r < 1 ? 1 : (r > 4 ? 4 : r);
+  // 6-bit (48-byte) units: at most 2 steps -- each unit is three loads, and
+  // more, smaller blocks stream better (Qwen3-Next-shaped verify step: R 1 /
+  // 2 / 3 / register-sized = 108 / 102 / 106 / 107 us)
+  constexpr int cap = UB == 48 ? 2 : 4;
+  return r < 1 ? 1 : (r > cap ? cap : r);
 }
 
 // Every (unit bytes, lanes per row, units per lane) pick_shape and
