@@ -240,3 +240,20 @@ def test_fused_routing_exact_ties_lower_id_first(n):
         for j, v in enumerate(row):
             if v % 2 == 1:
                 assert j > 0 and row[j - 1] == v - 1, f"tie order broken: {row}"
+
+
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("n", [1, 3, 8])
+def test_routing_512_experts_vs_oracle(n, fused):
+    """Top-10 of 512 softmax-renormalised experts (eight logits per lane in
+    the wave top-k) against the oracle: indices and weights bit-exact, on
+    both decode paths."""
+    h, e, i, k = 1024, 512, 512, 10
+    print(f"[fused] 512-expert routing n={n} fused={fused}", flush=True)
+    layer = _Layer(h, e, i, k, seed=44)
+    x = layer.x(n, seed=900 + n)
+    _, inds, wts = _run_path(layer, x, fused=fused)
+    xb = x.cpu().view(torch.int16).numpy().view(np.uint16)
+    ref_i, ref_w = O.softmax_topk(O.router_logits(xb, layer.gwb), k)
+    assert np.array_equal(inds.cpu().numpy(), ref_i)
+    assert np.array_equal(wts.cpu().numpy(), ref_w)
