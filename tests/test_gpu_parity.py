@@ -28,7 +28,8 @@ def _x_bits(rng, n, d):
 
 
 @pytest.mark.parametrize("n,d,e", [(64, 1024, 32), (1, 4096, 128), (8, 4096, 128),
-                                   (200, 4096, 128), (3, 7168, 384), (8, 2048, 512)])
+                                   (200, 4096, 128), (3, 7168, 384), (8, 2048, 512),
+                                   (517, 4096, 128), (1000, 2048, 513)])
 def test_router_logits_bit_exact(n, d, e):
     K = _k()
     rng = np.random.default_rng(n * 7 + e)
