@@ -154,9 +154,25 @@ size_t pmoe_moe_workspace(const pmoe_geom* g, int n, int k, int shared,
 int pmoe_moe_workspace_init(void* ws, size_t ws_bytes, void* stream);
 
 /* Synchronising read of the header's sticky error word into *error: bit 0 =
- * a grid barrier wait of the one-launch decode gave up after 0.5 s (results
- * of that call are invalid).  Zeroed only by pmoe_moe_workspace_init. */
+ * a grid barrier wait of the one-launch decode gave up after its spin limit
+ * (0.5 s by default); the layer output of that call, and of every later call
+ * on the workspace until it is re-initialised, is NaN.  Zeroed only by
+ * pmoe_moe_workspace_init. */
 int pmoe_moe_workspace_status(const void* ws, uint32_t* error, void* stream);
+
+/* Enqueue on stream a copy of the workspace's error word into host_dst
+ * (pinned host memory) without waiting: a caller that synchronises the
+ * stream anyway (to read routed ids) reads it after that sync at no extra
+ * cost.  No reference counterpart (the reference's mlx graph has no grid
+ * barrier that can time out). */
+int pmoe_moe_workspace_error_async(const void* ws, uint32_t* host_dst, void* stream);
+
+/* Debug: the one-launch decode's grid-barrier poll limit in 100 MHz
+ * realtime-clock ticks (0 restores the default, 0.5 s).  A tiny limit makes
+ * every wait give up at once, so tests can check that a timeout poisons the
+ * layer output with NaN and sets error bit 0 while every block still exits
+ * normally.  Applies to launches issued after the call. */
+int pmoe_set_barrier_spin(uint64_t ticks);
 
 /* The seam: y[n, k, :] = FFN_{inds[n,k]}(x[n, :]) as bf16 [n, k, hidden],
  * uncombined, in (token, k) order.  Expert e lives in slab slot table[e]
@@ -212,6 +228,12 @@ typedef struct pmoe_slab pmoe_slab;
 typedef struct {
   int64_t hits, misses, evictions, starved, installs, resident, slots,
       budget, reserve, stitched, bytes_copied;
+  /* prefill fetch groups: misses read into free slots (cache.py:2394-2401
+   * prefill_slot_reads), of those installed as resident, misses read into
+   * the stage (stage_reads, :1392-1425), misses with neither
+   * (prefill_slot_starved + stage_starved), and the stage's size */
+  int64_t prefill_slot_reads, prefill_installs, stage_reads, prefill_starved,
+      stage_slots;
 } pmoe_slab_stats;
 
 /* Slot policy + device table [n_layers, n_experts] int32 (-1 = absent).
@@ -242,6 +264,55 @@ int pmoe_slab_stitch(pmoe_slab* s);
  * table. */
 int pmoe_slab_publish(pmoe_slab* s, int layer, void* stream);
 
+/* Republish layer's row only if its host copy changed since the last upload
+ * (an install, an eviction by any layer's fetch, a prefill group's slots
+ * coming back).  Returns 1 if it enqueued an upload, 0 if the row was
+ * current, <0 on error.  Replaces flow_table's dirty-row upload
+ * (cache.py:843-859, _flow_mark :821-831). */
+int pmoe_slab_sync_table(pmoe_slab* s, int layer, void* stream);
+
+/* 1 if layer's device row is stale, 0 if current, <0 on error. */
+int pmoe_slab_dirty(pmoe_slab* s, int layer);
+
+/* Inspection: wait for the device, then copy layer's device row (what the
+ * kernels read) into out (n_experts int32).  The reference's flow table is
+ * an mx.array its caller can read the same way (cache.py:843-859). */
+int pmoe_slab_read_device_row(pmoe_slab* s, int layer, int32_t* out);
+
+/* Register slab slots [first_slot, first_slot + n_slots) (past the routed
+ * slots) as the prefill stage: slots prefill misses are read into when no
+ * free slot is left, never resident, handed back after each group.
+ * Replaces ensure_stage / the stage SlabStore (cache.py:1345-1390). */
+int pmoe_slab_set_stage(pmoe_slab* s, int first_slot, int n_slots);
+
+/* Free routed slots, free stage slots, and resident entries the budget
+ * still has room for (each may be NULL). */
+int pmoe_slab_capacity(pmoe_slab* s, int* free_slots, int* stage_free,
+                       int* budget_room);
+
+/* One prefill fetch group's policy step (_begin with prefill=True,
+ * PREFILL_TOUCH=0, PREFILL_SLAB=1, cache.py:2347-2453, then
+ * _install(..., "soft") :2306-2312): hits keep their recency and frequency;
+ * misses, in ascending id, take a free routed slot (never an eviction) and
+ * are installed as resident while the resident count is under the budget,
+ * else held by this group only; misses past the free slots take stage slots;
+ * misses past both are counted in *n_unplaced and get no slot.  The placed
+ * misses go to miss_ids/miss_slots (capacity n_ids), their count to *n_miss.
+ * *ticket names the group's held slots until pmoe_slab_prefill_done. */
+int pmoe_slab_prefill_request(pmoe_slab* s, int layer, const int32_t* ids,
+                              int n_ids, int32_t* miss_ids, int32_t* miss_slots,
+                              int* n_miss, int* n_unplaced, int* ticket);
+
+/* Enqueue the upload of the group's compute row: the layer's resident
+ * entries plus the slots the group holds. */
+int pmoe_slab_prefill_publish(pmoe_slab* s, int ticket, void* stream);
+
+/* The group's compute is enqueued: its held free-list and stage slots go
+ * back (_release_slot :1101-1116, _stage_return :1427-1440) and the layer's
+ * row is marked dirty.  Copies into those slots must be ordered after that
+ * compute by a fence (pmoe_copy_fence). */
+int pmoe_slab_prefill_done(pmoe_slab* s, int ticket);
+
 int pmoe_slab_stats_get(pmoe_slab* s, pmoe_slab_stats* out);
 
 /* ---- copy engine (replaces the native pread pool, _native_read.c:38-698:
@@ -265,8 +336,22 @@ int pmoe_copy_submit(pmoe_copy_engine* ce, void* dst, const void* src,
                      size_t bytes, int urgent);
 
 /* Issue every queued job (urgent first) and make stream wait for all of
- * them (event wait, no host block). */
+ * them (event wait, no host block); the copies first wait for everything
+ * already queued on stream.  Equals fence(stream) + issue + join(stream). */
 int pmoe_copy_flush(pmoe_copy_engine* ce, void* stream);
+
+/* Record the engine's fence on stream: copies issued after this wait for
+ * everything queued on stream up to here (a slot is never overwritten while
+ * a kernel queued before the fence may read it). */
+int pmoe_copy_fence(pmoe_copy_engine* ce, void* stream);
+
+/* Issue every queued job behind the latest fence, without making any
+ * stream wait for them (prefill group i+1's reads run under group i's
+ * compute, cache.py:2535-2578). */
+int pmoe_copy_issue(pmoe_copy_engine* ce);
+
+/* Make stream wait for every copy issued so far. */
+int pmoe_copy_join(pmoe_copy_engine* ce, void* stream);
 
 /* Block until every issued copy has finished; returns the first error. */
 int pmoe_copy_sync(pmoe_copy_engine* ce);
@@ -282,6 +367,36 @@ int64_t pmoe_copy_bytes(pmoe_copy_engine* ce);
 int pmoe_slab_fetch(pmoe_slab* s, pmoe_copy_engine* ce, const pmoe_geom* g,
                     void* slab, const void* host_store, int layer,
                     const int32_t* ids, int n_ids, int* n_miss, void* stream);
+
+/* One prefill fetch group through slab + engine: pmoe_slab_prefill_request,
+ * then each placed miss queued from the host store and issued behind the
+ * engine's latest fence (pmoe_copy_issue).  Nothing waits for the copies:
+ * before the group computes, the caller publishes its row
+ * (pmoe_slab_prefill_publish) and joins the copies (pmoe_copy_join).
+ * Replaces fetch_groups' per-group _begin(prefill=True) (cache.py:2535-2578). */
+int pmoe_slab_fetch_prefill(pmoe_slab* s, pmoe_copy_engine* ce,
+                            const pmoe_geom* g, void* slab,
+                            const void* host_store, int layer,
+                            const int32_t* ids, int n_ids, int* n_miss,
+                            int* n_unplaced, int* ticket);
+
+/* ---- measurement probes ---------------------------------------------------
+ * No reference counterpart.  Kernels of known HBM traffic that bench.py runs
+ * next to the kernels it measures: a streaming read with the expert
+ * stream's access pattern (16-byte non-temporal loads, 1 KB per wave
+ * instruction; the read ceiling), and a 16-byte copy (counter calibration:
+ * its FETCH_SIZE / WRITE_SIZE against the bytes it moves). */
+
+/* Bytes of the per-thread sink pmoe_probe_read writes (0 without a device). */
+size_t pmoe_probe_sink_bytes(void);
+
+/* Read `bytes` (a multiple of 16, 16-byte aligned) from src; sink receives
+ * one xor word per thread. */
+int pmoe_probe_read(const void* src, size_t bytes, void* sink, size_t sink_bytes,
+                    void* stream);
+
+/* Copy `bytes` (a multiple of 16, both 16-byte aligned) from src to dst. */
+int pmoe_probe_copy(void* dst, const void* src, size_t bytes, void* stream);
 
 /* ---- kernel timing --------------------------------------------------------
  * No reference counterpart (the reference splits a token's wall time with

@@ -583,6 +583,62 @@ class SlotPolicy:
             self._trim()
         return hits, placed
 
+    # ---- prefill fetch groups (cache.py:2347-2453 with prefill=True,
+    # PREFILL_TOUCH=0, PREFILL_SLAB=1; _install(..., "soft") :2306-2312;
+    # the stage of ensure_stage :1345-1390, _stage_return :1427-1440)
+
+    def set_stage(self, first_slot: int, n_slots: int) -> None:
+        self.stage_free = list(range(first_slot + n_slots - 1, first_slot - 1, -1))
+        self.groups = {}
+
+    def step_prefill(self, layer, ids):
+        """One prefill group.  Hits: counted, recency/frequency untouched.
+        Misses (ascending id): a free slot (never an eviction), installed at
+        MRU with no reuse credit while fewer than ``budget`` entries are
+        resident, else held for the group; past the free list, a stage slot;
+        past both, unplaced.  Returns (ticket, [(miss id, slot)], unplaced)."""
+        if not hasattr(self, "stage_free"):
+            self.set_stage(self.slots, 0)
+        ticket = next(t for t in range(64) if t not in self.groups)
+        held = {"layer": layer, "temp": [], "free": [], "stage": []}
+        placed, unplaced = [], 0
+        for e in sorted({int(i) for i in ids}):
+            key = (layer, e)
+            if key in self.lru:
+                self.hits += 1
+                continue
+            self.misses += 1
+            if self.free:
+                slot = self.free.pop()
+                if len(self.lru) < self.budget:
+                    self.slot_of[key] = slot
+                    self.lru[key] = slot
+                else:
+                    held["temp"].append((e, slot))
+                    held["free"].append(slot)
+            elif self.stage_free:
+                slot = self.stage_free.pop()
+                held["temp"].append((e, slot))
+                held["stage"].append(slot)
+            else:
+                unplaced += 1
+                continue
+            placed.append((e, slot))
+        self.groups[ticket] = held
+        return ticket, placed, unplaced
+
+    def compute_row(self, ticket, n_experts) -> np.ndarray:
+        g = self.groups[ticket]
+        row = self.table(g["layer"], n_experts)
+        for e, slot in g["temp"]:
+            row[e] = slot
+        return row
+
+    def prefill_done(self, ticket) -> None:
+        g = self.groups.pop(ticket)
+        self.free.extend(g["free"])
+        self.stage_free.extend(g["stage"])
+
     def stitch(self, layers, n_experts) -> bool:
         """Load every expert into a fixed slot: slot = layer_idx*E + e
         (cache.py:717-787 with the free list above)."""

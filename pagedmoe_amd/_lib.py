@@ -55,7 +55,8 @@ class RouteCfg(ctypes.Structure):
 class SlabStats(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int64) for n in (
         "hits", "misses", "evictions", "starved", "installs", "resident", "slots",
-        "budget", "reserve", "stitched", "bytes_copied")]
+        "budget", "reserve", "stitched", "bytes_copied", "prefill_slot_reads",
+        "prefill_installs", "stage_reads", "prefill_starved", "stage_slots")]
 
 
 _P = ctypes.c_void_p
@@ -79,6 +80,8 @@ SIGNATURES = {
     "pmoe_moe_workspace": (_SZ, [ctypes.POINTER(Geom), _I, _I, _I, _I]),
     "pmoe_moe_workspace_init": (_I, [_P, _SZ, _P]),
     "pmoe_moe_workspace_status": (_I, [_P, ctypes.POINTER(ctypes.c_uint32), _P]),
+    "pmoe_moe_workspace_error_async": (_I, [_P, _P, _P]),
+    "pmoe_set_barrier_spin": (_I, [ctypes.c_uint64]),
     "pmoe_switch_glu": (_I, [ctypes.POINTER(Geom), _P, _P, _I, _P, _P, _I, _I, _P, _P, _SZ, _P]),
     "pmoe_moe_experts": (_I, [ctypes.POINTER(Geom), _P, _P, _I, _P, _P, _P, _I, _I, _I, _P,
                               _P, _P, _SZ, _P]),
@@ -92,6 +95,15 @@ SIGNATURES = {
     "pmoe_slab_request": (_I, [_P, _I, _I32P, _I, _I32P, _I32P, ctypes.POINTER(_I)]),
     "pmoe_slab_stitch": (_I, [_P]),
     "pmoe_slab_publish": (_I, [_P, _I, _P]),
+    "pmoe_slab_sync_table": (_I, [_P, _I, _P]),
+    "pmoe_slab_dirty": (_I, [_P, _I]),
+    "pmoe_slab_read_device_row": (_I, [_P, _I, _I32P]),
+    "pmoe_slab_set_stage": (_I, [_P, _I, _I]),
+    "pmoe_slab_capacity": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    "pmoe_slab_prefill_request": (_I, [_P, _I, _I32P, _I, _I32P, _I32P, ctypes.POINTER(_I),
+                                       ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    "pmoe_slab_prefill_publish": (_I, [_P, _I, _P]),
+    "pmoe_slab_prefill_done": (_I, [_P, _I]),
     "pmoe_slab_stats_get": (_I, [_P, ctypes.POINTER(SlabStats)]),
     "pmoe_host_alloc": (_I, [ctypes.POINTER(_P), _SZ]),
     "pmoe_host_free": (_I, [_P]),
@@ -99,10 +111,19 @@ SIGNATURES = {
     "pmoe_copy_engine_destroy": (_I, [_P]),
     "pmoe_copy_submit": (_I, [_P, _P, _P, _SZ, _I]),
     "pmoe_copy_flush": (_I, [_P, _P]),
+    "pmoe_copy_fence": (_I, [_P, _P]),
+    "pmoe_copy_issue": (_I, [_P]),
+    "pmoe_copy_join": (_I, [_P, _P]),
     "pmoe_copy_sync": (_I, [_P]),
     "pmoe_copy_bytes": (ctypes.c_int64, [_P]),
     "pmoe_slab_fetch": (_I, [_P, _P, ctypes.POINTER(Geom), _P, _P, _I, _I32P, _I,
                              ctypes.POINTER(_I), _P]),
+    "pmoe_slab_fetch_prefill": (_I, [_P, _P, ctypes.POINTER(Geom), _P, _P, _I, _I32P, _I,
+                                     ctypes.POINTER(_I), ctypes.POINTER(_I),
+                                     ctypes.POINTER(_I)]),
+    "pmoe_probe_sink_bytes": (_SZ, []),
+    "pmoe_probe_read": (_I, [_P, _SZ, _P, _SZ, _P]),
+    "pmoe_probe_copy": (_I, [_P, _P, _SZ, _P]),
     "pmoe_profile_begin": (_I, [_I]),
     "pmoe_profile_end": (_I, []),
     "pmoe_profile_kernels": (_I, []),

@@ -88,22 +88,55 @@ class HostExpertStore:
             pass
 
 
+def default_stage_slots(g: Geom, n_experts: int) -> int:
+    """The prefill stage's size: four groups of PREFILL_STAGE_GROUP_MB (at
+    least 8 experts a group) and at least 32 slots, as ensure_stage sizes it
+    (cache.py:1358-1372), but never more than two layers' worth of experts:
+    a group holds at most one layer's distinct experts and at most two groups
+    are in flight (one computing, the next one's copies under it)."""
+    if not config.PREFILL_STAGE:
+        return 0
+    per = max(1, int(g.expert_bytes))
+    group = max(config.PREFILL_STAGE_GROUP_MB << 20, 8 * per)
+    return min(max(32, (4 * group) // per), 2 * int(n_experts))
+
+
+class PrefillGroup:
+    """One prefill fetch group's held slots (a native ticket) and its copy
+    counts."""
+
+    __slots__ = ("ticket", "ids", "n_miss", "n_unplaced")
+
+    def __init__(self, ticket: int, ids, n_miss: int, n_unplaced: int):
+        self.ticket = ticket
+        self.ids = list(ids)
+        self.n_miss = n_miss
+        self.n_unplaced = n_unplaced
+
+
 class ExpertCache:
     """Slot residency of the routed experts of ``layer_keys`` (E experts each)
     in a slab of ``slots`` routed slots, plus one pinned slot per layer for a
-    shared expert when ``n_shared`` is 1."""
+    shared expert when ``n_shared`` is 1, plus ``stage_slots`` prefill stage
+    slots (default: ``default_stage_slots``) that never hold resident experts.
+
+    Slab slot order: routed [0, slots), shared [slots, slots + layers),
+    stage after those."""
 
     def __init__(self, g: Geom, slots: int, layer_keys, n_experts: int, *,
                  host_store: HostExpertStore | None = None, n_shared: int = 0,
                  reserve_frac: float | None = None, lfru: bool | None = None,
-                 lfru_scan: int | None = None, device="cuda"):
+                 lfru_scan: int | None = None, stage_slots: int | None = None, device="cuda"):
         self.geom = g
         self.layer_keys = list(layer_keys)
         self._layer = {k: i for i, k in enumerate(self.layer_keys)}
         self.n_experts = int(n_experts)
         self.routed_slots = int(slots)
         self.n_shared = int(n_shared)
-        self.slab = SlabStore(g, self.routed_slots + self.n_shared * len(self.layer_keys), device)
+        self.stage_slots = (default_stage_slots(g, self.n_experts) if stage_slots is None
+                            else int(stage_slots))
+        self.stage_first = self.routed_slots + self.n_shared * len(self.layer_keys)
+        self.slab = SlabStore(g, self.stage_first + self.stage_slots, device)
         self.host_store = host_store
         self._h = ctypes.c_void_p()
         check(lib().pmoe_slab_create(
@@ -111,6 +144,8 @@ class ExpertCache:
             config.SLAB_RESERVE_FRAC if reserve_frac is None else reserve_frac,
             int(config.LFRU if lfru is None else lfru),
             config.LFRU_SCAN if lfru_scan is None else lfru_scan), "pmoe_slab_create")
+        check(lib().pmoe_slab_set_stage(self._h, self.stage_first, self.stage_slots),
+              "pmoe_slab_set_stage")
         self._ce = ctypes.c_void_p()
         if host_store is not None:
             check(lib().pmoe_copy_engine_create(ctypes.byref(self._ce), config.COPY_SPLIT_BYTES,
@@ -147,9 +182,34 @@ class ExpertCache:
         return np.array(out[:], np.int32)
 
     def flow_table(self, layer_key):
-        """Device pointer of the expert->slot table (-1 = not resident);
-        the reference's flow table (cache.py:843)."""
+        """Device pointer of the layer's expert->slot row (-1 = not
+        resident), republished first if its residency changed since the
+        last upload -- e.g. another layer's fetch evicted one of its experts
+        (the reference's flow_table, cache.py:843-859).  The upload is
+        enqueued on the current stream."""
+        self.sync_table(layer_key)
         return self.table_ptr(layer_key)
+
+    def sync_table(self, layer_key) -> bool:
+        """Republish the layer's device row if it is stale; True if it was."""
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        r = lib().pmoe_slab_sync_table(self._h, self.layer_index(layer_key), stream)
+        if r < 0:
+            check(r, "pmoe_slab_sync_table")
+        return r == 1
+
+    def device_table(self, layer_key) -> np.ndarray:
+        """The layer's device row as the kernels see it (synchronises)."""
+        out = (ctypes.c_int32 * self.n_experts)()
+        check(lib().pmoe_slab_read_device_row(self._h, self.layer_index(layer_key), out),
+              "pmoe_slab_read_device_row")
+        return np.array(out[:], np.int32)
+
+    def table_dirty(self, layer_key) -> bool:
+        r = lib().pmoe_slab_dirty(self._h, self.layer_index(layer_key))
+        if r < 0:
+            check(r, "pmoe_slab_dirty")
+        return r == 1
 
     def stitch_table(self, layer_key):
         return self.table_ptr(layer_key) if self.stitched else None
@@ -194,6 +254,67 @@ class ExpertCache:
                                     self.layer_index(layer_key), arr, len(ids),
                                     ctypes.byref(nm), stream), "pmoe_slab_fetch")
         return nm.value
+
+    # ------------------------------------------------------------- prefill
+
+    def capacity(self):
+        """(free routed slots, free stage slots, budget room)."""
+        f, st, room = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        check(lib().pmoe_slab_capacity(self._h, ctypes.byref(f), ctypes.byref(st),
+                                       ctypes.byref(room)), "pmoe_slab_capacity")
+        return f.value, st.value, room.value
+
+    def request_prefill(self, layer_key, expert_ids):
+        """Policy step only (no copies): (ticket, [(miss id, slot)], unplaced)."""
+        ids = [int(e) for e in expert_ids]
+        arr = (ctypes.c_int32 * max(1, len(ids)))(*ids)
+        mid = (ctypes.c_int32 * max(1, len(ids)))()
+        msl = (ctypes.c_int32 * max(1, len(ids)))()
+        nm, nu, t = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        check(lib().pmoe_slab_prefill_request(self._h, self.layer_index(layer_key), arr, len(ids),
+                                              mid, msl, ctypes.byref(nm), ctypes.byref(nu),
+                                              ctypes.byref(t)), "pmoe_slab_prefill_request")
+        return t.value, [(mid[i], msl[i]) for i in range(nm.value)], nu.value
+
+    def fence(self) -> None:
+        """Copies issued from now on wait for everything queued so far on
+        the current stream."""
+        check(lib().pmoe_copy_fence(self._ce, self._stream()), "pmoe_copy_fence")
+
+    def join(self) -> None:
+        """The current stream waits for every copy issued so far."""
+        check(lib().pmoe_copy_join(self._ce, self._stream()), "pmoe_copy_join")
+
+    def fetch_prefill(self, layer_key, expert_ids) -> PrefillGroup:
+        """One prefill fetch group (cache.py:2535-2578, _begin(prefill=True)):
+        policy step, then its misses copied behind the latest fence; nothing
+        waits for them yet.  Before the group computes: ``publish_group`` and
+        ``join``; after its compute is enqueued: ``prefill_done``."""
+        if self.host_store is None:
+            raise PmoeError("fetch_prefill needs a host expert store")
+        ids = sorted({int(e) for e in expert_ids})
+        arr = (ctypes.c_int32 * max(1, len(ids)))(*ids)
+        nm, nu, t = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        check(lib().pmoe_slab_fetch_prefill(self._h, self._ce, ctypes.byref(self.geom),
+                                            ctypes.c_void_p(self.slab.data_ptr),
+                                            ctypes.c_void_p(self.host_store.address),
+                                            self.layer_index(layer_key), arr, len(ids),
+                                            ctypes.byref(nm), ctypes.byref(nu), ctypes.byref(t)),
+              "pmoe_slab_fetch_prefill")
+        return PrefillGroup(t.value, ids, nm.value, nu.value)
+
+    def publish_group(self, group: PrefillGroup) -> None:
+        """Upload the group's compute row (resident + its held slots) on the
+        current stream."""
+        check(lib().pmoe_slab_prefill_publish(self._h, group.ticket, self._stream()),
+              "pmoe_slab_prefill_publish")
+
+    def prefill_done(self, group: PrefillGroup) -> None:
+        check(lib().pmoe_slab_prefill_done(self._h, group.ticket), "pmoe_slab_prefill_done")
+
+    @staticmethod
+    def _stream():
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
     def sync_copies(self) -> None:
         if self._ce.value:
@@ -253,6 +374,9 @@ class ExpertCache:
             "reserve": st.reserve, "stitched": bool(st.stitched),
             "read_gb": st.bytes_copied / 1e9, "h2d_gb": h2d / 1e9,
             "group_passes": self.group_passes,
+            "prefill_slot_reads": st.prefill_slot_reads, "prefill_installs": st.prefill_installs,
+            "stage_reads": st.stage_reads, "prefill_slot_starved": st.prefill_starved,
+            "stage_slots": st.stage_slots,
         }
 
     def close(self) -> None:

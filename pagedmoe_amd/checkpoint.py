@@ -21,11 +21,9 @@ unchanged.
 
 from __future__ import annotations
 
-import glob
 import json
 import os
 import re
-import struct
 from dataclasses import dataclass
 from pathlib import Path
 
@@ -42,7 +40,8 @@ _COMPS = ("weight", "scales", "biases")
 @dataclass(frozen=True)
 class TensorLoc:
     """Where one tensor lives: file, dtype string, shape, absolute byte
-    offset of its first element and its size (safetensors_index.py:61-89)."""
+    offset of its first element and its size (the record of
+    safetensors_index.py:61-89)."""
 
     file: str
     dtype: str
@@ -50,40 +49,78 @@ class TensorLoc:
     offset: int
     nbytes: int
 
+    def row_bytes(self) -> int:
+        """Bytes of one leading-index entry, from the trailing shape and the
+        element size; the stacked tensor's size must be a whole multiple."""
+        item = _ITEMSIZE.get(self.dtype)
+        if item is None:
+            raise PmoeError(f"{self.file}: dtype {self.dtype} has no fixed element size")
+        per = item * int(np.prod(self.shape[1:], dtype=np.int64))
+        if per * self.shape[0] != self.nbytes:
+            raise PmoeError(f"{self.file}: {self.nbytes} B is not {self.shape[0]} entries of "
+                            f"{per} B")
+        return per
+
     def expert_slice(self, e: int) -> "TensorLoc":
-        """experts[e] of a stacked [E, ...] tensor: one contiguous range."""
-        n = self.shape[0]
-        if not 0 <= e < n:
-            raise IndexError(f"expert {e} outside a stack of {n}")
-        stride = self.nbytes // n
-        return TensorLoc(self.file, self.dtype, tuple(self.shape[1:]), self.offset + e * stride,
-                         stride)
+        """Entry e of a stacked [E, ...] tensor (an expert's range)."""
+        if not 0 <= e < self.shape[0]:
+            raise IndexError(f"expert {e} outside a stack of {self.shape[0]}")
+        per = self.row_bytes()
+        return TensorLoc(self.file, self.dtype, tuple(self.shape[1:]), self.offset + per * e, per)
+
+
+def shard_files(model_dir) -> list:
+    """The checkpoint's safetensors shards: the files a
+    ``model.safetensors.index.json`` weight map names when the directory has
+    one, else every ``*.safetensors`` file in it, in name order."""
+    root = Path(model_dir)
+    index_file = root / "model.safetensors.index.json"
+    if index_file.is_file():
+        weight_map = json.loads(index_file.read_text()).get("weight_map", {})
+        return [root / name for name in sorted(set(weight_map.values()))]
+    return sorted(root.glob("*.safetensors"))
+
+
+def _header(path: Path):
+    """(absolute offset of the data section, {name: meta}) of one shard.
+
+    A safetensors file starts with a u64 little-endian length n, then n bytes
+    of JSON mapping each tensor to {dtype, shape, data_offsets} (offsets
+    relative to the data section, which starts at 8 + n), plus an optional
+    "__metadata__" entry."""
+    fd = os.open(path, os.O_RDONLY)
+    try:
+        size = os.fstat(fd).st_size
+        head = os.pread(fd, 8, 0)
+        n = int.from_bytes(head, "little") if len(head) == 8 else -1
+        if n < 2 or 8 + n > size:
+            raise PmoeError(f"{path}: not a safetensors file ({size} B, header length {n})")
+        meta = json.loads(os.pread(fd, n, 8))
+    finally:
+        os.close(fd)
+    meta.pop("__metadata__", None)
+    return 8 + n, meta, size
 
 
 def read_headers(model_dir) -> dict:
-    """Every tensor of ``model*.safetensors`` in model_dir -> TensorLoc.
-
-    The format: an 8-byte little-endian header size, that many bytes of JSON
-    ({name: {dtype, shape, data_offsets: [begin, end]}}, offsets relative to
-    the end of the header), then the raw data (safetensors_index.py:134-159)."""
-    files = sorted(glob.glob(str(Path(model_dir) / "model*.safetensors")))
+    """Every tensor of the checkpoint's shards -> TensorLoc, from the file
+    headers alone (no tensor data is read)."""
+    files = shard_files(model_dir)
     if not files:
-        raise FileNotFoundError(f"no model*.safetensors in {model_dir}")
+        raise FileNotFoundError(f"{model_dir}: no safetensors shards (no index file and no "
+                                "*.safetensors)")
     index = {}
     for path in files:
-        with open(path, "rb") as f:
-            (hsize,) = struct.unpack("<Q", f.read(8))
-            header = json.loads(f.read(hsize))
-        start = 8 + hsize
-        for name, meta in header.items():
-            if name == "__metadata__":
-                continue
-            begin, end = meta["data_offsets"]
-            shape = tuple(int(s) for s in meta["shape"])
-            loc = TensorLoc(path, meta["dtype"], shape, start + int(begin), int(end) - int(begin))
-            n = int(np.prod(shape, dtype=np.int64)) * _ITEMSIZE.get(loc.dtype, 0)
-            if _ITEMSIZE.get(loc.dtype) and n != loc.nbytes:
-                raise ValueError(f"{path}: {name} has {loc.nbytes} bytes for shape {shape} "
+        data, meta, size = _header(path)
+        for name, m in meta.items():
+            lo, hi = (int(v) for v in m["data_offsets"])
+            if not 0 <= lo <= hi or data + hi > size:
+                raise PmoeError(f"{path}: {name} spans [{lo}, {hi}) past the end of the file")
+            loc = TensorLoc(str(path), m["dtype"], tuple(int(d) for d in m["shape"]), data + lo,
+                            hi - lo)
+            item = _ITEMSIZE.get(loc.dtype)
+            if item and int(np.prod(loc.shape, dtype=np.int64)) * item != loc.nbytes:
+                raise ValueError(f"{path}: {name} has {loc.nbytes} bytes for shape {loc.shape} "
                                  f"{loc.dtype}")
             index[name] = loc
     return index

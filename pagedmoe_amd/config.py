@@ -2,7 +2,10 @@
 
 Names and defaults follow the reference's PAGED_MOE_* knobs that touch this
 path (config.py: SLAB_RESERVE_FRAC :718, LFRU/LFRU_SCAN :1477-1478, STITCH
-:1186); ``sync_from_environ()`` re-reads them (config.py:853).
+:1186, PREFILL_TOUCH :617, PREFILL_STAGE / PREFILL_STAGE_GROUP_MB
+:1603-1608, GROUP_BYTES :1531); ``sync_from_environ()`` re-reads them
+(config.py:853).  DECODE_MAX_TOKENS is the reference's _DECODE_MAX_TOKENS
+(streaming.py:69): calls of more tokens take the prefill residency policy.
 """
 
 from __future__ import annotations
@@ -30,16 +33,25 @@ LFRU_SCAN = 8             # entries scanned per eviction
 STITCH = True             # pin every expert in a fixed slot when the slab holds them all
 COPY_SPLIT_BYTES = 64 << 20  # H2D copy piece size (an expert of up to 64 MiB is one copy)
 COPY_STREAMS = 2          # copy streams of the engine
+DECODE_MAX_TOKENS = 20    # calls of more tokens are prefill (no touch, no eviction)
+PREFILL_STAGE = True      # stage slots for prefill misses that find no free slot
+PREFILL_STAGE_GROUP_MB = 384  # prefill fetch group size; the stage holds four groups
+GROUP_BYTES = 1024 << 20  # ceiling on one prefill fetch group
 
 
 def sync_from_environ() -> None:
     global SLAB_RESERVE_FRAC, LFRU, LFRU_SCAN, STITCH, COPY_SPLIT_BYTES, COPY_STREAMS
+    global DECODE_MAX_TOKENS, PREFILL_STAGE, PREFILL_STAGE_GROUP_MB, GROUP_BYTES
     SLAB_RESERVE_FRAC = _env("SLAB_RESERVE_FRAC", 0.1, float)
     LFRU = _env("LFRU", True, _bool)
     LFRU_SCAN = _env("LFRU_SCAN", 8, int)
     STITCH = _env("STITCH", True, _bool)
     COPY_SPLIT_BYTES = _env("COPY_SPLIT_KB", 65536, int) * 1024
     COPY_STREAMS = _env("COPY_STREAMS", 2, int)
+    DECODE_MAX_TOKENS = _env("DECODE_MAX_TOKENS", 20, int)
+    PREFILL_STAGE = _env("PREFILL_STAGE", True, _bool)
+    PREFILL_STAGE_GROUP_MB = _env("PREFILL_STAGE_GROUP_MB", 384, int)
+    GROUP_BYTES = _env("GROUP_MB", 1024, int) << 20
 
 
 sync_from_environ()

@@ -6,10 +6,15 @@
 // streams / SDMA engines share one expert (:213-241), and the first error of
 // a batch is the one reported (:131-156, :293-302).  Instead of pread into
 // unified memory, a piece is one hipMemcpyAsync from pinned host memory into
-// its slab slot.  Ordering with compute uses events only: at flush the copy
-// streams wait for everything already queued on the compute stream (so no
-// slot is overwritten while an earlier kernel may still read it), and the
-// compute stream waits for the copies.  All streams have default priority.
+// its slab slot.  Ordering with compute uses events only.  A fence is an
+// event recorded on the compute stream; issued copies first wait for the
+// latest fence, so no slot is overwritten while a kernel queued before the
+// fence may still read it.  A join makes a stream wait for every issued copy.
+// pmoe_copy_flush is fence at the stream's tail + issue + join, the decode
+// fetch's ordering.  A prefill fetch group fences before the previous group's
+// compute and joins only before its own, so its copies run under that
+// compute (cache.py:2535-2578: "While group i computes on the GPU, the reads
+// for group i+1 are already in flight").  All streams have default priority.
 #include <hip/hip_runtime.h>
 
 #include <deque>
@@ -27,7 +32,8 @@ struct pmoe_copy_engine {
   size_t split = size_t(64) << 20;  // whole experts: larger pieces copy faster
   std::vector<hipStream_t> streams;
   std::vector<hipEvent_t> done;
-  hipEvent_t start = nullptr;
+  hipEvent_t fence = nullptr;
+  bool fenced = false;
   std::deque<Job> urgent, normal;
   int64_t bytes = 0;
   int next_stream = 0;
@@ -63,7 +69,7 @@ extern "C" int pmoe_copy_engine_create(pmoe_copy_engine** out, size_t split_byte
   auto* ce = new (std::nothrow) pmoe_copy_engine();
   if (!ce) return pmoe::fail(PMOE_ENOMEM, "copy_engine_create: out of host memory");
   if (split_bytes > 0) ce->split = split_bytes;
-  hipError_t e = hipEventCreateWithFlags(&ce->start, hipEventDisableTiming);
+  hipError_t e = hipEventCreateWithFlags(&ce->fence, hipEventDisableTiming);
   for (int i = 0; i < n_streams && e == hipSuccess; ++i) {
     hipStream_t s = nullptr;
     hipEvent_t ev = nullptr;
@@ -88,7 +94,7 @@ extern "C" int pmoe_copy_engine_destroy(pmoe_copy_engine* ce) {
     (void)hipStreamDestroy(s);
   }
   for (hipEvent_t ev : ce->done) (void)hipEventDestroy(ev);
-  if (ce->start) (void)hipEventDestroy(ce->start);
+  if (ce->fence) (void)hipEventDestroy(ce->fence);
   delete ce;
   return PMOE_OK;
 }
@@ -103,14 +109,20 @@ extern "C" int pmoe_copy_submit(pmoe_copy_engine* ce, void* dst, const void* src
   return PMOE_OK;
 }
 
-extern "C" int pmoe_copy_flush(pmoe_copy_engine* ce, void* stream) {
+extern "C" int pmoe_copy_fence(pmoe_copy_engine* ce, void* stream) {
   pmoe::clear_error();
-  if (!ce) return pmoe::fail(PMOE_EINVAL, "copy_flush: null engine");
-  hipStream_t compute = static_cast<hipStream_t>(stream);
+  if (!ce) return pmoe::fail(PMOE_EINVAL, "copy_fence: null engine");
   std::lock_guard<std::mutex> lk(ce->mu);
+  PMOE_HIP(hipEventRecord(ce->fence, static_cast<hipStream_t>(stream)));
+  ce->fenced = true;
+  return PMOE_OK;
+}
+
+// Caller holds mu.
+static int issue_locked(pmoe_copy_engine* ce) {
   if (ce->urgent.empty() && ce->normal.empty()) return PMOE_OK;
-  PMOE_HIP(hipEventRecord(ce->start, compute));
-  for (hipStream_t s : ce->streams) PMOE_HIP(hipStreamWaitEvent(s, ce->start, 0));
+  if (ce->fenced)
+    for (hipStream_t s : ce->streams) PMOE_HIP(hipStreamWaitEvent(s, ce->fence, 0));
   int first_err = PMOE_OK;
   auto issue = [&](std::deque<pmoe_copy_engine::Job>& q) {
     while (!q.empty()) {
@@ -124,7 +136,7 @@ extern "C" int pmoe_copy_flush(pmoe_copy_engine* ce, void* stream) {
                                       static_cast<const uint8_t*>(job.src) + off, len,
                                       hipMemcpyHostToDevice, s);
         if (e != hipSuccess && first_err == PMOE_OK)
-          first_err = pmoe::hip_fail(e, "copy_flush: hipMemcpyAsync");
+          first_err = pmoe::hip_fail(e, "copy_issue: hipMemcpyAsync");
         else if (e == hipSuccess)
           ce->bytes += int64_t(len);
       }
@@ -132,11 +144,38 @@ extern "C" int pmoe_copy_flush(pmoe_copy_engine* ce, void* stream) {
   };
   issue(ce->urgent);
   issue(ce->normal);
-  for (size_t i = 0; i < ce->streams.size(); ++i) {
+  for (size_t i = 0; i < ce->streams.size(); ++i)
     PMOE_HIP(hipEventRecord(ce->done[i], ce->streams[i]));
-    PMOE_HIP(hipStreamWaitEvent(compute, ce->done[i], 0));
-  }
   return first_err;
+}
+
+extern "C" int pmoe_copy_issue(pmoe_copy_engine* ce) {
+  pmoe::clear_error();
+  if (!ce) return pmoe::fail(PMOE_EINVAL, "copy_issue: null engine");
+  std::lock_guard<std::mutex> lk(ce->mu);
+  return issue_locked(ce);
+}
+
+extern "C" int pmoe_copy_join(pmoe_copy_engine* ce, void* stream) {
+  pmoe::clear_error();
+  if (!ce) return pmoe::fail(PMOE_EINVAL, "copy_join: null engine");
+  std::lock_guard<std::mutex> lk(ce->mu);
+  for (hipEvent_t ev : ce->done)
+    PMOE_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(stream), ev, 0));
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_copy_flush(pmoe_copy_engine* ce, void* stream) {
+  pmoe::clear_error();
+  if (!ce) return pmoe::fail(PMOE_EINVAL, "copy_flush: null engine");
+  hipStream_t compute = static_cast<hipStream_t>(stream);
+  std::lock_guard<std::mutex> lk(ce->mu);
+  if (ce->urgent.empty() && ce->normal.empty()) return PMOE_OK;
+  PMOE_HIP(hipEventRecord(ce->fence, compute));
+  ce->fenced = true;
+  const int rc = issue_locked(ce);
+  for (hipEvent_t ev : ce->done) PMOE_HIP(hipStreamWaitEvent(compute, ev, 0));
+  return rc;
 }
 
 extern "C" int pmoe_copy_sync(pmoe_copy_engine* ce) {

@@ -43,8 +43,14 @@
 //     (no memset between launches: graph-safe).
 // Data crossing a barrier (logits, h) is stored and loaded at device scope,
 // which writes through / reads past the XCDs' L2s, so no cache writeback or
-// invalidate is needed.  A poll that has waited 0.5 s (100 MHz realtime
-// clock) sets error bit 0 and gives up, so a launch always ends.
+// invalidate is needed.  A poll that has waited its spin limit (0.5 s of the
+// 100 MHz realtime clock by default; pmoe_set_barrier_spin) sets error bit 0
+// of the workspace and gives up, so a launch always ends.  A block whose
+// barrier-2 wait gave up, and every block that sees the error bit after
+// barrier 2 (any block that gave up at barrier 1 set it before arriving
+// there), writes NaN for its output rows instead of the combine, so a
+// timed-out layer can never pass for a good one; the host reads the error
+// word at its next sync point.
 #include "gemv_common.h"
 #include "pmoe_internal.h"
 #include "pmoe_kernels.h"
@@ -70,6 +76,7 @@ constexpr int kFMaxH = 20480;          // bf16 h values staged in LDS in phase D
 #define PMOE_H_LDS 1
 #endif
 constexpr uint64_t kSpinTicks = 50000000ull;  // 0.5 s at 100 MHz
+uint64_t g_spin_ticks = kSpinTicks;           // host: limit passed to every launch
 #ifndef PMOE_RANK1
 #define PMOE_RANK1 1  // single-token routing by rank counts over the block
 #endif
@@ -91,6 +98,7 @@ struct FusedArgs {
   int32_t* inds_out;
   float* w_out;
   DecodeSync* sync;
+  uint64_t spin;               // barrier poll limit, realtime-clock ticks
   int n_blocks;
   int tile;                    // hidden rows per block in phase D
 };
@@ -132,10 +140,11 @@ __device__ __forceinline__ void shared_store(T* p, T v) {
 // a group resets the group's counter and arrives at arrive[i]; the block
 // that completes arrive[i] resets it and writes `tag` into every block's
 // flag line; each block's thread 0 polls its own line (no shared hot spot
-// while HBM is saturated).
-__device__ __forceinline__ void grid_barrier(DecodeSync* sy, int i, uint32_t tag,
-                                             uint32_t n_blocks, int mark = -1) {
-  __shared__ int s_last;
+// while HBM is saturated).  Returns true (block-uniform) when this block's
+// wait gave up after `spin` ticks.
+__device__ __forceinline__ bool grid_barrier(DecodeSync* sy, int i, uint32_t tag,
+                                             uint32_t n_blocks, uint64_t spin, int mark = -1) {
+  __shared__ int s_last, s_gave_up;
   __builtin_amdgcn_s_waitcnt(0);  // this wave's memory operations have completed
   __syncthreads();
   if (mark >= 0) trace_mark(nullptr, mark);
@@ -156,6 +165,7 @@ __device__ __forceinline__ void grid_barrier(DecodeSync* sy, int i, uint32_t tag
       if (mark >= 0 && last) trace_mark(nullptr, 14);
     }
     s_last = last;
+    s_gave_up = 0;
   }
   __syncthreads();
   uint8_t* flags = base + 256;
@@ -174,14 +184,16 @@ __device__ __forceinline__ void grid_barrier(DecodeSync* sy, int i, uint32_t tag
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     while (__hip_atomic_load(mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != tag) {
       __builtin_amdgcn_s_sleep(PMOE_POLL_SLEEP);
-      if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > spin) {
         __hip_atomic_fetch_or(&sy->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_gave_up = 1;
         break;
       }
     }
     if (mark >= 0) trace_mark(nullptr, 15);
   }
   __syncthreads();
+  return s_gave_up != 0;
 }
 
 __device__ __forceinline__ void fma8(float& acc, const uint4& a, const uint4& b) {
@@ -281,7 +293,7 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
     }
   }
   trace_mark(sy, 1);
-  grid_barrier(sy, 0, tag1, a.n_blocks);
+  grid_barrier(sy, 0, tag1, a.n_blocks, a.spin);
 
   // B: routing (every block, identical bits)
   trace_mark(sy, 2);
@@ -437,7 +449,10 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
   trace_mark(sy, 7);
   if (rank1) route_rank1_weights(rl, s_logit, L, blockIdx.x == 0 ? a.inds_out : nullptr, a.w_out);
   trace_mark(sy, 4);
-  grid_barrier(sy, 1, tag2, a.n_blocks, 12);
+  __shared__ int s_poison;
+  const bool late = grid_barrier(sy, 1, tag2, a.n_blocks, a.spin, 12);
+  if (threadIdx.x == 0)
+    s_poison = late || __hip_atomic_load(&sy->error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   trace_mark(sy, 5);
 
   // D: down rows of the block's tile into LDS, then the fixed-order combine
@@ -490,6 +505,7 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
     }
     __syncthreads();
     trace_mark(sy, 8);
+    const bool poison = s_poison != 0;
     for (int i = threadIdx.x; i < rt.n * tile; i += kFThreads) {
       const int n = i / tile, t = i - n * tile;
       const int o = row0 + t;
@@ -497,7 +513,7 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
       float acc = 0.0f;
       for (int col = 0; col < rt.kk; ++col)
         acc = __builtin_fmaf(L.w[n * rt.kk + col], s_y[(n * rt.kk + col) * tile + t], acc);
-      a.out[size_t(n) * a.dn.rows_out + o] = f2bf(acc);
+      a.out[size_t(n) * a.dn.rows_out + o] = poison ? uint16_t(0x7fc0) : f2bf(acc);
     }
   }
   trace_mark(sy, 6);
@@ -597,6 +613,12 @@ int fused_blocks(FusedFn fn, size_t lds) {
 
 }  // namespace
 
+extern "C" int pmoe_set_barrier_spin(uint64_t ticks) {
+  pmoe::clear_error();
+  g_spin_ticks = ticks ? ticks : kSpinTicks;
+  return PMOE_OK;
+}
+
 #ifdef PMOE_FUSED_TRACE
 extern "C" int pmoe_debug_trace(uint64_t* out, int n) {
   return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_trace), size_t(n) * sizeof(uint64_t)) == hipSuccess
@@ -641,6 +663,7 @@ int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int
   a.inds_out = inds_out;
   a.w_out = w_out;
   a.sync = sync;
+  a.spin = g_spin_ticks;
   a.n_blocks = blocks;
   a.tile = tile;
   ProfScope prof_scope(K_DECODE_FUSED, st);

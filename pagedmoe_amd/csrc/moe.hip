@@ -166,6 +166,26 @@ int check_geom(const pmoe_geom* g) {
   return PMOE_OK;
 }
 
+// The routing configuration, checked once before any path is chosen (the
+// one-launch decode, the three-launch decode and the prefill routing kernels
+// all assume it): a known scoring, 1 <= k <= min(16, E), and for sigmoid
+// scoring groups that divide E, hold at least 2 experts, and keep enough
+// experts for k.
+int check_route_cfg(const pmoe_route_cfg* rc) {
+  const int e = rc->n_experts, k = rc->top_k;
+  PMOE_REQUIRE(rc->scoring == PMOE_SCORE_SOFTMAX || rc->scoring == PMOE_SCORE_SIGMOID,
+               "routing: unknown scoring");
+  PMOE_REQUIRE(k >= 1 && k <= kRouteMaxK && k <= e, "routing: top_k must be 1..min(16, E)");
+  if (rc->scoring == PMOE_SCORE_SIGMOID) {
+    const int g = rc->n_group, tg = rc->topk_group;
+    PMOE_REQUIRE(g >= 1 && g <= 64 && e % g == 0, "routing: n_group must divide E and be <= 64");
+    PMOE_REQUIRE(tg >= 1 && tg <= g, "routing: topk_group must be 1..n_group");
+    PMOE_REQUIRE(g == 1 || e / g >= 2, "routing: groups need at least 2 experts");
+    PMOE_REQUIRE(k <= (e / g) * tg, "routing: top_k exceeds the experts of the kept groups");
+  }
+  return PMOE_OK;
+}
+
 // Dispatch + the three projections (+ SwiGLU) for rows = n*kk flat rows.
 // y receives [rows, hidden] (f32 when y_f32, else bf16).
 int run_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* table, int n_experts,
@@ -359,6 +379,16 @@ extern "C" int pmoe_moe_workspace_status(const void* ws, uint32_t* error, void* 
   return PMOE_OK;
 }
 
+extern "C" int pmoe_moe_workspace_error_async(const void* ws, uint32_t* host_dst,
+                                              void* stream) {
+  pmoe::clear_error();
+  PMOE_REQUIRE(ws != nullptr && host_dst != nullptr, "moe_workspace_error_async: null pointer");
+  const pmoe::DecodeSync* sy = static_cast<const pmoe::DecodeSync*>(ws);
+  PMOE_HIP(hipMemcpyAsync(host_dst, &sy->error, sizeof(uint32_t), hipMemcpyDeviceToHost,
+                          static_cast<hipStream_t>(stream)));
+  return PMOE_OK;
+}
+
 extern "C" int pmoe_switch_glu(const pmoe_geom* g, const void* slab, const int32_t* table,
                                int n_experts, const void* x, const int32_t* inds, int n, int k,
                                void* y, void* ws, size_t ws_bytes, void* stream) {
@@ -418,6 +448,8 @@ extern "C" int pmoe_moe_block(const pmoe_geom* g, const pmoe_route_cfg* rc_cfg, 
                "moe_block: null pointer");
   const int e = rc_cfg->n_experts, k = rc_cfg->top_k;
   PMOE_REQUIRE(n >= 0 && k > 0 && e > 0 && e <= 1023, "moe_block: bad shape");
+  rc = pmoe::check_route_cfg(rc_cfg);
+  if (rc) return rc;
   if (n == 0) return PMOE_OK;
   const int shared = shared_slot >= 0 ? 1 : 0;
   const size_t need = pmoe::carve(g, n, k, shared, e, nullptr, nullptr);

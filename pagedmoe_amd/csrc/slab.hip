@@ -3,14 +3,27 @@
 // Restates ExpertCache's slab policy (cache.py:410): free list popped LIFO so
 // the first allocation is slot 0 (:991, :1138-1139); a reserve of
 // max(4, int(slots*reserve_frac)) slots kept out of the resident budget
-// (:996-1002); per layer step: clear pins, classify ids (hit -> MRU,
+// (:996-1002); per decode layer step: clear pins, classify ids (hit -> MRU,
 // freq = min(8, freq+1), pin), give each miss a free slot or evict the least
 // recent unpinned non-stitch entry (_alloc_slot :1118-1159), install misses
 // with the LFRU second-chance trim (_install :2293, _evict_to_budget
 // :2236-2291).  The reference installs in read-completion order
 // (:2482-2519); here installs run in ascending expert id so the table is a
-// deterministic function of the request sequence.  The device table
-// [layers, experts] int32 (-1 = absent) is the flow table (:791-859).
+// deterministic function of the request sequence.
+//
+// Prefill fetch groups follow _begin(prefill=True) with PREFILL_TOUCH=0 and
+// PREFILL_SLAB=1 (:2347-2453) and install="soft" (_install :2306-2312):
+// hits keep their recency and frequency, misses take free slots only (never
+// an eviction) and become resident only while the resident count is under
+// the budget; the rest of a group's slots (free-list slots it could not
+// install, and slots of the prefill stage, ensure_stage :1345-1390) are held
+// by the group's ticket and handed back when the group is done
+// (_stage_return :1427-1440, _release_slot :1101-1116).
+//
+// The device table [layers, experts] int32 (-1 = absent) is the flow table
+// (:791-859).  A row is marked dirty whenever its host copy changes (an
+// install, an eviction by any layer's fetch, a group's slots coming back),
+// and pmoe_slab_sync_table republishes only dirty rows (flow_table :843-859).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -23,6 +36,7 @@ namespace {
 
 constexpr int kFreqMax = 8;
 constexpr int kPublishChunk = 512;
+constexpr int kMaxTickets = 64;
 
 struct TableChunk {
   int32_t v[kPublishChunk];
@@ -32,6 +46,14 @@ __global__ void publish_kernel(const TableChunk chunk, int count, int32_t* __res
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < count) dst[i] = chunk.v[i];
 }
+
+// Slots one prefill group holds for its own compute only.
+struct Ticket {
+  bool live = false;
+  int layer = -1;
+  std::vector<std::pair<int, int>> temp;  // (expert, slot) not installed as resident
+  std::vector<int> from_free, from_stage;
+};
 
 }  // namespace
 
@@ -44,10 +66,15 @@ struct pmoe_slab {
   std::vector<int> prev, next, slot_of, freq;
   std::vector<char> in_lru, stitch_key;
   int head = -1, tail = -1, lru_size = 0;
-  std::vector<char> pinned;               // per slot
+  std::vector<char> pinned;               // per routed slot
   std::vector<int> pinned_list;
   std::vector<int32_t> table;             // host [layers*E]
+  std::vector<char> dirty;                // per layer: host row not yet published
   int32_t* dtable = nullptr;              // device [layers*E]
+  // prefill stage: slab slots [stage_first, stage_first + stage_n)
+  int stage_first = 0, stage_n = 0;
+  std::vector<int> stage_free;            // stack
+  Ticket tickets[kMaxTickets];
   pmoe_slab_stats st{};
   std::mutex mu;
 
@@ -72,6 +99,10 @@ struct pmoe_slab {
     lru_unlink(k);
     lru_push_back(k);
   }
+  void set_entry(int k, int32_t slot) {
+    table[k] = slot;
+    dirty[k / n_experts] = 1;
+  }
   void pin(int slot) {
     if (slot >= 0 && !pinned[slot]) {
       pinned[slot] = 1;
@@ -88,7 +119,7 @@ struct pmoe_slab {
     freq[k] = 0;
     const int s = slot_of[k];
     slot_of[k] = -1;
-    table[k] = -1;
+    set_entry(k, -1);
     free_slots.push_back(s);
     ++st.evictions;
   }
@@ -109,6 +140,12 @@ struct pmoe_slab {
     ++st.starved;
     return -1;
   }
+  void install(int k, int slot) {
+    slot_of[k] = slot;
+    lru_push_back(k);
+    set_entry(k, slot);
+    ++st.installs;
+  }
   void trim() {
     const int scan = lfru ? lfru_scan : 0;
     while (lru_size > budget && lru_size > 1) {
@@ -128,6 +165,11 @@ struct pmoe_slab {
       if (victim < 0) break;
       evict(victim);
     }
+  }
+  int live_tickets() const {
+    int n = 0;
+    for (const Ticket& t : tickets) n += t.live;
+    return n;
   }
 };
 
@@ -159,6 +201,7 @@ extern "C" int pmoe_slab_create(pmoe_slab** out, int slots, int n_layers, int n_
   s->stitch_key.assign(keys, 0);
   s->pinned.assign(slots, 0);
   s->table.assign(keys, -1);
+  s->dirty.assign(n_layers, 0);
   s->st.slots = slots;
   s->st.reserve = s->reserve;
   s->st.budget = s->budget;
@@ -186,6 +229,28 @@ static int ensure_device_table(pmoe_slab* s) {
     s->dtable = nullptr;
     return pmoe::hip_fail(e, "slab: device table init");
   }
+  std::fill(s->dirty.begin(), s->dirty.end(), 0);
+  return PMOE_OK;
+}
+
+// Enqueue the upload of one row (its host entries, then the overlay of a
+// prefill ticket's temporary slots when one is given).  Caller holds mu.
+static int publish_row(pmoe_slab* s, int layer, const Ticket* overlay, hipStream_t st) {
+  int rc = ensure_device_table(s);
+  if (rc) return rc;
+  const int32_t* row = s->table.data() + size_t(layer) * s->n_experts;
+  int32_t* dst = s->dtable + size_t(layer) * s->n_experts;
+  for (int off = 0; off < s->n_experts; off += kPublishChunk) {
+    TableChunk c;
+    const int cnt = std::min(kPublishChunk, s->n_experts - off);
+    std::copy_n(row + off, cnt, c.v);
+    if (overlay)
+      for (const auto& es : overlay->temp)
+        if (es.first >= off && es.first < off + cnt) c.v[es.first - off] = es.second;
+    publish_kernel<<<(cnt + 255) / 256, 256, 0, st>>>(c, cnt, dst + off);
+    PMOE_LAUNCH_CHECK("publish_kernel");
+  }
+  s->dirty[layer] = overlay ? 1 : 0;  // an overlay row differs from the host row
   return PMOE_OK;
 }
 
@@ -209,16 +274,26 @@ extern "C" int pmoe_slab_host_table(pmoe_slab* s, int layer, int32_t* out) {
   return PMOE_OK;
 }
 
+// Sorted distinct ids, each checked against the expert count.
+static int unique_ids(pmoe_slab* s, const int32_t* ids, int n_ids, std::vector<int>& uniq,
+                      const char* who) {
+  uniq.assign(ids, ids + n_ids);
+  for (int e : uniq)
+    if (e < 0 || e >= s->n_experts)
+      return pmoe::fail(PMOE_EINVAL, std::string(who) + ": id out of range");
+  std::sort(uniq.begin(), uniq.end());
+  uniq.erase(std::unique(uniq.begin(), uniq.end()), uniq.end());
+  return PMOE_OK;
+}
+
 extern "C" int pmoe_slab_request(pmoe_slab* s, int layer, const int32_t* ids, int n_ids,
                                  int32_t* miss_ids, int32_t* miss_slots, int* n_miss) {
   pmoe::clear_error();
   if (!s || (n_ids > 0 && !ids) || !n_miss || layer < 0 || layer >= s->n_layers || n_ids < 0)
     return pmoe::fail(PMOE_EINVAL, "slab_request: bad argument");
-  std::vector<int> uniq(ids, ids + n_ids);
-  for (int e : uniq)
-    if (e < 0 || e >= s->n_experts) return pmoe::fail(PMOE_EINVAL, "slab_request: id out of range");
-  std::sort(uniq.begin(), uniq.end());
-  uniq.erase(std::unique(uniq.begin(), uniq.end()), uniq.end());
+  std::vector<int> uniq;
+  int rc = unique_ids(s, ids, n_ids, uniq, "slab_request");
+  if (rc) return rc;
   std::lock_guard<std::mutex> lk(s->mu);
   s->clear_pins();
   const int base = layer * s->n_experts;
@@ -240,21 +315,128 @@ extern "C" int pmoe_slab_request(pmoe_slab* s, int layer, const int32_t* ids, in
   for (int e : misses) {
     const int slot = s->alloc(true);
     if (slot < 0) continue;
-    s->slot_of[base + e] = slot;
     s->pin(slot);
     got.emplace_back(e, slot);
   }
   for (auto& es : got) {
-    const int k = base + es.first;
-    s->lru_push_back(k);
-    s->table[k] = es.second;
-    ++s->st.installs;
+    s->install(base + es.first, es.second);
     s->trim();
     if (miss_ids) miss_ids[placed] = es.first;
     if (miss_slots) miss_slots[placed] = es.second;
     ++placed;
   }
   *n_miss = placed;
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_slab_set_stage(pmoe_slab* s, int first_slot, int n_slots) {
+  pmoe::clear_error();
+  if (!s || n_slots < 0 || (n_slots > 0 && first_slot < s->slots))
+    return pmoe::fail(PMOE_EINVAL, "slab_set_stage: stage slots must follow the routed slots");
+  std::lock_guard<std::mutex> lk(s->mu);
+  if (s->live_tickets())
+    return pmoe::fail(PMOE_EINVAL, "slab_set_stage: a prefill group still holds stage slots");
+  s->stage_first = first_slot;
+  s->stage_n = n_slots;
+  s->stage_free.clear();
+  for (int i = n_slots - 1; i >= 0; --i) s->stage_free.push_back(first_slot + i);
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_slab_capacity(pmoe_slab* s, int* free_slots, int* stage_free,
+                                  int* budget_room) {
+  pmoe::clear_error();
+  if (!s) return pmoe::fail(PMOE_EINVAL, "slab_capacity: null slab");
+  std::lock_guard<std::mutex> lk(s->mu);
+  if (free_slots) *free_slots = int(s->free_slots.size());
+  if (stage_free) *stage_free = int(s->stage_free.size());
+  if (budget_room) *budget_room = std::max(0, s->budget - s->lru_size);
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_slab_prefill_request(pmoe_slab* s, int layer, const int32_t* ids, int n_ids,
+                                         int32_t* miss_ids, int32_t* miss_slots, int* n_miss,
+                                         int* n_unplaced, int* ticket) {
+  pmoe::clear_error();
+  if (!s || (n_ids > 0 && !ids) || !n_miss || !ticket || layer < 0 || layer >= s->n_layers ||
+      n_ids < 0)
+    return pmoe::fail(PMOE_EINVAL, "slab_prefill_request: bad argument");
+  std::vector<int> uniq;
+  int rc = unique_ids(s, ids, n_ids, uniq, "slab_prefill_request");
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(s->mu);
+  int t = -1;
+  for (int i = 0; i < kMaxTickets && t < 0; ++i)
+    if (!s->tickets[i].live) t = i;
+  if (t < 0) return pmoe::fail(PMOE_EINVAL, "slab_prefill_request: too many open prefill groups");
+  Ticket& tk = s->tickets[t];
+  tk = Ticket();
+  tk.live = true;
+  tk.layer = layer;
+  const int base = layer * s->n_experts;
+  int placed = 0, unplaced = 0;
+  for (int e : uniq) {
+    const int k = base + e;
+    if (s->in_lru[k]) {  // hit: recency and frequency untouched
+      ++s->st.hits;
+      continue;
+    }
+    ++s->st.misses;
+    int slot = s->alloc(false);
+    if (slot >= 0) {
+      ++s->st.prefill_slot_reads;
+      if (s->lru_size < s->budget) {  // soft install: only into room under the budget
+        s->install(k, slot);
+        ++s->st.prefill_installs;
+      } else {
+        tk.temp.emplace_back(e, slot);
+        tk.from_free.push_back(slot);
+      }
+    } else if (!s->stage_free.empty()) {
+      slot = s->stage_free.back();
+      s->stage_free.pop_back();
+      tk.temp.emplace_back(e, slot);
+      tk.from_stage.push_back(slot);
+      ++s->st.stage_reads;
+    } else {
+      ++s->st.prefill_starved;
+      ++unplaced;
+      continue;
+    }
+    if (miss_ids) miss_ids[placed] = e;
+    if (miss_slots) miss_slots[placed] = slot;
+    ++placed;
+  }
+  *n_miss = placed;
+  if (n_unplaced) *n_unplaced = unplaced;
+  *ticket = t;
+  return PMOE_OK;
+}
+
+static Ticket* live_ticket(pmoe_slab* s, int ticket) {
+  if (ticket < 0 || ticket >= kMaxTickets || !s->tickets[ticket].live) return nullptr;
+  return &s->tickets[ticket];
+}
+
+extern "C" int pmoe_slab_prefill_publish(pmoe_slab* s, int ticket, void* stream) {
+  pmoe::clear_error();
+  if (!s) return pmoe::fail(PMOE_EINVAL, "slab_prefill_publish: null slab");
+  std::lock_guard<std::mutex> lk(s->mu);
+  Ticket* tk = live_ticket(s, ticket);
+  if (!tk) return pmoe::fail(PMOE_EINVAL, "slab_prefill_publish: no such open prefill group");
+  return publish_row(s, tk->layer, tk, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pmoe_slab_prefill_done(pmoe_slab* s, int ticket) {
+  pmoe::clear_error();
+  if (!s) return pmoe::fail(PMOE_EINVAL, "slab_prefill_done: null slab");
+  std::lock_guard<std::mutex> lk(s->mu);
+  Ticket* tk = live_ticket(s, ticket);
+  if (!tk) return pmoe::fail(PMOE_EINVAL, "slab_prefill_done: no such open prefill group");
+  for (int slot : tk->from_free) s->free_slots.push_back(slot);
+  for (int slot : tk->from_stage) s->stage_free.push_back(slot);
+  if (!tk->temp.empty()) s->dirty[tk->layer] = 1;
+  *tk = Ticket();
   return PMOE_OK;
 }
 
@@ -269,9 +451,8 @@ extern "C" int pmoe_slab_stitch(pmoe_slab* s) {
     if (s->in_lru[k]) continue;
     const int slot = s->alloc(false);
     if (slot < 0) return 0;
-    s->slot_of[k] = slot;
-    s->lru_push_back(k);
-    s->table[k] = slot;
+    s->install(k, slot);
+    --s->st.installs;  // a stitch load is not a demand install
   }
   for (int k = 0; k < total; ++k) s->stitch_key[k] = 1;
   s->budget = s->slots;
@@ -284,20 +465,42 @@ extern "C" int pmoe_slab_publish(pmoe_slab* s, int layer, void* stream) {
   pmoe::clear_error();
   if (!s || layer < 0 || layer >= s->n_layers)
     return pmoe::fail(PMOE_EINVAL, "slab_publish: bad argument");
-  hipStream_t st = static_cast<hipStream_t>(stream);
   std::lock_guard<std::mutex> lk(s->mu);
-  int rc = ensure_device_table(s);
-  if (rc) return rc;
-  const int32_t* row = s->table.data() + size_t(layer) * s->n_experts;
-  int32_t* dst = s->dtable + size_t(layer) * s->n_experts;
-  for (int off = 0; off < s->n_experts; off += kPublishChunk) {
-    TableChunk c;
-    const int cnt = std::min(kPublishChunk, s->n_experts - off);
-    std::copy_n(row + off, cnt, c.v);
-    publish_kernel<<<(cnt + 255) / 256, 256, 0, st>>>(c, cnt, dst + off);
-    PMOE_LAUNCH_CHECK("publish_kernel");
+  return publish_row(s, layer, nullptr, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pmoe_slab_sync_table(pmoe_slab* s, int layer, void* stream) {
+  pmoe::clear_error();
+  if (!s || layer < 0 || layer >= s->n_layers)
+    return pmoe::fail(PMOE_EINVAL, "slab_sync_table: bad argument");
+  std::lock_guard<std::mutex> lk(s->mu);
+  if (s->dtable && !s->dirty[layer]) return 0;
+  const int rc = publish_row(s, layer, nullptr, static_cast<hipStream_t>(stream));
+  return rc ? rc : 1;
+}
+
+extern "C" int pmoe_slab_read_device_row(pmoe_slab* s, int layer, int32_t* out) {
+  pmoe::clear_error();
+  if (!s || !out || layer < 0 || layer >= s->n_layers)
+    return pmoe::fail(PMOE_EINVAL, "slab_read_device_row: bad argument");
+  int32_t* src = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(s->mu);
+    int rc = ensure_device_table(s);
+    if (rc) return rc;
+    src = s->dtable + size_t(layer) * s->n_experts;
   }
+  PMOE_HIP(hipDeviceSynchronize());
+  PMOE_HIP(hipMemcpy(out, src, size_t(s->n_experts) * sizeof(int32_t), hipMemcpyDeviceToHost));
   return PMOE_OK;
+}
+
+extern "C" int pmoe_slab_dirty(pmoe_slab* s, int layer) {
+  pmoe::clear_error();
+  if (!s || layer < 0 || layer >= s->n_layers)
+    return pmoe::fail(PMOE_EINVAL, "slab_dirty: bad argument");
+  std::lock_guard<std::mutex> lk(s->mu);
+  return s->dirty[layer] ? 1 : 0;
 }
 
 extern "C" int pmoe_slab_stats_get(pmoe_slab* s, pmoe_slab_stats* out) {
@@ -306,7 +509,24 @@ extern "C" int pmoe_slab_stats_get(pmoe_slab* s, pmoe_slab_stats* out) {
   std::lock_guard<std::mutex> lk(s->mu);
   s->st.resident = s->lru_size;
   s->st.stitched = s->stitched ? 1 : 0;
+  s->st.stage_slots = s->stage_n;
   *out = s->st;
+  return PMOE_OK;
+}
+
+// Copy the placed misses of one request from the host store into the slab.
+static int submit_misses(pmoe_slab* s, pmoe_copy_engine* ce, const pmoe_geom* g, void* slab,
+                         const void* host_store, int layer, const int32_t* mid,
+                         const int32_t* msl, int nm) {
+  const size_t eb = size_t(g->expert_bytes);
+  for (int i = 0; i < nm; ++i) {
+    const size_t src = (size_t(layer) * s->n_experts + size_t(mid[i])) * eb;
+    const int rc = pmoe_copy_submit(ce, static_cast<uint8_t*>(slab) + size_t(msl[i]) * eb,
+                                    static_cast<const uint8_t*>(host_store) + src, eb, 1);
+    if (rc) return rc;
+  }
+  std::lock_guard<std::mutex> lk(s->mu);
+  s->st.bytes_copied += int64_t(nm) * int64_t(eb);
   return PMOE_OK;
 }
 
@@ -320,21 +540,35 @@ extern "C" int pmoe_slab_fetch(pmoe_slab* s, pmoe_copy_engine* ce, const pmoe_ge
   int nm = 0;
   int rc = pmoe_slab_request(s, layer, ids, n_ids, mid.data(), msl.data(), &nm);
   if (rc) return rc;
-  const size_t eb = size_t(g->expert_bytes);
-  for (int i = 0; i < nm; ++i) {
-    const size_t src = (size_t(layer) * s->n_experts + size_t(mid[i])) * eb;
-    rc = pmoe_copy_submit(ce, static_cast<uint8_t*>(slab) + size_t(msl[i]) * eb,
-                          static_cast<const uint8_t*>(host_store) + src, eb, 1);
-    if (rc) return rc;
-  }
-  {
-    std::lock_guard<std::mutex> lk(s->mu);
-    s->st.bytes_copied += int64_t(nm) * int64_t(eb);
-  }
+  rc = submit_misses(s, ce, g, slab, host_store, layer, mid.data(), msl.data(), nm);
+  if (rc) return rc;
   rc = pmoe_slab_publish(s, layer, stream);
   if (rc) return rc;
   rc = pmoe_copy_flush(ce, stream);
   if (rc) return rc;
   *n_miss = nm;
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_slab_fetch_prefill(pmoe_slab* s, pmoe_copy_engine* ce, const pmoe_geom* g,
+                                       void* slab, const void* host_store, int layer,
+                                       const int32_t* ids, int n_ids, int* n_miss,
+                                       int* n_unplaced, int* ticket) {
+  pmoe::clear_error();
+  if (!s || !ce || !g || !slab || !host_store || !n_miss || !ticket || n_ids < 0)
+    return pmoe::fail(PMOE_EINVAL, "slab_fetch_prefill: bad argument");
+  std::vector<int32_t> mid(size_t(n_ids) + 1), msl(size_t(n_ids) + 1);
+  int nm = 0, nu = 0, t = -1;
+  int rc = pmoe_slab_prefill_request(s, layer, ids, n_ids, mid.data(), msl.data(), &nm, &nu, &t);
+  if (rc) return rc;
+  rc = submit_misses(s, ce, g, slab, host_store, layer, mid.data(), msl.data(), nm);
+  if (!rc) rc = pmoe_copy_issue(ce);
+  if (rc) {
+    (void)pmoe_slab_prefill_done(s, t);
+    return rc;
+  }
+  *n_miss = nm;
+  if (n_unplaced) *n_unplaced = nu;
+  *ticket = t;
   return PMOE_OK;
 }

@@ -18,6 +18,12 @@ from ._lib import Geom, RouteCfg, check, lib
 
 _WS: dict = {}
 _MOE_WS: dict = {}
+# Workspaces handed out before a larger call replaced them.  They are never
+# freed: a HIP graph captured over an earlier call keeps their raw pointers,
+# and a replay must not write into memory torch has given to another tensor.
+_RETIRED: dict = {"dispatch": [], "MoE": []}
+# Pinned host words the workspaces' error words are copied into at sync points.
+_ERR_HOST: dict = {}
 
 
 def _ptr(t):
@@ -41,14 +47,30 @@ def _need(t, dtype, name, ndim=None):
         raise ValueError(f"{name}: expected {ndim} dims, got {tuple(t.shape)}")
 
 
+def _grown(cache: dict, key, nbytes: int, device, what: str):
+    """The cached buffer of at least nbytes, or a new one that replaces it
+    (the old one is retired, not freed).  Growth is by at least 1.5x, so a
+    sequence of larger calls retires only a few buffers.  Growing while the
+    current stream is being captured into a graph raises: the capture would
+    hold a pointer that a later, larger eager call cannot replace."""
+    buf = cache.get(key)
+    if buf is not None and buf.numel() >= nbytes:
+        return buf, False
+    if torch.cuda.is_current_stream_capturing():
+        raise _lib.PmoeError(f"{what} workspace would grow to {nbytes} B during graph capture; "
+                             "run the largest call once before capturing")
+    size = max(int(nbytes), 256)
+    if buf is not None:
+        size = max(size, buf.numel() * 3 // 2)
+        _RETIRED[what].append(buf)
+    buf = torch.empty(size, dtype=torch.uint8, device=device)
+    cache[key] = buf
+    return buf, True
+
+
 def workspace(nbytes: int, device) -> torch.Tensor:
     """A cached uint8 scratch tensor of at least nbytes on device."""
-    key = (torch.device(device).index or 0)
-    buf = _WS.get(key)
-    if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
-        _WS[key] = buf
-    return buf
+    return _grown(_WS, torch.device(device).index or 0, nbytes, device, "dispatch")[0]
 
 
 # ---------------------------------------------------------------- routing
@@ -164,15 +186,63 @@ def moe_workspace(g: Geom, n: int, k: int, shared: int, n_experts: int, device,
     the cached buffer is separate from the dispatch scratch so nothing else
     ever writes the header.  fresh=True returns a new, private buffer."""
     nb = max(int(lib().pmoe_moe_workspace(ctypes.byref(g), n, k, shared, n_experts)), 256)
-    key = (torch.device(device).index or 0)
-    buf = None if fresh else _MOE_WS.get(key)
-    if buf is None or buf.numel() < nb:
+    if fresh:
         buf = torch.empty(nb, dtype=torch.uint8, device=device)
         check(lib().pmoe_moe_workspace_init(_ptr(buf), buf.numel(), _stream()),
               "pmoe_moe_workspace_init")
-        if not fresh:
-            _MOE_WS[key] = buf
+        return buf
+    buf, new = _grown(_MOE_WS, torch.device(device).index or 0, nb, device, "MoE")
+    if new:
+        check(lib().pmoe_moe_workspace_init(_ptr(buf), buf.numel(), _stream()),
+              "pmoe_moe_workspace_init")
     return buf
+
+
+def _live_moe_workspaces():
+    return list(_MOE_WS.values()) + _RETIRED["MoE"]
+
+
+def note_workspace_errors() -> None:
+    """Enqueue, on the current stream, copies of every cached MoE
+    workspace's error word into pinned host memory (no wait).  A caller that
+    synchronises the stream next reads them with ``raise_workspace_errors``."""
+    for ws in _live_moe_workspaces():
+        host = _ERR_HOST.get(ws.data_ptr())
+        if host is None:
+            host = _ERR_HOST[ws.data_ptr()] = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        check(lib().pmoe_moe_workspace_error_async(_ptr(ws), _ptr(host), _stream()),
+              "pmoe_moe_workspace_error_async")
+
+
+def raise_workspace_errors() -> None:
+    """After a stream sync that followed ``note_workspace_errors``: raise
+    PmoeError if a grid barrier of the one-launch decode timed out (those
+    layer outputs are NaN).  The failed workspace is re-initialised first,
+    so the next call runs normally."""
+    bad = [ws for ws in _live_moe_workspaces()
+           if int(_ERR_HOST.get(ws.data_ptr(), torch.zeros(1, dtype=torch.int32))[0]) != 0]
+    if not bad:
+        return
+    for ws in bad:
+        _ERR_HOST[ws.data_ptr()].zero_()
+        check(lib().pmoe_moe_workspace_init(_ptr(ws), ws.numel(), _stream()),
+              "pmoe_moe_workspace_init")
+    raise _lib.PmoeError("one-launch decode: a grid-barrier wait timed out (a block was not "
+                         "resident in time); the affected layer outputs are NaN")
+
+
+def check_workspace_errors() -> None:
+    """Synchronising form of note + raise, for sync points of their own
+    (get_stats)."""
+    note_workspace_errors()
+    torch.cuda.current_stream().synchronize()
+    raise_workspace_errors()
+
+
+def set_barrier_spin(ticks: int) -> None:
+    """Debug: grid-barrier poll limit of later one-launch decode calls in
+    100 MHz ticks (0 = the default 0.5 s); see pmoe_set_barrier_spin."""
+    check(lib().pmoe_set_barrier_spin(int(ticks)), "pmoe_set_barrier_spin")
 
 
 def workspace_error(ws: torch.Tensor) -> int:

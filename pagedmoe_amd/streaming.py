@@ -19,6 +19,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
+from . import config
 from . import kernels as K
 from ._lib import geom as make_geom
 from .cache import ExpertCache
@@ -73,7 +74,13 @@ class StreamedSwitchGLU(nn.Module):
     GPU.  Otherwise the routed ids reach the host (the one sync per layer the
     reference also pays, streaming.py:1103-1129), the cache copies the misses
     from the pinned host store and publishes the expert->slot table, and the
-    expert kernels read the slab through that table."""
+    expert kernels read the slab through that table.
+
+    Calls of at most ``config.DECODE_MAX_TOKENS`` tokens use the decode
+    residency policy (hits move to MRU, misses may evict).  Longer calls are
+    prefill (streaming.py:1313+, cache.py:2535-2578): fetch groups that never
+    evict and leave the decode hot set's recency alone, each group's copies
+    issued while the previous group computes."""
 
     def __init__(self, layer_key, original: QuantizedSwitchGLU | None, cache: ExpertCache,
                  ring=None, predictor=None):
@@ -86,19 +93,31 @@ class StreamedSwitchGLU(nn.Module):
         self.hidden, self.inter, self.bits = g.hidden, g.inter, g.bits
         self.n_experts = cache.n_experts
         self.last_ids: list[int] = []
+        # prefill fetch groups of the last call: the first group's ids, then
+        # ("open" | "after_done", ids) for each later group -- requested while
+        # the previous group still held its slots, or after it gave them back
+        self.last_groups: list = []
 
     @property
     def geom(self):
         return self.cache.geom
 
-    def plan_groups(self, indices: torch.Tensor) -> list:
-        """The layer's distinct routed ids (one host sync) split into fetch
-        groups that each fit the slab's routed slots; already resident ids
-        go first so they are not evicted by their own layer.  A single
-        group is the normal case; several happen only when one layer routes
-        to more experts than the slab holds (long prefill chunks on a small
-        slab), the bounded-memory grouping of cache.py:2535-2578."""
+    def routed_ids(self, indices: torch.Tensor) -> list:
+        """The layer's distinct routed ids, ascending (one host sync).  The
+        sync also carries the MoE workspaces' error words: a timed-out grid
+        barrier of an earlier one-launch decode raises here."""
+        K.note_workspace_errors()
         ids = [e for e in torch.unique(indices.reshape(-1)).tolist() if 0 <= e < self.n_experts]
+        K.raise_workspace_errors()
+        return ids
+
+    def plan_groups(self, indices: torch.Tensor) -> list:
+        """Decode-policy fetch groups: the distinct routed ids split into
+        groups that each fit the slab's routed slots, already resident ids
+        first so they are not evicted by their own layer.  One group is the
+        normal case; several happen only when a decode call routes to more
+        experts than the slab holds."""
+        ids = self.routed_ids(indices)
         cap = self.cache.routed_slots
         if len(ids) <= cap:
             return [ids]
@@ -106,47 +125,116 @@ class StreamedSwitchGLU(nn.Module):
         ordered = [e for e in ids if table[e] >= 0] + [e for e in ids if table[e] < 0]
         return [sorted(ordered[i:i + cap]) for i in range(0, len(ordered), cap)]
 
-    def prepare(self, indices: torch.Tensor) -> int:
-        """Make this layer's routed experts resident (they must fit in one
-        fetch group); returns the table pointer to compute with."""
-        if not self.cache.stitched:
-            groups = self.plan_groups(indices)
-            if len(groups) != 1:
-                raise RuntimeError("routed experts exceed the slab; use run_groups")
-            self.cache.fetch(self.layer_key, groups[0])
-            self.last_ids = groups[0]
-        return self.cache.table_ptr(self.layer_key)
+    def passes(self, indices: torch.Tensor):
+        """Make the routed experts resident, one fetch group at a time.
+        Yields (member ids, or None when this pass covers every routed id;
+        device table pointer); the caller enqueues the pass's compute before
+        resuming the generator, and must run it to the end."""
+        c, lk = self.cache, self.layer_key
+        if c.stitched:
+            yield None, c.table_ptr(lk)
+            return
+        n_tokens = indices.reshape(-1, indices.shape[-1]).shape[0]
+        if n_tokens <= config.DECODE_MAX_TOKENS:
+            yield from self._decode_passes(self.plan_groups(indices))
+        else:
+            yield from self._prefill_passes(self.routed_ids(indices))
 
-    def run_groups(self, x2: torch.Tensor, ind2: torch.Tensor, groups: list) -> torch.Tensor:
-        """Per-slot outputs [N, K, D] computed one fetch group at a time:
-        each pass sees only its group's ids (others dropped to zero rows) and
-        its rows are merged by selection, so every row is bit-identical to a
-        single pass over a slab that holds all of them."""
-        c = self.cache
-        y = None
+    def _decode_passes(self, groups):
+        c, lk = self.cache, self.layer_key
         for grp in groups:
-            c.fetch(self.layer_key, grp)
-            member = torch.isin(ind2, torch.tensor(grp, dtype=torch.int32, device=ind2.device))
-            ind_g = torch.where(member, ind2, torch.full_like(ind2, -1))
-            y_g = K.switch_glu(c.geom, c.slab.buf, c.table_ptr(self.layer_key), self.n_experts,
-                               x2, ind_g)
-            y = y_g if y is None else torch.where(member[..., None], y_g, y)
-        c.group_passes += len(groups)
+            c.fetch(lk, grp)
+            yield (None if len(groups) == 1 else grp), c.table_ptr(lk)
+        c.group_passes += len(groups) - 1
         self.last_ids = [e for grp in groups for e in grp]
+
+    def _prefill_passes(self, ids):
+        """Prefill fetch groups: resident ids (hits) ride with the first
+        group; the misses are cut into groups no larger than the stage's
+        group size and the free + stage slots left.  Group i+1's policy step
+        and copies are issued right after group i's compute is enqueued, so
+        they run under it; its copies wait only for the compute before
+        group i (the slots group i holds are not handed out until then)."""
+        c, lk = self.cache, self.layer_key
+        table = c.host_table(lk)
+        hits = [e for e in ids if table[e] >= 0]
+        pending = [e for e in ids if table[e] < 0]
+        per = int(c.geom.expert_bytes)
+        group_max = max(1, min(config.GROUP_BYTES,
+                               max(config.PREFILL_STAGE_GROUP_MB << 20, 8 * per)) // per)
+
+        def take():
+            free, stage, _ = c.capacity()
+            n = min(group_max, free + stage, len(pending))
+            grp = pending[:n]
+            del pending[:n]
+            return grp
+
+        c.fence()
+        first = hits + take()
+        if pending and len(first) == len(hits):
+            # no free or stage slot at all: the decode policy (which evicts)
+            # for every miss
+            yield from self._decode_passes([hits] + self._cut(pending) if hits else
+                                           self._cut(pending))
+            return
+        cur = c.fetch_prefill(lk, first)
+        self.last_groups = [cur.ids]
+        single = not pending
+        n_pass = 0
+        while cur is not None:
+            c.publish_group(cur)
+            c.join()
+            c.fence()
+            yield (None if single else cur.ids), c.table_ptr(lk)
+            n_pass += 1
+            nxt = None
+            if pending:
+                grp = take()
+                if not grp:
+                    # the current group holds every slot left: it goes back
+                    # first, and the next copies wait for its compute
+                    c.prefill_done(cur)
+                    cur = None
+                    c.fence()
+                    grp = take()
+                if grp:
+                    nxt = c.fetch_prefill(lk, grp)
+                    self.last_groups.append(("after_done" if cur is None else "open", nxt.ids))
+            if cur is not None:
+                c.prefill_done(cur)
+            cur = nxt
+        c.sync_table(lk)
+        c.group_passes += n_pass - 1
+        self.last_ids = list(ids)
+
+    def _cut(self, ids):
+        cap = self.cache.routed_slots
+        return [ids[i:i + cap] for i in range(0, len(ids), cap)]
+
+    def run_passes(self, ind2: torch.Tensor, compute) -> torch.Tensor:
+        """Per-slot outputs [N, K, D] over every pass of ``passes``:
+        ``compute(ids, table)`` runs one pass.  A pass over a subset of the
+        routed ids sees the others dropped to -1 (zero rows), and its rows are
+        merged by selection, so every row is bit-identical to a single pass
+        over a slab that holds every routed expert."""
+        y = None
+        for member, table in self.passes(ind2):
+            if member is None:
+                y = compute(ind2, table)
+                continue
+            keep = torch.isin(ind2, torch.tensor(member, dtype=torch.int32, device=ind2.device))
+            y_g = compute(torch.where(keep, ind2, torch.full_like(ind2, -1)), table)
+            y = y_g if y is None else torch.where(keep[..., None], y_g, y)
         return y
 
     def forward(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         lead = indices.shape
         x2 = x.reshape(-1, self.hidden).to(torch.bfloat16).contiguous()
         ind2 = indices.reshape(-1, lead[-1]).to(torch.int32).contiguous()
-        if not self.cache.stitched:
-            groups = self.plan_groups(ind2)
-            if len(groups) > 1:
-                return self.run_groups(x2, ind2, groups).reshape(*lead, self.hidden)
-            self.cache.fetch(self.layer_key, groups[0])
-            self.last_ids = groups[0]
-        table = self.cache.table_ptr(self.layer_key)
-        y = K.switch_glu(self.cache.geom, self.cache.slab.buf, table, self.n_experts, x2, ind2)
+        c = self.cache
+        y = self.run_passes(ind2, lambda ids, table: K.switch_glu(
+            c.geom, c.slab.buf, table, self.n_experts, x2, ids))
         return y.reshape(*lead, self.hidden)
 
 
@@ -187,13 +275,17 @@ class _MoEBlock(nn.Module):
                 inds, w = K.route_sigmoid_group_topk(logits, self._score_bias(), self.n_group,
                                                      self.topk_group, self.top_k,
                                                      self.norm_topk_prob, self.routed_scale)
-            groups = sm.plan_groups(inds)
-            if len(groups) == 1:
-                sm.cache.fetch(sm.layer_key, groups[0])
-                table = sm.cache.table_ptr(sm.layer_key)
-                out = K.moe_experts(g, slab, table, n_exp, x2, inds, w, shared_slot, sg)
-            else:
-                y = sm.run_groups(x2, inds, groups)
+            out = None
+            y = None
+            for member, tab in sm.passes(inds):
+                if member is None:
+                    out = K.moe_experts(g, slab, tab, n_exp, x2, inds, w, shared_slot, sg)
+                    continue
+                keep = torch.isin(inds, torch.tensor(member, dtype=torch.int32, device=x2.device))
+                y_g = K.switch_glu(g, slab, tab, n_exp, x2,
+                                   torch.where(keep, inds, torch.full_like(inds, -1)))
+                y = y_g if y is None else torch.where(keep[..., None], y_g, y)
+            if out is None:
                 shared_y = shared_logit = None
                 if shared_slot >= 0:
                     one = torch.full((1,), shared_slot, dtype=torch.int32, device=x2.device)
@@ -273,27 +365,27 @@ class SigmoidGroupMoEBlock(_MoEBlock):
 
 # ---------------------------------------------------------------- model surgery
 
+def _layer_order(path: str) -> tuple:
+    """Sort key of a module path: its integer components in order
+    ("model.layers.12.mlp.switch_mlp" -> (12,)), so layers sort numerically
+    and paths without an index come first."""
+    return tuple(int(p) for p in path.split(".") if p.isdecimal())
+
+
 def find_switch_glus(model: nn.Module):
-    """All QuantizedSwitchGLU modules with their tree paths, in layer order
-    (streaming.py:2512-2526)."""
+    """[(path, module)] of every QuantizedSwitchGLU in ``model``, in layer
+    order (replaces streaming.py:2512-2526)."""
     found = [(p, m) for p, m in model.named_modules() if isinstance(m, QuantizedSwitchGLU)]
-
-    def layer_num(path):
-        for part in path.split("."):
-            if part.isdigit():
-                return int(part)
-        return 0
-
-    found.sort(key=lambda kv: layer_num(kv[0]))
-    return found
+    return sorted(found, key=lambda pm: _layer_order(pm[0]))
 
 
-def _resolve_parent(model, path: str):
-    parts = path.split(".")
-    obj = model
-    for p in parts[:-1]:
-        obj = obj[int(p)] if p.isdigit() else getattr(obj, p)
-    return obj, parts[-1]
+def _swap_module(model: nn.Module, path: str, new: nn.Module) -> None:
+    """Put ``new`` where ``path`` names a submodule.  nn.Module registers a
+    child under its attribute name and nn.ModuleList under the decimal index
+    string, so one setattr on the parent covers both."""
+    parent_path, _, name = path.rpartition(".")
+    parent = model.get_submodule(parent_path) if parent_path else model
+    setattr(parent, name, new)
 
 
 def build_cache_for(model: nn.Module, slots: int, model_path=None, **kw) -> ExpertCache:
@@ -353,15 +445,9 @@ def patch_model(model: nn.Module, cache: ExpertCache, tensor_index=None, prefetc
     glus = find_switch_glus(model)
     if not glus:
         raise ValueError("no QuantizedSwitchGLU modules found - this model has no MoE layers")
-    streamed = []
-    for path, module in glus:
-        s = StreamedSwitchGLU(path, module, cache)
-        parent, attr = _resolve_parent(model, path)
-        if attr.isdigit():
-            parent[int(attr)] = s
-        else:
-            setattr(parent, attr, s)
-        streamed.append(s)
+    streamed = [StreamedSwitchGLU(path, module, cache) for path, module in glus]
+    for (path, _), s in zip(glus, streamed):
+        _swap_module(model, path, s)
     model._pagedmoe_cache = cache
     model._pagedmoe_ring = streamed
     if cache.n_experts * len(glus) <= cache.routed_slots:
@@ -371,6 +457,7 @@ def patch_model(model: nn.Module, cache: ExpertCache, tensor_index=None, prefetc
 
 def get_stats(model: nn.Module) -> dict:
     """Residency counters of a patched model (loader.py:1003)."""
+    K.check_workspace_errors()
     cache = getattr(model, "_pagedmoe_cache", None)
     if cache is None:
         return {}

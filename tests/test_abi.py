@@ -58,3 +58,32 @@ def test_workspace_query_is_host_only():
     g = _lib.geom(4096, 1536, 4)
     nb = _lib.lib().pmoe_moe_workspace(ctypes.byref(g), 8, 8, 0, 128)
     assert nb > 8 * 8 * 1536 * 2 + 8 * 8 * 4096 * 4
+
+
+@pytest.mark.parametrize("n", [1, 2])
+@pytest.mark.parametrize("cfg", [
+    dict(scoring=0, n_experts=8, top_k=9),                                  # k > E
+    dict(scoring=1, n_experts=30, top_k=4, n_group=8, topk_group=4),        # E % n_group
+    dict(scoring=1, n_experts=32, top_k=4, n_group=8, topk_group=9),        # topk_group > n_group
+    dict(scoring=1, n_experts=32, top_k=9, n_group=8, topk_group=2),        # k > kept experts
+    dict(scoring=7, n_experts=32, top_k=4),                                 # unknown scoring
+])
+def test_moe_block_rejects_bad_routing_before_any_launch(n, cfg):
+    """pmoe_moe_block validates the routing config once, before it chooses
+    the one-launch (n = 1) or three-launch (n = 2) decode; the host rejects
+    it, so nothing is launched and the dummy pointers are never read."""
+    lib = _lib.lib()
+    g = _lib.geom(1024, 512, 4)
+    rc = _lib.RouteCfg()
+    rc.scoring = cfg["scoring"]
+    rc.n_experts = cfg["n_experts"]
+    rc.top_k = cfg["top_k"]
+    rc.norm_topk_prob = 1
+    rc.n_group = cfg.get("n_group", 1)
+    rc.topk_group = cfg.get("topk_group", 1)
+    rc.routed_scale = 1.0
+    dummy = ctypes.c_void_p(0x1000)
+    r = lib.pmoe_moe_block(ctypes.byref(g), ctypes.byref(rc), dummy, dummy, dummy, dummy, None,
+                           dummy, n, -1, None, dummy, dummy, dummy, dummy, 1 << 30, None)
+    assert r == -1, lib.pmoe_last_error()
+    assert b"routing" in lib.pmoe_last_error()

@@ -257,3 +257,81 @@ def test_routing_512_experts_vs_oracle(n, fused):
     ref_i, ref_w = O.softmax_topk(O.router_logits(xb, layer.gwb), k)
     assert np.array_equal(inds.cpu().numpy(), ref_i)
     assert np.array_equal(wts.cpu().numpy(), ref_w)
+
+
+def test_barrier_timeout_poisons_output_and_is_reported():
+    """A grid-barrier wait that gives up (forced from the host with a
+    one-tick spin limit on the kernel's own bounded wait, so every block
+    still exits normally) sets error bit 0, leaves NaN in the layer output
+    instead of a plausible wrong answer, and raises PmoeError at the next
+    host sync point, which also re-initialises the workspace."""
+    from pagedmoe_amd._lib import PmoeError
+    K = _k()
+    layer = _Layer(4096, 128, 1536, 8, seed=9)
+    ws = K.moe_workspace(layer.g, 1, 8, 0, 128, DEV)   # the cached one the sync points read
+    x = layer.x(1, seed=900)
+    good, _, _ = layer.run(x, ws=ws)
+    torch.cuda.synchronize()
+    assert K.workspace_error(ws) == 0
+    print("[fused] barrier spin limit 1 tick", flush=True)
+    K.set_barrier_spin(1)
+    try:
+        bad, _, _ = layer.run(x, ws=ws)
+        torch.cuda.synchronize()
+    finally:
+        K.set_barrier_spin(0)
+    assert K.workspace_error(ws) & 1
+    assert torch.isnan(bad.float()).all(), "a timed-out layer wrote finite outputs"
+    with pytest.raises(PmoeError, match="timed out"):
+        K.check_workspace_errors()
+    again, _, _ = layer.run(x, ws=ws)
+    torch.cuda.synchronize()
+    assert K.workspace_error(ws) == 0
+    assert torch.equal(again.view(torch.int16), good.view(torch.int16))
+
+
+def test_graph_on_cached_workspace_survives_a_larger_call(monkeypatch):
+    """A graph captured over the cached workspace keeps its raw pointer; a
+    later, larger eager call (a prefill) replaces the cached workspace but
+    must not free the old one, so replays stay bit-identical to eager runs.
+    Growing the workspace during a capture is refused."""
+    from pagedmoe_amd._lib import PmoeError
+    K = _k()
+    dev = torch.device(DEV).index or 0
+    old = K._MOE_WS.pop(dev, None)
+    if old is not None:
+        K._RETIRED["MoE"].append(old)
+    layer = _Layer(1024, 32, 512, 4, seed=11)
+    out = torch.empty((1, 1024), dtype=torch.bfloat16, device=DEV)
+    inds = torch.empty((1, 4), dtype=torch.int32, device=DEV)
+    wts = torch.empty((1, 4), dtype=torch.float32, device=DEV)
+    x = torch.empty((1, 1024), dtype=torch.bfloat16, device=DEV)
+    x.copy_(layer.x(1, seed=1100))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        layer.run(x, out=out, inds=inds, weights=wts)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    captured = K._MOE_WS[dev].data_ptr()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        layer.run(x, out=out, inds=inds, weights=wts)
+    torch.cuda.synchronize()
+    big, _, _ = layer.run(layer.x(512, seed=1101))      # grows the cached workspace
+    torch.cuda.synchronize()
+    assert K._MOE_WS[dev].data_ptr() != captured
+    assert any(b.data_ptr() == captured for b in K._RETIRED["MoE"])
+    filler = torch.full((64 << 20,), 7, dtype=torch.uint8, device=DEV)  # reuses freed memory
+    for rep in range(3):
+        x.copy_(layer.x(1, seed=1110 + rep))
+        graph.replay()
+        torch.cuda.synchronize()
+        ref, ri, rw = layer.run(x.clone())
+        torch.cuda.synchronize()
+        assert torch.equal(ri, inds) and torch.equal(rw, wts)
+        assert torch.equal(ref.view(torch.int16), out.view(torch.int16)), rep
+    del filler, big
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    with pytest.raises(PmoeError, match="during graph capture"):
+        K.moe_workspace(layer.g, 4096, 4, 0, 32, DEV)

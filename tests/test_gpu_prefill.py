@@ -121,11 +121,30 @@ def test_prefill_sigmoid_shared_vs_oracle():
     check_close(out.float().cpu().numpy(), ref, "prefill sigmoid + shared")
 
 
+def _tile_boundary_tokens(inds, tile_m):
+    """Tokens whose rows sit at the row-tile edges of the heaviest expert:
+    the first and last row of every 128-row tile, and the partial last tile's
+    last row.  The dispatch orders an expert's rows by flat index
+    (token * K + slot), so the expert's p-th row is its p-th occurrence in
+    the flat routing."""
+    flat = inds.reshape(-1)
+    counts = np.bincount(flat, minlength=int(flat.max()) + 1)
+    heavy = int(np.argmax(counts))
+    rows = np.flatnonzero(flat == heavy)
+    pos = {0, len(rows) - 1}
+    for t0 in range(0, len(rows), tile_m):
+        pos.update({t0, min(t0 + tile_m - 1, len(rows) - 1)})
+    k = inds.shape[1]
+    return sorted({int(rows[p]) // k for p in pos})
+
+
 def test_prefill_qwen3_235b_2048_tokens_sampled():
     """Full prefill shape: D4096/E128/I1536 top-8 4-bit, 2048 tokens with
     router logits skewed by a N(0,1) per-expert bias.  Routing of every token
-    bit-exact (C oracle router); the layer output of 12 sampled tokens within
-    tolerance of the fp32 C restatement of the experts."""
+    bit-exact (C oracle router); the layer output of the tokens at the
+    heaviest expert's row-tile edges (first and last row of each 128-row tile,
+    the partial last tile) and of 6 random tokens within tolerance of the
+    fp32 C restatement of the experts."""
     K = _k()
     from pagedmoe_amd._lib import geom
     from pagedmoe_amd.slab import SlabStore
@@ -147,7 +166,7 @@ def test_prefill_qwen3_235b_2048_tokens_sampled():
     assert np.array_equal(gi.cpu().numpy(), ref_i)
     assert np.array_equal(gwt.cpu().numpy(), ref_w)
     out = out.float().cpu().numpy()
-    sample = rng.choice(2048, 12, replace=False)
+    sample = _tile_boundary_tokens(ref_i, 128) + [int(t) for t in rng.choice(2048, 6, replace=False)]
     cache = {}
     for t in sample:
         x = O.bf16_to_f32(xb[t])
@@ -164,8 +183,9 @@ def test_prefill_qwen3_next_1024_tokens_sampled():
     """Full Qwen3-Next prefill shape: D2048/E512/I512 top-10 6-bit plus a
     sigmoid-gated shared expert, 1024 tokens (10,240 routed rows over 512
     experts, ~20 per expert: one partial tile each).  Routing of every token
-    bit-exact (C oracle router); the layer output of 10 sampled tokens within
-    tolerance of the fp32 C restatement of the experts."""
+    bit-exact (C oracle router); the layer output of the tokens at the
+    heaviest expert's tile edges and of 6 random tokens within tolerance of
+    the fp32 C restatement of the experts."""
     K = _k()
     from pagedmoe_amd._lib import geom
     from pagedmoe_amd.slab import SlabStore
@@ -188,7 +208,7 @@ def test_prefill_qwen3_next_1024_tokens_sampled():
     out = out.float().cpu().numpy()
     gate_logit = C.router_logits(xb, sgb)[:, 0].astype(np.float64)
     shared = slot_to_expert(slab, E)
-    sample = rng.choice(1024, 10, replace=False)
+    sample = _tile_boundary_tokens(ref_i, 128) + [int(t) for t in rng.choice(1024, 6, replace=False)]
     cache = {}
     for t in sample:
         x = O.bf16_to_f32(xb[t])

@@ -357,3 +357,124 @@ def test_paged_block_reads_experts_from_a_safetensors_checkpoint(tmp_path):
             check_close(out.float().cpu().numpy(), ref, f"checkpoint paging step {step} layer {li}")
     assert cache.stats()["misses"] > 0
     cache.close()
+
+
+# ---------------------------------------------------------------- prefill residency
+
+def _replay_prefill(pol, layer, groups):
+    """The oracle policy over one prefill call's fetch groups, in the order
+    the seam issued them (a group opened while the previous one still held
+    its slots, or after it gave them back)."""
+    t, _, _ = pol.step_prefill(layer, groups[0])
+    for how, ids in groups[1:]:
+        if how == "after_done":
+            pol.prefill_done(t)
+            t, _, _ = pol.step_prefill(layer, ids)
+        else:
+            t2, _, _ = pol.step_prefill(layer, ids)
+            pol.prefill_done(t)
+            t = t2
+    pol.prefill_done(t)
+
+
+@pytest.mark.parametrize("stage", [6, 64])
+def test_prefill_groups_keep_the_decode_hot_set(stage):
+    """32-token calls take the prefill policy (cache.py:2347-2453 with
+    prefill=True): hits are not touched, misses never evict, and groups whose
+    copies run under the previous group's compute give rows bit-identical to
+    the resident module.  With a 6-slot stage a call needs several groups
+    that reuse stage slots; with 64, one group.  Tables and counters follow
+    the oracle policy replayed over the same groups, and the decode hot set
+    survives the prefill."""
+    from pagedmoe_amd.cache import ExpertCache, HostExpertStore
+
+    _, S = _mods()
+    spec = O.LayerSpec(1024, 32, 512, 4)
+    model, _ = _softmax_model(spec, 2, seed=120)
+    resident = [layer.mlp.switch_mlp for layer in model.layers]
+    glus = S.find_switch_glus(model)
+    g = glus[0][1].geom
+    store = HostExpertStore(g, 2, spec.experts)
+    for li, (_, m) in enumerate(glus):
+        for e in range(spec.experts):
+            store.write_from_slot(li, e, m.slab, e)
+    cache = ExpertCache(g, 16, [p for p, _ in glus], spec.experts, host_store=store,
+                        stage_slots=stage)
+    streamed = S.patch_model(model, cache)
+    assert not cache.stitched
+    pol = O.SlotPolicy(16)
+    pol.set_stage(cache.stage_first, stage)
+    rng = np.random.default_rng(121)
+    hot = [3, 7, 11, 19]
+
+    def call(li, n, ids):
+        x = bits_to_bf16_tensor(O.bf16_round(rng.standard_normal((n, spec.hidden),
+                                                                 dtype=np.float32)), DEV)
+        ind = torch.from_numpy(ids.astype(np.int32)).to(DEV)
+        got = streamed[li](x, ind)
+        ref = resident[li](x, ind)
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), (li, n)
+
+    for _ in range(3):  # decode: the hot set becomes resident with reuse credit
+        for li in range(2):
+            ids = np.array([hot], dtype=np.int32)
+            call(li, 1, ids)
+            pol.step(streamed[li].layer_key, ids.reshape(-1))
+    ev0 = cache.stats()["evictions"]
+    for li in range(2):
+        ids = np.stack([rng.choice(spec.experts, spec.top_k, replace=False) for _ in range(32)])
+        call(li, 32, ids)
+        groups = streamed[li].last_groups
+        _replay_prefill(pol, streamed[li].layer_key, groups)
+        if stage == 6:
+            assert len(groups) >= 3, groups
+        for lk in (s.layer_key for s in streamed):
+            assert np.array_equal(cache.host_table(lk), pol.table(lk, spec.experts)), lk
+    st = cache.stats()
+    assert st["evictions"] == ev0, "a prefill call evicted"
+    assert (st["hits"], st["misses"]) == (pol.hits, pol.misses)
+    for s in streamed:
+        t = cache.host_table(s.layer_key)
+        assert all(t[e] >= 0 for e in hot), "the decode hot set was flushed by a prefill"
+    # the device rows are the persistent tables again (the groups' held
+    # slots are not visible once the call is over)
+    for s in streamed:
+        assert not cache.table_dirty(s.layer_key)
+        assert np.array_equal(cache.device_table(s.layer_key), cache.host_table(s.layer_key))
+    cache.close()
+    store.close()
+
+
+def test_flow_table_republishes_rows_another_layer_evicted():
+    """Layer 0's fetch evicts layer 1's expert; layer 1's device row is then
+    stale until flow_table(layer 1) republishes it (cache.py:821-859), after
+    which it shows -1 for that expert."""
+    from pagedmoe_amd.cache import ExpertCache, HostExpertStore
+
+    _, S = _mods()
+    spec = O.LayerSpec(1024, 16, 512, 4)
+    model, _ = _softmax_model(spec, 2, seed=130)
+    glus = S.find_switch_glus(model)
+    g = glus[0][1].geom
+    store = HostExpertStore(g, 2, spec.experts)
+    for li, (_, m) in enumerate(glus):
+        for e in range(spec.experts):
+            store.write_from_slot(li, e, m.slab, e)
+    keys = [p for p, _ in glus]
+    cache = ExpertCache(g, 8, keys, spec.experts, host_store=store, stage_slots=0)  # budget 4
+
+    device_row = cache.device_table
+    cache.fetch(keys[1], [5])
+    cache.fetch(keys[0], [0, 1, 2])
+    torch.cuda.synchronize()
+    assert device_row(keys[1])[5] >= 0
+    assert not cache.table_dirty(keys[1])
+    cache.fetch(keys[0], [3])            # 5 resident > budget 4: layer 1's 5 is the LRU head
+    assert cache.host_table(keys[1])[5] == -1
+    assert cache.table_dirty(keys[1])
+    assert device_row(keys[1])[5] >= 0   # stale until republished
+    cache.flow_table(keys[1])
+    assert device_row(keys[1])[5] == -1
+    assert not cache.table_dirty(keys[1])
+    cache.close()
+    store.close()

@@ -480,3 +480,136 @@ def test_plain_lru_brute_force():
                     victim = next(v for v in lru if v not in ids)
                     lru.remove(victim)
         assert [e for (_, e) in pol.lru] == lru
+
+
+class _OracleSlots:
+    """slot_kats adapter over the oracle's SlotPolicy (layer 0)."""
+
+    def __init__(self, slots, lfru=True, stage=None):
+        self.pol = O.SlotPolicy(slots, lfru=lfru)
+        if stage is not None:
+            self.pol.set_stage(*stage)
+
+    def step(self, ids):
+        return self.pol.step(0, ids)[1]
+
+    def prefill(self, ids):
+        return self.pol.step_prefill(0, ids)
+
+    def compute_row(self, ticket):
+        row = self.pol.compute_row(ticket, 64)
+        return {e: int(s) for e, s in enumerate(row) if s >= 0}
+
+    def done(self, ticket):
+        self.pol.prefill_done(ticket)
+
+    def table(self):
+        return {e: int(s) for e, s in enumerate(self.pol.table(0, 64)) if s >= 0}
+
+    @property
+    def evictions(self):
+        return self.pol.evictions
+
+
+@pytest.mark.parametrize("name", ["LFRU_SECOND_CHANCE", "PINNED_OVER_BUDGET"])
+def test_lfru_known_answer(name):
+    """Hand-worked traces of the LFRU second chance (cache.py:2236-2291)."""
+    from tests import slot_kats
+    kat = getattr(slot_kats, name)
+    slot_kats.run_decode_kat(_OracleSlots(kat["slots"]), kat)
+
+
+def test_plain_lru_known_answer():
+    from tests import slot_kats
+    kat = slot_kats.PLAIN_LRU
+    slot_kats.run_decode_kat(_OracleSlots(kat["slots"], lfru=False), kat)
+
+
+@pytest.mark.parametrize("name", ["PREFILL_AFTER_DECODE", "PREFILL_COLD"])
+def test_prefill_known_answer(name):
+    """Prefill groups never evict and leave the decode hot set's recency
+    alone (cache.py:2347-2453 with prefill=True, _install soft :2306-2312)."""
+    from tests import slot_kats
+    kat = getattr(slot_kats, name)
+    slot_kats.run_prefill_kat(_OracleSlots(kat["slots"], stage=kat["stage"]), kat)
+
+
+class _ListLFRU:
+    """An LFRU slab written as a plain list (LRU first) plus a counter dict,
+    from the reference's description alone (cache.py:2236-2291 second chance,
+    :2367-2378 reuse credit, :1118-1159 slot choice, :991 free list)."""
+
+    def __init__(self, slots, scan=8, cap=8):
+        self.free = list(range(slots))[::-1]
+        self.budget = slots - max(4, int(slots * 0.1))
+        self.scan, self.cap = scan, cap
+        self.order, self.count, self.where = [], {}, {}
+        self.evicted = 0
+        self.reprieves = 0
+
+    def _drop(self, e):
+        self.order.remove(e)
+        del self.count[e]
+        self.evicted += 1
+        return self.where.pop(e)
+
+    def step(self, ids):
+        ids = sorted(set(int(i) for i in ids))
+        keep = set()
+        fresh = []
+        for e in ids:
+            if e in self.where:
+                self.order.remove(e)
+                self.order.append(e)
+                self.count[e] = min(self.cap, self.count[e] + 1)
+                keep.add(self.where[e])
+            else:
+                fresh.append(e)
+        got = []
+        for e in fresh:
+            if self.free:
+                slot = self.free.pop()
+            else:
+                cand = [v for v in self.order if self.where[v] not in keep]
+                if not cand:
+                    continue
+                slot = self._drop(cand[0])
+            keep.add(slot)
+            got.append((e, slot))
+        for e, slot in got:
+            self.where[e] = slot
+            self.count[e] = 0
+            self.order.append(e)
+            while len(self.order) > max(self.budget, 1):
+                for _ in range(self.scan):
+                    if len(self.order) <= 1 or self.count[self.order[0]] == 0:
+                        break
+                    head = self.order.pop(0)
+                    self.count[head] //= 2
+                    self.order.append(head)
+                    self.reprieves += 1
+                cand = [v for v in self.order if self.where[v] not in keep]
+                if not cand:
+                    break
+                self.free.append(self._drop(cand[0]))
+        return got
+
+
+@pytest.mark.parametrize("seed,slots,experts,k", [(0, 24, 60, 4), (1, 40, 100, 8), (2, 12, 30, 3)])
+def test_lfru_matches_list_implementation(seed, slots, experts, k):
+    """The oracle's LFRU against the list-plus-counter restatement over
+    random Zipf-skewed traces (so reuse credit and second chances occur)."""
+    rng = np.random.default_rng(seed)
+    pop = 1.0 / np.arange(1, experts + 1) ** 1.1
+    pop /= pop.sum()
+    pol = O.SlotPolicy(slots)
+    ref = _ListLFRU(slots)
+    for _ in range(600):
+        ids = rng.choice(experts, k, replace=False, p=pop).tolist()
+        _, placed = pol.step(0, ids)
+        got = ref.step(ids)
+        assert placed == got
+        assert [e for (_, e) in pol.lru] == ref.order
+        assert {e: pol.freq.get((0, e), 0) for (_, e) in pol.lru} == ref.count
+    assert pol.evictions == ref.evicted
+    assert ref.reprieves > 50      # the second-chance branch is exercised
