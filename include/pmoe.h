@@ -208,6 +208,24 @@ int pmoe_moe_block(const pmoe_geom* g, const pmoe_route_cfg* rc,
                    float* weights_out, void* ws, size_t ws_bytes,
                    void* stream);
 
+/* pmoe_moe_block without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * workspace is a static 32 MiB device array of the library, one per GPU,
+ * held until the process ends; its address is looked up on the first call
+ * on each device, which also zeroes its synchronisation header with a
+ * kernel.  Nothing is allocated.  Calls whose workspace would exceed 32 MiB
+ * (prefill-sized batches: pmoe_moe_workspace(g, n, k, shared, E) > 32 MiB)
+ * return PMOE_ESPACE before anything is launched.  Every call on a GPU
+ * shares that GPU's array, so calls that overlap on one GPU (several
+ * streams or threads) race; serialise them. */
+int pmoe_moe_block_noalloc(const pmoe_geom* g, const pmoe_route_cfg* rc,
+                           const void* slab, const int32_t* table,
+                           const void* gate_w, const float* score_bias,
+                           const float* logit_bias, const void* x, int n,
+                           int shared_slot, const void* shared_gate, void* out,
+                           int32_t* inds_out, float* weights_out, void* stream);
+
 /* Weighted combine of per-slot outputs: out[n] = bf16(fma over k of
  * weights[n,k] * y[n,k,:], then + s * shared_y[n,:]) with s = 1, or
  * sigmoid(shared_logit[n]) when shared_logit != NULL.  y bf16 [n, k, hidden],

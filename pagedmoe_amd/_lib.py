@@ -87,6 +87,8 @@ SIGNATURES = {
                               _P, _P, _SZ, _P]),
     "pmoe_moe_block": (_I, [ctypes.POINTER(Geom), ctypes.POINTER(RouteCfg), _P, _P, _P, _P, _P,
                             _P, _I, _I, _P, _P, _P, _P, _P, _SZ, _P]),
+    "pmoe_moe_block_noalloc": (_I, [ctypes.POINTER(Geom), ctypes.POINTER(RouteCfg), _P, _P, _P,
+                                    _P, _P, _P, _I, _I, _P, _P, _P, _P, _P]),
     "pmoe_combine": (_I, [_P, _P, _I, _I, _I, _P, _P, _P, _P]),
     "pmoe_slab_create": (_I, [ctypes.POINTER(_P), _I, _I, _I, _F, _I, _I]),
     "pmoe_slab_destroy": (_I, [_P]),

@@ -6,6 +6,9 @@
 // shared-expert add (restated tests/test_stream.py:198).  The combine is a
 // fixed-order fp32 reduction: out[n] = fma over k = 0..K-1 of w[n,k]*y[n,k],
 // then the shared expert, so results do not depend on scheduling.
+#include <mutex>
+#include <string>
+
 #include "pmoe_internal.h"
 #include "pmoe_kernels.h"
 #include "route_common.h"
@@ -489,6 +492,77 @@ extern "C" int pmoe_moe_block(const pmoe_geom* g, const pmoe_route_cfg* rc_cfg, 
                                    weights_out, n, k, shared_slot,
                                    static_cast<const uint16_t*>(shared_gate), n,
                                    static_cast<uint16_t*>(out), w, st);
+}
+
+// ---------------------------------------------------------------- no allocation
+//
+// pmoe_moe_block for callers that cannot allocate (code under HIP graph
+// capture, tight serving loops, harnesses that forbid hipMalloc): the
+// workspace is carved from `scratch`, a file-scope device array of
+// kStaticScratchBytes that each GPU holds until the process ends.  In host
+// code `scratch` only names the symbol: its device address is looked up with
+// hipGetSymbolAddress once per device (with that device current) and kept in
+// g_scratch_ptr[device]; only that address is ever passed to kernels.  The
+// same first call zeroes the array's synchronisation header with a kernel;
+// every later call leaves the header consistent, as pmoe_moe_block does for
+// a caller's workspace.  All calls on one GPU share the array, so calls that
+// overlap on one GPU (two streams, two threads) race.
+
+namespace {
+
+constexpr size_t kStaticScratchBytes = size_t(32) << 20;
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+static int scratch_for_device(void** out, hipStream_t st) {
+  int dev = -1;
+  PMOE_HIP(hipGetDevice(&dev));
+  PMOE_REQUIRE(dev >= 0 && dev < kMaxDevices, "moe_block_noalloc: device index out of range");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    PMOE_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    workspace_init_kernel<<<64, 256, 0, st>>>(static_cast<uint32_t*>(p),
+                                              int(pmoe::kSyncBytes / 4));
+    PMOE_LAUNCH_CHECK("workspace_init_kernel (static scratch)");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_moe_block_noalloc(const pmoe_geom* g, const pmoe_route_cfg* rc_cfg,
+                                      const void* slab, const int32_t* table, const void* gate_w,
+                                      const float* score_bias, const float* logit_bias,
+                                      const void* x, int n, int shared_slot,
+                                      const void* shared_gate, void* out, int32_t* inds_out,
+                                      float* weights_out, void* stream) {
+  pmoe::clear_error();
+  int rc = pmoe::check_geom(g);
+  if (rc) return rc;
+  PMOE_REQUIRE(rc_cfg != nullptr, "moe_block_noalloc: null routing config");
+  PMOE_REQUIRE(n >= 0 && rc_cfg->top_k > 0 && rc_cfg->n_experts > 0 &&
+                   rc_cfg->n_experts <= 1023,
+               "moe_block_noalloc: bad shape");
+  const size_t need = pmoe::carve(g, n, rc_cfg->top_k, shared_slot >= 0 ? 1 : 0,
+                                  rc_cfg->n_experts, nullptr, nullptr);
+  if (need > kStaticScratchBytes)
+    return pmoe::fail(PMOE_ESPACE, "moe_block_noalloc: this call needs " + std::to_string(need) +
+                                       " bytes of scratch; the static scratch holds " +
+                                       std::to_string(kStaticScratchBytes) +
+                                       " (decode-sized batches); use pmoe_moe_block with a "
+                                       "caller workspace");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  rc = scratch_for_device(&ws, st);
+  if (rc) return rc;
+  return pmoe_moe_block(g, rc_cfg, slab, table, gate_w, score_bias, logit_bias, x, n, shared_slot,
+                        shared_gate, out, inds_out, weights_out, ws, kStaticScratchBytes, stream);
 }
 
 extern "C" int pmoe_combine(const void* y, const float* weights, int n, int k, int hidden,
