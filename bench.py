@@ -11,14 +11,22 @@ N(0, 1) bf16; every step routes a fresh token.  Steps cycle over `--layers`
 distinct layers (default 8, ~11 GB of experts) so no step finds the previous
 step's experts in the 256 MB last-level cache.
 
-The timed loop replays a HIP graph of `--layers` x 4 consecutive layer steps
-(launch overhead excluded, as in the reference's one-graph-per-token decode);
-inputs are resident in HBM before timing starts, and HIP events on the replay
-stream bracket the timed replays.  roofline.achieved = algorithmic
-expert-weight bytes per launch / the dominant kernel's average duration: for
-the one-launch decode layer (the batch-1 default) a step is that one launch,
-so its duration is the event-timed graph step; for the three-launch decode a
-second, eager pass brackets every kernel with HIP events.
+The timed loop replays a HIP graph of G consecutive layer steps, G the
+largest divisor of `--steps` up to 64, `--steps`/G times, so exactly
+`--steps` steps are timed (launch overhead excluded, as in the reference's
+one-graph-per-token decode); inputs are resident in HBM before timing starts,
+and HIP events on the replay stream bracket the timed replays.  Before that,
+untimed: `--warmup` eager steps, one eager pass of G steps with every kernel
+bracketed by HIP events (per-kernel durations), one pass of G steps to warm
+the capture stream and one warm replay; "warmup" in the JSON line counts all
+of them.  roofline.achieved = algorithmic expert-weight bytes per launch /
+the dominant kernel's average duration: for the one-launch decode layer (the
+batch-1 default) a step is that one launch, so its duration is the
+event-timed graph step; for the three-launch decode it is the kernel's
+event-timed eager average.  roofline.traffic comes from the rocprofv3
+FETCH_SIZE + WRITE_SIZE profile committed under profiles/, scaled by the
+probe kernels' counters, and only when that profile's source hash matches
+the kernel sources being run.
 
 Prints ONE JSON line.  `--gpus N` with N > 1 exits: this build runs on one GPU.
 """
@@ -69,6 +77,53 @@ def build_layers(g, spec, n_layers, device, seed=0):
     return slab, gate, tables
 
 
+# kernel -> the sources its code comes from (the traffic profile is valid
+# only for the build of these files it was measured on)
+KERNEL_SOURCES = {
+    "decode_fused_kernel": ["decode_fused.hip", "gemv_common.h", "route_common.h",
+                            "pmoe_internal.h", "pmoe_kernels.h"],
+    "gateup_routed_kernel": ["decode.hip", "gemv_common.h", "route_common.h",
+                             "pmoe_internal.h", "pmoe_kernels.h"],
+    "prefill": ["prefill.hip", "dispatch.hip", "moe.hip", "pmoe_internal.h", "pmoe_kernels.h"],
+}
+
+
+def source_hash(kernel: str) -> str:
+    import hashlib
+    h = hashlib.sha256()
+    for name in KERNEL_SOURCES[kernel]:
+        h.update(name.encode())
+        h.update((ROOT / "pagedmoe_amd" / "csrc" / name).read_bytes())
+    return h.hexdigest()[:16]
+
+
+def load_traffic(name: str, kernel: str):
+    """(bytes per launch, note) from profiles/traffic_<name>.json when its
+    source hash matches the current sources of `kernel`."""
+    f = ROOT / "profiles" / f"traffic_{name}.json"
+    if not f.exists():
+        return None, f"no profiles/{f.name}"
+    try:
+        tf = json.loads(f.read_text())
+    except (ValueError, OSError) as e:
+        return None, f"profiles/{f.name}: {e}"
+    if tf.get("kernel") != kernel:
+        return None, f"profiles/{f.name} is for {tf.get('kernel')}, not {kernel}"
+    if tf.get("source_hash") != source_hash(kernel):
+        return None, (f"profiles/{f.name} was measured on other sources "
+                      f"({tf.get('source_hash')} vs {source_hash(kernel)})")
+    return tf.get("bytes_per_launch"), f"profiles/{f.name} (source {tf['source_hash']})"
+
+
+def graph_len(steps: int, cap: int = 64) -> int:
+    """Largest divisor of steps that is at most cap: the graph length that
+    lets whole replays time exactly `steps` steps."""
+    for n in range(min(cap, steps), 0, -1):
+        if steps % n == 0:
+            return n
+    return 1
+
+
 def run_decode(args, g, spec, slab, gate, tables, batch, device):
     import torch
 
@@ -77,7 +132,7 @@ def run_decode(args, g, spec, slab, gate, tables, batch, device):
 
     E, D, k = spec["experts"], spec["hidden"], spec["top_k"]
     L = args.layers
-    seq = L * 4                                   # layer steps per graph
+    seq = graph_len(args.steps)                   # layer steps per graph
     rc = K.route_cfg(spec["scoring"], E, k)
     gen = torch.Generator(device=device)
     gen.manual_seed(1000 + batch)
@@ -96,17 +151,15 @@ def run_decode(args, g, spec, slab, gate, tables, batch, device):
         for i in range(seq):
             step(i)
 
-    # eager warmup (also validates the call path)
-    for _ in range(max(1, args.warmup // seq + 1)):
-        run_seq()
+    # eager warmup (also validates the call path): exactly --warmup steps
+    for i in range(args.warmup):
+        step(i % seq)
     torch.cuda.synchronize()
 
-    # per-kernel durations: eager pass with event brackets
+    # per-kernel durations: one eager pass with event brackets
     with KernelTimer() as kt:
-        for _ in range(max(1, args.steps // seq)):
-            run_seq()
+        run_seq()
     torch.cuda.synchronize()
-    reps_timer = max(1, args.steps // seq)
 
     # graph of `seq` layer steps
     graph = torch.cuda.CUDAGraph()
@@ -118,10 +171,9 @@ def run_decode(args, g, spec, slab, gate, tables, batch, device):
     torch.cuda.synchronize()
     with torch.cuda.graph(graph):
         run_seq()
-    for _ in range(max(1, args.warmup // seq)):
-        graph.replay()
+    graph.replay()
     torch.cuda.synchronize()
-    reps = max(1, args.steps // seq)
+    reps = args.steps // seq
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -156,6 +208,9 @@ def run_decode(args, g, spec, slab, gate, tables, batch, device):
         "gpu_ms_per_step": gpu_ms,
         "tokens_per_s": batch / (ms / 1e3),
         "steps_timed": steps_timed,
+        "graph_steps": seq,
+        "graph_replays_timed": reps,
+        "untimed_steps": args.warmup + 3 * seq,
         "eager_ms_per_step": eager_ms,
         "mean_unique_experts": mean_unique,
         "expert_bytes_per_step": mean_unique * int(g.expert_bytes),
@@ -182,7 +237,8 @@ def run_decode(args, g, spec, slab, gate, tables, batch, device):
     res["_layer_bytes"] = layer_bytes
     res["layer_expert_gbs"] = res["expert_bytes_per_step"] / (ms * 1e-3) / 1e9
     res["_gateup_step_bytes"] = step_bytes_gu
-    del reps_timer
+    if ws is not None:
+        res["workspace_error"] = K.workspace_error(ws)
     return res
 
 
@@ -435,39 +491,77 @@ def run_qwen3_next(args, device, layers=2):
     return out
 
 
-def measured_ceilings(device):
-    """What this box sustains, to put the spec peaks in context: HBM
-    bandwidth of a 2 GiB device-to-device copy (read + write bytes / time)
-    and of a 2 GiB fp32 reduction (torch.sum, read bytes / time), and the bf16
-    dense GEMM rate of torch.matmul (hipBLASLt) at the prefill
-    gate/up shape (16384 x 4096 x 3072, the same 412 GFLOP)."""
+def _probe(device):
+    import ctypes
+
     import torch
 
+    from pagedmoe_amd._lib import check, lib
+
+    sink = torch.empty(int(lib().pmoe_probe_sink_bytes()), dtype=torch.uint8, device=device)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def read(t, off=0, nbytes=None):
+        nbytes = t.numel() - off if nbytes is None else nbytes
+        check(lib().pmoe_probe_read(ctypes.c_void_p(t.data_ptr() + off), nbytes,
+                                    ctypes.c_void_p(sink.data_ptr()), sink.numel(), stream),
+              "pmoe_probe_read")
+
+    def copy(dst, src):
+        check(lib().pmoe_probe_copy(ctypes.c_void_p(dst.data_ptr()),
+                                    ctypes.c_void_p(src.data_ptr()), src.numel(), stream),
+              "pmoe_probe_copy")
+
+    return read, copy
+
+
+def measured_ceilings(device, layer_bytes):
+    """What this box sustains, next to the spec peaks, measured with this
+    library's probe kernels (pmoe_probe_read / pmoe_probe_copy, HIP events):
+    a 2 GiB streaming read with the expert stream's access pattern; the same
+    read over one batch-1 layer's expert volume, cycling 8 disjoint regions
+    (more than the 256 MB last-level cache) so no pass finds its bytes in
+    cache; a 1 GiB device copy (read + write bytes); and torch.matmul's
+    (hipBLASLt) dense bf16 GEMM at the prefill gate/up shape
+    (16384 x 4096 x 3072, 412 GFLOP) -- a library figure at one shape, not a
+    ceiling for the hand-written kernels."""
+    import torch
+
+    read, copy = _probe(device)
     res = {}
-    src = torch.empty(1 << 30, dtype=torch.int16, device=device)
-    dst = torch.empty_like(src)
+    buf = torch.empty(2 << 30, dtype=torch.uint8, device=device)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for _ in range(2):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
+        read(buf)
+    ev0.record()
     for _ in range(10):
-        dst.copy_(src)
+        read(buf)
+    ev1.record()
     torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / 10
-    res["hbm_copy_gbs"] = 2 * src.numel() * 2 / dt / 1e9
-    del dst
-    srcf = src.view(torch.float32)  # fp32 reduction: torch's vectorised read path
-    for _ in range(2):
-        srcf.sum()
+    res["hbm_read_gbs"] = buf.numel() * 10 / (ev0.elapsed_time(ev1) * 1e-3) / 1e9
+    lb = int(layer_bytes) // 256 * 256
+    regions = 8
+    for r in range(regions):
+        read(buf, r * lb, lb)
+    ev0.record()
+    for rep in range(40):
+        read(buf, (rep % regions) * lb, lb)
+    ev1.record()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
+    per = ev0.elapsed_time(ev1) * 1e-3 / 40
+    res["layer_volume_read_bytes"] = lb
+    res["layer_volume_read_us"] = per * 1e6
+    res["layer_volume_read_gbs"] = lb / per / 1e9
+    half = buf.numel() // 2
+    src, dst = buf[:half], buf[half:]
+    copy(dst, src)
+    ev0.record()
     for _ in range(10):
-        srcf.sum()
+        copy(dst, src)
+    ev1.record()
     torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / 10
-    res["hbm_read_gbs"] = src.numel() * 2 / dt / 1e9
-    del srcf
-    del src
+    res["hbm_copy_gbs"] = 2 * half * 10 / (ev0.elapsed_time(ev1) * 1e-3) / 1e9
+    del buf, src, dst
     m, k, n = 16384, 4096, 3072
     a = torch.randn(m, k, device=device, dtype=torch.bfloat16)
     b = torch.randn(n, k, device=device, dtype=torch.bfloat16)
@@ -481,6 +575,8 @@ def measured_ceilings(device):
     dt = (time.perf_counter() - t0) / 10
     res["dense_bf16_gemm_tflops"] = 2.0 * m * k * n / dt / 1e12
     res["dense_bf16_gemm_shape"] = [m, k, n]
+    res["probe"] = ("pmoe_probe_read: 16-byte non-temporal loads, 1 KB per wave instruction, "
+                    "4 loads in flight per lane; pmoe_probe_copy: 16-byte loads and stores")
     del a, b, c
     return res
 
@@ -506,17 +602,22 @@ def pmc_run(args, g, spec, slab, gate, tables, device):
         K.moe_block(g, rc, slab.buf, tables[layer], gate[layer], x[i], inds=inds[i], ws=ws,
                     logit_bias=None if lb is None else lb[layer])
     torch.cuda.synchronize()
-    # calibration: one elementwise kernel reading and writing 256 MiB
-    src = torch.ones(64 << 20, dtype=torch.float32, device=device)
-    dst = torch.empty_like(src)
-    torch.cuda.synchronize()
-    torch.mul(src, 1.0, out=dst)
+    # calibration in the same process: the probe read of 256 MiB (its
+    # FETCH_SIZE against 256 MiB scales that counter) and the probe copy of
+    # 256 MiB (its WRITE_SIZE against 256 MiB scales that one)
+    read, copy = _probe(device)
+    cal = torch.empty(512 << 20, dtype=torch.uint8, device=device)
+    read(cal[:256 << 20])
+    copy(cal[256 << 20:], cal[:256 << 20])
     torch.cuda.synchronize()
     ids = inds.cpu().numpy().reshape(args.steps, -1)
     uniq = sum(len(set(r.tolist())) for r in ids) / args.steps
+    kernel = "prefill" if args.batch > 256 else (
+        "decode_fused_kernel" if args.batch == 1 else "gateup_routed_kernel")
     print(json.dumps({"pmc_run": True, "steps": args.steps, "batch": args.batch,
-                      "mean_unique_experts": uniq, "copy_read_bytes": 256 << 20,
-                      "copy_write_bytes": 256 << 20,
+                      "source_hash": source_hash(kernel), "source_kernel": kernel,
+                      "mean_unique_experts": uniq, "probe_read_bytes": 256 << 20,
+                      "probe_copy_read_bytes": 256 << 20, "probe_copy_write_bytes": 256 << 20,
                       "gateup_bytes_per_step": uniq * 2 * int(g.nbytes[0] + g.nbytes[1] + g.nbytes[2]),
                       "down_bytes_per_step": uniq * int(g.nbytes[6] + g.nbytes[7] + g.nbytes[8])}),
           flush=True)
@@ -563,7 +664,7 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=640)
-    ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--workload", default="qwen3-235b-decode", choices=sorted(WORKLOADS))
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--layers", type=int, default=8)
@@ -624,10 +725,11 @@ def main():
             f"({100 * rp['mfma_frac_layer']:.1f}% of bf16 MFMA peak), kernels {rp['kernels']}")
         extra["prefill_2048"] = rp
     if not args.no_extra:
-        ceil = measured_ceilings(device)
-        log(f"measured ceilings: HBM copy {ceil['hbm_copy_gbs']:.0f} GB/s, read "
-            f"{ceil['hbm_read_gbs']:.0f} GB/s, dense bf16 GEMM "
-            f"{ceil['dense_bf16_gemm_tflops']:.0f} TFLOP/s")
+        ceil = measured_ceilings(device, main_res["_layer_bytes"])
+        log(f"measured ceilings: HBM read {ceil['hbm_read_gbs']:.0f} GB/s (2 GiB), "
+            f"{ceil['layer_volume_read_gbs']:.0f} GB/s ({ceil['layer_volume_read_bytes'] / 1e6:.0f}"
+            f" MB, {ceil['layer_volume_read_us']:.1f} us), copy {ceil['hbm_copy_gbs']:.0f} GB/s, "
+            f"dense bf16 GEMM {ceil['dense_bf16_gemm_tflops']:.0f} TFLOP/s")
         extra["measured_ceilings"] = ceil
         if "prefill_2048" in extra:
             rp = extra["prefill_2048"]
@@ -664,19 +766,13 @@ def main():
         achieved = main_res["gateup_gbs"]
         alg = main_res["_gateup_step_bytes"]
         what = "gateup_routed_kernel (gate+up+SwiGLU of the routed experts)"
+    traffic, traffic_note = load_traffic(f"{args.workload}_b{args.batch}", kname)
     roofline = {"bound": "hbm", "kernel": what,
                 "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                "traffic_source": traffic_note,
                 "avg_launch_us": ku["avg_us"],
                 "algorithmic_bytes_per_launch": alg}
-    traffic_file = ROOT / "profiles" / f"traffic_{args.workload}_b{args.batch}.json"
-    if traffic_file.exists():
-        try:
-            tf = json.loads(traffic_file.read_text())
-            if tf.get("kernel") == kname:
-                roofline["traffic"] = tf.get("bytes_per_launch")
-        except (ValueError, OSError):
-            pass
     main_res.pop("_gateup_step_bytes", None)
     main_res.pop("_layer_bytes", None)
 
@@ -687,14 +783,16 @@ def main():
         log(f"cpu baseline: {cpu['value']:.1f} tok/s on {cpu['cores']} threads")
 
     if "measured_ceilings" in extra:
-        roofline["frac_of_measured_hbm_read"] = achieved / extra["measured_ceilings"]["hbm_read_gbs"]
+        mc = extra["measured_ceilings"]
+        roofline["frac_of_probe_read_2gib"] = achieved / mc["hbm_read_gbs"]
+        roofline["frac_of_probe_read_layer_volume"] = achieved / mc["layer_volume_read_gbs"]
     line = {
         "metric": "MoE-layer tokens/s + % HBM roofline (decode) / % MFMA peak (prefill)",
         "value": main_res["tokens_per_s"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": main_res["steps_timed"],
-        "warmup": args.warmup,
+        "warmup": main_res["untimed_steps"],
         "ms_per_step": main_res["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
@@ -705,7 +803,12 @@ def main():
                    "experts": 128, "moe_intermediate": 1536, "top_k": 8,
                    "routing": "softmax+renorm", "bits": 4, "group": 64,
                    "batch": args.batch, "layers_cycled": args.layers,
-                   "timing": "HIP graph replay of layer steps"},
+                   "timing": (f"{main_res['graph_replays_timed']} HIP graph replays of "
+                              f"{main_res['graph_steps']} layer steps"),
+                   "warmup_detail": (f"{args.warmup} eager steps (--warmup), "
+                                     f"{main_res['graph_steps']} event-bracketed eager steps, "
+                                     f"{main_res['graph_steps']} capture-warm steps, 1 warm "
+                                     f"replay of {main_res['graph_steps']}")},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "extra": {"decode": main_res, **extra},
