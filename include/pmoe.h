@@ -252,6 +252,8 @@ typedef struct {
    * (prefill_slot_starved + stage_starved), and the stage's size */
   int64_t prefill_slot_reads, prefill_installs, stage_reads, prefill_starved,
       stage_slots;
+  /* flow decode: misses admitted (a read started into a slot) */
+  int64_t flow_admits;
 } pmoe_slab_stats;
 
 /* Slot policy + device table [n_layers, n_experts] int32 (-1 = absent).
@@ -296,6 +298,25 @@ int pmoe_slab_dirty(pmoe_slab* s, int layer);
  * kernels read) into out (n_experts int32).  The reference's flow table is
  * an mx.array its caller can read the same way (cache.py:843-859). */
 int pmoe_slab_read_device_row(pmoe_slab* s, int layer, int32_t* out);
+
+/* Flow decode's residency update for one layer (flow_admit, cache.py:861-
+ * 910): with clear_pins, the pins of the last fetch are dropped first (once
+ * per token).  Resident ids get the recency and reuse credit of a fetch hit;
+ * other ids are counted as misses and, unless an earlier admit already
+ * started their read, take a slot (evicting the least recent entry) and
+ * become pending: neither resident nor free, absent from the table, until
+ * pmoe_slab_install.  The placed misses go to miss_ids/miss_slots (capacity
+ * n_ids).  The caller must know that no queued kernel reads an evicted slot
+ * (the reference fences the previous token first) and copies each placed
+ * miss into its slot. */
+int pmoe_slab_admit(pmoe_slab* s, int layer, const int32_t* ids, int n_ids,
+                    int32_t* miss_ids, int32_t* miss_slots, int* n_miss,
+                    int clear_pins);
+
+/* Install pending (admitted) experts whose copies have landed: resident at
+ * MRU, in the table, with the LFRU trim (the reference's install on arrival,
+ * _attach_staging(install_now=True) :2866-2910). */
+int pmoe_slab_install(pmoe_slab* s, int layer, const int32_t* ids, int n_ids);
 
 /* Register slab slots [first_slot, first_slot + n_slots) (past the routed
  * slots) as the prefill stage: slots prefill misses are read into when no
@@ -365,8 +386,19 @@ int pmoe_copy_fence(pmoe_copy_engine* ce, void* stream);
 
 /* Issue every queued job behind the latest fence, without making any
  * stream wait for them (prefill group i+1's reads run under group i's
- * compute, cache.py:2535-2578). */
-int pmoe_copy_issue(pmoe_copy_engine* ce);
+ * compute, cache.py:2535-2578).  With batch non-NULL the issued copies also
+ * form a batch whose completion can be queried, joined and released below
+ * (flow decode installs an admitted expert once its read has landed). */
+int pmoe_copy_issue(pmoe_copy_engine* ce, int* batch);
+
+/* 1 when every copy of the batch has completed, 0 if not yet, <0 on error. */
+int pmoe_copy_batch_done(pmoe_copy_engine* ce, int batch);
+
+/* Make stream wait for the batch's copies. */
+int pmoe_copy_batch_join(pmoe_copy_engine* ce, int batch, void* stream);
+
+/* Return the batch record (its copies need not have completed). */
+int pmoe_copy_batch_release(pmoe_copy_engine* ce, int batch);
 
 /* Make stream wait for every copy issued so far. */
 int pmoe_copy_join(pmoe_copy_engine* ce, void* stream);

@@ -639,6 +639,43 @@ class SlotPolicy:
         self.free.extend(g["free"])
         self.stage_free.extend(g["stage"])
 
+    # ---- flow decode (flow_admit, cache.py:861-910; install on arrival,
+    # _attach_staging(install_now=True) :2866-2910)
+
+    def admit(self, layer, ids, clear_pins=True):
+        """Resident ids: MRU + reuse credit.  Others: a miss; unless already
+        pending, a slot (evicting) and pending until ``install``.  Stops at the
+        first miss that finds no slot.  Returns [(miss id, slot)]."""
+        if not hasattr(self, "pending"):
+            self.pending = {}
+        if clear_pins:
+            self.pinned.clear()
+        placed = []
+        for e in sorted({int(i) for i in ids}):
+            key = (layer, e)
+            if key in self.lru:
+                self.hits += 1
+                self.lru.move_to_end(key)
+                self.freq[key] = min(self.freq_max, self.freq.get(key, 0) + 1)
+                continue
+            self.misses += 1
+            if key in self.pending:
+                continue
+            slot = self._alloc(True)
+            if slot is None:
+                break
+            self.pending[key] = slot
+            placed.append((e, slot))
+        return placed
+
+    def install(self, layer, ids):
+        for e in sorted({int(i) for i in ids}):
+            key = (layer, e)
+            slot = self.pending.pop(key)
+            self.slot_of[key] = slot
+            self.lru[key] = slot
+            self._trim()
+
     def stitch(self, layers, n_experts) -> bool:
         """Load every expert into a fixed slot: slot = layer_idx*E + e
         (cache.py:717-787 with the free list above)."""

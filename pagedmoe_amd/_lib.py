@@ -56,7 +56,7 @@ class SlabStats(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int64) for n in (
         "hits", "misses", "evictions", "starved", "installs", "resident", "slots",
         "budget", "reserve", "stitched", "bytes_copied", "prefill_slot_reads",
-        "prefill_installs", "stage_reads", "prefill_starved", "stage_slots")]
+        "prefill_installs", "stage_reads", "prefill_starved", "stage_slots", "flow_admits")]
 
 
 _P = ctypes.c_void_p
@@ -100,6 +100,8 @@ SIGNATURES = {
     "pmoe_slab_sync_table": (_I, [_P, _I, _P]),
     "pmoe_slab_dirty": (_I, [_P, _I]),
     "pmoe_slab_read_device_row": (_I, [_P, _I, _I32P]),
+    "pmoe_slab_admit": (_I, [_P, _I, _I32P, _I, _I32P, _I32P, ctypes.POINTER(_I), _I]),
+    "pmoe_slab_install": (_I, [_P, _I, _I32P, _I]),
     "pmoe_slab_set_stage": (_I, [_P, _I, _I]),
     "pmoe_slab_capacity": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "pmoe_slab_prefill_request": (_I, [_P, _I, _I32P, _I, _I32P, _I32P, ctypes.POINTER(_I),
@@ -114,7 +116,10 @@ SIGNATURES = {
     "pmoe_copy_submit": (_I, [_P, _P, _P, _SZ, _I]),
     "pmoe_copy_flush": (_I, [_P, _P]),
     "pmoe_copy_fence": (_I, [_P, _P]),
-    "pmoe_copy_issue": (_I, [_P]),
+    "pmoe_copy_issue": (_I, [_P, ctypes.POINTER(_I)]),
+    "pmoe_copy_batch_done": (_I, [_P, _I]),
+    "pmoe_copy_batch_join": (_I, [_P, _I, _P]),
+    "pmoe_copy_batch_release": (_I, [_P, _I]),
     "pmoe_copy_join": (_I, [_P, _P]),
     "pmoe_copy_sync": (_I, [_P]),
     "pmoe_copy_bytes": (ctypes.c_int64, [_P]),

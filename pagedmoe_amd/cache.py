@@ -7,7 +7,8 @@ step, and a full "stitch" when every expert fits (cache.py:717-787).  Misses
 are copied from a pinned host expert store into their slots by the native copy
 engine on side streams; the compute stream waits on events, never the host.
 The reference's misses come from SSD preads; the host store stands in for the
-page cache / checkpoint (loading real checkpoints into it is the next step).
+page cache and is filled from a quantized safetensors checkpoint
+(checkpoint.py) or from resident modules.
 """
 
 from __future__ import annotations
@@ -112,6 +113,17 @@ class PrefillGroup:
         self.ids = list(ids)
         self.n_miss = n_miss
         self.n_unplaced = n_unplaced
+
+
+class FlowBatch:
+    """One token's admitted misses (flow decode): the copy batch that brings
+    them in and the (layer key, expert ids) to install once it has landed."""
+
+    __slots__ = ("batch", "items")
+
+    def __init__(self, batch: int, items):
+        self.batch = batch
+        self.items = items
 
 
 class ExpertCache:
@@ -312,6 +324,68 @@ class ExpertCache:
     def prefill_done(self, group: PrefillGroup) -> None:
         check(lib().pmoe_slab_prefill_done(self._h, group.ticket), "pmoe_slab_prefill_done")
 
+    # ------------------------------------------------------------- flow
+
+    def flow_admit(self, batch) -> FlowBatch | None:
+        """Flow decode's residency update for one token (flow_admit,
+        cache.py:861-910): ``batch`` = [(layer key, ids)] of the last token's
+        routing.  Hits get recency and reuse credit; misses take slots
+        (evicting) and are copied in from the host store as one copy batch
+        behind a fence at the current stream's tail, with nothing waiting for
+        it.  The caller must have waited for every kernel queued before (an
+        evicted slot is overwritten) and installs the batch once it has
+        landed (``flow_install_ready``).  None when nothing was admitted."""
+        if self.host_store is None:
+            raise PmoeError("flow_admit needs a host expert store")
+        items = []
+        eb = int(self.geom.expert_bytes)
+        for i, (layer_key, ids) in enumerate(batch):
+            ids = sorted({int(e) for e in ids})
+            li = self.layer_index(layer_key)
+            arr = (ctypes.c_int32 * max(1, len(ids)))(*ids)
+            mid = (ctypes.c_int32 * max(1, len(ids)))()
+            msl = (ctypes.c_int32 * max(1, len(ids)))()
+            nm = ctypes.c_int()
+            check(lib().pmoe_slab_admit(self._h, li, arr, len(ids), mid, msl, ctypes.byref(nm),
+                                        int(i == 0)), "pmoe_slab_admit")
+            placed = [(mid[j], msl[j]) for j in range(nm.value)]
+            for e, slot in placed:
+                check(lib().pmoe_copy_submit(
+                    self._ce, ctypes.c_void_p(self.slab.data_ptr + slot * eb),
+                    ctypes.c_void_p(self.host_store.address + (li * self.n_experts + e) * eb),
+                    eb, 1), "pmoe_copy_submit")
+            if placed:
+                items.append((layer_key, [e for e, _ in placed]))
+        if not items:
+            return None
+        self.fence()
+        b = ctypes.c_int()
+        check(lib().pmoe_copy_issue(self._ce, ctypes.byref(b)), "pmoe_copy_issue")
+        return FlowBatch(b.value, items)
+
+    def flow_install_ready(self, batches, wait: bool = False) -> list:
+        """Install every admitted batch whose copies have landed (all of them
+        with ``wait``): the current stream waits on the batch's copy events,
+        then its experts become resident (table rows dirty, republished by
+        ``sync_table``).  Returns the batches still in flight."""
+        left = []
+        stream = self._stream()
+        for fb in batches:
+            if not wait:
+                r = lib().pmoe_copy_batch_done(self._ce, fb.batch)
+                if r < 0:
+                    check(r, "pmoe_copy_batch_done")
+                if r == 0:
+                    left.append(fb)
+                    continue
+            check(lib().pmoe_copy_batch_join(self._ce, fb.batch, stream), "pmoe_copy_batch_join")
+            for layer_key, ids in fb.items:
+                arr = (ctypes.c_int32 * len(ids))(*ids)
+                check(lib().pmoe_slab_install(self._h, self.layer_index(layer_key), arr, len(ids)),
+                      "pmoe_slab_install")
+            check(lib().pmoe_copy_batch_release(self._ce, fb.batch), "pmoe_copy_batch_release")
+        return left
+
     @staticmethod
     def _stream():
         return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -376,7 +450,7 @@ class ExpertCache:
             "group_passes": self.group_passes,
             "prefill_slot_reads": st.prefill_slot_reads, "prefill_installs": st.prefill_installs,
             "stage_reads": st.stage_reads, "prefill_slot_starved": st.prefill_starved,
-            "stage_slots": st.stage_slots,
+            "stage_slots": st.stage_slots, "flow_admits": st.flow_admits,
         }
 
     def close(self) -> None:

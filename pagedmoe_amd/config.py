@@ -4,7 +4,9 @@ Names and defaults follow the reference's PAGED_MOE_* knobs that touch this
 path (config.py: SLAB_RESERVE_FRAC :718, LFRU/LFRU_SCAN :1477-1478, STITCH
 :1186, PREFILL_TOUCH :617, PREFILL_STAGE / PREFILL_STAGE_GROUP_MB
 :1603-1608, GROUP_BYTES :1531); ``sync_from_environ()`` re-reads them
-(config.py:853).  DECODE_MAX_TOKENS is the reference's _DECODE_MAX_TOKENS
+(config.py:853); FUSED_PREFILL :1633 and ATTN_SUB_CHUNK :1562 for the
+fused prefill pass; FLOW / FLOW_WARMUP / FLOW_WARM_HIT :1218-1237 for flow
+decode.  DECODE_MAX_TOKENS is the reference's _DECODE_MAX_TOKENS
 (streaming.py:69): calls of more tokens take the prefill residency policy.
 """
 
@@ -37,11 +39,18 @@ DECODE_MAX_TOKENS = 20    # calls of more tokens are prefill (no touch, no evict
 PREFILL_STAGE = True      # stage slots for prefill misses that find no free slot
 PREFILL_STAGE_GROUP_MB = 384  # prefill fetch group size; the stage holds four groups
 GROUP_BYTES = 1024 << 20  # ceiling on one prefill fetch group
+FUSED_PREFILL = True      # long calls sub-chunk attention, run the MoE once
+FLOW = False              # decode tokens with no host sync inside (residency once per token)
+FLOW_WARMUP = 2           # tokens after a prefill that take the per-layer path first
+FLOW_WARM_HIT = 0.9       # hit-rate EMA the per-layer path must reach before flow resumes
+ATTN_SUB_CHUNK = 2048     # rows per attention sub-chunk, at most
+ATTN_SCORE_MB = 1024      # fp32 score matrix (heads x rows x keys) of one sub-chunk, at most
 
 
 def sync_from_environ() -> None:
     global SLAB_RESERVE_FRAC, LFRU, LFRU_SCAN, STITCH, COPY_SPLIT_BYTES, COPY_STREAMS
     global DECODE_MAX_TOKENS, PREFILL_STAGE, PREFILL_STAGE_GROUP_MB, GROUP_BYTES
+    global FUSED_PREFILL, ATTN_SUB_CHUNK, ATTN_SCORE_MB, FLOW, FLOW_WARMUP, FLOW_WARM_HIT
     SLAB_RESERVE_FRAC = _env("SLAB_RESERVE_FRAC", 0.1, float)
     LFRU = _env("LFRU", True, _bool)
     LFRU_SCAN = _env("LFRU_SCAN", 8, int)
@@ -52,6 +61,12 @@ def sync_from_environ() -> None:
     PREFILL_STAGE = _env("PREFILL_STAGE", True, _bool)
     PREFILL_STAGE_GROUP_MB = _env("PREFILL_STAGE_GROUP_MB", 384, int)
     GROUP_BYTES = _env("GROUP_MB", 1024, int) << 20
+    FUSED_PREFILL = _env("FUSED_PREFILL", True, _bool)
+    ATTN_SUB_CHUNK = _env("ATTN_SUB_CHUNK", 2048, int)
+    ATTN_SCORE_MB = _env("ATTN_SCORE_MB", 1024, int)
+    FLOW = _env("FLOW", False, _bool)
+    FLOW_WARMUP = _env("FLOW_WARMUP", 2, int)
+    FLOW_WARM_HIT = _env("FLOW_WARM_HIT", 0.9, float)
 
 
 sync_from_environ()

@@ -23,12 +23,21 @@
 
 #include "pmoe_internal.h"
 
+constexpr int kMaxBatches = 64;
+
 struct pmoe_copy_engine {
   struct Job {
     void* dst;
     const void* src;
     size_t bytes;
   };
+  // An issued set of copies whose completion is tracked on its own: one
+  // event per copy stream, recorded right after the batch's copies.
+  struct Batch {
+    bool live = false;
+    std::vector<hipEvent_t> ev;
+  };
+  Batch batches[kMaxBatches];
   size_t split = size_t(64) << 20;  // whole experts: larger pieces copy faster
   std::vector<hipStream_t> streams;
   std::vector<hipEvent_t> done;
@@ -78,6 +87,12 @@ extern "C" int pmoe_copy_engine_create(pmoe_copy_engine** out, size_t split_byte
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
     if (e == hipSuccess) ce->done.push_back(ev);
   }
+  for (int b = 0; b < kMaxBatches && e == hipSuccess; ++b)
+    for (int i = 0; i < n_streams && e == hipSuccess; ++i) {
+      hipEvent_t ev = nullptr;
+      e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+      if (e == hipSuccess) ce->batches[b].ev.push_back(ev);
+    }
   if (e != hipSuccess) {
     pmoe_copy_engine_destroy(ce);
     return pmoe::hip_fail(e, "copy_engine_create");
@@ -94,6 +109,8 @@ extern "C" int pmoe_copy_engine_destroy(pmoe_copy_engine* ce) {
     (void)hipStreamDestroy(s);
   }
   for (hipEvent_t ev : ce->done) (void)hipEventDestroy(ev);
+  for (auto& b : ce->batches)
+    for (hipEvent_t ev : b.ev) (void)hipEventDestroy(ev);
   if (ce->fence) (void)hipEventDestroy(ce->fence);
   delete ce;
   return PMOE_OK;
@@ -149,11 +166,61 @@ static int issue_locked(pmoe_copy_engine* ce) {
   return first_err;
 }
 
-extern "C" int pmoe_copy_issue(pmoe_copy_engine* ce) {
+extern "C" int pmoe_copy_issue(pmoe_copy_engine* ce, int* batch) {
   pmoe::clear_error();
   if (!ce) return pmoe::fail(PMOE_EINVAL, "copy_issue: null engine");
   std::lock_guard<std::mutex> lk(ce->mu);
-  return issue_locked(ce);
+  int b = -1;
+  if (batch) {
+    for (int i = 0; i < kMaxBatches && b < 0; ++i)
+      if (!ce->batches[i].live) b = i;
+    if (b < 0) return pmoe::fail(PMOE_EINVAL, "copy_issue: every batch record is in use");
+  }
+  const int rc = issue_locked(ce);
+  if (rc) return rc;
+  if (batch) {
+    for (size_t i = 0; i < ce->streams.size(); ++i)
+      PMOE_HIP(hipEventRecord(ce->batches[b].ev[i], ce->streams[i]));
+    ce->batches[b].live = true;
+    *batch = b;
+  }
+  return PMOE_OK;
+}
+
+static pmoe_copy_engine::Batch* live_batch(pmoe_copy_engine* ce, int b) {
+  if (!ce || b < 0 || b >= kMaxBatches || !ce->batches[b].live) return nullptr;
+  return &ce->batches[b];
+}
+
+extern "C" int pmoe_copy_batch_done(pmoe_copy_engine* ce, int batch) {
+  pmoe::clear_error();
+  std::lock_guard<std::mutex> lk(ce->mu);
+  auto* b = live_batch(ce, batch);
+  if (!b) return pmoe::fail(PMOE_EINVAL, "copy_batch_done: no such batch");
+  for (hipEvent_t ev : b->ev) {
+    const hipError_t e = hipEventQuery(ev);
+    if (e == hipErrorNotReady) return 0;
+    if (e != hipSuccess) return pmoe::hip_fail(e, "copy_batch_done: hipEventQuery");
+  }
+  return 1;
+}
+
+extern "C" int pmoe_copy_batch_join(pmoe_copy_engine* ce, int batch, void* stream) {
+  pmoe::clear_error();
+  std::lock_guard<std::mutex> lk(ce->mu);
+  auto* b = live_batch(ce, batch);
+  if (!b) return pmoe::fail(PMOE_EINVAL, "copy_batch_join: no such batch");
+  for (hipEvent_t ev : b->ev) PMOE_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(stream), ev, 0));
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_copy_batch_release(pmoe_copy_engine* ce, int batch) {
+  pmoe::clear_error();
+  std::lock_guard<std::mutex> lk(ce->mu);
+  auto* b = live_batch(ce, batch);
+  if (!b) return pmoe::fail(PMOE_EINVAL, "copy_batch_release: no such batch");
+  b->live = false;
+  return PMOE_OK;
 }
 
 extern "C" int pmoe_copy_join(pmoe_copy_engine* ce, void* stream) {

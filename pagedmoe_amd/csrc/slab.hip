@@ -65,6 +65,7 @@ struct pmoe_slab {
   // LRU over dense keys (layer*E + e): head = least recent, tail = most recent
   std::vector<int> prev, next, slot_of, freq;
   std::vector<char> in_lru, stitch_key;
+  std::vector<char> pending;              // per key: admitted, its copy not yet installed
   int head = -1, tail = -1, lru_size = 0;
   std::vector<char> pinned;               // per routed slot
   std::vector<int> pinned_list;
@@ -199,6 +200,7 @@ extern "C" int pmoe_slab_create(pmoe_slab** out, int slots, int n_layers, int n_
   s->freq.assign(keys, 0);
   s->in_lru.assign(keys, 0);
   s->stitch_key.assign(keys, 0);
+  s->pending.assign(keys, 0);
   s->pinned.assign(slots, 0);
   s->table.assign(keys, -1);
   s->dirty.assign(n_layers, 0);
@@ -295,8 +297,11 @@ extern "C" int pmoe_slab_request(pmoe_slab* s, int layer, const int32_t* ids, in
   int rc = unique_ids(s, ids, n_ids, uniq, "slab_request");
   if (rc) return rc;
   std::lock_guard<std::mutex> lk(s->mu);
-  s->clear_pins();
   const int base = layer * s->n_experts;
+  for (int e : uniq)
+    if (s->pending[base + e])
+      return pmoe::fail(PMOE_EINVAL, "slab_request: an admitted expert's copy is not installed");
+  s->clear_pins();
   std::vector<int> misses;
   for (int e : uniq) {
     const int k = base + e;
@@ -326,6 +331,63 @@ extern "C" int pmoe_slab_request(pmoe_slab* s, int layer, const int32_t* ids, in
     ++placed;
   }
   *n_miss = placed;
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_slab_admit(pmoe_slab* s, int layer, const int32_t* ids, int n_ids,
+                               int32_t* miss_ids, int32_t* miss_slots, int* n_miss,
+                               int clear_pins) {
+  pmoe::clear_error();
+  if (!s || (n_ids > 0 && !ids) || !n_miss || layer < 0 || layer >= s->n_layers || n_ids < 0)
+    return pmoe::fail(PMOE_EINVAL, "slab_admit: bad argument");
+  std::vector<int> uniq;
+  int rc = unique_ids(s, ids, n_ids, uniq, "slab_admit");
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(s->mu);
+  if (clear_pins) s->clear_pins();
+  const int base = layer * s->n_experts;
+  int placed = 0;
+  for (int e : uniq) {
+    const int k = base + e;
+    if (s->in_lru[k]) {
+      ++s->st.hits;
+      s->move_to_end(k);
+      s->freq[k] = std::min(kFreqMax, s->freq[k] + 1);
+      continue;
+    }
+    ++s->st.misses;
+    if (s->pending[k]) continue;  // its read is already in flight
+    const int slot = s->alloc(true);
+    if (slot < 0) break;          // nothing evictable: admit no more of this layer
+    s->pending[k] = 1;
+    s->slot_of[k] = slot;
+    ++s->st.flow_admits;
+    if (miss_ids) miss_ids[placed] = e;
+    if (miss_slots) miss_slots[placed] = slot;
+    ++placed;
+  }
+  *n_miss = placed;
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_slab_install(pmoe_slab* s, int layer, const int32_t* ids, int n_ids) {
+  pmoe::clear_error();
+  if (!s || (n_ids > 0 && !ids) || layer < 0 || layer >= s->n_layers || n_ids < 0)
+    return pmoe::fail(PMOE_EINVAL, "slab_install: bad argument");
+  std::vector<int> uniq;
+  int rc = unique_ids(s, ids, n_ids, uniq, "slab_install");
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(s->mu);
+  const int base = layer * s->n_experts;
+  for (int e : uniq)
+    if (!s->pending[base + e])
+      return pmoe::fail(PMOE_EINVAL, "slab_install: expert was not admitted");
+  for (int e : uniq) {
+    const int k = base + e;
+    s->pending[k] = 0;
+    s->install(k, s->slot_of[k]);
+    s->trim();
+  }
   return PMOE_OK;
 }
 
@@ -369,11 +431,15 @@ extern "C" int pmoe_slab_prefill_request(pmoe_slab* s, int layer, const int32_t*
   for (int i = 0; i < kMaxTickets && t < 0; ++i)
     if (!s->tickets[i].live) t = i;
   if (t < 0) return pmoe::fail(PMOE_EINVAL, "slab_prefill_request: too many open prefill groups");
+  const int base = layer * s->n_experts;
+  for (int e : uniq)
+    if (s->pending[base + e])
+      return pmoe::fail(PMOE_EINVAL,
+                        "slab_prefill_request: an admitted expert's copy is not installed");
   Ticket& tk = s->tickets[t];
   tk = Ticket();
   tk.live = true;
   tk.layer = layer;
-  const int base = layer * s->n_experts;
   int placed = 0, unplaced = 0;
   for (int e : uniq) {
     const int k = base + e;
@@ -562,7 +628,7 @@ extern "C" int pmoe_slab_fetch_prefill(pmoe_slab* s, pmoe_copy_engine* ce, const
   int rc = pmoe_slab_prefill_request(s, layer, ids, n_ids, mid.data(), msl.data(), &nm, &nu, &t);
   if (rc) return rc;
   rc = submit_misses(s, ce, g, slab, host_store, layer, mid.data(), msl.data(), nm);
-  if (!rc) rc = pmoe_copy_issue(ce);
+  if (!rc) rc = pmoe_copy_issue(ce, nullptr);
   if (rc) {
     (void)pmoe_slab_prefill_done(s, t);
     return rc;

@@ -1,0 +1,167 @@
+"""The streamed MoE layers of one model, in order, and their per-token state.
+
+Counterpart of the reference's PrefetchRing (streaming.py:1404-2299), which
+patch_model returns.  Here it carries flow decode: a decode token whose MoE
+layers never wait on the host (streaming.py:675-749, cache.py:791-910).
+
+Flow decode.  The slot table is already on the GPU and the expert kernels
+read it directly, computing an exact zero row for every routed expert that
+is not resident -- the seam's contract for a dropped slot
+(streaming.py:715-719) -- so a layer needs no host round trip at all.  What
+the host still has to do is residency, once per token instead of once per
+layer (``begin_token``, the reference's flow_pump, streaming.py:706-711):
+
+1. wait for the previous token's kernels (one fence per token; nothing still
+   queued may read a slot about to be overwritten);
+2. install the admitted experts whose copies have landed (the compute stream
+   is made to wait on their copy events, so no stale line survives);
+3. admit the previous token's routing of every layer (cache.py:861-910):
+   resident ids get recency and reuse credit, misses take a slot, possibly
+   evicting, and are copied in behind the fence -- they become usable in a
+   later token, never in the middle of one;
+4. republish every changed table row on the compute stream.
+
+The token's layers then run with no host sync; a routed expert that is not
+resident contributes nothing to that token (the reference's flow graph omits
+it the same way, streaming.py:700-702).  Tokens of more than
+``config.DECODE_MAX_TOKENS`` rows (prefill) drop flow state and take the
+ordinary path, and after a prefill ``config.FLOW_WARMUP`` tokens plus a hit
+rate of ``config.FLOW_WARM_HIT`` are required before flow resumes
+(config.py:1218-1237).  Because nothing in a flow token syncs, a token's
+layers can be captured in one HIP graph and replayed after each
+``begin_token``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import config
+
+
+class PrefetchRing:
+    """Sequence of the model's StreamedSwitchGLU layers (iterable and
+    indexable like the list patch_model used to return) plus flow state."""
+
+    def __init__(self, layers, cache):
+        self.layers = list(layers)
+        self.cache = cache
+        for i, layer in enumerate(self.layers):
+            layer.ring = self
+            layer.ring_index = i
+        self.flow = bool(config.FLOW)
+        self.auto_pump = True          # layer 0 calls begin_token itself
+        self.token_flow = False        # the current token runs as a flow token
+        self._routes: dict = {}        # layer index -> routing of the last flow token
+        self._noted = False            # _routes hold a token not admitted yet
+        self._pending: list = []       # admitted copy batches not installed yet
+        self._fence = torch.cuda.Event()
+        self._fenced = False
+        self._since_prefill = 0
+        self._hit_ema = 0.0
+        self._token_stats = None
+        self.flow_tokens = 0
+        self.sync_tokens = 0
+
+    # ---- sequence protocol over the layers
+    def __len__(self):
+        return len(self.layers)
+
+    def __iter__(self):
+        return iter(self.layers)
+
+    def __getitem__(self, i):
+        return self.layers[i]
+
+    # ---- token boundaries
+    def _flow_ready(self) -> bool:
+        return (self.flow and self._since_prefill >= int(config.FLOW_WARMUP)
+                and self._hit_ema >= float(config.FLOW_WARM_HIT))
+
+    def layer_call(self, index: int, n_tokens: int) -> bool:
+        """Called by each layer on entry; returns True when this call runs
+        as part of a flow token.  Layer 0 opens the token."""
+        if n_tokens > config.DECODE_MAX_TOKENS:
+            if index == 0:
+                self.flow_drop()
+                self._since_prefill = 0
+                self._hit_ema = 0.0
+            return False
+        if index == 0:
+            self._close_token_stats()
+            self.token_flow = self._flow_ready()
+            if self.token_flow and self.auto_pump:
+                self.begin_token()
+            self._since_prefill += 1
+            st = self.cache.raw_stats()
+            self._token_stats = (st.hits, st.misses)
+            if self.token_flow:
+                self.flow_tokens += 1
+            else:
+                self.sync_tokens += 1
+        return self.token_flow
+
+    def _close_token_stats(self):
+        if self._token_stats is None:
+            return
+        st = self.cache.raw_stats()
+        h, m = st.hits - self._token_stats[0], st.misses - self._token_stats[1]
+        if h + m:
+            self._hit_ema = 0.5 * self._hit_ema + 0.5 * (h / (h + m))
+        self._token_stats = None
+
+    def begin_token(self, replayed: bool = False) -> None:
+        """flow_pump: fence, install landed copies, admit the last token's
+        routing, republish changed rows.  With ``auto_pump`` False (a token
+        captured in a graph) the caller runs this before each token, with
+        ``replayed`` True once a replay of the captured token has run (the
+        routing tensors noted during capture then hold that replay's ids).
+        Copies into evicted slots are fenced on the compute stream's tail, so
+        the host fence is not needed for safety, only to read the routing."""
+        c = self.cache
+        if self._fenced:
+            self._fence.synchronize()
+            self._fenced = False
+        self._pending = c.flow_install_ready(self._pending)
+        batch = []
+        if self._noted or replayed:
+            for i in sorted(self._routes):
+                ids = sorted({int(e) for e in self._routes[i].reshape(-1).tolist()
+                              if 0 <= int(e) < c.n_experts})
+                batch.append((self.layers[i].layer_key, ids))
+        self._noted = False
+        if batch:
+            fb = c.flow_admit(batch)
+            if fb is not None:
+                self._pending.append(fb)
+        for layer in self.layers:
+            c.sync_table(layer.layer_key)
+
+    def note(self, index: int, inds: torch.Tensor) -> None:
+        """A flow layer's routing (device tensor, read at the next
+        begin_token); the last layer fences the token.  Under graph capture
+        the tensor is the graph's own output, refreshed by every replay."""
+        self._routes[index] = inds
+        if torch.cuda.is_current_stream_capturing():
+            return
+        self._noted = True
+        if index == len(self.layers) - 1:
+            self._fence.record()
+            self._fenced = True
+
+    def flow_drop(self) -> None:
+        """Leave flow: wait for and install every admitted copy, forget the
+        last token's routing (a prefill replaces it)."""
+        if self._fenced:
+            self._fence.synchronize()
+            self._fenced = False
+        self._pending = self.cache.flow_install_ready(self._pending, wait=True)
+        self._routes.clear()
+        self._noted = False
+        for layer in self.layers:
+            self.cache.sync_table(layer.layer_key)
+
+    def stats(self) -> dict:
+        return {"flow": self.flow, "flow_tokens": self.flow_tokens,
+                "sync_tokens": self.sync_tokens, "pending_batches": len(self._pending),
+                "hit_ema": self._hit_ema}

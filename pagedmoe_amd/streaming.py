@@ -23,6 +23,7 @@ from . import config
 from . import kernels as K
 from ._lib import geom as make_geom
 from .cache import ExpertCache
+from .ring import PrefetchRing
 from .slab import SlabStore
 
 PROJS = ("gate_proj", "up_proj", "down_proj")
@@ -88,6 +89,7 @@ class StreamedSwitchGLU(nn.Module):
         self.layer_key = layer_key
         self.cache = cache
         self.ring = ring
+        self.ring_index = -1
         self.pred = predictor
         g = cache.geom
         self.hidden, self.inter, self.bits = g.hidden, g.inter, g.bits
@@ -228,11 +230,22 @@ class StreamedSwitchGLU(nn.Module):
             y = y_g if y is None else torch.where(keep[..., None], y_g, y)
         return y
 
+    def flow_call(self, n_tokens: int) -> bool:
+        """Enter this layer's call on the ring; True for a flow token."""
+        return self.ring is not None and self.ring.layer_call(self.ring_index, n_tokens)
+
     def forward(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         lead = indices.shape
         x2 = x.reshape(-1, self.hidden).to(torch.bfloat16).contiguous()
         ind2 = indices.reshape(-1, lead[-1]).to(torch.int32).contiguous()
         c = self.cache
+        if not c.stitched and self.flow_call(ind2.shape[0]):
+            # flow token: the device table as published at the token's start,
+            # no host round trip; non-resident experts give zero rows
+            y = K.switch_glu(c.geom, c.slab.buf, c.table_ptr(self.layer_key), self.n_experts,
+                             x2, ind2)
+            self.ring.note(self.ring_index, ind2)
+            return y.reshape(*lead, self.hidden)
         y = self.run_passes(ind2, lambda ids, table: K.switch_glu(
             c.geom, c.slab.buf, table, self.n_experts, x2, ids))
         return y.reshape(*lead, self.hidden)
@@ -266,6 +279,17 @@ class _MoEBlock(nn.Module):
         rc = self._route_cfg()
         sg = self.shared_expert_gate if self.use_shared else None
         sm = self.switch_mlp
+        if (isinstance(sm, StreamedSwitchGLU) and not sm.cache.stitched
+                and sm.flow_call(x2.shape[0])):
+            # flow token: the whole block on the GPU against the device table
+            # published at the token's start (streaming.py:675-724)
+            out, inds, w = K.moe_block(g, rc, slab, sm.cache.table_ptr(sm.layer_key),
+                                       self.gate_weight, x2, score_bias=self._score_bias(),
+                                       logit_bias=self.logit_bias, shared_slot=shared_slot,
+                                       shared_gate=sg)
+            sm.ring.note(sm.ring_index, inds)
+            self.last_routing = (inds, w)
+            return out.reshape(shape)
         if isinstance(sm, StreamedSwitchGLU) and not sm.cache.stitched:
             # route, then make the routed experts resident, then compute
             logits = K.router_logits(x2, self.gate_weight, self.logit_bias)
@@ -433,12 +457,13 @@ def build_cache_for(model: nn.Module, slots: int, model_path=None, **kw) -> Expe
 def patch_model(model: nn.Module, cache: ExpertCache, tensor_index=None, prefetch_depth: int = 0,
                 predict_mode: str | None = None, model_path: str | None = None):
     """Replace every QuantizedSwitchGLU with a StreamedSwitchGLU over
-    ``cache`` (streaming.py:2575-2688, same arguments).  Returns the list of
-    streamed layers (the reference returns its PrefetchRing).  The cache's
-    layer keys must be the module paths.  ``tensor_index``/``model_path``
-    locate checkpoint bytes in the reference; here the cache's pinned host
-    store already holds them, so they are accepted and unused.  Speculative
-    prefetch is not part of this path: ``predict_mode`` "on" raises."""
+    ``cache`` (streaming.py:2575-2688, same arguments).  Returns the
+    PrefetchRing over the streamed layers (ring.py), which also indexes and
+    iterates like the list of layers.  The cache's layer keys must be the
+    module paths.  ``tensor_index``/``model_path`` locate checkpoint bytes in
+    the reference; here the cache's pinned host store already holds them, so
+    they are accepted and unused.  Speculative prefetch is not part of this
+    path: ``predict_mode`` "on" raises."""
     if predict_mode not in (None, "off", "auto"):
         raise NotImplementedError(f"predict_mode={predict_mode!r}: speculative prefetch is not built")
     del tensor_index, model_path, prefetch_depth
@@ -448,11 +473,12 @@ def patch_model(model: nn.Module, cache: ExpertCache, tensor_index=None, prefetc
     streamed = [StreamedSwitchGLU(path, module, cache) for path, module in glus]
     for (path, _), s in zip(glus, streamed):
         _swap_module(model, path, s)
+    ring = PrefetchRing(streamed, cache)
     model._pagedmoe_cache = cache
-    model._pagedmoe_ring = streamed
+    model._pagedmoe_ring = ring
     if cache.n_experts * len(glus) <= cache.routed_slots:
         cache.load_stitch()
-    return streamed
+    return ring
 
 
 def get_stats(model: nn.Module) -> dict:
@@ -461,4 +487,8 @@ def get_stats(model: nn.Module) -> dict:
     cache = getattr(model, "_pagedmoe_cache", None)
     if cache is None:
         return {}
-    return {"cache": cache.stats()}
+    out = {"cache": cache.stats()}
+    ring = getattr(model, "_pagedmoe_ring", None)
+    if ring is not None:
+        out["ring"] = ring.stats()
+    return out

@@ -17,6 +17,11 @@ implementation under test:
 * the free list is list(range(slots - 1, -1, -1)) popped from the end
   (:991, :1138-1139) and a released slot is appended (_release_slot :1116).
 
+* flow decode: flow_admit (:861-910: clear pins; resident ids get MRU and
+  reuse credit; other ids are misses and, unless their read is already in
+  flight, take a slot with eviction allowed) and install on arrival
+  (_attach_staging(install_now=True) :2866-2910 -> _install).
+
 A policy adapter exposes: step(ids) -> [(miss id, slot)] (decode),
 prefill(ids) -> (ticket, [(miss id, slot)], unplaced), done(ticket),
 table() -> {expert: slot} of resident entries, evictions -> int.
@@ -100,6 +105,33 @@ PREFILL_COLD = dict(
     then_placed=[(30, 13)],
     then_evicted=[0],
 )
+
+
+# Flow admission, 8 slots (budget 4).  Admit {0,1,2}: three misses, pending
+# in slots 0..2, nothing resident.  Install them.  Admit {0,3}: 0 is a hit
+# (MRU, freq 1), 3 a miss -> slot 3.  Admit {3} again before it lands: a miss,
+# no second read.  Install 3 (4 resident).  Admit {4,5}: slots 4, 5.
+# Install them: 4 makes 5 resident, the trim evicts the head 1 (freq 0); 5
+# then evicts 2.  Final table {0:0, 3:3, 4:4, 5:5}; hits 1, misses 7.
+FLOW_ADMIT = dict(
+    slots=8,
+    script=[("admit", [0, 1, 2], [(0, 0), (1, 1), (2, 2)]), ("install", [0, 1, 2]),
+            ("admit", [0, 3], [(3, 3)]), ("admit", [3], []), ("install", [3]),
+            ("admit", [4, 5], [(4, 4), (5, 5)]), ("install", [4, 5])],
+    final={0: 0, 3: 3, 4: 4, 5: 5},
+    hits=1, misses=7, evictions=2,
+)
+
+
+def run_flow_kat(policy, kat):
+    for op in kat["script"]:
+        if op[0] == "admit":
+            assert policy.admit(op[1]) == op[2], op
+        else:
+            policy.install(op[1])
+    assert policy.table() == kat["final"], policy.table()
+    assert (policy.hits, policy.misses, policy.evictions) == (kat["hits"], kat["misses"],
+                                                              kat["evictions"])
 
 
 def run_decode_kat(policy, kat):

@@ -478,3 +478,220 @@ def test_flow_table_republishes_rows_another_layer_evicted():
     assert not cache.table_dirty(keys[1])
     cache.close()
     store.close()
+
+
+def test_fused_prefill_streams_the_experts_once_per_prompt(monkeypatch):
+    """Fused prefill pass (prefill_fused.py) on a 2-layer toy decoder whose
+    MoE blocks page experts through a 16-slot cache: a 96-token call with
+    32-row attention sub-chunks runs each MoE block once over all 96 tokens
+    (one fetch pass per layer), and its output matches the stock call, whose
+    MoE also runs once; chunking the model call instead runs each MoE three
+    times and reads more experts."""
+    import math
+
+    from pagedmoe_amd import config, prefill_fused as PF
+
+    _, S = _mods()
+    spec = O.LayerSpec(1024, 32, 512, 4)
+
+    class Cache:
+        def __init__(self):
+            self.k = self.v = None
+
+        @property
+        def offset(self):
+            return 0 if self.k is None else self.k.shape[2]
+
+        def update_and_fetch(self, k, v):
+            self.k = k if self.k is None else torch.cat([self.k, k], 2)
+            self.v = v if self.v is None else torch.cat([self.v, v], 2)
+            return self.k, self.v
+
+    class Attn(nn.Module):
+        n_heads = 4
+
+        def __init__(self, seed):
+            super().__init__()
+            g = torch.Generator(device=DEV).manual_seed(seed)
+            self.w = [torch.randn(1024, 1024, generator=g, device=DEV) / 32 for _ in range(4)]
+
+        def forward(self, x, mask, cache):
+            b, t, d = x.shape
+            q, k, v = (z.reshape(b, t, 4, d // 4).transpose(1, 2).contiguous()
+                       for z in (x @ self.w[0], x @ self.w[1], x @ self.w[2]))
+            k, v = cache.update_and_fetch(k, v)
+            s = q @ k.transpose(-1, -2).contiguous() / math.sqrt(d // 4) + mask
+            return (torch.softmax(s, -1) @ v).transpose(1, 2).reshape(b, t, d) @ self.w[3]
+
+    class Norm(nn.Module):
+        def forward(self, x):
+            return x / torch.sqrt((x * x).mean(-1, keepdim=True) + 1e-6)
+
+    class Layer(nn.Module):
+        def __init__(self, moe, seed):
+            super().__init__()
+            self.self_attn, self.mlp = Attn(seed), moe
+            self.input_layernorm, self.post_attention_layernorm = Norm(), Norm()
+
+        def forward(self, x, mask=None, cache=None):
+            h = x + self.self_attn(self.input_layernorm(x), mask, cache)
+            return h + self.mlp(self.post_attention_layernorm(h)).float()
+
+    moe_model, _ = _softmax_model(spec, 2, seed=140)
+    cache = S.build_cache_for(moe_model, slots=16)
+    S.patch_model(moe_model, cache)
+    model = nn.Module()
+    model.layers = nn.ModuleList([Layer(moe_model.layers[i].mlp, 141 + i) for i in range(2)])
+
+    def run(x, caches):
+        t, off = x.shape[1], caches[0].offset
+        q = torch.arange(off, off + t, device=DEV)[:, None]
+        mask = torch.where(torch.arange(off + t, device=DEV)[None, :] <= q, 0.0, float("-inf"))
+        for layer, c in zip(model.layers, caches):
+            x = layer(x, mask, c)
+        return x
+
+    calls = []
+    for layer in model.layers:
+        orig = type(layer.mlp).forward
+        layer.mlp.forward = (lambda m, o: lambda x: (calls.append(x.shape[1]), o(m, x))[1])(
+            layer.mlp, orig)
+    x = torch.randn(1, 96, 1024, device=DEV)
+    ref = run(x, [Cache(), Cache()])
+    assert calls == [96, 96]
+    monkeypatch.setattr(config, "ATTN_SUB_CHUNK", 32)
+    assert PF.install(model)
+    try:
+        calls.clear()
+        got = run(x, [Cache(), Cache()])
+        assert calls == [96, 96]            # one MoE pass per layer for the whole prompt
+        assert all(PF.attention_plan(layer, 96, 0) == [(0, 32), (32, 64), (64, 96)]
+                   for layer in model.layers)
+        check_close(got.cpu().numpy(), ref.cpu().numpy(), "fused prefill vs stock")
+        calls.clear()
+        caches = [Cache(), Cache()]
+        for c0 in range(0, 96, 32):         # the model call chunked instead
+            run(x[:, c0:c0 + 32], caches)
+        assert calls == [32, 32] * 3
+    finally:
+        PF.uninstall()
+    cache.close()
+
+
+# ---------------------------------------------------------------- flow decode
+
+def _flow_model(monkeypatch, seed, slots=16):
+    from pagedmoe_amd import config
+    _, S = _mods()
+    spec = O.LayerSpec(1024, 32, 512, 4)
+    model, ol = _softmax_model(spec, 2, seed=seed)
+    cache = S.build_cache_for(model, slots=slots)
+    ring = S.patch_model(model, cache)
+    monkeypatch.setattr(config, "FLOW_WARMUP", 1)
+    monkeypatch.setattr(config, "FLOW_WARM_HIT", 0.0)
+    ring.flow = True
+    return spec, model, ol, cache, ring
+
+
+def _masked_ref(spec, xb, layer_oracle, table):
+    gw, experts, _, _ = layer_oracle
+    ref_i, ref_w, y, _ = O.moe_layer_f64(spec, xb, gw, experts)
+    keep = (table[ref_i] >= 0).astype(np.float64)        # non-resident: zero row
+    return ref_i, ref_w, O.combine_f64(y * keep[..., None], ref_w), keep
+
+
+def test_flow_decode_tokens_without_host_sync(monkeypatch):
+    """Flow decode (streaming.py:675-724, cache.py:861-910): after one
+    per-layer warm-up token, each token's layers run with no host round trip
+    (the routed-id sync is never reached), against the device table
+    published at the token's start.  Every flow token's routing is bit-exact
+    and its output equals the oracle with the non-resident experts' rows
+    zeroed; the last token's misses are admitted at the next token's start,
+    so a repeated routing's experts become resident a few tokens later."""
+    _, S = _mods()
+    spec, model, ol, cache, ring = _flow_model(monkeypatch, seed=150)
+    assert not cache.stitched
+    rng = np.random.default_rng(151)
+    xs = [O.bf16_round(rng.standard_normal((1, spec.hidden), dtype=np.float32))
+          for _ in range(2)]
+    orig = S.StreamedSwitchGLU.routed_ids
+    in_flow = {"on": False}
+
+    def guarded(self, indices):
+        assert not in_flow["on"], "a flow token synced on its routed ids"
+        return orig(self, indices)
+
+    monkeypatch.setattr(S.StreamedSwitchGLU, "routed_ids", guarded)
+    kept = []
+    for t in range(12):
+        xb = xs[min(t, 1)]                  # warm-up token on x0, then x1 repeated: its
+        # experts miss at first, are admitted, and become resident
+        in_flow["on"] = t >= 1
+        outs = [layer.mlp(bits_to_bf16_tensor(xb, DEV)) for layer in model.layers]
+        torch.cuda.synchronize()
+        assert ring.token_flow == (t >= 1)
+        if t == 0:
+            continue
+        for li, layer in enumerate(model.layers):
+            lk = ring[li].layer_key
+            table = cache.host_table(lk)
+            assert np.array_equal(cache.device_table(lk), table), (t, li)
+            ref_i, ref_w, ref, keep = _masked_ref(spec, xb, ol[li], table)
+            gi, gwt = layer.mlp.last_routing
+            assert np.array_equal(gi.cpu().numpy(), ref_i) and np.array_equal(gwt.cpu().numpy(), ref_w)
+            check_close(outs[li].float().cpu().numpy(), ref, f"flow token {t} layer {li}")
+            kept.append(keep.mean())
+    assert ring.flow_tokens == 11 and ring.sync_tokens == 1
+    assert kept[-1] == 1.0 and min(kept) < 1.0    # misses got admitted
+    assert cache.stats()["flow_admits"] > 0
+    cache.close()
+
+
+def test_flow_token_captured_in_a_graph(monkeypatch):
+    """A flow token's two MoE layers captured once as a HIP graph and
+    replayed after each begin_token (auto_pump off): residency changes between
+    replays reach the graph through the republished device tables, and every
+    replay matches the oracle with the non-resident rows zeroed."""
+    spec, model, ol, cache, ring = _flow_model(monkeypatch, seed=160)
+    rng = np.random.default_rng(161)
+    x = torch.empty((1, spec.hidden), dtype=torch.bfloat16, device=DEV)
+    outs = [torch.empty((1, spec.hidden), dtype=torch.bfloat16, device=DEV) for _ in range(2)]
+    xs = [O.bf16_round(rng.standard_normal((1, spec.hidden), dtype=np.float32))
+          for _ in range(2)]
+    x.copy_(bits_to_bf16_tensor(xs[0], DEV))
+    for _ in range(2):                      # warm-up token, then one eager flow token
+        for layer in model.layers:
+            layer.mlp(x)
+    torch.cuda.synchronize()
+    assert ring.token_flow
+    ring.auto_pump = False
+    ring.begin_token()
+
+    def token():
+        for li, layer in enumerate(model.layers):
+            outs[li].copy_(layer.mlp(x))
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        token()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    ring.begin_token()
+    with torch.cuda.graph(graph):
+        token()
+    torch.cuda.synchronize()
+    for rep in range(6):
+        xb = xs[rep % 2]
+        x.copy_(bits_to_bf16_tensor(xb, DEV))
+        ring.begin_token(replayed=rep > 0)
+        tables = [cache.host_table(ring[li].layer_key) for li in range(2)]
+        print(f"[flow] graph replay {rep}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        for li in range(2):
+            _, _, ref, _ = _masked_ref(spec, xb, ol[li], tables[li])
+            check_close(outs[li].float().cpu().numpy(), ref, f"flow graph replay {rep} layer {li}")
+    ring.auto_pump = True
+    cache.close()

@@ -510,6 +510,25 @@ class _OracleSlots:
     def evictions(self):
         return self.pol.evictions
 
+    @property
+    def hits(self):
+        return self.pol.hits
+
+    @property
+    def misses(self):
+        return self.pol.misses
+
+    def admit(self, ids):
+        return self.pol.admit(0, ids)
+
+    def install(self, ids):
+        self.pol.install(0, ids)
+
+
+def test_flow_admit_known_answer():
+    from tests import slot_kats
+    slot_kats.run_flow_kat(_OracleSlots(8), slot_kats.FLOW_ADMIT)
+
 
 @pytest.mark.parametrize("name", ["LFRU_SECOND_CHANCE", "PINNED_OVER_BUDGET"])
 def test_lfru_known_answer(name):

@@ -57,6 +57,19 @@ class NativeSlab:
     def done(self, ticket):
         _lib.check(self.lib.pmoe_slab_prefill_done(self.h, ticket), "prefill_done")
 
+    def admit(self, layer, ids, clear_pins=True):
+        arr = (ctypes.c_int32 * max(1, len(ids)))(*ids)
+        mid = (ctypes.c_int32 * max(1, len(ids)))()
+        msl = (ctypes.c_int32 * max(1, len(ids)))()
+        nm = ctypes.c_int()
+        _lib.check(self.lib.pmoe_slab_admit(self.h, layer, arr, len(ids), mid, msl,
+                                            ctypes.byref(nm), int(clear_pins)), "admit")
+        return [(mid[i], msl[i]) for i in range(nm.value)]
+
+    def install(self, layer, ids):
+        arr = (ctypes.c_int32 * max(1, len(ids)))(*ids)
+        _lib.check(self.lib.pmoe_slab_install(self.h, layer, arr, len(ids)), "install")
+
     def dirty(self, layer):
         return self.lib.pmoe_slab_dirty(self.h, layer)
 
@@ -98,6 +111,59 @@ class _NativeKat:
     @property
     def evictions(self):
         return self.nat.stats().evictions
+
+    @property
+    def hits(self):
+        return self.nat.stats().hits
+
+    @property
+    def misses(self):
+        return self.nat.stats().misses
+
+    def admit(self, ids):
+        return self.nat.admit(0, ids)
+
+    def install(self, ids):
+        self.nat.install(0, ids)
+
+
+def test_native_flow_admit_known_answer():
+    from tests import slot_kats
+    slot_kats.run_flow_kat(_NativeKat(8), slot_kats.FLOW_ADMIT)
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_flow_admission_matches_oracle(seed):
+    """Flow tokens: admit every layer's routing (pins cleared once per token),
+    then install a random subset of the pending reads (copies land in any
+    order); placements, tables and counters equal to the oracle's.  A
+    pending expert cannot be fetched by the decode or prefill policy."""
+    rng = np.random.default_rng(10 + seed)
+    slots, layers, experts = 40, 3, 50
+    nat = NativeSlab(slots, layers, experts)
+    pol = O.SlotPolicy(slots)
+    pending = []
+    for _ in range(300):
+        for layer in range(layers):
+            ids = rng.choice(experts, 6, replace=False).tolist()
+            placed = nat.admit(layer, ids, clear_pins=layer == 0)
+            assert placed == pol.admit(layer, ids, clear_pins=layer == 0)
+            pending += [(layer, e) for e, _ in placed]
+        rng.shuffle(pending)
+        land, pending = pending[:len(pending) // 2], pending[len(pending) // 2:]
+        for layer in range(layers):
+            ids = [e for lyr, e in land if lyr == layer]
+            if ids:
+                nat.install(layer, ids)
+                pol.install(layer, ids)
+        for layer in range(layers):
+            assert np.array_equal(nat.table(layer), pol.table(layer, experts))
+        st = nat.stats()
+        assert (st.hits, st.misses, st.evictions) == (pol.hits, pol.misses, pol.evictions)
+    if pending:
+        layer, e = pending[0]
+        with pytest.raises(_lib.PmoeError, match="not installed"):
+            nat.request(layer, [e])
 
 
 @pytest.mark.parametrize("name", ["LFRU_SECOND_CHANCE", "PINNED_OVER_BUDGET"])
