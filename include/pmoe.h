@@ -242,6 +242,7 @@ int pmoe_combine(const void* y, const float* weights, int n, int k, int hidden,
  *      _evict_to_budget :2236-2291, stitch :717-787, flow table :791-859) -- */
 
 typedef struct pmoe_slab pmoe_slab;
+typedef struct pmoe_copy_engine pmoe_copy_engine;  /* the copy engine, below */
 
 typedef struct {
   int64_t hits, misses, evictions, starved, installs, resident, slots,
@@ -254,6 +255,9 @@ typedef struct {
       stage_slots;
   /* flow decode: misses admitted (a read started into a slot) */
   int64_t flow_admits;
+  /* speculative reads started, claimed by their layer's fetch (of which
+   * not yet landed at the claim), and handed back unclaimed */
+  int64_t spec_started, spec_claims, spec_claims_late, spec_dropped;
 } pmoe_slab_stats;
 
 /* Slot policy + device table [n_layers, n_experts] int32 (-1 = absent).
@@ -318,6 +322,27 @@ int pmoe_slab_admit(pmoe_slab* s, int layer, const int32_t* ids, int n_ids,
  * _attach_staging(install_now=True) :2866-2910). */
 int pmoe_slab_install(pmoe_slab* s, int layer, const int32_t* ids, int n_ids);
 
+/* The copy engine speculative reads go through (one of its own, so demand
+ * copies never queue behind guesses on a stream).  NULL turns speculation
+ * off; only allowed while no guess is outstanding. */
+int pmoe_slab_set_spec_engine(pmoe_slab* s, pmoe_copy_engine* ce);
+
+/* Prediction-driven prefetch (ExpertCache.prefetch, cache.py:2853, with
+ * evict_ok=False): for ids in priority order, skipping resident, pending and
+ * already staged ones, take a free slot (never an eviction) while fewer than
+ * max_staged guesses are outstanding, and start its read from the host store
+ * through the speculation engine, behind that engine's latest fence.
+ * *n_started receives the reads started.  A guess is claimed by its layer's
+ * pmoe_slab_fetch (or pmoe_slab_request); a fetch hands back that layer's
+ * unclaimed guesses, whose slots return once their reads have landed. */
+int pmoe_slab_speculate(pmoe_slab* s, const pmoe_geom* g, void* slab,
+                        const void* host_store, int layer, const int32_t* ids,
+                        int n_ids, int max_staged, int* n_started);
+
+/* Hand back every outstanding guess (flow decode and prefill do not claim
+ * them). */
+int pmoe_slab_drop_staged(pmoe_slab* s);
+
 /* Register slab slots [first_slot, first_slot + n_slots) (past the routed
  * slots) as the prefill stage: slots prefill misses are read into when no
  * free slot is left, never resident, handed back after each group.
@@ -357,8 +382,6 @@ int pmoe_slab_stats_get(pmoe_slab* s, pmoe_slab_stats* out);
 /* ---- copy engine (replaces the native pread pool, _native_read.c:38-698:
  *      urgent/normal queues, split pieces, promote, first-error latch) ----- */
 
-typedef struct pmoe_copy_engine pmoe_copy_engine;
-
 /* Pinned host memory (hipHostMalloc) for the host expert store. */
 int pmoe_host_alloc(void** out, size_t bytes);
 int pmoe_host_free(void* p);
@@ -396,6 +419,9 @@ int pmoe_copy_batch_done(pmoe_copy_engine* ce, int batch);
 
 /* Make stream wait for the batch's copies. */
 int pmoe_copy_batch_join(pmoe_copy_engine* ce, int batch, void* stream);
+
+/* Block the host until the batch's copies have completed. */
+int pmoe_copy_batch_wait(pmoe_copy_engine* ce, int batch);
 
 /* Return the batch record (its copies need not have completed). */
 int pmoe_copy_batch_release(pmoe_copy_engine* ce, int batch);

@@ -527,6 +527,10 @@ class SlotPolicy:
             self._evict(key)
             if self.free:
                 return self.free.pop()
+        staged = self.__dict__.get("staged")
+        if staged:  # give up an unclaimed guess, the latest first (cache.py:1149-1157)
+            key = next(reversed(staged))
+            return staged.pop(key)
         self.starved += 1
         return None
 
@@ -554,10 +558,14 @@ class SlotPolicy:
 
     def step(self, layer, ids):
         """One layer fetch.  Returns (hit ids, [(miss id, slot)]) with misses
-        installed.  ``ids`` is taken as a set, visited ascending."""
+        installed.  ``ids`` is taken as a set, visited ascending.  A staged
+        guess (``speculate``) is claimed: a hit installed at its slot, no
+        read (cache.py:2379-2386); the layer's unclaimed guesses are handed
+        back (their slots drain to the free list at the next settle)."""
         self.pinned.clear()
+        staged = self.__dict__.setdefault("staged", OrderedDict())
         ids = sorted({int(e) for e in ids})
-        hits, misses = [], []
+        hits, misses, claimed = [], [], []
         for e in ids:
             key = (layer, e)
             if key in self.lru:
@@ -565,6 +573,12 @@ class SlotPolicy:
                 self.lru.move_to_end(key)
                 self.freq[key] = min(self.freq_max, self.freq.get(key, 0) + 1)
                 self.pinned.add(self.slot_of[key])
+                hits.append(e)
+            elif key in staged:
+                self.hits += 1
+                slot = staged.pop(key)
+                self.pinned.add(slot)
+                claimed.append((e, slot))
                 hits.append(e)
             else:
                 self.misses += 1
@@ -574,14 +588,56 @@ class SlotPolicy:
             slot = self._alloc(True)
             if slot is None:
                 continue
-            self.slot_of[(layer, e)] = slot
             self.pinned.add(slot)
             placed.append((e, slot))
-        for e, slot in placed:
+        for e, slot in sorted(claimed + placed):
             key = (layer, e)
+            self.slot_of[key] = slot
             self.lru[key] = slot
             self._trim()
+        self._drop_staged(lambda key: key[0] == layer)
         return hits, placed
+
+    # ---- speculation (ExpertCache.prefetch cache.py:2853 with
+    # evict_ok=False; staging and claim :2379-2386)
+
+    def speculate(self, layer, ids, max_staged):
+        """Guesses in priority order into free slots only, while fewer than
+        max_staged are outstanding.  Returns [(id, slot)] started."""
+        self.settle()
+        staged = self.__dict__.setdefault("staged", OrderedDict())
+        pending = getattr(self, "pending", {})
+        got = []
+        for e in ids:
+            key = (layer, int(e))
+            if key in self.lru or key in pending or key in staged or any(k == key for k, _ in got):
+                continue
+            if len(staged) + len(got) >= max_staged or not self.free:
+                break
+            got.append((key, self.free.pop()))
+        for key, slot in got:
+            staged[key] = slot
+        return [(key[1], slot) for key, slot in got]
+
+    def _drop_staged(self, which):
+        staged = self.__dict__.setdefault("staged", OrderedDict())
+        drain = self.__dict__.setdefault("draining", [])
+        for key in [k for k in staged if which(k)]:
+            drain.append(staged.pop(key))
+
+    def drop_all_staged(self):
+        staged = self.__dict__.setdefault("staged", OrderedDict())
+        drain = self.__dict__.setdefault("draining", [])
+        while staged:
+            key = next(reversed(staged))
+            drain.append(staged.pop(key))
+        self.settle()
+
+    def settle(self):
+        """Handed-back guesses' reads have landed: their slots are free."""
+        drain = self.__dict__.setdefault("draining", [])
+        self.free.extend(drain)
+        drain.clear()
 
     # ---- prefill fetch groups (cache.py:2347-2453 with prefill=True,
     # PREFILL_TOUCH=0, PREFILL_SLAB=1; _install(..., "soft") :2306-2312;

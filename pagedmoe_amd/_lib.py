@@ -56,7 +56,8 @@ class SlabStats(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int64) for n in (
         "hits", "misses", "evictions", "starved", "installs", "resident", "slots",
         "budget", "reserve", "stitched", "bytes_copied", "prefill_slot_reads",
-        "prefill_installs", "stage_reads", "prefill_starved", "stage_slots", "flow_admits")]
+        "prefill_installs", "stage_reads", "prefill_starved", "stage_slots", "flow_admits",
+        "spec_started", "spec_claims", "spec_claims_late", "spec_dropped")]
 
 
 _P = ctypes.c_void_p
@@ -102,6 +103,10 @@ SIGNATURES = {
     "pmoe_slab_read_device_row": (_I, [_P, _I, _I32P]),
     "pmoe_slab_admit": (_I, [_P, _I, _I32P, _I, _I32P, _I32P, ctypes.POINTER(_I), _I]),
     "pmoe_slab_install": (_I, [_P, _I, _I32P, _I]),
+    "pmoe_slab_set_spec_engine": (_I, [_P, _P]),
+    "pmoe_slab_speculate": (_I, [_P, ctypes.POINTER(Geom), _P, _P, _I, _I32P, _I, _I,
+                                 ctypes.POINTER(_I)]),
+    "pmoe_slab_drop_staged": (_I, [_P]),
     "pmoe_slab_set_stage": (_I, [_P, _I, _I]),
     "pmoe_slab_capacity": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "pmoe_slab_prefill_request": (_I, [_P, _I, _I32P, _I, _I32P, _I32P, ctypes.POINTER(_I),
@@ -119,6 +124,7 @@ SIGNATURES = {
     "pmoe_copy_issue": (_I, [_P, ctypes.POINTER(_I)]),
     "pmoe_copy_batch_done": (_I, [_P, _I]),
     "pmoe_copy_batch_join": (_I, [_P, _I, _P]),
+    "pmoe_copy_batch_wait": (_I, [_P, _I]),
     "pmoe_copy_batch_release": (_I, [_P, _I]),
     "pmoe_copy_join": (_I, [_P, _P]),
     "pmoe_copy_sync": (_I, [_P]),

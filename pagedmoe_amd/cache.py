@@ -159,11 +159,22 @@ class ExpertCache:
         check(lib().pmoe_slab_set_stage(self._h, self.stage_first, self.stage_slots),
               "pmoe_slab_set_stage")
         self._ce = ctypes.c_void_p()
+        self._ce_spec = ctypes.c_void_p()
         if host_store is not None:
             check(lib().pmoe_copy_engine_create(ctypes.byref(self._ce), config.COPY_SPLIT_BYTES,
                                                 config.COPY_STREAMS), "pmoe_copy_engine_create")
+            # speculative reads get an engine (and stream) of their own, so a
+            # demand copy never queues behind a guess on one stream
+            check(lib().pmoe_copy_engine_create(ctypes.byref(self._ce_spec),
+                                                config.COPY_SPLIT_BYTES, 1),
+                  "pmoe_copy_engine_create")
+            check(lib().pmoe_slab_set_spec_engine(self._h, self._ce_spec),
+                  "pmoe_slab_set_spec_engine")
+        self.reserve = max(4, int(self.routed_slots * (config.SLAB_RESERVE_FRAC
+                                                       if reserve_frac is None else reserve_frac)))
         self.stitched = False
         self.group_passes = 0
+        self.spec_log = None     # a list records fetch / speculate calls (tests replay them)
 
     @classmethod
     def from_budget(cls, budget_bytes: int, g: Geom, layer_keys, n_experts: int, **kw):
@@ -257,6 +268,8 @@ class ExpertCache:
         if self.host_store is None:
             raise PmoeError("fetch needs a host expert store")
         ids = [int(e) for e in expert_ids]
+        if self.spec_log is not None:
+            self.spec_log.append(("fetch", layer_key, list(ids)))
         arr = (ctypes.c_int32 * max(1, len(ids)))(*ids)
         nm = ctypes.c_int()
         stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -323,6 +336,45 @@ class ExpertCache:
 
     def prefill_done(self, group: PrefillGroup) -> None:
         check(lib().pmoe_slab_prefill_done(self._h, group.ticket), "pmoe_slab_prefill_done")
+
+    # ------------------------------------------------------------- speculation
+
+    def spec_fence(self) -> None:
+        """Speculative reads issued from now on wait for everything queued
+        so far on the current stream (recorded before a layer's compute, so
+        the guesses it issues afterwards run under that compute)."""
+        if self._ce_spec.value:
+            check(lib().pmoe_copy_fence(self._ce_spec, self._stream()), "pmoe_copy_fence")
+
+    def speculate(self, layer_key, expert_ids, max_staged: int | None = None) -> int:
+        """Start speculative reads (prediction-driven prefetch,
+        cache.py:2853) of expert_ids, in priority order, into free slots
+        only; a guess is claimed by the layer's next fetch.  At most
+        ``max_staged`` (default: the reserve) guesses are outstanding.
+        Returns the reads started."""
+        if not self._ce_spec.value:
+            return 0
+        ids = [int(e) for e in expert_ids]
+        cap = self.reserve if max_staged is None else int(max_staged)
+        if self.spec_log is not None:
+            self.spec_log.append(("speculate", layer_key, list(ids), cap))
+        arr = (ctypes.c_int32 * max(1, len(ids)))(*ids)
+        n = ctypes.c_int()
+        check(lib().pmoe_slab_speculate(self._h, ctypes.byref(self.geom),
+                                        ctypes.c_void_p(self.slab.data_ptr),
+                                        ctypes.c_void_p(self.host_store.address),
+                                        self.layer_index(layer_key), arr, len(ids), cap,
+                                        ctypes.byref(n)), "pmoe_slab_speculate")
+        return n.value
+
+    def drop_staged(self) -> None:
+        """Hand back every outstanding guess (flow decode, prefill)."""
+        check(lib().pmoe_slab_drop_staged(self._h), "pmoe_slab_drop_staged")
+
+    def sync_spec(self) -> None:
+        """Block until every speculative read has landed."""
+        if self._ce_spec.value:
+            check(lib().pmoe_copy_sync(self._ce_spec), "pmoe_copy_sync")
 
     # ------------------------------------------------------------- flow
 
@@ -451,9 +503,17 @@ class ExpertCache:
             "prefill_slot_reads": st.prefill_slot_reads, "prefill_installs": st.prefill_installs,
             "stage_reads": st.stage_reads, "prefill_slot_starved": st.prefill_starved,
             "stage_slots": st.stage_slots, "flow_admits": st.flow_admits,
+            "spec_started": st.spec_started, "spec_claims": st.spec_claims,
+            "spec_claims_late": st.spec_claims_late, "spec_dropped": st.spec_dropped,
         }
 
     def close(self) -> None:
+        if self._ce_spec.value:
+            lib().pmoe_copy_sync(self._ce_spec)
+            lib().pmoe_slab_drop_staged(self._h)
+            lib().pmoe_slab_set_spec_engine(self._h, None)
+            lib().pmoe_copy_engine_destroy(self._ce_spec)
+            self._ce_spec = ctypes.c_void_p()
         if self._ce.value:
             lib().pmoe_copy_engine_destroy(self._ce)
             self._ce = ctypes.c_void_p()

@@ -6,7 +6,10 @@ path (config.py: SLAB_RESERVE_FRAC :718, LFRU/LFRU_SCAN :1477-1478, STITCH
 :1603-1608, GROUP_BYTES :1531); ``sync_from_environ()`` re-reads them
 (config.py:853); FUSED_PREFILL :1633 and ATTN_SUB_CHUNK :1562 for the
 fused prefill pass; FLOW / FLOW_WARMUP / FLOW_WARM_HIT :1218-1237 for flow
-decode.  DECODE_MAX_TOKENS is the reference's _DECODE_MAX_TOKENS
+decode; PREDICT_DEPTH :747, PREDICT_SLACK :761 and PREFETCH_DEPTH :722 for
+speculative prefetch (PREFETCH_DEPTH defaults to 0 here: the previous-token
+heuristic pays off with the reference's SSD queue, not a PCIe copy engine).
+DECODE_MAX_TOKENS is the reference's _DECODE_MAX_TOKENS
 (streaming.py:69): calls of more tokens take the prefill residency policy.
 """
 
@@ -43,6 +46,9 @@ FUSED_PREFILL = True      # long calls sub-chunk attention, run the MoE once
 FLOW = False              # decode tokens with no host sync inside (residency once per token)
 FLOW_WARMUP = 2           # tokens after a prefill that take the per-layer path first
 FLOW_WARM_HIT = 0.9       # hit-rate EMA the per-layer path must reach before flow resumes
+PREDICT_DEPTH = 3         # route prediction: layers predicted ahead per stride
+PREDICT_SLACK = 2         # extra experts per predicted layer beyond its top-k
+PREFETCH_DEPTH = 0        # previous-token heuristic: next layers' last ids (0 = off)
 ATTN_SUB_CHUNK = 2048     # rows per attention sub-chunk, at most
 ATTN_SCORE_MB = 1024      # fp32 score matrix (heads x rows x keys) of one sub-chunk, at most
 
@@ -51,6 +57,7 @@ def sync_from_environ() -> None:
     global SLAB_RESERVE_FRAC, LFRU, LFRU_SCAN, STITCH, COPY_SPLIT_BYTES, COPY_STREAMS
     global DECODE_MAX_TOKENS, PREFILL_STAGE, PREFILL_STAGE_GROUP_MB, GROUP_BYTES
     global FUSED_PREFILL, ATTN_SUB_CHUNK, ATTN_SCORE_MB, FLOW, FLOW_WARMUP, FLOW_WARM_HIT
+    global PREDICT_DEPTH, PREDICT_SLACK, PREFETCH_DEPTH
     SLAB_RESERVE_FRAC = _env("SLAB_RESERVE_FRAC", 0.1, float)
     LFRU = _env("LFRU", True, _bool)
     LFRU_SCAN = _env("LFRU_SCAN", 8, int)
@@ -67,6 +74,9 @@ def sync_from_environ() -> None:
     FLOW = _env("FLOW", False, _bool)
     FLOW_WARMUP = _env("FLOW_WARMUP", 2, int)
     FLOW_WARM_HIT = _env("FLOW_WARM_HIT", 0.9, float)
+    PREDICT_DEPTH = _env("PREDICT_DEPTH", 3, int)
+    PREDICT_SLACK = _env("PREDICT_SLACK", 2, int)
+    PREFETCH_DEPTH = _env("PREFETCH_DEPTH", 0, int)
 
 
 sync_from_environ()

@@ -214,6 +214,19 @@ extern "C" int pmoe_copy_batch_join(pmoe_copy_engine* ce, int batch, void* strea
   return PMOE_OK;
 }
 
+extern "C" int pmoe_copy_batch_wait(pmoe_copy_engine* ce, int batch) {
+  pmoe::clear_error();
+  std::vector<hipEvent_t> evs;
+  {
+    std::lock_guard<std::mutex> lk(ce->mu);
+    auto* b = live_batch(ce, batch);
+    if (!b) return pmoe::fail(PMOE_EINVAL, "copy_batch_wait: no such batch");
+    evs = b->ev;
+  }
+  for (hipEvent_t ev : evs) PMOE_HIP(hipEventSynchronize(ev));
+  return PMOE_OK;
+}
+
 extern "C" int pmoe_copy_batch_release(pmoe_copy_engine* ce, int batch) {
   pmoe::clear_error();
   std::lock_guard<std::mutex> lk(ce->mu);

@@ -20,6 +20,16 @@
 // by the group's ticket and handed back when the group is done
 // (_stage_return :1427-1440, _release_slot :1101-1116).
 //
+// Speculative reads (prediction-driven prefetch: ExpertCache.prefetch
+// cache.py:2853, _prefetch_locked with evict_ok=False, staging _raw_ready,
+// claim in _begin via _drop_raw :2379-2386) go through a second copy engine
+// into free slots only, never evicting.  A staged guess is neither resident
+// nor in the table; the fetch of its layer claims it (installed at its slot
+// with no new read; the compute stream joins its copy batch, and a claim
+// whose copy had not landed yet counts as a miss, as an in-flight read does
+// in the reference) and hands back the layer's unclaimed guesses, whose slots
+// return to the free list only once their copies have landed.
+//
 // The device table [layers, experts] int32 (-1 = absent) is the flow table
 // (:791-859).  A row is marked dirty whenever its host copy changes (an
 // install, an eviction by any layer's fetch, a group's slots coming back),
@@ -37,6 +47,7 @@ namespace {
 constexpr int kFreqMax = 8;
 constexpr int kPublishChunk = 512;
 constexpr int kMaxTickets = 64;
+constexpr int kMaxSpecBatches = 64;  // the copy engine's batch records
 
 struct TableChunk {
   int32_t v[kPublishChunk];
@@ -76,6 +87,13 @@ struct pmoe_slab {
   int stage_first = 0, stage_n = 0;
   std::vector<int> stage_free;            // stack
   Ticket tickets[kMaxTickets];
+  // speculation: staged[key] = slot of a guess whose read was started
+  std::vector<int> staged_slot, staged_batch;
+  std::vector<int> staged_keys;
+  std::vector<std::pair<int, int>> draining;  // (slot, batch) of dropped guesses
+  int batch_refs[kMaxSpecBatches] = {};
+  pmoe_copy_engine* spec_ce = nullptr;
+  std::vector<std::pair<int, int>> claims;    // (key, batch) of the last request
   pmoe_slab_stats st{};
   std::mutex mu;
 
@@ -138,6 +156,20 @@ struct pmoe_slab {
       free_slots.pop_back();
       return s;
     }
+    // nothing evictable: give up an unclaimed guess, the latest staged first
+    // (cache.py:1149-1157); its read must land before the slot is reused
+    if (!staged_keys.empty() && spec_ce) {
+      const int k = staged_keys.back();
+      const int slot = staged_slot[k], b = staged_batch[k];
+      if (pmoe_copy_batch_wait(spec_ce, b) == PMOE_OK) {
+        staged_slot[k] = -1;
+        staged_batch[k] = -1;
+        staged_keys.pop_back();
+        ++st.spec_dropped;
+        if (--batch_refs[b] == 0) (void)pmoe_copy_batch_release(spec_ce, b);
+        return slot;
+      }
+    }
     ++st.starved;
     return -1;
   }
@@ -166,6 +198,20 @@ struct pmoe_slab {
       if (victim < 0) break;
       evict(victim);
     }
+  }
+  // a guess leaves the staged set; its slot drains back once its read lands
+  void drop_staged(int k) {
+    draining.emplace_back(staged_slot[k], staged_batch[k]);
+    staged_slot[k] = -1;
+    staged_batch[k] = -1;
+    staged_keys.erase(std::find(staged_keys.begin(), staged_keys.end(), k));
+    ++st.spec_dropped;
+  }
+  void drop_layer_staged(int layer) {
+    std::vector<int> keys;
+    for (int k : staged_keys)
+      if (k / n_experts == layer) keys.push_back(k);
+    for (int k : keys) drop_staged(k);
   }
   int live_tickets() const {
     int n = 0;
@@ -201,6 +247,8 @@ extern "C" int pmoe_slab_create(pmoe_slab** out, int slots, int n_layers, int n_
   s->in_lru.assign(keys, 0);
   s->stitch_key.assign(keys, 0);
   s->pending.assign(keys, 0);
+  s->staged_slot.assign(keys, -1);
+  s->staged_batch.assign(keys, -1);
   s->pinned.assign(slots, 0);
   s->table.assign(keys, -1);
   s->dirty.assign(n_layers, 0);
@@ -302,7 +350,9 @@ extern "C" int pmoe_slab_request(pmoe_slab* s, int layer, const int32_t* ids, in
     if (s->pending[base + e])
       return pmoe::fail(PMOE_EINVAL, "slab_request: an admitted expert's copy is not installed");
   s->clear_pins();
+  s->claims.clear();
   std::vector<int> misses;
+  std::vector<std::pair<int, int>> claimed;  // (expert, slot): installed with the misses
   for (int e : uniq) {
     const int k = base + e;
     if (s->in_lru[k]) {
@@ -310,6 +360,16 @@ extern "C" int pmoe_slab_request(pmoe_slab* s, int layer, const int32_t* ids, in
       s->move_to_end(k);
       s->freq[k] = std::min(kFreqMax, s->freq[k] + 1);
       s->pin(s->slot_of[k]);
+    } else if (s->staged_slot[k] >= 0) {  // a guess claimed: no new read
+      ++s->st.hits;
+      ++s->st.spec_claims;
+      const int slot = s->staged_slot[k];
+      s->claims.emplace_back(k, s->staged_batch[k]);
+      s->staged_slot[k] = -1;
+      s->staged_batch[k] = -1;
+      s->staged_keys.erase(std::find(s->staged_keys.begin(), s->staged_keys.end(), k));
+      s->pin(slot);
+      claimed.emplace_back(e, slot);
     } else {
       ++s->st.misses;
       misses.push_back(e);
@@ -323,13 +383,21 @@ extern "C" int pmoe_slab_request(pmoe_slab* s, int layer, const int32_t* ids, in
     s->pin(slot);
     got.emplace_back(e, slot);
   }
-  for (auto& es : got) {
+  // installs (claimed guesses and placed misses) in ascending expert id, each
+  // followed by the trim, once every entry of this step is pinned
+  std::vector<std::pair<int, int>> all(claimed);
+  all.insert(all.end(), got.begin(), got.end());
+  std::sort(all.begin(), all.end());
+  for (auto& es : all) {
     s->install(base + es.first, es.second);
     s->trim();
+  }
+  for (auto& es : got) {
     if (miss_ids) miss_ids[placed] = es.first;
     if (miss_slots) miss_slots[placed] = es.second;
     ++placed;
   }
+  s->drop_layer_staged(layer);  // this layer's guesses it did not route
   *n_miss = placed;
   return PMOE_OK;
 }
@@ -345,6 +413,7 @@ extern "C" int pmoe_slab_admit(pmoe_slab* s, int layer, const int32_t* ids, int 
   if (rc) return rc;
   std::lock_guard<std::mutex> lk(s->mu);
   if (clear_pins) s->clear_pins();
+  s->drop_layer_staged(layer);
   const int base = layer * s->n_experts;
   int placed = 0;
   for (int e : uniq) {
@@ -389,6 +458,97 @@ extern "C" int pmoe_slab_install(pmoe_slab* s, int layer, const int32_t* ids, in
     s->trim();
   }
   return PMOE_OK;
+}
+
+extern "C" int pmoe_slab_set_spec_engine(pmoe_slab* s, pmoe_copy_engine* ce) {
+  pmoe::clear_error();
+  if (!s) return pmoe::fail(PMOE_EINVAL, "slab_set_spec_engine: null slab");
+  std::lock_guard<std::mutex> lk(s->mu);
+  if (!s->staged_keys.empty() || !s->draining.empty())
+    return pmoe::fail(PMOE_EINVAL, "slab_set_spec_engine: speculative reads outstanding");
+  s->spec_ce = ce;
+  return PMOE_OK;
+}
+
+// Caller holds mu.  Dropped guesses whose reads have landed give back their
+// slots; batch records nothing references any more are released.
+static int settle_spec(pmoe_slab* s) {
+  if (!s->spec_ce) return PMOE_OK;
+  std::vector<std::pair<int, int>> keep;
+  for (auto& sb : s->draining) {
+    const int r = pmoe_copy_batch_done(s->spec_ce, sb.second);
+    if (r < 0) return r;
+    if (r == 0) {
+      keep.push_back(sb);
+      continue;
+    }
+    s->free_slots.push_back(sb.first);
+    if (--s->batch_refs[sb.second] == 0) {
+      const int rc = pmoe_copy_batch_release(s->spec_ce, sb.second);
+      if (rc) return rc;
+    }
+  }
+  s->draining.swap(keep);
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_slab_speculate(pmoe_slab* s, const pmoe_geom* g, void* slab,
+                                   const void* host_store, int layer, const int32_t* ids,
+                                   int n_ids, int max_staged, int* n_started) {
+  pmoe::clear_error();
+  if (!s || !g || !slab || !host_store || (n_ids > 0 && !ids) || !n_started || layer < 0 ||
+      layer >= s->n_layers || n_ids < 0)
+    return pmoe::fail(PMOE_EINVAL, "slab_speculate: bad argument");
+  *n_started = 0;
+  std::lock_guard<std::mutex> lk(s->mu);
+  if (!s->spec_ce) return pmoe::fail(PMOE_EINVAL, "slab_speculate: no speculation engine");
+  int rc = settle_spec(s);
+  if (rc) return rc;
+  const int base = layer * s->n_experts;
+  std::vector<std::pair<int, int>> got;  // (key, slot)
+  for (int i = 0; i < n_ids; ++i) {
+    const int e = ids[i];
+    if (e < 0 || e >= s->n_experts) return pmoe::fail(PMOE_EINVAL, "slab_speculate: id out of range");
+    const int k = base + e;
+    if (s->in_lru[k] || s->pending[k] || s->staged_slot[k] >= 0) continue;
+    bool dup = false;
+    for (auto& ks : got) dup |= ks.first == k;
+    if (dup) continue;
+    if (int(s->staged_keys.size() + got.size()) >= max_staged || s->free_slots.empty()) break;
+    got.emplace_back(k, s->free_slots.back());
+    s->free_slots.pop_back();
+  }
+  if (got.empty()) return PMOE_OK;
+  const size_t eb = size_t(g->expert_bytes);
+  for (auto& ks : got) {
+    rc = pmoe_copy_submit(s->spec_ce, static_cast<uint8_t*>(slab) + size_t(ks.second) * eb,
+                          static_cast<const uint8_t*>(host_store) + size_t(ks.first) * eb, eb, 0);
+    if (rc) break;
+  }
+  int b = -1;
+  if (!rc) rc = pmoe_copy_issue(s->spec_ce, &b);
+  if (rc) {  // nothing staged: the slots go back
+    for (auto it = got.rbegin(); it != got.rend(); ++it) s->free_slots.push_back(it->second);
+    return rc;
+  }
+  for (auto& ks : got) {
+    s->staged_slot[ks.first] = ks.second;
+    s->staged_batch[ks.first] = b;
+    s->staged_keys.push_back(ks.first);
+  }
+  s->batch_refs[b] = int(got.size());
+  s->st.spec_started += int64_t(got.size());
+  s->st.bytes_copied += int64_t(got.size()) * int64_t(eb);
+  *n_started = int(got.size());
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_slab_drop_staged(pmoe_slab* s) {
+  pmoe::clear_error();
+  if (!s) return pmoe::fail(PMOE_EINVAL, "slab_drop_staged: null slab");
+  std::lock_guard<std::mutex> lk(s->mu);
+  while (!s->staged_keys.empty()) s->drop_staged(s->staged_keys.back());
+  return settle_spec(s);
 }
 
 extern "C" int pmoe_slab_set_stage(pmoe_slab* s, int first_slot, int n_slots) {
@@ -436,6 +596,7 @@ extern "C" int pmoe_slab_prefill_request(pmoe_slab* s, int layer, const int32_t*
     if (s->pending[base + e])
       return pmoe::fail(PMOE_EINVAL,
                         "slab_prefill_request: an admitted expert's copy is not installed");
+  s->drop_layer_staged(layer);
   Ticket& tk = s->tickets[t];
   tk = Ticket();
   tk.live = true;
@@ -604,8 +765,35 @@ extern "C" int pmoe_slab_fetch(pmoe_slab* s, pmoe_copy_engine* ce, const pmoe_ge
     return pmoe::fail(PMOE_EINVAL, "slab_fetch: bad argument");
   std::vector<int32_t> mid(size_t(n_ids) + 1), msl(size_t(n_ids) + 1);
   int nm = 0;
-  int rc = pmoe_slab_request(s, layer, ids, n_ids, mid.data(), msl.data(), &nm);
+  int rc;
+  {
+    std::lock_guard<std::mutex> lk(s->mu);
+    rc = settle_spec(s);
+  }
   if (rc) return rc;
+  rc = pmoe_slab_request(s, layer, ids, n_ids, mid.data(), msl.data(), &nm);
+  if (rc) return rc;
+  {
+    // claimed guesses: the compute stream waits for their reads; one that
+    // had not landed counts as a miss (cache.py:2387-2401)
+    std::lock_guard<std::mutex> lk(s->mu);
+    for (auto& kb : s->claims) {
+      const int done = pmoe_copy_batch_done(s->spec_ce, kb.second);
+      if (done < 0) return done;
+      if (!done) {
+        --s->st.hits;
+        ++s->st.misses;
+        ++s->st.spec_claims_late;
+      }
+      rc = pmoe_copy_batch_join(s->spec_ce, kb.second, stream);
+      if (rc) return rc;
+      if (--s->batch_refs[kb.second] == 0) {
+        rc = pmoe_copy_batch_release(s->spec_ce, kb.second);
+        if (rc) return rc;
+      }
+    }
+    s->claims.clear();
+  }
   rc = submit_misses(s, ce, g, slab, host_store, layer, mid.data(), msl.data(), nm);
   if (rc) return rc;
   rc = pmoe_slab_publish(s, layer, stream);

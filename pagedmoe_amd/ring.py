@@ -1,8 +1,25 @@
 """The streamed MoE layers of one model, in order, and their per-token state.
 
 Counterpart of the reference's PrefetchRing (streaming.py:1404-2299), which
-patch_model returns.  Here it carries flow decode: a decode token whose MoE
-layers never wait on the host (streaming.py:675-749, cache.py:791-910).
+patch_model returns.  It carries speculative prefetch and flow decode (a
+decode token whose MoE layers never wait on the host, streaming.py:675-749,
+cache.py:791-910).
+
+Speculative prefetch (route prediction, streaming.py:2013-2299).  After a
+decode layer L has enqueued its compute, the routers of layers L+2 ..
+L+1+PREDICT_DEPTH (on a stride of PREDICT_DEPTH layers, so each layer is
+predicted once) run on layer L's last-token hidden state, their top-k +
+PREDICT_SLACK ids are chosen on the GPU (the same routing kernels as the
+demand path), and the ids ride layer L+1's routing sync to the host -- no
+sync of their own.  After layer L+1's fetch and compute are enqueued, the
+guesses are issued as speculative reads into free slots
+(ExpertCache.speculate: a separate copy engine, never an eviction), so they
+run under the compute of the layers between; the target layer's fetch
+claims the ones it routes.  Precision is counted the reference's way:
+predicted ids issued and used at the target's demand (pred_issued,
+pred_used).  The targets start two layers out because the ids reach the host
+one layer later (streaming.py:2002).  PREFETCH_DEPTH adds the previous-token
+heuristic: the next layers' last routed ids (streaming.py:2283-2299).
 
 Flow decode.  The slot table is already on the GPU and the expert kernels
 read it directly, computing an exact zero row for every routed expert that
@@ -62,6 +79,16 @@ class PrefetchRing:
         self._token_stats = None
         self.flow_tokens = 0
         self.sync_tokens = 0
+        # speculative prefetch
+        self.predict_depth = int(config.PREDICT_DEPTH)
+        self.prefetch_depth = int(config.PREFETCH_DEPTH)
+        self.slack = int(config.PREDICT_SLACK)
+        self._pred_gpu: list = []      # [(target index, device ids)] not yet on the host
+        self._pred_host: list = []     # [(target index, ids)] waiting to be issued
+        self.predicted: dict = {}      # target index -> ids guessed for its next fetch
+        self.pred_issued = 0
+        self.pred_used = 0
+        self.spec_reads = 0
 
     # ---- sequence protocol over the layers
     def __len__(self):
@@ -122,6 +149,7 @@ class PrefetchRing:
         if self._fenced:
             self._fence.synchronize()
             self._fenced = False
+        c.drop_staged()                  # flow tokens claim no guesses
         self._pending = c.flow_install_ready(self._pending)
         batch = []
         if self._noted or replayed:
@@ -149,6 +177,57 @@ class PrefetchRing:
             self._fence.record()
             self._fenced = True
 
+    # ---- speculative prefetch
+    def _router_of(self, index):
+        blk = getattr(self.layers[index], "pred", None)
+        return blk if blk is not None and hasattr(blk, "predict_ids") else None
+
+    def predict(self, index: int, x2: torch.Tensor) -> None:
+        """Enqueue the route prediction of the layers this stride covers on
+        the last token's hidden state (device ids; no sync)."""
+        d = self.predict_depth
+        if d <= 0 or index % d != 0:
+            return
+        x_last = x2[-1:]
+        for tgt in range(index + 2, index + 2 + d):
+            if tgt >= len(self.layers):
+                break
+            blk = self._router_of(tgt)
+            if blk is not None:
+                self._pred_gpu.append((tgt, blk.predict_ids(x_last, self.slack)))
+
+    def collect_predictions(self) -> None:
+        """After a routing sync: the pending predictions are complete; bring
+        their ids to the host (a small copy, no extra wait)."""
+        for tgt, ids in self._pred_gpu:
+            self._pred_host.append((tgt, sorted({int(e) for e in ids.reshape(-1).tolist()})))
+        self._pred_gpu = []
+
+    def note_demand(self, index: int, ids) -> None:
+        """A layer's fetch: score its prediction (pred_issued / pred_used)."""
+        guess = self.predicted.pop(index, None)
+        if guess:
+            self.pred_issued += len(guess)
+            self.pred_used += len(guess & set(int(e) for e in ids))
+
+    def speculate(self, index: int, x2: torch.Tensor) -> None:
+        """After layer ``index`` enqueued its compute: issue the collected
+        guesses for layers still ahead, the previous-token heuristic, and
+        the next prediction."""
+        c = self.cache
+        if c.stitched or self.token_flow:
+            return
+        ready, self._pred_host = self._pred_host, []
+        for tgt, ids in ready:
+            if tgt > index:
+                self.predicted.setdefault(tgt, set()).update(ids)
+                self.spec_reads += c.speculate(self.layers[tgt].layer_key, ids)
+        for d in range(1, self.prefetch_depth + 1):
+            nxt = self.layers[(index + d) % len(self.layers)]
+            if nxt.last_ids:
+                self.spec_reads += c.speculate(nxt.layer_key, nxt.last_ids)
+        self.predict(index, x2)
+
     def flow_drop(self) -> None:
         """Leave flow: wait for and install every admitted copy, forget the
         last token's routing (a prefill replaces it)."""
@@ -158,10 +237,16 @@ class PrefetchRing:
         self._pending = self.cache.flow_install_ready(self._pending, wait=True)
         self._routes.clear()
         self._noted = False
+        self._pred_gpu, self._pred_host = [], []
+        self.predicted.clear()
+        self.cache.drop_staged()
         for layer in self.layers:
             self.cache.sync_table(layer.layer_key)
 
     def stats(self) -> dict:
         return {"flow": self.flow, "flow_tokens": self.flow_tokens,
                 "sync_tokens": self.sync_tokens, "pending_batches": len(self._pending),
-                "hit_ema": self._hit_ema}
+                "hit_ema": self._hit_ema, "predict_depth": self.predict_depth,
+                "pred_issued": self.pred_issued, "pred_used": self.pred_used,
+                "pred_precision": self.pred_used / self.pred_issued if self.pred_issued else None,
+                "spec_reads": self.spec_reads}

@@ -111,6 +111,8 @@ class StreamedSwitchGLU(nn.Module):
         K.note_workspace_errors()
         ids = [e for e in torch.unique(indices.reshape(-1)).tolist() if 0 <= e < self.n_experts]
         K.raise_workspace_errors()
+        if self.ring is not None:
+            self.ring.collect_predictions()   # they rode this sync
         return ids
 
     def plan_groups(self, indices: torch.Tensor) -> list:
@@ -144,8 +146,11 @@ class StreamedSwitchGLU(nn.Module):
 
     def _decode_passes(self, groups):
         c, lk = self.cache, self.layer_key
+        if self.ring is not None:
+            self.ring.note_demand(self.ring_index, [e for grp in groups for e in grp])
         for grp in groups:
             c.fetch(lk, grp)
+            c.spec_fence()        # guesses issued after this compute may run under it
             yield (None if len(groups) == 1 else grp), c.table_ptr(lk)
         c.group_passes += len(groups) - 1
         self.last_ids = [e for grp in groups for e in grp]
@@ -248,6 +253,8 @@ class StreamedSwitchGLU(nn.Module):
             return y.reshape(*lead, self.hidden)
         y = self.run_passes(ind2, lambda ids, table: K.switch_glu(
             c.geom, c.slab.buf, table, self.n_experts, x2, ids))
+        if self.ring is not None and ind2.shape[0] <= config.DECODE_MAX_TOKENS:
+            self.ring.speculate(self.ring_index, x2)
         return y.reshape(*lead, self.hidden)
 
 
@@ -318,6 +325,8 @@ class _MoEBlock(nn.Module):
                     if sg is not None:
                         shared_logit = K.router_logits(x2, sg.reshape(1, -1)).reshape(-1)
                 out = K.combine(y, w, shared_y, shared_logit)
+            if sm.ring is not None and x2.shape[0] <= config.DECODE_MAX_TOKENS:
+                sm.ring.speculate(sm.ring_index, x2)
             self.last_routing = (inds, w)
             return out.reshape(shape)
         if table is None:
@@ -327,6 +336,12 @@ class _MoEBlock(nn.Module):
                                    shared_slot=shared_slot, shared_gate=sg)
         self.last_routing = (inds, w)
         return out.reshape(shape)
+
+
+def _predict_ids_softmax(blk, x, slack):
+    logits = K.router_logits(x, blk.gate_weight, blk.logit_bias)
+    m = min(blk.top_k + max(0, slack), 16, blk.gate_weight.shape[0])
+    return K.route_softmax_topk(logits, m, False)[0]
 
 
 class SoftmaxMoEBlock(_MoEBlock):
@@ -353,6 +368,12 @@ class SoftmaxMoEBlock(_MoEBlock):
 
     def _route_cfg(self):
         return K.route_cfg("softmax", self.gate_weight.shape[0], self.top_k, self.norm_topk_prob)
+
+    def predict_ids(self, x, slack: int = 0):
+        """This block's router on another layer's hidden state: top-(k +
+        slack) ids (softmax is monotonic, so the top of the logits), device
+        int32 [N, k + slack]; route prediction (streaming.py:2069-2110)."""
+        return _predict_ids_softmax(self, x, slack)
 
 
 class SigmoidGroupMoEBlock(_MoEBlock):
@@ -385,6 +406,16 @@ class SigmoidGroupMoEBlock(_MoEBlock):
     def _route_cfg(self):
         return K.route_cfg("sigmoid", self.gate_weight.shape[0], self.top_k, self.norm_topk_prob,
                            self.n_group, self.topk_group, self.routed_scale)
+
+    def predict_ids(self, x, slack: int = 0):
+        """Route prediction with this block's grouped top-k (the router
+        returns the selected ids, streaming.py:2046-2068); slack widens the
+        final top-k within the kept groups."""
+        logits = K.router_logits(x, self.gate_weight)
+        e = self.gate_weight.shape[0]
+        m = min(self.top_k + max(0, slack), 16, (e // self.n_group) * self.topk_group)
+        return K.route_sigmoid_group_topk(logits, self.e_score_correction_bias, self.n_group,
+                                          self.topk_group, m, True, 1.0)[0]
 
 
 # ---------------------------------------------------------------- model surgery
@@ -462,18 +493,28 @@ def patch_model(model: nn.Module, cache: ExpertCache, tensor_index=None, prefetc
     iterates like the list of layers.  The cache's layer keys must be the
     module paths.  ``tensor_index``/``model_path`` locate checkpoint bytes in
     the reference; here the cache's pinned host store already holds them, so
-    they are accepted and unused.  Speculative prefetch is not part of this
-    path: ``predict_mode`` "on" raises."""
-    if predict_mode not in (None, "off", "auto"):
-        raise NotImplementedError(f"predict_mode={predict_mode!r}: speculative prefetch is not built")
-    del tensor_index, model_path, prefetch_depth
+    they are accepted and unused.  ``predict_mode`` "off" turns route
+    prediction off ("auto"/"on"/None: config.PREDICT_DEPTH layers ahead);
+    ``prefetch_depth`` > 0 turns on the previous-token heuristic.  Speculation
+    only reads into free slots, so it never changes an output."""
+    if predict_mode not in (None, "off", "auto", "on"):
+        raise ValueError(f"predict_mode={predict_mode!r}: expected off, auto or on")
+    del tensor_index, model_path
     glus = find_switch_glus(model)
     if not glus:
         raise ValueError("no QuantizedSwitchGLU modules found - this model has no MoE layers")
     streamed = [StreamedSwitchGLU(path, module, cache) for path, module in glus]
     for (path, _), s in zip(glus, streamed):
         _swap_module(model, path, s)
+    for (path, _), s in zip(glus, streamed):
+        parent_path = path.rpartition(".")[0]
+        parent = model.get_submodule(parent_path) if parent_path else None
+        s.pred = parent if isinstance(parent, _MoEBlock) else None
     ring = PrefetchRing(streamed, cache)
+    if predict_mode == "off":
+        ring.predict_depth = 0
+    if prefetch_depth:
+        ring.prefetch_depth = int(prefetch_depth)
     model._pagedmoe_cache = cache
     model._pagedmoe_ring = ring
     if cache.n_experts * len(glus) <= cache.routed_slots:

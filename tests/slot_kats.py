@@ -123,6 +123,26 @@ FLOW_ADMIT = dict(
 )
 
 
+# Speculation, 16 slots (budget 12, free list [15, 14, 13, 12] once 0..11 are
+# resident).  Guesses [20, 21, 5, 22, 23, 24] with at most 3 outstanding: 20,
+# 21 take slots 12, 13; 5 is resident (skipped); 22 takes 14; the cap stops
+# the rest.  A fetch of {20, 22, 30}: 20 and 22 are claimed (hits, no read),
+# 30 misses into slot 15; installing 20, 22, 30 in id order evicts the LRU
+# heads 0, 1, 2 (slots back to the free list in that order); the unclaimed
+# guess 21 is handed back, and its slot 13 returns once its read has landed.
+SPECULATION = dict(
+    slots=16,
+    warm=list(range(12)),
+    guesses=[20, 21, 5, 22, 23, 24], max_staged=3,
+    started=[(20, 12), (21, 13), (22, 14)],
+    fetch=[20, 22, 30],
+    fetch_placed=[(30, 15)],
+    evicted=[0, 1, 2],
+    hits=2, misses=12 + 1,
+    free_after_settle=[0, 1, 2, 13],
+)
+
+
 def run_flow_kat(policy, kat):
     for op in kat["script"]:
         if op[0] == "admit":

@@ -139,7 +139,7 @@ def test_streamed_switch_paging_matches_resident_and_policy():
     model, _ = _softmax_model(spec, 3, seed=50)
     resident = [layer.mlp.switch_mlp for layer in model.layers]
     cache = S.build_cache_for(model, slots=16)
-    streamed = S.patch_model(model, cache)
+    streamed = S.patch_model(model, cache, predict_mode="off")
     assert not cache.stitched
     assert all(isinstance(layer.mlp.switch_mlp, S.StreamedSwitchGLU) for layer in model.layers)
     pol = O.SlotPolicy(16)
@@ -400,7 +400,7 @@ def test_prefill_groups_keep_the_decode_hot_set(stage):
             store.write_from_slot(li, e, m.slab, e)
     cache = ExpertCache(g, 16, [p for p, _ in glus], spec.experts, host_store=store,
                         stage_slots=stage)
-    streamed = S.patch_model(model, cache)
+    streamed = S.patch_model(model, cache, predict_mode="off")
     assert not cache.stitched
     pol = O.SlotPolicy(16)
     pol.set_stage(cache.stage_first, stage)
@@ -695,3 +695,59 @@ def test_flow_token_captured_in_a_graph(monkeypatch):
             check_close(outs[li].float().cpu().numpy(), ref, f"flow graph replay {rep} layer {li}")
     ring.auto_pump = True
     cache.close()
+
+
+# ---------------------------------------------------------------- speculative prefetch
+
+def test_route_prediction_speculates_without_changing_outputs():
+    """4 layers x 32 experts, 24 routed slots: after each decode layer the
+    routers of the layers two and three ahead run on its hidden state, their
+    guesses are read into free slots behind the layer's compute, and the
+    target layer's fetch claims the ones it routes (cache.py:2853,
+    streaming.py:2013-2299).  Outputs stay bit-identical to a
+    paged twin with prediction off; every fetch and speculate call, replayed
+    on the oracle policy
+    (copies settled in between), gives the same tables and counters; the
+    residual-stream inputs (each layer adds a small update) make the guesses
+    useful, and precision is counted."""
+    _, S = _mods()
+    spec = O.LayerSpec(1024, 32, 512, 4)
+    model, _ = _softmax_model(spec, 4, seed=170)
+    twin, _ = _softmax_model(spec, 4, seed=170)        # same weights, prediction off
+    cache = S.build_cache_for(model, slots=24)
+    ring = S.patch_model(model, cache, predict_mode="on")
+    twin_cache = S.build_cache_for(twin, slots=24)
+    S.patch_model(twin, twin_cache, predict_mode="off")
+    assert ring.predict_depth == 3 and all(s.pred is not None for s in ring)
+    cache.spec_log = []
+    rng = np.random.default_rng(171)
+    for t in range(10):
+        h = torch.from_numpy(rng.standard_normal((1, spec.hidden), dtype=np.float32)).to(DEV)
+        for li, layer in enumerate(model.layers):
+            xb = h.to(torch.bfloat16)
+            got = layer.mlp(xb)
+            ref = twin.layers[li].mlp(xb)
+            assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), (t, li)
+            torch.cuda.synchronize()
+            cache.sync_spec()
+            h = h + 0.05 * torch.from_numpy(rng.standard_normal(
+                (1, spec.hidden), dtype=np.float32)).to(DEV)
+    pol = O.SlotPolicy(24)
+    keys = [s.layer_key for s in ring]
+    for op in cache.spec_log:
+        if op[0] == "fetch":
+            pol.settle()
+            pol.step(op[1], op[2])
+        else:
+            pol.speculate(op[1], op[2], op[3])
+    for lk in keys:
+        assert np.array_equal(cache.host_table(lk), pol.table(lk, spec.experts)), lk
+    st = cache.stats()
+    assert (st["hits"], st["misses"], st["evictions"]) == (pol.hits, pol.misses, pol.evictions)
+    r = ring.stats()
+    assert st["spec_started"] > 0 and st["spec_claims"] > 0 and st["spec_claims_late"] == 0
+    assert r["pred_issued"] > 0 and r["pred_precision"] > 0.3, r
+    print(f"[spec] {r} {st['spec_started']} started, {st['spec_claims']} claimed", flush=True)
+    assert st["misses"] < twin_cache.stats()["misses"]     # claimed guesses were misses there
+    cache.close()
+    twin_cache.close()

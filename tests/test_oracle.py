@@ -525,6 +525,24 @@ class _OracleSlots:
         self.pol.install(0, ids)
 
 
+def test_speculation_known_answer():
+    """Guesses take free slots only, a fetch claims them as hits with no
+    read, and hands back its layer's unclaimed guesses (cache.py:2853,
+    :2379-2386)."""
+    from tests import slot_kats
+    kat = slot_kats.SPECULATION
+    pol = O.SlotPolicy(kat["slots"])
+    pol.step(0, kat["warm"])
+    assert pol.speculate(0, kat["guesses"], kat["max_staged"]) == kat["started"]
+    before = set(e for (_, e) in pol.lru)
+    _, placed = pol.step(0, kat["fetch"])
+    assert placed == kat["fetch_placed"]
+    assert sorted(before - set(e for (_, e) in pol.lru)) == kat["evicted"]
+    assert (pol.hits, pol.misses, pol.evictions) == (kat["hits"], kat["misses"], 3)
+    pol.settle()
+    assert pol.free == kat["free_after_settle"]
+
+
 def test_flow_admit_known_answer():
     from tests import slot_kats
     slot_kats.run_flow_kat(_OracleSlots(8), slot_kats.FLOW_ADMIT)
