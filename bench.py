@@ -409,6 +409,155 @@ def run_paging(args, device, tokens=256, warm=96):
     return res
 
 
+def run_paging_predicted(args, device, n_layers=5, tokens=96, warm=32, auto_tokens=480,
+                         slots_per_layer=96, alpha=0.25):
+    """The DeepSeek-V3/Kimi-K2-shaped layers paged through a slab of 96
+    routed slots per layer, decoded through SigmoidGroupMoEBlocks (router,
+    sigmoid + correction bias, 8 groups / top-4 / top-8, scale 2.5, shared
+    expert), with and without route prediction.  Synthetic residual stream:
+    each layer's input is the previous one's plus alpha * N(0, 1), and a
+    per-expert logit bias of -1.1 * log(rank) (ranks through a fixed
+    permutation) skews popularity toward a Zipf(1.1)-like profile.  Both runs
+    see the same tokens and share one pinned host store; reports per mode
+    tokens/s, stall per token, hit rate, misses per token, and for prediction
+    the precision and the speculative reads started and claimed; a third run
+    leaves the choice to the A/B governor (predict mode "auto") over
+    auto_tokens tokens and reports what it decided."""
+    import numpy as np
+    import torch
+
+    from pagedmoe_amd import config as CF
+    from pagedmoe_amd._lib import KernelTimer, geom
+    from pagedmoe_amd.cache import ExpertCache, HostExpertStore
+    from pagedmoe_amd.slab import SlabStore
+    from pagedmoe_amd.streaming import SigmoidGroupMoEBlock, StreamedSwitchGLU, patch_model
+
+    D, E, I, k = 7168, 384, 2048, 8
+    g = geom(D, I, 4)
+    t0 = time.perf_counter()
+    store = HostExpertStore(g, n_layers, E)
+    tmp = SlabStore(g, 1, device, zero=False)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(44)
+
+    def synth(slab, slot):
+        for prefix, rows, cols in (("gate_proj", I, D), ("up_proj", I, D), ("down_proj", D, I)):
+            slab.quantize_into(slot, prefix, torch.randn((rows, cols), generator=gen,
+                                                         device=device) * 0.02)
+
+    for e in range(E):                 # one set of synthetic experts, every layer a copy
+        synth(tmp, 0)
+        store.write_from_slot(0, e, tmp, 0)
+    one = store.bytes[:E * store.expert_bytes]
+    for li in range(1, n_layers):
+        store.bytes[li * E * store.expert_bytes:(li + 1) * E * store.expert_bytes] = one
+    rng = np.random.default_rng(45)
+    gates = [(torch.randn((E, D), generator=gen, device=device) * 0.02).to(torch.bfloat16)
+             for _ in range(n_layers)]
+    corr = [torch.from_numpy((rng.standard_normal(E) * 0.01).astype(np.float32)).to(device)
+            for _ in range(n_layers)]
+    skew = []
+    for _ in range(n_layers):
+        rank = np.empty(E)
+        rank[rng.permutation(E)] = np.arange(1, E + 1)
+        skew.append(torch.from_numpy((-1.1 * np.log(rank)).astype(np.float32)).to(device))
+    setup_s = time.perf_counter() - t0
+
+    class Layer(torch.nn.Module):
+        def __init__(self, mlp):
+            super().__init__()
+            self.mlp = mlp
+
+    def build(mode):
+        keys = [f"layers.{li}.mlp.switch_mlp" for li in range(n_layers)]
+        cache = ExpertCache(g, slots_per_layer * n_layers, keys, E, host_store=store,
+                            n_shared=1, device=device, stage_slots=0)
+        for li in range(n_layers):
+            cache.slab.slot_bytes(cache.shared_slot(keys[li])).copy_(tmp_shared)
+        model = torch.nn.Module()
+        blocks = []
+        for li in range(n_layers):
+            st = StreamedSwitchGLU(keys[li], None, cache)
+            blk = SigmoidGroupMoEBlock(gates[li], corr[li], st, top_k=k, n_group=8, topk_group=4,
+                                       routed_scaling_factor=2.5)
+            blk.logit_bias = skew[li]
+            blocks.append(blk)
+        model.layers = torch.nn.ModuleList([Layer(b) for b in blocks])
+        # patch_model's ring over the streamed seams already in place
+        from pagedmoe_amd.ring import PrefetchRing
+        ring = PrefetchRing([b.switch_mlp for b in blocks], cache)
+        for b in blocks:
+            b.switch_mlp.pred = b
+        ring.governor.set_mode(mode)
+        return model, cache, ring
+
+    tmp_shared = torch.empty(int(g.expert_bytes), dtype=torch.uint8, device=device)
+    synth(tmp, 0)
+    tmp_shared.copy_(tmp.slot_bytes(0))
+    tmp.release()
+    del patch_model
+    out = {"config": {"workload": "DeepSeek-V3/Kimi-K2-shaped paged decode, route prediction",
+                      "layers": n_layers, "hidden": D, "experts": E, "shared_experts": 1,
+                      "moe_intermediate": I, "top_k": k, "bits": 4,
+                      "slab_slots": slots_per_layer * n_layers,
+                      "residual_update": f"x_(l+1) = x_l + {alpha} * N(0,1)",
+                      "popularity": "logit bias -1.1*log(rank), ranks permuted (seed 45)",
+                      "predict_depth": CF.PREDICT_DEPTH, "predict_slack": CF.PREDICT_SLACK,
+                      "tokens_timed": tokens, "warmup_tokens": warm, "setup_s": setup_s}}
+    for name, mode in (("no_prediction", "off"), ("prediction", "on"), ("governor", "auto")):
+        model, cache, ring = build(mode)
+        n_tok = auto_tokens if mode == "auto" else tokens
+        trng = np.random.default_rng(46)
+
+        def token():
+            h = torch.from_numpy(trng.standard_normal((1, D)).astype(np.float32)).to(device)
+            for layer in model.layers:
+                layer.mlp(h.to(torch.bfloat16))
+                h = h + alpha * torch.from_numpy(
+                    trng.standard_normal((1, D)).astype(np.float32)).to(device)
+
+        for _ in range(warm):
+            token()
+        torch.cuda.synchronize()
+        st0 = cache.stats()
+        r0 = ring.stats()
+        with KernelTimer() as kt:
+            c0 = time.perf_counter()
+            for _ in range(n_tok):
+                token()
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - c0
+        st1 = cache.stats()
+        r1 = ring.stats()
+        tokens_run = n_tok
+        hits = st1["hits"] - st0["hits"]
+        misses = st1["misses"] - st0["misses"]
+        kern_s = sum(tot for tot, _ in kt.result.values()) / 1e3
+        issued = r1["pred_issued"] - r0["pred_issued"]
+        used = r1["pred_used"] - r0["pred_used"]
+        t = tokens_run
+        out[name] = {
+            "tokens": t, "tokens_per_s": t / wall, "ms_per_token": wall * 1e3 / t,
+            "stall_ms_per_token": max(0.0, wall - kern_s) * 1e3 / t,
+            "kernel_ms_per_token": kern_s * 1e3 / t,
+            "hit_rate": hits / max(1, hits + misses), "misses_per_token": misses / t,
+            "h2d_gb_per_token": (st1["h2d_gb"] - st0["h2d_gb"]) / t,
+            "spec_started_per_token": (st1["spec_started"] - st0["spec_started"]) / t,
+            "spec_claims_per_token": (st1["spec_claims"] - st0["spec_claims"]) / t,
+            "spec_claims_late_per_token": (st1["spec_claims_late"] - st0["spec_claims_late"]) / t,
+            "pred_precision": used / issued if issued else None,
+        }
+        if mode == "auto":
+            out[name]["governor"] = ring.governor.describe()
+            out[name]["governor_log"] = list(ring.governor.log)
+        cache.close()
+    store.close()
+    out["note"] = ("stall = wall time - sum of kernel times; speculative reads use their own "
+                   "copy stream and free slots only; precision = predicted ids routed at the "
+                   "target layer / predicted ids")
+    return out
+
+
 def run_qwen3_next(args, device, layers=2):
     """Qwen3-Next-shaped layer (hidden 2048, 512 experts + 1 gated shared
     expert, moe_intermediate 512, top-10 softmax+renorm, 6-bit g64, all
@@ -674,6 +823,8 @@ def main():
                     help="skip the batch-8 and prefill lines in extra")
     ap.add_argument("--no-paging", action="store_true",
                     help="skip the DeepSeek-shaped paging leg in extra")
+    ap.add_argument("--no-predict", action="store_true",
+                    help="skip the multi-layer paged decode leg with route prediction")
     ap.add_argument("--no-next", action="store_true",
                     help="skip the Qwen3-Next-shaped (6-bit) leg in extra")
     ap.add_argument("--prefill-reps", type=int, default=5,
@@ -751,6 +902,14 @@ def main():
         log(f"deepseek paging: {rg['tokens_per_s']:.0f} tok/s, hit rate {rg['hit_rate']:.3f}, "
             f"stall {rg['stall_ms_per_token']:.3f} ms/token, H2D {rg['h2d_gbs'] or 0:.1f} GB/s")
         extra["deepseek_paging"] = rg
+    if not args.no_extra and not args.no_paging and not args.no_predict:
+        rp = run_paging_predicted(args, device)
+        for nm in ("no_prediction", "prediction", "governor"):
+            r = rp[nm]
+            log(f"deepseek paged decode, {nm}: {r['ms_per_token']:.2f} ms/token, stall "
+                f"{r['stall_ms_per_token']:.2f}, hit rate {r['hit_rate']:.3f}, precision "
+                f"{r['pred_precision']} {r.get('governor_log', '')}")
+        extra["deepseek_paging_predicted"] = rp
 
     if "decode_fused" in main_res["kernels"]:
         kname = "decode_fused_kernel"

@@ -8,7 +8,8 @@ path (config.py: SLAB_RESERVE_FRAC :718, LFRU/LFRU_SCAN :1477-1478, STITCH
 fused prefill pass; FLOW / FLOW_WARMUP / FLOW_WARM_HIT :1218-1237 for flow
 decode; PREDICT_DEPTH :747, PREDICT_SLACK :761 and PREFETCH_DEPTH :722 for
 speculative prefetch (PREFETCH_DEPTH defaults to 0 here: the previous-token
-heuristic pays off with the reference's SSD queue, not a PCIe copy engine).
+heuristic pays off with the reference's SSD queue, not a PCIe copy engine);
+PREDICT and the governor knobs :735-741.
 DECODE_MAX_TOKENS is the reference's _DECODE_MAX_TOKENS
 (streaming.py:69): calls of more tokens take the prefill residency policy.
 """
@@ -49,6 +50,13 @@ FLOW_WARM_HIT = 0.9       # hit-rate EMA the per-layer path must reach before fl
 PREDICT_DEPTH = 3         # route prediction: layers predicted ahead per stride
 PREDICT_SLACK = 2         # extra experts per predicted layer beyond its top-k
 PREFETCH_DEPTH = 0        # previous-token heuristic: next layers' last ids (0 = off)
+PREDICT = "auto"          # route prediction: on, off, or auto (A/B governor decides)
+PREDICT_WINDOW = 8        # governor: decode tokens per window
+PREDICT_MIN_TOKENS = 96   # governor: tokens of evidence per state before deciding
+PREDICT_MARGIN = 1.03     # governor: how much faster a state must measure
+PREDICT_Z = 2.0           # governor: error bars the gap must also clear
+PREDICT_MAX_PROBE = 6     # governor: inconclusive after this many times the evidence -> off
+PREDICT_HOLD = 128        # governor: windows a decision is kept before re-probing
 ATTN_SUB_CHUNK = 2048     # rows per attention sub-chunk, at most
 ATTN_SCORE_MB = 1024      # fp32 score matrix (heads x rows x keys) of one sub-chunk, at most
 
@@ -57,7 +65,8 @@ def sync_from_environ() -> None:
     global SLAB_RESERVE_FRAC, LFRU, LFRU_SCAN, STITCH, COPY_SPLIT_BYTES, COPY_STREAMS
     global DECODE_MAX_TOKENS, PREFILL_STAGE, PREFILL_STAGE_GROUP_MB, GROUP_BYTES
     global FUSED_PREFILL, ATTN_SUB_CHUNK, ATTN_SCORE_MB, FLOW, FLOW_WARMUP, FLOW_WARM_HIT
-    global PREDICT_DEPTH, PREDICT_SLACK, PREFETCH_DEPTH
+    global PREDICT_DEPTH, PREDICT_SLACK, PREFETCH_DEPTH, PREDICT, PREDICT_WINDOW
+    global PREDICT_MIN_TOKENS, PREDICT_MARGIN, PREDICT_Z, PREDICT_MAX_PROBE, PREDICT_HOLD
     SLAB_RESERVE_FRAC = _env("SLAB_RESERVE_FRAC", 0.1, float)
     LFRU = _env("LFRU", True, _bool)
     LFRU_SCAN = _env("LFRU_SCAN", 8, int)
@@ -77,6 +86,13 @@ def sync_from_environ() -> None:
     PREDICT_DEPTH = _env("PREDICT_DEPTH", 3, int)
     PREDICT_SLACK = _env("PREDICT_SLACK", 2, int)
     PREFETCH_DEPTH = _env("PREFETCH_DEPTH", 0, int)
+    PREDICT = _env("PREDICT", "auto", str).strip().lower()
+    PREDICT_WINDOW = _env("PREDICT_WINDOW", 8, int)
+    PREDICT_MIN_TOKENS = _env("PREDICT_MIN_TOKENS", 96, int)
+    PREDICT_MARGIN = _env("PREDICT_MARGIN", 1.03, float)
+    PREDICT_Z = _env("PREDICT_Z", 2.0, float)
+    PREDICT_MAX_PROBE = _env("PREDICT_MAX_PROBE", 6, int)
+    PREDICT_HOLD = _env("PREDICT_HOLD", 128, int)
 
 
 sync_from_environ()

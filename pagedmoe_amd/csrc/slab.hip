@@ -515,31 +515,33 @@ extern "C" int pmoe_slab_speculate(pmoe_slab* s, const pmoe_geom* g, void* slab,
     for (auto& ks : got) dup |= ks.first == k;
     if (dup) continue;
     if (int(s->staged_keys.size() + got.size()) >= max_staged || s->free_slots.empty()) break;
+    // every outstanding guess holds one of the engine's batch records
+    if (int(s->staged_keys.size() + s->draining.size() + got.size()) >= kMaxSpecBatches - 1) break;
     got.emplace_back(k, s->free_slots.back());
     s->free_slots.pop_back();
   }
   if (got.empty()) return PMOE_OK;
+  // one copy batch per guess: a claim waits for its own read only
   const size_t eb = size_t(g->expert_bytes);
-  for (auto& ks : got) {
+  size_t started = 0;
+  for (; started < got.size(); ++started) {
+    const auto& ks = got[started];
     rc = pmoe_copy_submit(s->spec_ce, static_cast<uint8_t*>(slab) + size_t(ks.second) * eb,
                           static_cast<const uint8_t*>(host_store) + size_t(ks.first) * eb, eb, 0);
+    int b = -1;
+    if (!rc) rc = pmoe_copy_issue(s->spec_ce, &b);
     if (rc) break;
-  }
-  int b = -1;
-  if (!rc) rc = pmoe_copy_issue(s->spec_ce, &b);
-  if (rc) {  // nothing staged: the slots go back
-    for (auto it = got.rbegin(); it != got.rend(); ++it) s->free_slots.push_back(it->second);
-    return rc;
-  }
-  for (auto& ks : got) {
     s->staged_slot[ks.first] = ks.second;
     s->staged_batch[ks.first] = b;
     s->staged_keys.push_back(ks.first);
+    s->batch_refs[b] = 1;
   }
-  s->batch_refs[b] = int(got.size());
-  s->st.spec_started += int64_t(got.size());
-  s->st.bytes_copied += int64_t(got.size()) * int64_t(eb);
-  *n_started = int(got.size());
+  for (size_t i = got.size(); i-- > started;) s->free_slots.push_back(got[i].second);
+  s->st.spec_started += int64_t(started);
+  s->st.bytes_copied += int64_t(started) * int64_t(eb);
+  *n_started = int(started);
+  if (rc && started == 0) return rc;
+  pmoe::clear_error();  // a guess that could not start is not an error of the call
   return PMOE_OK;
 }
 

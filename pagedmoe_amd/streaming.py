@@ -411,7 +411,7 @@ class SigmoidGroupMoEBlock(_MoEBlock):
         """Route prediction with this block's grouped top-k (the router
         returns the selected ids, streaming.py:2046-2068); slack widens the
         final top-k within the kept groups."""
-        logits = K.router_logits(x, self.gate_weight)
+        logits = K.router_logits(x, self.gate_weight, self.logit_bias)
         e = self.gate_weight.shape[0]
         m = min(self.top_k + max(0, slack), 16, (e // self.n_group) * self.topk_group)
         return K.route_sigmoid_group_topk(logits, self.e_score_correction_bias, self.n_group,
@@ -493,9 +493,10 @@ def patch_model(model: nn.Module, cache: ExpertCache, tensor_index=None, prefetc
     iterates like the list of layers.  The cache's layer keys must be the
     module paths.  ``tensor_index``/``model_path`` locate checkpoint bytes in
     the reference; here the cache's pinned host store already holds them, so
-    they are accepted and unused.  ``predict_mode`` "off" turns route
-    prediction off ("auto"/"on"/None: config.PREDICT_DEPTH layers ahead);
-    ``prefetch_depth`` > 0 turns on the previous-token heuristic.  Speculation
+    they are accepted and unused.  ``predict_mode`` "on" / "off" pins route
+    prediction (config.PREDICT_DEPTH layers ahead); "auto" lets the ring's A/B
+    governor decide from measured tokens/s (None: config.PREDICT, default
+    auto).  ``prefetch_depth`` > 0 turns on the previous-token heuristic.  Speculation
     only reads into free slots, so it never changes an output."""
     if predict_mode not in (None, "off", "auto", "on"):
         raise ValueError(f"predict_mode={predict_mode!r}: expected off, auto or on")
@@ -511,8 +512,8 @@ def patch_model(model: nn.Module, cache: ExpertCache, tensor_index=None, prefetc
         parent = model.get_submodule(parent_path) if parent_path else None
         s.pred = parent if isinstance(parent, _MoEBlock) else None
     ring = PrefetchRing(streamed, cache)
-    if predict_mode == "off":
-        ring.predict_depth = 0
+    if predict_mode is not None:
+        ring.governor.set_mode(predict_mode)
     if prefetch_depth:
         ring.prefetch_depth = int(prefetch_depth)
     model._pagedmoe_cache = cache
