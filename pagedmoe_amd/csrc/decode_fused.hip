@@ -110,9 +110,9 @@ constexpr bool kCoherentLoads = true;
 
 #ifdef PMOE_FUSED_TRACE
 // Debug builds: every block's thread 0 records realtime stamps per phase.
-__device__ uint64_t g_trace[1024 * 16];
+__device__ uint64_t g_trace[1024 * 32];
 __device__ __forceinline__ void trace_mark(DecodeSync*, int i) {
-  if (threadIdx.x == 0) g_trace[blockIdx.x * 16 + i] = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0) g_trace[blockIdx.x * 32 + i] = __builtin_amdgcn_s_memrealtime();
 }
 #else
 __device__ __forceinline__ void trace_mark(DecodeSync*, int) {}
@@ -258,6 +258,7 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
   const int gw = blockIdx.x * kFWaves + wave;
   const int n_waves = a.n_blocks * kFWaves;
   DecodeSync* sy = a.sync;
+  trace_mark(sy, 16);  // entry
 
   // this launch's barrier tags: 2*epoch + 1 and 2*epoch + 2 (never 0, the
   // initial flag value; consecutive launches differ)
