@@ -51,6 +51,11 @@
 // there), writes NaN for its output rows instead of the combine, so a
 // timed-out layer can never pass for a good one; the host reads the error
 // word at its next sync point.
+#ifdef PMOE_FUSED_TRACE
+namespace pmoe { namespace { __device__ uint64_t g_trace[1024 * 32]; } }
+#define PMOE_ROUTE_MARK(i) \
+  do { if (threadIdx.x == 0) pmoe::g_trace[blockIdx.x * 32 + (i)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#endif
 #include "gemv_common.h"
 #include "pmoe_internal.h"
 #include "pmoe_kernels.h"
@@ -110,7 +115,6 @@ constexpr bool kCoherentLoads = true;
 
 #ifdef PMOE_FUSED_TRACE
 // Debug builds: every block's thread 0 records realtime stamps per phase.
-__device__ uint64_t g_trace[1024 * 32];
 __device__ __forceinline__ void trace_mark(DecodeSync*, int i) {
   if (threadIdx.x == 0) g_trace[blockIdx.x * 32 + i] = __builtin_amdgcn_s_memrealtime();
 }
@@ -210,8 +214,9 @@ __device__ __forceinline__ void fma8(float& acc, const uint4& a, const uint4& b)
 // Logit (token t, row e) in router_logits_kernel's order: lane l owns
 // d = 512p + 8l + j, fma over p then j, xor butterfly over the lanes; the
 // bias is added to routed rows only.  The loads of 8 passes are issued
-// together (one memory round trip for hidden <= 4096).
-__device__ void router_pair(const FusedArgs& a, const RouteDev& rt, int e, int t) {
+// together (one memory round trip for hidden <= 4096).  Every lane returns
+// the logit.
+__device__ float router_dot(const FusedArgs& a, const RouteDev& rt, int e, int t) {
   const int lane = threadIdx.x & 63;
   const int d = a.gu.cols;
   const uint16_t* wrow = e < rt.e ? a.gate_w + size_t(e) * d : a.gate_extra;
@@ -235,10 +240,12 @@ __device__ void router_pair(const FusedArgs& a, const RouteDev& rt, int e, int t
     }
   }
   const float sum = wave_sum_bfly(acc);
-  if (lane == 0) {
-    const bool biased = a.logit_bias && e < rt.e;
-    shared_store(&a.logits[size_t(t) * rt.ld + e], biased ? sum + a.logit_bias[e] : sum);
-  }
+  return a.logit_bias && e < rt.e ? sum + a.logit_bias[e] : sum;
+}
+
+__device__ void router_pair(const FusedArgs& a, const RouteDev& rt, int e, int t) {
+  const float v = router_dot(a, rt, e, t);
+  if ((threadIdx.x & 63) == 0) shared_store(&a.logits[size_t(t) * rt.ld + e], v);
 }
 
 template <int UG, int LG, int GG, int RG, int UD, int LD, int GD, int RD, int EPL>
@@ -520,6 +527,325 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
   trace_mark(sy, 6);
 }
 
+// ------------------------------------------------- expert-per-XCD launch
+//
+// The same layer for one token with top-8 softmax routing (no shared
+// expert), laid out so that each of the 8 picks is streamed by one block
+// group: the blocks with b % 8 == x (group x) run pick x, the x-th expert of
+// the top-8 list.  The dispatcher deals blocks round robin over the 8 XCDs
+// (from wherever the previous dispatch left off), so a group shares one XCD
+// and its L2; correctness does not depend on that, only speed does.
+//
+// No phase waits at a barrier.  Everything one block needs from another
+// travels as tagged data at device scope and is polled until the tag of
+// this launch appears, so each block goes on the moment its own inputs
+// exist:
+//   A  logit e is computed once, by wave 0 of block e (router_dot, the
+//      order of router_logits_kernel), and published as a 64-bit word
+//      (tag << 32 | fp32 bits);
+//   B  every block polls the E logit words into LDS and routes
+//      (route_rank1_select: the same bits everywhere); slot of pick x;
+//   C  the gate/up rows of pick x are dealt over the group's waves; h is
+//      published as 32-bit words (tag & 0xFFFF << 16 | bf16) into the
+//      group's L2 (plain stores; a group spread over two XCDs would never see
+//      them and time out, loudly); each wave requests the weights of its
+//      first down tile half way through its last gate/up item (requested
+//      with its first rows, they lengthen the gate/up stream);
+//   D  each block polls its group's h row into LDS; wave w of the group
+//      computes down tile w (8 or 16 rows) of pick x into fp32 partial x,
+//      then adds 1 to the tile's counter; the wave that brings it to a
+//      multiple of 8 (the last of the 8 groups) reads the 8 partials and
+//      writes acc = fma(w_x, y_x, acc) over x = 0..7 -- the order of the
+//      grid-wide launch, so the outputs are bit for bit the same.
+// The tag numbers the launch: thread 0 of every block adds 1 to its group's
+// launch counter at entry, and counter / blocks-per-group (a power of two,
+// so the sequence wraps cleanly) + 1 is the tag, the same in every block
+// since all groups' counters advance alike.  Every launch rewrites every
+// logit and h word (h of a non-resident pick as zeros), so a word's tag is
+// at most one launch old and a 16-bit h tag cannot alias.  Tags make the
+// exchange order-free: a word is taken when its tag matches, whenever it
+// arrives.  A poll that has waited the spin limit sets error bit 0 and the
+// block goes on poisoned: its h words and partial rows are NaN, which every
+// output that depends on them inherits through the combine.
+constexpr int kXcdPollSleep = 1;
+
+template <class T>
+__device__ __forceinline__ T device_load(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int UG, int LG, int GG, int RG, int UD, int LD, int GD, int RD>
+__global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(const FusedArgs a,
+                                                               const RouteDev rt) {
+  constexpr int RPW = 64 / LG;
+  constexpr int kRows = RG * RPW;           // gate/up rows per item
+  constexpr int kHD = RD > 1 ? RD / 2 : 1;  // down steps per half
+  constexpr int kSub = RD * (64 / LD);      // down rows per tile
+  static_assert(kSub == 8 || kSub == 16, "down tiles of 8 or 16 rows");
+  __shared__ RouteLds L;
+  __shared__ Rank1Lds R1;
+  __shared__ __align__(16) float s_logit[128];
+  __shared__ int32_t s_table[128];
+  __shared__ __align__(16) uint16_t s_h[kXcdMaxInter];
+  __shared__ __align__(16) float s_y[kFWaves][kXcdCount][16];  // per wave: partial rows
+  __shared__ uint32_t s_tag;
+  __shared__ int s_slot;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int xcd = blockIdx.x % kXcdCount;  // group
+  const int per_xcd = a.n_blocks / kXcdCount;
+  const int lw = (blockIdx.x / kXcdCount) * kFWaves + wave;  // wave index within the group
+  const int n_lw = per_xcd * kFWaves;
+  DecodeSync* sy = a.sync;
+  uint8_t* hdr = reinterpret_cast<uint8_t*>(sy);
+  uint64_t* lgx = reinterpret_cast<uint64_t*>(hdr + kXcdLogitOffset);
+  uint32_t* hx = reinterpret_cast<uint32_t*>(hdr + kXcdHOffset) + size_t(xcd) * kXcdMaxInter;
+  float* part = reinterpret_cast<float*>(hdr + kXcdPartOffset);
+  const uint64_t t_entry = __builtin_amdgcn_s_memrealtime();
+  trace_mark(sy, 16);
+#ifdef PMOE_FUSED_TRACE
+  if (threadIdx.x == 0) {
+    g_trace[blockIdx.x * 32 + 24] = __builtin_amdgcn_s_memtime();
+    g_trace[blockIdx.x * 32 + 25] = __builtin_amdgcn_s_memrealtime();
+  }
+#endif
+  // the launch counter and the slot table are requested first; their
+  // values are used after the router, so their round trips overlap it
+  uint32_t old = 0;
+  if (threadIdx.x == 0)
+    old = __hip_atomic_fetch_add(
+        reinterpret_cast<uint32_t*>(hdr + kXcdCounterOffset + xcd * kDecodeFlagStride), 1u,
+        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int32_t tab = int(threadIdx.x) < rt.e ? a.gu.table[threadIdx.x] : -1;
+
+  // A: logit e by wave 0 of block e.  (Vector loads and stores share one
+  // counter, so a wave that waits for a load also waits for the device-scope
+  // stores it issued before: the slot table goes to LDS before the logit
+  // store, and waves 2-3, which store nothing, poll the logits.)
+  trace_mark(sy, 0);
+  if (wave == 0) {
+    const uint32_t my_tag = __builtin_amdgcn_readfirstlane(old) / uint32_t(per_xcd) + 1u;
+    if (int(threadIdx.x) < rt.e) s_table[threadIdx.x] = tab;
+    for (int e = blockIdx.x; e < rt.e; e += a.n_blocks) {
+      const float v = router_dot(a, rt, e, 0);
+      if (lane == 0)
+        __hip_atomic_store(&lgx[e], (uint64_t(my_tag) << 32) | __float_as_uint(v),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (lane == 0) s_tag = my_tag;
+  } else if (int(threadIdx.x) < rt.e) {
+    s_table[threadIdx.x] = tab;
+  }
+  trace_mark(sy, 1);
+  __syncthreads();
+  const uint32_t tag = s_tag;
+
+  // B: every logit of this launch into LDS (threads 128.. poll), then routing
+  bool late = false;
+  const int li = int(threadIdx.x) - 128;
+  if (li >= 0 && li < rt.e) {
+    while (true) {
+      const uint64_t w = device_load(&lgx[li]);
+      if (uint32_t(w >> 32) == tag) {
+        s_logit[li] = __uint_as_float(uint32_t(w));
+        break;
+      }
+      if (__builtin_amdgcn_s_memrealtime() - t_entry > a.spin) {
+        late = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(kXcdPollSleep);
+    }
+  }
+  const bool bad_logits = __syncthreads_or(late) != 0;
+  trace_mark(sy, 2);
+  RouteDev rl = rt;
+  rl.logits = s_logit;
+  route_rank1_select(rl, s_logit, L, R1);
+  trace_mark(sy, 18);
+  if (threadIdx.x == 0) {
+    if (bad_logits)
+      __hip_atomic_fetch_or(&sy->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int e = L.ids[xcd];  // always < rt.e: the ranks are a permutation
+    s_slot = e >= 0 && e < rt.e ? s_table[e] : -1;
+  }
+  __syncthreads();
+  trace_mark(sy, 3);
+  const int slot = s_slot;
+
+  // C: gate/up rows of the pick, two row steps in flight per wave (as in the
+  // grid-wide launch's single-row items); h words carry the tag
+  const uint32_t htag = (tag & 0xFFFFu) << 16;
+  const int n_tiles = (a.dn.rows_out + kSub - 1) / kSub;
+  const int pre_row = lw * kSub;
+  const bool pre = slot >= 0 && lw < n_tiles;
+  GemvRegs<UD, LD, GD, kHD, false> qd1, qd2;
+  auto prefetch_down = [&](int half) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (pre) {
+      if (half == 0) gemv_load<UD, LD, GD, kHD, false>(a.dn, slot, pre_row, qd1);
+      if (half == 1 && RD > 1)
+        gemv_load<UD, LD, GD, kHD, false>(a.dn, slot, pre_row + kHD * (64 / LD), qd2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  {
+    const int items = (a.gu.rows_out + kRows - 1) / kRows;
+    const int g_sub = lane % LG, g_rsub = lane / LG;
+    // h stays in the group's XCD: a plain store lands in its L2 (and is
+    // acknowledged there), where the group's device-scope reads find it
+    auto put_h = [&](int o, float hv) {
+      const uint32_t bits = bad_logits ? 0x7fc0u : (slot < 0 ? 0u : uint32_t(f2bf(hv)));
+      hx[o] = htag | bits;
+    };
+    GroupAct<UG> act[GG];
+    if (slot >= 0 && lw < items) gemv_load_act<UG, LG, GG>(a.gu.act, a.gu.cols, act);
+    auto item = [&](int it, auto last_tag) {
+      constexpr bool LAST = decltype(last_tag)::value;
+      const int wrow0 = it * kRows;
+      const int o = wrow0 + g_sub * RPW + g_rsub;
+      if (slot < 0) {  // not resident: this launch's h words are zeros
+        if (g_sub < RG && o < a.gu.rows_out) put_h(o, 0.0f);
+        return;
+      }
+      GemvRegs<UG, LG, GG, 1, true> q[2];
+      gemv_load<UG, LG, GG, 1, true>(a.gu, slot, wrow0, q[0]);
+      gemv_load<UG, LG, GG, 1, true>(a.gu, slot, wrow0 + RPW, q[1]);
+      float hv = 0.0f;
+#pragma unroll
+      for (int st = 0; st < RG; ++st) {
+        __builtin_amdgcn_sched_barrier(0);
+        gemv_rows<UG, LG, GG, 1, true, Collect, true>(a.gu, q[st & 1], act, wrow0 + st * RPW,
+                                                      collect_fn(hv, g_sub - st));
+        __builtin_amdgcn_sched_barrier(0);
+        if (st + 2 < RG) gemv_load<UG, LG, GG, 1, true>(a.gu, slot, wrow0 + (st + 2) * RPW, q[st & 1]);
+        if (LAST && st == RG / 2 - 1) prefetch_down(0);
+      }
+      if (g_sub < RG && o < a.gu.rows_out) put_h(o, hv);
+      if (LAST) prefetch_down(1);
+    };
+    const int mine = lw < items ? (items - 1 - lw) / n_lw + 1 : 0;
+    for (int j = 0; j + 1 < mine; ++j) item(lw + j * n_lw, std::false_type{});
+    if (mine > 0) {
+      item(lw + (mine - 1) * n_lw, std::true_type{});
+    } else {
+      prefetch_down(0);
+      prefetch_down(1);
+    }
+  }
+  trace_mark(sy, 7);
+
+  // D: the group's h row into LDS (every word of this launch), then the down
+  // tiles of the pick and the combine
+  bool poison = bad_logits;
+  if (slot >= 0) {
+    // 4 words a thread per poll (one 16-byte load, two 8-byte device-scope
+    // reads); a chunk is kept once all 4 carry this launch's tag
+    bool h_late = false;
+    for (int c = threadIdx.x; c < a.dn.cols / 4; c += kFThreads) {
+      const uint64_t* src = reinterpret_cast<const uint64_t*>(hx) + 2 * c;
+      while (true) {
+        const uint64_t w0 = device_load(src), w1 = device_load(src + 1);
+        const uint32_t t = uint32_t(w0) & uint32_t(w0 >> 32) & uint32_t(w1) & uint32_t(w1 >> 32);
+        const uint32_t u = uint32_t(w0) | uint32_t(w0 >> 32) | uint32_t(w1) | uint32_t(w1 >> 32);
+        if ((t & 0xFFFF0000u) == htag && (u & 0xFFFF0000u) == htag) {
+          *reinterpret_cast<uint2*>(&s_h[4 * c]) =
+              make_uint2((uint32_t(w0) & 0xFFFFu) | (uint32_t(w0 >> 32) << 16),
+                         (uint32_t(w1) & 0xFFFFu) | (uint32_t(w1 >> 32) << 16));
+          break;
+        }
+        if (__builtin_amdgcn_s_memrealtime() - t_entry > a.spin) {
+          h_late = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(kXcdPollSleep);
+      }
+    }
+    if (__syncthreads_or(h_late)) {
+      poison = true;
+      if (threadIdx.x == 0)
+        __hip_atomic_fetch_or(&sy->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  trace_mark(sy, 8);
+  const float kNaN = __uint_as_float(0x7fc00000u);
+  float* yx = part + size_t(xcd) * kXcdMaxHidden;
+  constexpr int kQ = kSub / 4;  // 16-byte chunks of a tile
+  for (int tl = lw; tl < n_tiles; tl += n_lw) {
+    const int row0 = tl * kSub;
+    float* own = s_y[wave][xcd];
+    if (slot < 0) {  // not resident: exact zero rows (streaming.py:715-719)
+      if (lane < kSub) own[lane] = poison ? kNaN : 0.0f;
+    } else {
+      if (tl != lw) {
+        gemv_load<UD, LD, GD, kHD, false>(a.dn, slot, row0, qd1);
+        if (RD > 1) gemv_load<UD, LD, GD, kHD, false>(a.dn, slot, row0 + kHD * (64 / LD), qd2);
+      }
+      GroupAct<UD> act[GD];
+      gemv_load_act<UD, LD, GD>(s_h, a.dn.cols, act);
+      auto to_own = [&](int, int o, float v) { own[o - row0] = poison ? kNaN : v; };
+      gemv_rows<UD, LD, GD, kHD, false>(a.dn, qd1, act, row0, to_own);
+      if (RD > 1) gemv_rows<UD, LD, GD, kHD, false>(a.dn, qd2, act, row0 + kHD * (64 / LD), to_own);
+    }
+    wave_lds_sync();
+    trace_mark(sy, 11);
+    // rows past rows_out are never read: a tile's partial is stored whole
+    if (lane < kQ)
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(yx + row0) + 2 * lane,
+                         *reinterpret_cast<const uint64_t*>(own + 4 * lane), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT),
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(yx + row0) + 2 * lane + 1,
+                         *reinterpret_cast<const uint64_t*>(own + 4 * lane + 2), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // the partial has reached device scope
+    uint32_t old = 0;
+    if (lane == 0)
+      old = __hip_atomic_fetch_add(
+          reinterpret_cast<uint32_t*>(hdr + kXcdTileOffset + size_t(tl) * kXcdTileStride), 1u,
+          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    trace_mark(sy, 19);
+    if (old % kXcdCount != kXcdCount - 1) continue;
+    // last of the 8: the other groups' partials of the tile into LDS
+    if (lane < kXcdCount * kQ) {
+      const int x = lane / kQ, c = lane % kQ;
+      if (x != xcd) {
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(
+            part + size_t(x) * kXcdMaxHidden + row0 + 4 * c);
+        *reinterpret_cast<uint64_t*>(&s_y[wave][x][4 * c]) = device_load(src);
+        *reinterpret_cast<uint64_t*>(&s_y[wave][x][4 * c + 2]) = device_load(src + 1);
+      }
+    }
+    wave_lds_sync();
+    trace_mark(sy, 20);
+    // the combine weights of the picks, as route_rank1_weights computes them
+    const int k = rt.k;
+    const int ik = lane < k ? L.ids[lane] : 0;
+    const float pv = lane < k ? s_logit[ik] : 0.0f;
+    const float m = lane_value(pv, 0);
+    const float ej = lane < k ? pexp(pv - m) : 0.0f;
+    float ssum = 0.0f;
+    for (int j = 0; j < k; ++j) ssum = ssum + lane_value(ej, j);
+    const float wk = ej / ssum;
+    const int o = row0 + lane;
+    if (lane < kSub && o < a.dn.rows_out) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int x = 0; x < kXcdCount; ++x) acc = __builtin_fmaf(lane_value(wk, x), s_y[wave][x][lane], acc);
+      a.out[o] = f2bf(acc);
+    }
+  }
+  // the routing outputs, off the critical path
+  if (blockIdx.x == 0) route_rank1_weights(rl, s_logit, L, a.inds_out, a.w_out);
+  trace_mark(sy, 6);
+#ifdef PMOE_FUSED_TRACE
+  if (threadIdx.x == 0) {
+    g_trace[blockIdx.x * 32 + 26] = __builtin_amdgcn_s_memtime();
+    g_trace[blockIdx.x * 32 + 27] = __builtin_amdgcn_s_memrealtime();
+  }
+#endif
+}
+
 // ---------------------------------------------------------------- host side
 
 // Row steps per wave item: weights of one item stay in registers next to the
@@ -547,17 +873,30 @@ struct Entry {
   int sub_rows;  // down rows per wave item
 };
 
+// Gate/up row steps per wave item and down row steps per down item (~16
+// rows; 8 when a step already covers 8 rows).  Both split in two halves:
+// even step counts (down: 1 when a step already covers 8 rows).
+template <int UG, int GG>
+constexpr int gateup_steps() {
+  return (fused_r<UG, GG, true>(6) & ~1) < 2 ? 2 : (fused_r<UG, GG, true>(6) & ~1);
+}
+template <int UD, int LD, int GD>
+constexpr int down_steps() {
+  constexpr int RPW_D = 64 / LD;
+  return RPW_D >= 8 ? 1 : ((fused_r<UD, GD, false>(16 / RPW_D) & ~1) < 2
+                               ? 2 : (fused_r<UD, GD, false>(16 / RPW_D) & ~1));
+}
+
 template <int UG, int LG, int GG, int UD, int LD, int GD, int EPL>
 Entry make_entry() {
-  // down items of ~16 rows (8 when a step already covers 8 rows): the
-  // tile of a block is about hidden / CUs rows
-  constexpr int RPW_D = 64 / LD;
-  // both item sizes split in two halves: even step counts (down: 1 when a
-  // step already covers 8 rows)
-  constexpr int RG = (fused_r<UG, GG, true>(6) & ~1) < 2 ? 2 : (fused_r<UG, GG, true>(6) & ~1);
-  constexpr int RD = RPW_D >= 8 ? 1 : ((fused_r<UD, GD, false>(16 / RPW_D) & ~1) < 2
-                                           ? 2 : (fused_r<UD, GD, false>(16 / RPW_D) & ~1));
+  constexpr int RG = gateup_steps<UG, GG>(), RD = down_steps<UD, LD, GD>();
   return {&decode_fused_kernel<UG, LG, GG, RG, UD, LD, GD, RD, EPL>, RD * (64 / LD)};
+}
+
+template <int UG, int LG, int GG, int UD, int LD, int GD>
+Entry make_xcd_entry() {
+  constexpr int RG = gateup_steps<UG, GG>(), RD = down_steps<UD, LD, GD>();
+  return {&decode_xcd_kernel<UG, LG, GG, RG, UD, LD, GD, RD>, RD * (64 / LD)};
 }
 
 // Supported (gate/up row shape, down row shape) pairs, from gateup_shape and
@@ -588,6 +927,33 @@ const std::map<Variant, Entry>& variants() {
     return v;
   }();
   return m;
+}
+
+// Expert-per-XCD variants (key epl = 0): the shapes of the grid-wide table
+// except the 6-bit 48-lane-group down rows, whose gate/up + down prefetch
+// registers exceed 256 VGPRs (those shapes keep the grid-wide launch).
+const std::map<Variant, Entry>& xcd_variants() {
+  static const std::map<Variant, Entry> m = [] {
+    std::map<Variant, Entry> v;
+#define PMOE_XV(B, UG, LG, GG, UD, LD, GD) \
+  v[{B, UG, LG, GG, UD, LD, GD, 0}] = make_xcd_entry<UG, LG, GG, UD, LD, GD>();
+    PMOE_XV(4, 16, 32, 1, 16, 16, 1)
+    PMOE_XV(4, 32, 64, 2, 16, 64, 1)
+    PMOE_XV(4, 16, 64, 2, 16, 16, 3)
+    PMOE_XV(4, 16, 64, 2, 16, 64, 1)
+    PMOE_XV(4, 16, 64, 1, 16, 16, 1)
+    PMOE_XV(4, 16, 64, 1, 16, 8, 3)
+    PMOE_XV(6, 48, 16, 1, 48, 8, 1)
+    PMOE_XV(6, 48, 32, 1, 48, 8, 1)
+#undef PMOE_XV
+    return v;
+  }();
+  return m;
+}
+
+bool xcd_enabled() {
+  const char* v = getenv("PMOE_DECODE_XCD");
+  return !(v && v[0] == '0');
 }
 
 // Blocks per launch: one per CU, provided the kernel fits one block per CU
@@ -638,6 +1004,38 @@ int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int
   const int epl = (rt.e + 63) / 64;
   const int epl_t = epl <= 2 ? 2 : (epl <= 4 ? 4 : (epl <= 8 ? 8 : 0));
   if (sg.lpr == 0 || sd.lpr == 0 || epl_t == 0) return kDecodeFusedDeclined;
+  FusedArgs a{};
+  a.x = x;
+  a.gate_w = gate_w;
+  a.gate_extra = gate_extra;
+  a.logit_bias = logit_bias;
+  a.logits = const_cast<float*>(rt.logits);
+  a.gu = gu;
+  a.dn = dn;
+  a.out = out;
+  a.inds_out = inds_out;
+  a.w_out = w_out;
+  a.sync = sync;
+  a.spin = g_spin_ticks;
+  // One token, top-8 softmax, no shared expert: the expert-per-XCD launch
+  // when the grid splits into 8 groups of a power-of-two block count.
+  if (xcd_enabled() && rank1_route_ok(rt) && rt.k == kXcdCount && rt.kk == rt.k && !gate_extra &&
+      dn.cols <= kXcdMaxInter && dn.rows_out <= kXcdMaxHidden && rt.e + 128 <= kFThreads) {
+    const auto xt = xcd_variants().find({bits, sg.ub, sg.lpr, sg.gpl, sd.ub, sd.lpr, sd.gpl, 0});
+    if (xt != xcd_variants().end()) {
+      const int blocks = fused_blocks(xt->second.fn, 0);
+      const int per_xcd = blocks / kXcdCount;
+      const int n_tiles = (dn.rows_out + xt->second.sub_rows - 1) / xt->second.sub_rows;
+      if (blocks > 0 && blocks <= kDecodeMaxBlocks && blocks % kXcdCount == 0 &&
+          (per_xcd & (per_xcd - 1)) == 0 && n_tiles <= kXcdMaxTiles) {
+        a.n_blocks = blocks;
+        ProfScope prof_scope(K_DECODE_FUSED, st);
+        xt->second.fn<<<blocks, kFThreads, 0, st>>>(a, rt);
+        PMOE_LAUNCH_CHECK("decode_xcd_kernel");
+        return PMOE_OK;
+      }
+    }
+  }
   const auto& vs = variants();
   const auto it = vs.find({bits, sg.ub, sg.lpr, sg.gpl, sd.ub, sd.lpr, sd.gpl, epl_t});
   if (it == vs.end()) return kDecodeFusedDeclined;
@@ -652,19 +1050,6 @@ int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int
   blocks = fused_blocks(en.fn, lds);
   if (blocks <= 0 || blocks > kDecodeMaxBlocks || blocks * tile < dn.rows_out)
     return kDecodeFusedDeclined;
-  FusedArgs a{};
-  a.x = x;
-  a.gate_w = gate_w;
-  a.gate_extra = gate_extra;
-  a.logit_bias = logit_bias;
-  a.logits = const_cast<float*>(rt.logits);
-  a.gu = gu;
-  a.dn = dn;
-  a.out = out;
-  a.inds_out = inds_out;
-  a.w_out = w_out;
-  a.sync = sync;
-  a.spin = g_spin_ticks;
   a.n_blocks = blocks;
   a.tile = tile;
   ProfScope prof_scope(K_DECODE_FUSED, st);

@@ -82,21 +82,41 @@ size_t decode_record_bytes();
 struct DecodeSync {
   uint32_t arrive[2];  // groups arrived at barrier 1 / barrier 2
   uint32_t epoch;      // launches completed on this workspace
-  uint32_t error;      // sticky: bit 0 = a barrier wait timed out
+  uint32_t error;      // sticky: bit 0 = a barrier or data wait timed out
 };
 constexpr int kDecodeMaxBlocks = 512;
 constexpr int kDecodeGroup = 16;  // blocks per arrival group
 constexpr int kDecodeMaxGroups = kDecodeMaxBlocks / kDecodeGroup;
 constexpr size_t kDecodeFlagStride = 128;  // bytes between two blocks' flags
 constexpr size_t kDecodeGroupOffset = 256 + kDecodeMaxBlocks * kDecodeFlagStride;
+// Expert-per-XCD launch (decode_fused.hip): one launch counter per block
+// group (its own 128-byte line; each of the group's blocks adds 1 per
+// launch, so counter / blocks-per-group numbers the launch), one arrival
+// counter per down tile (64 bytes apart; 8 arrivals per launch), the router
+// logits as tagged 64-bit words (launch tag << 32 | fp32 bits), each group's
+// h as tagged 32-bit words (tag & 0xFFFF << 16 | bf16), and each group's
+// fp32 down partials.  Counters only grow and tags name the launch, so
+// nothing is cleared between launches.
+constexpr int kXcdCount = 8;
+constexpr int kXcdMaxHidden = 8192;
+constexpr int kXcdMaxInter = 8192;
+constexpr int kXcdMaxTiles = 1024;
+constexpr size_t kXcdTileStride = 64;
+constexpr size_t kXcdCounterOffset = kDecodeGroupOffset + 2 * kDecodeMaxGroups * kDecodeFlagStride;
+constexpr size_t kXcdTileOffset = kXcdCounterOffset + kXcdCount * kDecodeFlagStride;
+constexpr size_t kXcdLogitOffset = kXcdTileOffset + kXcdMaxTiles * kXcdTileStride;
+constexpr size_t kXcdHOffset = kXcdLogitOffset + 1024 * sizeof(uint64_t);
+constexpr size_t kXcdPartOffset =
+    kXcdHOffset + size_t(kXcdCount) * kXcdMaxInter * sizeof(uint32_t);
 constexpr size_t kDecodeSyncBytes =
-    kDecodeGroupOffset + 2 * kDecodeMaxGroups * kDecodeFlagStride;
+    kXcdPartOffset + size_t(kXcdCount) * kXcdMaxHidden * sizeof(float);
 constexpr int kDecodeFusedDeclined = 1;  // shape not covered: use decode_routed
 
 // Whole decode layer in one persistent launch (decode_fused.hip): router
 // logits into rt.logits, routing, gate/up into gu.out (h), down + combine
-// into out.  Returns kDecodeFusedDeclined (nothing launched) for shapes it
-// does not cover.
+// into out; one token with top-8 softmax routing and no shared expert takes
+// the expert-per-XCD form.  Returns kDecodeFusedDeclined (nothing launched)
+// for shapes it does not cover.
 int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int bits,
                  const uint16_t* x, const uint16_t* gate_w, const uint16_t* gate_extra,
                  const float* logit_bias, int32_t* inds_out, float* w_out, uint16_t* out,

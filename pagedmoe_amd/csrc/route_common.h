@@ -15,6 +15,10 @@
 
 #include "pmoe_internal.h"
 
+#ifndef PMOE_ROUTE_MARK
+#define PMOE_ROUTE_MARK(i)  // debug builds: a timestamp after each block barrier
+#endif
+
 namespace pmoe {
 
 constexpr int kRouteMaxK = 16;
@@ -274,7 +278,7 @@ __device__ void route_block(const RouteDev& r, RouteLds& L, WaveTmp* W, int32_t*
 // Top-k selection of ONE token over at most 128 routed experts (softmax +
 // renorm scoring), logits in LDS, with a block of at least 512 threads.
 // Expert i is picked at rank #{j : K_j > K_i}, K = order_key << 32 | ~id
-// (ties to the lower id), counted by 4 lanes over 32 experts each; picks
+// (ties to the lower id), counted in 4 quarters of 32 keys each; picks
 // come out in rank order -- the order of wave_topk (value descending, lower
 // id first).  Wave 0 lists the picks (L.ids), the active experts in
 // ascending id order (L.active, shared expert last) and their count; the
@@ -283,10 +287,10 @@ __device__ void route_block(const RouteDev& r, RouteLds& L, WaveTmp* W, int32_t*
 // route_block's.
 struct Rank1Lds {
   uint64_t key[128];
-  int32_t rank[128];
+  int32_t part[4][128];  // counts over each quarter of the keys
 };
 
-__device__ __forceinline__ bool rank1_route_ok(const RouteDev& r) {
+__host__ __device__ __forceinline__ bool rank1_route_ok(const RouteDev& r) {
   return r.scoring == PMOE_SCORE_SOFTMAX && r.norm && r.n == 1 && r.e <= 128 && r.k <= r.e &&
          r.k <= kRouteMaxK;
 }
@@ -298,24 +302,34 @@ __device__ __forceinline__ void route_rank1_select(const RouteDev& r, const floa
   if (tid < 128)
     R.key[tid] = tid < e ? (uint64_t(order_key(lg[tid])) << 32) | uint32_t(~tid) : 0ull;
   __syncthreads();
+  PMOE_ROUTE_MARK(28);
   if (tid < 512) {
-    const int i = tid >> 2, q = tid & 3;  // expert i, quarter q of the comparisons
+    // expert i against quarter q of the keys; q is the same for the whole
+    // wave, so every read is one address broadcast to all lanes (quarters
+    // sit 256 bytes apart, on the same banks: spread over a wave's lanes
+    // they would conflict on every read)
+    const int q = (tid >> 6) & 3, i = (tid & 63) | ((tid >> 8) << 6);
     const uint64_t ki = R.key[i];
     const ulonglong2* kv = reinterpret_cast<const ulonglong2*>(R.key + 32 * q);
+    ulonglong2 kj[16];  // all 16 reads in flight before the first compare
+#pragma unroll
+    for (int c = 0; c < 16; ++c) kj[c] = kv[c];
+    __builtin_amdgcn_sched_barrier(0);
     int cnt = 0;
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
-      const ulonglong2 kj = kv[c];
-      cnt += kj.x > ki ? 1 : 0;
-      cnt += kj.y > ki ? 1 : 0;
+      cnt += kj[c].x > ki ? 1 : 0;
+      cnt += kj[c].y > ki ? 1 : 0;
     }
-    cnt += __float_as_int(xor_lane<1>(__int_as_float(cnt)));
-    cnt += __float_as_int(xor_lane<2>(__int_as_float(cnt)));
-    if (q == 0) R.rank[i] = i < e ? cnt : 0x7fffffff;
+    R.part[q][i] = cnt;
   }
   __syncthreads();
+  PMOE_ROUTE_MARK(29);
   if (tid < 64) {
-    const int r0 = R.rank[lane], r1 = R.rank[lane + 64];
+    auto rank_of = [&](int i) {
+      return i < e ? R.part[0][i] + R.part[1][i] + R.part[2][i] + R.part[3][i] : 0x7fffffff;
+    };
+    const int r0 = rank_of(lane), r1 = rank_of(lane + 64);
     const bool sel0 = r0 < k, sel1 = r1 < k;
     if (sel0) L.ids[r0] = lane;
     if (sel1) L.ids[r1] = lane + 64;
@@ -333,6 +347,7 @@ __device__ __forceinline__ void route_rank1_select(const RouteDev& r, const floa
     }
   }
   __syncthreads();
+  PMOE_ROUTE_MARK(30);
 }
 
 // The combine weights of route_rank1_select's picks, by wave 0, exactly as

@@ -219,16 +219,26 @@ def raise_workspace_errors() -> None:
     PmoeError if a grid barrier of the one-launch decode timed out (those
     layer outputs are NaN).  The failed workspace is re-initialised first,
     so the next call runs normally."""
-    bad = [ws for ws in _live_moe_workspaces()
-           if int(_ERR_HOST.get(ws.data_ptr(), torch.zeros(1, dtype=torch.int32))[0]) != 0]
+    words = {ws.data_ptr(): int(_ERR_HOST.get(ws.data_ptr(),
+                                              torch.zeros(1, dtype=torch.int32))[0])
+             for ws in _live_moe_workspaces()}
+    bad = [ws for ws in _live_moe_workspaces() if words[ws.data_ptr()] != 0]
     if not bad:
         return
+    err = 0
     for ws in bad:
+        err |= words[ws.data_ptr()]
         _ERR_HOST[ws.data_ptr()].zero_()
         check(lib().pmoe_moe_workspace_init(_ptr(ws), ws.numel(), _stream()),
               "pmoe_moe_workspace_init")
-    raise _lib.PmoeError("one-launch decode: a grid-barrier wait timed out (a block was not "
-                         "resident in time); the affected layer outputs are NaN")
+    what = []
+    if err & 1:
+        what.append("a barrier wait timed out (a block was not resident in time)")
+    if err & 2:
+        what.append("the blocks of one group of the expert-per-XCD launch ran on "
+                    "different XCDs")
+    raise _lib.PmoeError("one-launch decode: " + "; ".join(what or [f"error word {err:#x}"])
+                         + "; the affected layer outputs are NaN")
 
 
 def check_workspace_errors() -> None:

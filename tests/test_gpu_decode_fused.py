@@ -4,9 +4,18 @@ The fused kernel runs the same GEMV arithmetic and combine order as the
 three-launch decode (router, gate/up, down+combine), so its outputs must be
 bit-identical to that path on the same inputs; routing must equal the oracle
 bit for bit.  The grid-barrier counters in the workspace header must be back
-at zero after every call and the launch epoch must count the calls (checked
-through repeated calls, batch-size changes and HIP-graph replays); the sticky
-error word must stay 0.
+at zero after every call and the launch epoch must count the grid-wide calls
+(checked through repeated calls, batch-size changes and HIP-graph replays);
+the sticky error word must stay 0.
+
+One token with top-8 softmax routing and no shared expert takes the
+expert-per-XCD form (pick x streamed by block group x, logits and h
+exchanged as tagged words, the last of 8 groups combining each down tile).
+Its counters only grow, by exact amounts per call (blocks-per-group on each
+group's launch counter, 8 on each down-tile counter), which is how these
+tests tell that it ran; its outputs must equal the grid-wide launch's and
+the three-launch path's bit for bit, also under HIP-graph replay (where the
+dispatcher starts the grid mid-cycle over the XCDs).
 """
 
 import os
@@ -74,17 +83,19 @@ class _Layer:
                               shared_gate=self.sgate, ws=ws, out=out, inds=inds, weights=weights)
 
 
-def _run_path(layer, x, fused, ws=None):
-    old = os.environ.get("PMOE_DECODE_FUSED")
+def _run_path(layer, x, fused, ws=None, xcd=True):
+    saved = {v: os.environ.get(v) for v in ("PMOE_DECODE_FUSED", "PMOE_DECODE_XCD")}
     os.environ["PMOE_DECODE_FUSED"] = "1" if fused else "0"
+    os.environ["PMOE_DECODE_XCD"] = "1" if xcd else "0"
     try:
         out, inds, wts = layer.run(x, ws=ws)
         torch.cuda.synchronize()
     finally:
-        if old is None:
-            del os.environ["PMOE_DECODE_FUSED"]
-        else:
-            os.environ["PMOE_DECODE_FUSED"] = old
+        for v, old in saved.items():
+            if old is None:
+                del os.environ[v]
+            else:
+                os.environ[v] = old
     return out.clone(), inds.clone(), wts.clone()
 
 
@@ -105,6 +116,31 @@ SYNC_BYTES = GROUP_OFFSET + 2 * 32 * 128
 def _assert_group_counters_reset(ws):
     grp = ws[GROUP_OFFSET:SYNC_BYTES].cpu().view(torch.int32).numpy()
     assert not grp.any(), f"group arrival counters not reset: {np.nonzero(grp)}"
+
+
+# Expert-per-XCD launch: 8 group launch counters (128 bytes apart), then
+# 1024 down-tile counters (64 bytes apart).
+XCD_OFFSET = SYNC_BYTES
+TILE_OFFSET = XCD_OFFSET + 8 * 128
+
+
+def _xcd_counters(ws):
+    xc = ws[XCD_OFFSET:TILE_OFFSET].cpu().view(torch.int32).numpy()[::32]
+    tc = ws[TILE_OFFSET:TILE_OFFSET + 1024 * 64].cpu().view(torch.int32).numpy()[::16]
+    return xc, tc
+
+
+def _assert_xcd_calls(ws, calls, hidden=None):
+    """The expert-per-XCD launch ran exactly `calls` times on ws: every
+    group's launch counter holds blocks-per-group per call, and each down
+    tile (8 or 16 rows) covering `hidden` counted 8 arrivals per call."""
+    per_xcd = torch.cuda.get_device_properties(0).multi_processor_count // 8
+    xc, tc = _xcd_counters(ws)
+    assert (xc == per_xcd * calls).all(), f"group counters {xc} after {calls} calls"
+    used = int(np.count_nonzero(tc))
+    assert (tc[:used] == 8 * calls).all() and not tc[used:].any(), f"tile counters {tc[:used + 2]}"
+    if calls and hidden:
+        assert used in ((hidden + 7) // 8, (hidden + 15) // 16), f"{used} tiles for {hidden} rows"
 
 
 CASES = {
@@ -157,9 +193,10 @@ def test_fused_qwen3_235b_vs_oracle_and_reuse_across_batches():
         check_close(out.float().cpu().numpy(), ref, f"fused reuse n={n}")
     header = ws[:16].cpu().view(torch.int32).numpy()
     assert header[0] == 0 and header[1] == 0, f"barrier counters not reset: {header}"
-    assert header[2] == 4, f"launch epoch {header[2]} after 4 calls"
+    assert header[2] == 2, f"launch epoch {header[2]} after 2 grid-wide calls"
     assert header[3] == 0, "barrier timeout flagged"
     _assert_group_counters_reset(ws)
+    _assert_xcd_calls(ws, 2, 4096)    # the two single-token calls
 
 
 def test_fused_graph_replays_match_eager():
@@ -208,6 +245,48 @@ def test_fused_graph_replays_match_eager():
     header = ws[:16].cpu().view(torch.int32).numpy()
     assert header[0] == 0 and header[1] == 0, f"barrier counters not reset: {header}"
     _assert_group_counters_reset(ws)
+    _assert_xcd_calls(ws, steps * 5, 4096)   # eager warm-up + 4 replays
+
+
+XCD_CASES = {
+    # hidden, experts, inter, bits
+    "qwen3-235b": (4096, 128, 1536, 4),
+    "qwen3-30b": (2048, 128, 768, 4),
+    "small": (1024, 64, 512, 4),
+    "small-6bit": (1024, 64, 512, 6),
+}
+
+
+@pytest.mark.parametrize("name", sorted(XCD_CASES))
+def test_xcd_split_matches_grid_wide_and_three_launch(name):
+    """Expert-per-XCD launch against the grid-wide launch and the
+    three-launch path on the same inputs, with every third expert absent
+    from the slot table (exact zero rows): routing and outputs bit for bit,
+    three calls on one workspace, counters advanced exactly."""
+    K = _k()
+    h, e, i, bits = XCD_CASES[name]
+    print(f"[xcd] case {name}", flush=True)
+    layer = _Layer(h, e, i, 8, bits, seed=61)
+    layer.table[::3] = -1
+    ws_x = K.moe_workspace(layer.g, 1, 8, 0, e, DEV, fresh=True)
+    ws_g = K.moe_workspace(layer.g, 1, 8, 0, e, DEV, fresh=True)
+    absent_hit = False
+    for call in range(3):
+        x = layer.x(1, seed=610 + call)
+        a = _run_path(layer, x, fused=True, ws=ws_x, xcd=True)
+        b = _run_path(layer, x, fused=True, ws=ws_g, xcd=False)
+        c = _run_path(layer, x, fused=False)
+        for other, what in ((b, "grid-wide launch"), (c, "three-launch path")):
+            assert torch.equal(a[1], other[1]), f"call {call}: indices differ from the {what}"
+            assert torch.equal(a[2], other[2]), f"call {call}: weights differ from the {what}"
+            assert torch.equal(a[0].view(torch.int16), other[0].view(torch.int16)), (
+                f"call {call}: outputs differ from the {what}: max |d| "
+                f"{(a[0].float() - other[0].float()).abs().max().item():.3e}")
+        absent_hit |= bool((a[1] % 3 == 0).any())
+    assert absent_hit, "no absent expert was picked: the zero-row case went untested"
+    _assert_xcd_calls(ws_x, 3, h)
+    _assert_xcd_calls(ws_g, 0)
+    assert K.workspace_error(ws_x) == 0 and K.workspace_error(ws_g) == 0
 
 
 @pytest.mark.parametrize("n", [1, 2])
@@ -259,21 +338,24 @@ def test_routing_512_experts_vs_oracle(n, fused):
     assert np.array_equal(wts.cpu().numpy(), ref_w)
 
 
-def test_barrier_timeout_poisons_output_and_is_reported():
-    """A grid-barrier wait that gives up (forced from the host with a
-    one-tick spin limit on the kernel's own bounded wait, so every block
-    still exits normally) sets error bit 0, leaves NaN in the layer output
-    instead of a plausible wrong answer, and raises PmoeError at the next
-    host sync point, which also re-initialises the workspace."""
+@pytest.mark.parametrize("xcd", [True, False])
+def test_barrier_timeout_poisons_output_and_is_reported(xcd, monkeypatch):
+    """A barrier wait that gives up (forced from the host with a one-tick
+    spin limit on the kernel's own bounded wait, so every block still exits
+    normally) sets error bit 0, leaves NaN in the layer output instead of a
+    plausible wrong answer, and raises PmoeError at the next host sync point,
+    which also re-initialises the workspace -- for the expert-per-XCD launch
+    and the grid-wide one."""
     from pagedmoe_amd._lib import PmoeError
     K = _k()
+    monkeypatch.setenv("PMOE_DECODE_XCD", "1" if xcd else "0")
     layer = _Layer(4096, 128, 1536, 8, seed=9)
     ws = K.moe_workspace(layer.g, 1, 8, 0, 128, DEV)   # the cached one the sync points read
     x = layer.x(1, seed=900)
     good, _, _ = layer.run(x, ws=ws)
     torch.cuda.synchronize()
     assert K.workspace_error(ws) == 0
-    print("[fused] barrier spin limit 1 tick", flush=True)
+    print(f"[fused] barrier spin limit 1 tick, xcd={xcd}", flush=True)
     K.set_barrier_spin(1)
     try:
         bad, _, _ = layer.run(x, ws=ws)
