@@ -1029,7 +1029,7 @@ int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int
       if (blocks > 0 && blocks <= kDecodeMaxBlocks && blocks % kXcdCount == 0 &&
           (per_xcd & (per_xcd - 1)) == 0 && n_tiles <= kXcdMaxTiles) {
         a.n_blocks = blocks;
-        ProfScope prof_scope(K_DECODE_FUSED, st);
+        ProfScope prof_scope(K_DECODE_XCD, st);
         xt->second.fn<<<blocks, kFThreads, 0, st>>>(a, rt);
         PMOE_LAUNCH_CHECK("decode_xcd_kernel");
         return PMOE_OK;

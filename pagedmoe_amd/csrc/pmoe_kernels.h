@@ -16,6 +16,7 @@ enum KernelId {
   K_PREFILL_GATEUP,
   K_PREFILL_DOWN,
   K_DECODE_FUSED,
+  K_DECODE_XCD,
   K_COUNT
 };
 

@@ -162,7 +162,8 @@ def test_fused_matches_three_launch_bit_exact(name, n):
     layer = _Layer(h, e, i, k, bits, sc, shared, sg, seed=21, n_group=ng, topk_group=tg,
                    scale=scale)
     x = layer.x(n, seed=100 + n)
-    assert "decode_fused" in _fused_launches(layer, x), "fused path not taken"
+    launched = _fused_launches(layer, x)
+    assert "decode_fused" in launched or "decode_xcd" in launched, "fused path not taken"
     a = _run_path(layer, x, fused=True)
     b = _run_path(layer, x, fused=False)
     assert torch.equal(a[1], b[1]), "routing indices differ"
