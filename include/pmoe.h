@@ -143,20 +143,26 @@ int pmoe_dequant(const uint32_t* q, const uint16_t* scales,
 size_t pmoe_moe_workspace(const pmoe_geom* g, int n, int k, int shared,
                           int n_experts);
 
-/* A MoE workspace starts with a 73,984-byte synchronisation header (grid
+/* Rows per tile of the prefill expert GEMMs (the dispatch's row tiles of one
+ * expert).  No reference counterpart (mlx's gather_qmm tiles internally);
+ * for callers and tests that reason about tile edges. */
+int pmoe_prefill_tile_rows(void);
+
+/* A MoE workspace starts with a 673,024-byte synchronisation header (grid
  * barrier counters, launch epoch and per-block flags of the one-launch
- * decode layer).  It must be zero before the first pmoe_moe_block call on
- * that workspace and is kept consistent by every call after that, so it
- * must not be overwritten between calls.  This enqueues the zeroing on
- * stream (a kernel, so it may be captured in a graph).  No reference
- * counterpart: the reference's decode runs as mlx graph ops with no
- * workspace (streaming.py:587-641). */
+ * decode layer; launch and tile counters, tagged logit and h words and the
+ * down partials of its expert-per-XCD form).  It must be zero before the
+ * first pmoe_moe_block call on that workspace and is kept consistent by
+ * every call after that, so it must not be overwritten between calls.  This
+ * enqueues the zeroing on stream (a kernel, so it may be captured in a
+ * graph).  No reference counterpart: the reference's decode runs as mlx
+ * graph ops with no workspace (streaming.py:587-641). */
 int pmoe_moe_workspace_init(void* ws, size_t ws_bytes, void* stream);
 
 /* Synchronising read of the header's sticky error word into *error: bit 0 =
- * a grid barrier wait of the one-launch decode gave up after its spin limit
- * (0.5 s by default); the layer output of that call, and of every later call
- * on the workspace until it is re-initialised, is NaN.  Zeroed only by
+ * a barrier or data wait of the one-launch decode gave up after its spin
+ * limit (0.5 s by default); the layer output of that call, and of every later
+ * call on the workspace until it is re-initialised, is NaN.  Zeroed only by
  * pmoe_moe_workspace_init. */
 int pmoe_moe_workspace_status(const void* ws, uint32_t* error, void* stream);
 

@@ -9,15 +9,19 @@
 //     tile's rows p (sorted positions) and 128 columns c of moe_intermediate;
 //   down_mfma_kernel:   y[order[p], d] = h_p . Wd[d] for 256 columns d of hidden.
 //
-// Work split (256 threads = 4 waves): the tile's activation rows are staged
-// through LDS one 64-wide quantization group at a time (double buffered) and
-// shared by the 4 waves; each wave owns 64 weight rows (gate+up rows of 32
-// columns, or 64 down rows), loads their packed words straight from HBM, and
-// dequantizes them in registers into the MFMA B operand, so every weight
-// byte is read and dequantized once per tile.  v_mfma_f32_32x32x16_bf16,
-// fp32 accumulators.  The dequantized weight is bf16(fma(s, q, b)), the
-// format's bf16 dequantization (quant.hip), like the bf16 tile loads of mlx's
-// quantized GEMMs.
+// Work split (512 threads = 8 waves, two per SIMD): the tile's activation
+// rows are staged through LDS one 64-wide quantization group at a time
+// (double buffered) and shared by the 8 waves; each wave owns 32 weight rows
+// (32 gate rows, 32 up rows, or 32 down rows: lane m of either lane half
+// holds row m), loads their packed words straight from HBM, and dequantizes
+// them in registers into the MFMA B operand, so every weight byte is read and
+// dequantized once per tile.  One projection per wave keeps a wave within
+// 256 registers (64 accumulators), so two waves share each SIMD and one
+// covers the other's memory waits and dequant; the gate/up kernel pairs gate
+// wave w with up wave w + 4 (the same rows and columns) through LDS for the
+// SwiGLU.  v_mfma_f32_32x32x16_bf16, fp32 accumulators.  The dequantized
+// weight is bf16(fma(s, q, b)), the format's bf16 dequantization
+// (quant.hip), like the bf16 tile loads of mlx's quantized GEMMs.
 //
 // K order.  For MFMA step s (16 of the group's 64 k) and lane half h, lane
 // element i holds k = 32h + 8s + i: each lane's weight operand for a whole
@@ -38,7 +42,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kTileM = 128;          // rows per dispatch tile
 constexpr int kMB = kTileM / 32;     // 32-row MFMA blocks per tile
 constexpr int kLdsRow = 72;          // bf16 per staged row (64 + 8 pad: 144 B)
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
+constexpr int kStageSteps = kTileM * 8 / kThreads;  // 16-byte pieces per thread per group
 constexpr int kGuCols = 128;         // moe_intermediate columns per gate/up block
 constexpr int kDnCols = 256;         // hidden columns per down block
 
@@ -82,22 +87,6 @@ __device__ __forceinline__ TileInfo tile_info(const PrefillArgs& a, int t) {
 // ---------------------------------------------------------------- dequant
 
 __device__ __forceinline__ float bf_lo(uint32_t v) { return __uint_as_float(v << 16); }
-
-// 8 consecutive 4-bit values of one word (low nibble first) -> bf16(s*q+b).
-__device__ __forceinline__ bf16x8 deq8_4(uint32_t w, float s, float b) {
-  const uint32_t lo = w & 0x0F0F0F0Fu;         // q0 q2 q4 q6
-  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // q1 q3 q5 q7
-  bf16x8 r;
-  r[0] = (__bf16)__builtin_fmaf(s, float(uint8_t(lo)), b);
-  r[1] = (__bf16)__builtin_fmaf(s, float(uint8_t(hi)), b);
-  r[2] = (__bf16)__builtin_fmaf(s, float(uint8_t(lo >> 8)), b);
-  r[3] = (__bf16)__builtin_fmaf(s, float(uint8_t(hi >> 8)), b);
-  r[4] = (__bf16)__builtin_fmaf(s, float(uint8_t(lo >> 16)), b);
-  r[5] = (__bf16)__builtin_fmaf(s, float(uint8_t(hi >> 16)), b);
-  r[6] = (__bf16)__builtin_fmaf(s, float(lo >> 24), b);
-  r[7] = (__bf16)__builtin_fmaf(s, float(hi >> 24), b);
-  return r;
-}
 
 // Byte n of v as float (v_cvt_f32_ubyteN).  Written as asm so the compiler
 // keeps the shared nibble masks instead of re-extracting each field.
@@ -177,42 +166,34 @@ __device__ __forceinline__ void load_words(LaneWords<BITS>& lw, const uint8_t* p
   }
 }
 
-template <int BITS>
-__device__ __forceinline__ void dequant_group(const LaneWords<BITS>& lw, float s, float b,
-                                              bf16x8 (&out)[4]) {
-  if constexpr (BITS == 4) {
-#pragma unroll
-    for (int st = 0; st < 4; ++st) out[st] = deq8_4(lw.w[st], s, b);
-  } else {
-    out[0] = deq8_6<0>(lw.w, s, b);
-    out[1] = deq8_6<1>(lw.w, s, b);
-    out[2] = deq8_6<2>(lw.w, s, b);
-    out[3] = deq8_6<3>(lw.w, s, b);
-  }
-}
-
 // ---------------------------------------------------------------- staging
 
 // One group (64 values) of the tile's activation rows -> registers.
-// Piece p = 256*j + t (j < kMB) of the 16-byte pieces is row p / 8,
-// chunk p % 8, so each load instruction covers whole 128-byte row segments.
-// Rows past the tile re-load the tile's last row: every load stays in bounds
-// and the code has no branch; the MFMA rows they feed are never stored.
+// Piece p = kThreads*j + t (j < kStageSteps) of the 16-byte pieces is row
+// p / 8, chunk p % 8, so each load instruction covers whole 128-byte row
+// segments.  Rows past the tile re-load the tile's last row: every load
+// stays in bounds and the code has no branch; the MFMA rows they feed are
+// never stored.
 struct StageRows {
   const uint16_t* base;
-  uint32_t off[kMB];  // element offset of each staged row
+  uint32_t off[kStageSteps];  // element offset of each staged row
 };
 
 struct StageRegs {
-  u32x4 v[kMB];
+  u32x4 v[kStageSteps];
 };
 
-// Only the first NMB 32-row blocks are staged.
+// Only the pieces of the first NMB 32-row blocks are staged.
+template <int NMB>
+constexpr int stage_steps() {
+  return (32 * NMB * 8 + kThreads - 1) / kThreads;
+}
+
 template <int NMB>
 __device__ __forceinline__ void stage_load(const StageRows& sr, int g, StageRegs& x) {
   const int c = threadIdx.x & 7;
 #pragma unroll
-  for (int j = 0; j < NMB; ++j)
+  for (int j = 0; j < stage_steps<NMB>(); ++j)
     x.v[j] = *reinterpret_cast<const u32x4*>(sr.base + sr.off[j] + g * 64 + c * 8);
 }
 
@@ -221,45 +202,34 @@ __device__ __forceinline__ void stage_store(uint16_t* lds, const StageRegs& x) {
   const int c = threadIdx.x & 7;
   const int r0 = threadIdx.x >> 3;
 #pragma unroll
-  for (int j = 0; j < NMB; ++j)
-    *reinterpret_cast<u32x4*>(lds + (32 * j + r0) * kLdsRow + c * 8) = x.v[j];
+  for (int j = 0; j < stage_steps<NMB>(); ++j)
+    *reinterpret_cast<u32x4*>(lds + ((kThreads / 8) * j + r0) * kLdsRow + c * 8) = x.v[j];
 }
 
 // ---------------------------------------------------------------- main loop
 
-// Per-lane weight rows: two rows (gate+up of one column, or two down rows),
-// with their scale/bias rows (bf16, one per group, read 8 groups at a time).
-struct LaneRows {
-  const uint8_t* w0;
-  const uint8_t* w1;
-  const u32x4* s0;
-  const u32x4* b0;
-  const u32x4* s1;
-  const u32x4* b1;
+// The lane's weight row (half of each group: lane half h) with its scale and
+// bias rows (bf16, one per group, read 8 groups at a time).
+struct LaneRow {
+  const uint8_t* w;
+  const u32x4* s;
+  const u32x4* b;
 };
 
-template <int BITS>
-struct WSet {
-  LaneWords<BITS> w0, w1;
-};
-
-// Scales and biases of 8 consecutive groups for both rows.
+// Scales and biases of 8 consecutive groups.
 struct SBlk {
-  u32x4 s0, b0, s1, b1;
+  u32x4 s, b;
 };
 
 template <int BITS>
-__device__ __forceinline__ void load_wset(WSet<BITS>& ws, const LaneRows& lr, int g) {
+__device__ __forceinline__ void load_group(LaneWords<BITS>& lw, const LaneRow& lr, int g) {
   constexpr int kGroupBytes = 64 * BITS / 8;
-  load_words<BITS>(ws.w0, lr.w0 + size_t(g) * kGroupBytes);
-  load_words<BITS>(ws.w1, lr.w1 + size_t(g) * kGroupBytes);
+  load_words<BITS>(lw, lr.w + size_t(g) * kGroupBytes);
 }
 
-__device__ __forceinline__ void load_sblk(SBlk& sb, const LaneRows& lr, int blk) {
-  sb.s0 = lr.s0[blk];
-  sb.b0 = lr.b0[blk];
-  sb.s1 = lr.s1[blk];
-  sb.b1 = lr.b1[blk];
+__device__ __forceinline__ void load_sblk(SBlk& sb, const LaneRow& lr, int blk) {
+  sb.s = lr.s[blk];
+  sb.b = lr.b[blk];
 }
 
 // bf16 entry i (0..7) of 8 packed in a u32x4, as float.
@@ -268,27 +238,24 @@ __device__ __forceinline__ float bf_at(const u32x4& v, int i) {
   return __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
 }
 
-// Dequant job jb (0..15) of a weight set: half jb & 1 (4 values) of MFMA
-// step (jb >> 1) & 3 of row 0 (jb < 8) or row 1, with the group's
-// scale/bias at entry i of sb.  Sixteen small jobs per group let the
-// dequant spread evenly between the MFMAs.
+// Dequant job jb (0..7) of a group: half jb & 1 (4 values) of MFMA step
+// jb >> 1, with the group's scale/bias at entry i of sb.  Eight small jobs
+// per group let the dequant spread evenly between the MFMAs.
 template <int BITS>
-__device__ __forceinline__ void dequant_job(const WSet<BITS>& ws, const SBlk& sb, int i, int jb,
-                                            bf16x8 (&o0)[4], bf16x8 (&o1)[4]) {
-  const bool r1 = jb >= 8;
-  const int st = (jb >> 1) & 3;
-  const LaneWords<BITS>& lw = r1 ? ws.w1 : ws.w0;
-  const float s = bf_at(r1 ? sb.s1 : sb.s0, i);
-  const float b = bf_at(r1 ? sb.b1 : sb.b0, i);
-  bf16x8& o = r1 ? o1[st] : o0[st];
+__device__ __forceinline__ void dequant_job(const LaneWords<BITS>& lw, const SBlk& sb, int i,
+                                            int jb, bf16x8 (&o)[4]) {
+  const int st = jb >> 1;
+  const float s = bf_at(sb.s, i);
+  const float b = bf_at(sb.b, i);
+  bf16x8& out = o[st];
   if constexpr (BITS == 4) {
     const uint32_t w = lw.w[st];
     const uint32_t lo = w & 0x0F0F0F0Fu;
     const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
     if (jb & 1)
-      deq4_half<1>(lo, hi, s, b, o);
+      deq4_half<1>(lo, hi, s, b, out);
     else
-      deq4_half<0>(lo, hi, s, b, o);
+      deq4_half<0>(lo, hi, s, b, out);
   } else {
     bf16x8 t;
     switch (st) {
@@ -298,66 +265,59 @@ __device__ __forceinline__ void dequant_job(const WSet<BITS>& ws, const SBlk& sb
       default: t = deq8_6<3>(lw.w, s, b); break;
     }
     if (jb & 1) {
-      o[4] = t[4]; o[5] = t[5]; o[6] = t[6]; o[7] = t[7];
+      out[4] = t[4]; out[5] = t[5]; out[6] = t[6]; out[7] = t[7];
     } else {
-      o[0] = t[0]; o[1] = t[1]; o[2] = t[2]; o[3] = t[3];
+      out[0] = t[0]; out[1] = t[1]; out[2] = t[2]; out[3] = t[3];
     }
   }
 }
 
-// acc0/acc1[mb] = A_tile(mb) . B0/B1 over the whole reduction, for the
-// tile's first NMB 32-row blocks.  Software pipeline (per quantization group
-// j): weights of group j+3 and activations of group j+2 are in flight, group
-// j+1's weights are dequantized while group j's MFMAs run, and group j+1's
+// acc[mb] = A_tile(mb) . B over the whole reduction, for the tile's first
+// NMB 32-row blocks.  Software pipeline (per quantization group j): weights
+// of group j+3 and activations of group j+2 are in flight, group j+1's
+// weights are dequantized while group j's MFMAs run, and group j+1's
 // activations go to the other LDS buffer.  Scales/biases arrive 8 groups at
 // a time, one block ahead.  The loop is unrolled by 8 so the register rings
 // are indexed statically; loads past the end clamp to the last group (their
 // data is unused).  n_groups is a multiple of 8.
 template <int BITS, int NMB>
-__device__ __forceinline__ void gemm_tile(int n_groups, const StageRows& rows,
-                                          const LaneRows& lr, uint16_t* lds,
-                                          f32x16 (&acc0)[kMB], f32x16 (&acc1)[kMB]) {
+__device__ __forceinline__ void gemm_tile(int n_groups, const StageRows& rows, const LaneRow& lr,
+                                          uint16_t* lds, f32x16 (&acc)[kMB]) {
   const int lane = threadIdx.x & 63;
   const int m = lane & 31;
   const int h = lane >> 5;
   const int last = n_groups - 1;
   const int last_blk = (n_groups >> 3) - 1;
 #pragma unroll
-  for (int mb = 0; mb < kMB; ++mb) {
-    acc0[mb] = f32x16{};
-    acc1[mb] = f32x16{};
-  }
-  WSet<BITS> W[4];
-  StageRegs X[NMB > 4 ? 1 : 2];
+  for (int mb = 0; mb < kMB; ++mb) acc[mb] = f32x16{};
+  LaneWords<BITS> W[4];
+  StageRegs X[2];
   SBlk S[2];
-  bf16x8 B0[2][4], B1[2][4];
+  bf16x8 B[2][4];
   load_sblk(S[0], lr, 0);
   load_sblk(S[1], lr, min(1, last_blk));
-  load_wset<BITS>(W[0], lr, 0);
-  load_wset<BITS>(W[1], lr, min(1, last));
-  load_wset<BITS>(W[2], lr, min(2, last));
-  // activations: two groups ahead when registers allow, else one
-  constexpr int XD = NMB > 4 ? 1 : 2;
+  load_group<BITS>(W[0], lr, 0);
+  load_group<BITS>(W[1], lr, min(1, last));
+  load_group<BITS>(W[2], lr, min(2, last));
   stage_load<NMB>(rows, 0, X[0]);
   stage_store<NMB>(lds, X[0]);
-  if constexpr (XD == 2) stage_load<NMB>(rows, min(1, last), X[1]);
+  stage_load<NMB>(rows, min(1, last), X[1]);
 #pragma unroll
-  for (int jb = 0; jb < 16; ++jb) dequant_job<BITS>(W[0], S[0], 0, jb, B0[0], B1[0]);
+  for (int jb = 0; jb < 8; ++jb) dequant_job<BITS>(W[0], S[0], 0, jb, B[0]);
   __syncthreads();
 
   for (int j0 = 0; j0 < n_groups; j0 += 8) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int j = j0 + u;
-      load_wset<BITS>(W[(u + 3) & 3], lr, min(j + 3, last));
-      if constexpr (XD == 2)
-        stage_load<NMB>(rows, min(j + 2, last), X[u & 1]);
-      else
-        stage_load<NMB>(rows, min(j + 1, last), X[0]);
+      load_group<BITS>(W[(u + 3) & 3], lr, min(j + 3, last));
+      stage_load<NMB>(rows, min(j + 2, last), X[u & 1]);
       const uint16_t* xs = lds + (u & 1) * (kTileM * kLdsRow) + m * kLdsRow + 32 * h;
-      // Fragment f = (mb, st): two MFMAs (gate/up or two down rows).  The
-      // next group's dequant is spread over the fragments and the LDS
-      // reads run two fragments ahead; sched_barrier keeps that order.
+      // Fragment f = (mb, st): one MFMA.  The next group's dequant is
+      // spread over the fragments and the LDS reads run two fragments
+      // ahead; sched_barrier keeps that order.  (Step-major order, with
+      // consecutive MFMAs on different accumulators, measured slower: the
+      // second wave on the SIMD already fills the accumulation latency.)
       constexpr int NF = 4 * NMB;
       const SBlk& sn = u < 7 ? S[0] : S[1];
       const int si = (u + 1) & 7;
@@ -369,16 +329,14 @@ __device__ __forceinline__ void gemm_tile(int n_groups, const StageRows& rows,
         if (f + 2 < NF)
           A[(f + 2) % 3] = *reinterpret_cast<const bf16x8*>(
               xs + ((f + 2) >> 2) * 32 * kLdsRow + 8 * ((f + 2) & 3));
-        acc0[f >> 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[f % 3], B0[u & 1][f & 3],
-                                                               acc0[f >> 2], 0, 0, 0);
-        acc1[f >> 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[f % 3], B1[u & 1][f & 3],
-                                                               acc1[f >> 2], 0, 0, 0);
+        acc[f >> 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[f % 3], B[u & 1][f & 3],
+                                                              acc[f >> 2], 0, 0, 0);
 #pragma unroll
-        for (int jb = 16 * f / NF; jb < 16 * (f + 1) / NF; ++jb)
-          dequant_job<BITS>(W[(u + 1) & 3], sn, si, jb, B0[(u + 1) & 1], B1[(u + 1) & 1]);
+        for (int jb = 8 * f / NF; jb < 8 * (f + 1) / NF; ++jb)
+          dequant_job<BITS>(W[(u + 1) & 3], sn, si, jb, B[(u + 1) & 1]);
         __builtin_amdgcn_sched_barrier(0);
       }
-      stage_store<NMB>(lds + ((u + 1) & 1) * (kTileM * kLdsRow), X[XD == 2 ? (u + 1) & 1 : 0]);
+      stage_store<NMB>(lds + ((u + 1) & 1) * (kTileM * kLdsRow), X[(u + 1) & 1]);
       if (u == 7) {
         S[0] = S[1];
         load_sblk(S[1], lr, min((j0 >> 3) + 2, last_blk));
@@ -393,17 +351,13 @@ __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 *
 
 template <int BITS>
 __device__ __forceinline__ void gemm_tile_any(int nmb, int n_groups, const StageRows& rows,
-                                              const LaneRows& lr, uint16_t* lds,
-                                              f32x16 (&acc0)[kMB], f32x16 (&acc1)[kMB]) {
+                                              const LaneRow& lr, uint16_t* lds,
+                                              f32x16 (&acc)[kMB]) {
   switch (nmb) {
-    case 1: gemm_tile<BITS, 1>(n_groups, rows, lr, lds, acc0, acc1); break;
-    case 2: gemm_tile<BITS, 2>(n_groups, rows, lr, lds, acc0, acc1); break;
-    case 3: gemm_tile<BITS, 3>(n_groups, rows, lr, lds, acc0, acc1); break;
-    case 4: gemm_tile<BITS, kMB >= 4 ? 4 : 1>(n_groups, rows, lr, lds, acc0, acc1); break;
-    case 5: gemm_tile<BITS, kMB >= 5 ? 5 : 1>(n_groups, rows, lr, lds, acc0, acc1); break;
-    case 6: gemm_tile<BITS, kMB >= 6 ? 6 : 1>(n_groups, rows, lr, lds, acc0, acc1); break;
-    case 7: gemm_tile<BITS, kMB >= 7 ? 7 : 1>(n_groups, rows, lr, lds, acc0, acc1); break;
-    default: gemm_tile<BITS, kMB>(n_groups, rows, lr, lds, acc0, acc1); break;
+    case 1: gemm_tile<BITS, 1>(n_groups, rows, lr, lds, acc); break;
+    case 2: gemm_tile<BITS, 2>(n_groups, rows, lr, lds, acc); break;
+    case 3: gemm_tile<BITS, 3>(n_groups, rows, lr, lds, acc); break;
+    default: gemm_tile<BITS, kMB>(n_groups, rows, lr, lds, acc); break;
   }
 }
 
@@ -426,16 +380,25 @@ __device__ __forceinline__ bool xcd_work(int n_cols, int n_tiles, int& tile, int
 
 // ---------------------------------------------------------------- kernels
 
+// LDS of one block: the activation staging buffers, reused after the main
+// loop by the gate/up epilogue for the up waves' accumulators.
+constexpr int kStageBytes = 2 * kTileM * kLdsRow * 2;
+constexpr int kUpBytes = 4 * kMB * 16 * 64 * 4;  // 4 up waves x accumulators
+constexpr int kLdsBytes = kStageBytes > kUpBytes ? kStageBytes : kUpBytes;
+
 template <int BITS>
 __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(const PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kTileM * kLdsRow];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_raw[kLdsBytes];
+  uint16_t* lds = reinterpret_cast<uint16_t*>(lds_raw);
   int t, cb;
   if (!xcd_work(a.out_cols / kGuCols, *a.n_tiles, t, cb)) return;
   const TileInfo ti = tile_info(a, t);
   if (ti.slot < 0) return;  // the down kernel writes this tile's zero rows
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int col = cb * kGuCols + wave * 32 + (lane & 31);
+  const int up = wave >> 2;   // waves 0-3: gate rows, 4-7: the same up rows
+  const int wq = wave & 3;
+  const int col = cb * kGuCols + wq * 32 + (lane & 31);
   const uint8_t* base = a.slab + size_t(ti.slot) * size_t(a.expert_bytes);
   const size_t row_bytes = size_t(a.cols) * BITS / 8;
   const int groups = a.cols / 64;
@@ -444,25 +407,31 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(const PrefillArgs
   StageRows rows;
   rows.base = a.act;
 #pragma unroll
-  for (int j = 0; j < kMB; ++j) {
-    const int r = min(32 * j + int(threadIdx.x >> 3), ti.m - 1);
+  for (int j = 0; j < kStageSteps; ++j) {
+    const int r = min((kThreads / 8) * j + int(threadIdx.x >> 3), ti.m - 1);
     rows.off[j] = uint32_t(a.order[ti.p0 + r] / a.kk) * uint32_t(a.cols);
   }
-  const u32x4* sp0 = reinterpret_cast<const u32x4*>(base + a.s0);
-  const u32x4* bp0 = reinterpret_cast<const u32x4*>(base + a.b0);
-  const u32x4* sp1 = reinterpret_cast<const u32x4*>(base + a.s1);
-  const u32x4* bp1 = reinterpret_cast<const u32x4*>(base + a.b1);
   const int blks = groups / 8;
-  LaneRows lr;
-  lr.w0 = base + a.w0 + col * row_bytes + h * kHalf;
-  lr.w1 = base + a.w1 + col * row_bytes + h * kHalf;
-  lr.s0 = sp0 + size_t(col) * blks;
-  lr.b0 = bp0 + size_t(col) * blks;
-  lr.s1 = sp1 + size_t(col) * blks;
-  lr.b1 = bp1 + size_t(col) * blks;
-  f32x16 accg[kMB], accu[kMB];
+  LaneRow lr;
+  lr.w = base + (up ? a.w1 : a.w0) + col * row_bytes + h * kHalf;
+  lr.s = reinterpret_cast<const u32x4*>(base + (up ? a.s1 : a.s0)) + size_t(col) * blks;
+  lr.b = reinterpret_cast<const u32x4*>(base + (up ? a.b1 : a.b0)) + size_t(col) * blks;
+  f32x16 acc[kMB];
   const int nmb = (ti.m + 31) >> 5;
-  gemm_tile_any<BITS>(nmb, groups, rows, lr, lds, accg, accu);
+  gemm_tile_any<BITS>(nmb, groups, rows, lr, lds, acc);
+  // SwiGLU: up wave wq + 4 hands its accumulators (the same rows and
+  // columns, lane for lane) to gate wave wq through LDS (the staging
+  // buffers are free: the main loop ended with a block barrier)
+  float* ul = reinterpret_cast<float*>(lds_raw);
+  if (up) {
+#pragma unroll
+    for (int mb = 0; mb < kMB; ++mb)
+      if (mb < nmb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ul[((wq * kMB + mb) * 16 + r) * 64 + lane] = acc[mb][r];
+  }
+  __syncthreads();
+  if (up) return;
   uint16_t* hout = static_cast<uint16_t*>(a.out);
 #pragma unroll
   for (int mb = 0; mb < kMB; ++mb) {
@@ -470,7 +439,8 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(const PrefillArgs
     for (int r = 0; r < 16; ++r) {
       const int row = mb * 32 + acc_row(r, h);
       if (row < ti.m) {
-        const float v = silu_fast(accg[mb][r]) * accu[mb][r];
+        const float u = ul[((wq * kMB + mb) * 16 + r) * 64 + lane];
+        const float v = silu_fast(acc[mb][r]) * u;
         hout[size_t(ti.p0 + row) * a.out_cols + col] = f2bf(v);
       }
     }
@@ -485,19 +455,15 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(const PrefillArgs a
   const TileInfo ti = tile_info(a, t);
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int col0 = cb * kDnCols + wave * 64 + (lane & 31);
-  const int col1 = col0 + 32;
+  const int col = cb * kDnCols + wave * 32 + (lane & 31);
   const int h = lane >> 5;
   if (ti.slot < 0) {  // not resident: exact zero rows (streaming.py:715-719)
     for (int row = h; row < ti.m; row += 2) {
       const size_t o = size_t(a.order[ti.p0 + row]) * a.out_cols;
-      if (a.out_f32) {
-        static_cast<float*>(a.out)[o + col0] = 0.0f;
-        static_cast<float*>(a.out)[o + col1] = 0.0f;
-      } else {
-        static_cast<uint16_t*>(a.out)[o + col0] = 0;
-        static_cast<uint16_t*>(a.out)[o + col1] = 0;
-      }
+      if (a.out_f32)
+        static_cast<float*>(a.out)[o + col] = 0.0f;
+      else
+        static_cast<uint16_t*>(a.out)[o + col] = 0;
     }
     return;
   }
@@ -508,23 +474,18 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(const PrefillArgs a
   StageRows rows;
   rows.base = a.act;
 #pragma unroll
-  for (int j = 0; j < kMB; ++j) {
-    const int r = min(32 * j + int(threadIdx.x >> 3), ti.m - 1);
+  for (int j = 0; j < kStageSteps; ++j) {
+    const int r = min((kThreads / 8) * j + int(threadIdx.x >> 3), ti.m - 1);
     rows.off[j] = uint32_t(ti.p0 + r) * uint32_t(a.cols);
   }
-  const u32x4* sp = reinterpret_cast<const u32x4*>(base + a.s0);
-  const u32x4* bp = reinterpret_cast<const u32x4*>(base + a.b0);
   const int blks = groups / 8;
-  LaneRows lr;
-  lr.w0 = base + a.w0 + col0 * row_bytes + h * kHalf;
-  lr.w1 = base + a.w0 + col1 * row_bytes + h * kHalf;
-  lr.s0 = sp + size_t(col0) * blks;
-  lr.b0 = bp + size_t(col0) * blks;
-  lr.s1 = sp + size_t(col1) * blks;
-  lr.b1 = bp + size_t(col1) * blks;
-  f32x16 acc0[kMB], acc1[kMB];
+  LaneRow lr;
+  lr.w = base + a.w0 + col * row_bytes + h * kHalf;
+  lr.s = reinterpret_cast<const u32x4*>(base + a.s0) + size_t(col) * blks;
+  lr.b = reinterpret_cast<const u32x4*>(base + a.b0) + size_t(col) * blks;
+  f32x16 acc[kMB];
   const int nmb = (ti.m + 31) >> 5;
-  gemm_tile_any<BITS>(nmb, groups, rows, lr, lds, acc0, acc1);
+  gemm_tile_any<BITS>(nmb, groups, rows, lr, lds, acc);
 #pragma unroll
   for (int mb = 0; mb < kMB; ++mb) {
 #pragma unroll
@@ -532,13 +493,10 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(const PrefillArgs a
       const int row = mb * 32 + acc_row(r, h);
       if (row < ti.m) {
         const size_t o = size_t(a.order[ti.p0 + row]) * a.out_cols;
-        if (a.out_f32) {
-          static_cast<float*>(a.out)[o + col0] = acc0[mb][r];
-          static_cast<float*>(a.out)[o + col1] = acc1[mb][r];
-        } else {
-          static_cast<uint16_t*>(a.out)[o + col0] = f2bf(acc0[mb][r]);
-          static_cast<uint16_t*>(a.out)[o + col1] = f2bf(acc1[mb][r]);
-        }
+        if (a.out_f32)
+          static_cast<float*>(a.out)[o + col] = acc[mb][r];
+        else
+          static_cast<uint16_t*>(a.out)[o + col] = f2bf(acc[mb][r]);
       }
     }
   }
@@ -547,6 +505,12 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(const PrefillArgs a
 }  // namespace
 
 int prefill_tile_m() { return kTileM; }
+
+}  // namespace pmoe
+
+extern "C" int pmoe_prefill_tile_rows(void) { return pmoe::prefill_tile_m(); }
+
+namespace pmoe {
 
 // The MFMA path pays off once experts see tens of rows; below that the
 // weight-streaming GEMV (decode.hip) is as fast and needs no tile list.

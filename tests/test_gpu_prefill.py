@@ -5,7 +5,7 @@ Routing and dispatch stay bit-exact; expert outputs and layer outputs are
 held to tests/util tolerance against the float64 oracle (small shapes) or the
 oracle's fp32 C restatement on sampled tokens (full Qwen3-235B shapes).
 Router logits are skewed by a per-expert bias so expert loads are uneven and
-heavy experts span several 128-row tiles.
+heavy experts span several row tiles.
 """
 
 import numpy as np
@@ -67,7 +67,7 @@ def test_prefill_moe_block_vs_oracle(bits):
     xb = _x(rng, 512, spec.hidden)
     ref_i, ref_w, _, ref = O.moe_layer_f64(spec, xb, gw, experts, logit_bias=lb)
     counts = np.bincount(ref_i.reshape(-1), minlength=spec.experts)
-    assert counts.max() > 128, "skew should give an expert several tiles"
+    assert counts.max() > _tile_rows(), "skew should give an expert several tiles"
     g, slab = _slab(spec, experts)
     table = torch.arange(spec.experts, dtype=torch.int32, device=DEV)
     rc = K.route_cfg("softmax", spec.experts, spec.top_k)
@@ -121,9 +121,14 @@ def test_prefill_sigmoid_shared_vs_oracle():
     check_close(out.float().cpu().numpy(), ref, "prefill sigmoid + shared")
 
 
+def _tile_rows():
+    from pagedmoe_amd import _lib
+    return int(_lib.lib().pmoe_prefill_tile_rows())
+
+
 def _tile_boundary_tokens(inds, tile_m):
     """Tokens whose rows sit at the row-tile edges of the heaviest expert:
-    the first and last row of every 128-row tile, and the partial last tile's
+    the first and last row of every row tile, and the partial last tile's
     last row.  The dispatch orders an expert's rows by flat index
     (token * K + slot), so the expert's p-th row is its p-th occurrence in
     the flat routing."""
@@ -142,7 +147,7 @@ def test_prefill_qwen3_235b_2048_tokens_sampled():
     """Full prefill shape: D4096/E128/I1536 top-8 4-bit, 2048 tokens with
     router logits skewed by a N(0,1) per-expert bias.  Routing of every token
     bit-exact (C oracle router); the layer output of the tokens at the
-    heaviest expert's row-tile edges (first and last row of each 128-row tile,
+    heaviest expert's row-tile edges (first and last row of each row tile,
     the partial last tile) and of 6 random tokens within tolerance of the
     fp32 C restatement of the experts."""
     K = _k()
@@ -166,7 +171,7 @@ def test_prefill_qwen3_235b_2048_tokens_sampled():
     assert np.array_equal(gi.cpu().numpy(), ref_i)
     assert np.array_equal(gwt.cpu().numpy(), ref_w)
     out = out.float().cpu().numpy()
-    sample = _tile_boundary_tokens(ref_i, 128) + [int(t) for t in rng.choice(2048, 6, replace=False)]
+    sample = _tile_boundary_tokens(ref_i, _tile_rows()) + [int(t) for t in rng.choice(2048, 6, replace=False)]
     cache = {}
     for t in sample:
         x = O.bf16_to_f32(xb[t])
@@ -208,7 +213,7 @@ def test_prefill_qwen3_next_1024_tokens_sampled():
     out = out.float().cpu().numpy()
     gate_logit = C.router_logits(xb, sgb)[:, 0].astype(np.float64)
     shared = slot_to_expert(slab, E)
-    sample = _tile_boundary_tokens(ref_i, 128) + [int(t) for t in rng.choice(1024, 6, replace=False)]
+    sample = _tile_boundary_tokens(ref_i, _tile_rows()) + [int(t) for t in rng.choice(1024, 6, replace=False)]
     cache = {}
     for t in sample:
         x = O.bf16_to_f32(xb[t])
