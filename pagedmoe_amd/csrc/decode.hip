@@ -77,8 +77,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PMOE_MIN_WA
 // PRE: the routing record was written by route_record_kernel (several
 // tokens); otherwise every block routes its one token itself and block (0, 0)
 // publishes the record.
+// More than 8 logits per lane (over 512 experts): the routing prologue's
+// per-lane logit, key and payload arrays need more registers than the GEMV's
+// occupancy floor leaves, so those variants run with two waves per SIMD.
+template <int EPL>
+constexpr int routed_min_waves() {
+  return EPL > 8 ? 2 : PMOE_MIN_WAVES;
+}
+
 template <int UB, int LPR, int GPL, int R, int EPL, bool PRE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PMOE_MIN_WAVES, 8))) void
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(routed_min_waves<EPL>(), 8))) void
 gateup_routed_kernel(const GemvArgs a, const RouteDev rt, int32_t* inds_out, float* w_out,
                      RouteRecord* rec) {
   constexpr int RPW = 64 / LPR;
@@ -122,16 +130,22 @@ gateup_routed_kernel(const GemvArgs a, const RouteDev rt, int32_t* inds_out, flo
   gemv_expert<UB, LPR, GPL, R, true>(a, slot, s_m, s_rows, wrow0, act_row, store);
 }
 
-// Routing of several tokens at once (one wave per token, 16 waves), written
-// to the record and the routing outputs.
+// Routing of several tokens at once (one wave per token, 16 waves; 8 with
+// more than 8 logits per lane, whose arrays need 256 registers a wave),
+// written to the record and the routing outputs.
 template <int EPL>
-__global__ __launch_bounds__(1024) void route_record_kernel(const RouteDev rt, int32_t* inds_out,
-                                                             float* w_out, RouteRecord* rec,
-                                                             const int32_t* table, int n_experts,
-                                                             int shared_slot) {
+constexpr int route_record_waves() {
+  return EPL > 8 ? 8 : 16;
+}
+
+template <int EPL>
+__global__ __launch_bounds__(64 * route_record_waves<EPL>()) void route_record_kernel(
+    const RouteDev rt, int32_t* inds_out, float* w_out, RouteRecord* rec, const int32_t* table,
+    int n_experts, int shared_slot) {
+  constexpr int NW = route_record_waves<EPL>();
   __shared__ RouteLds L;
-  __shared__ WaveTmp W[16];
-  route_block<EPL, 16>(rt, L, W, inds_out, w_out);
+  __shared__ WaveTmp W[NW];
+  route_block<EPL, NW>(rt, L, W, inds_out, w_out);
   publish_route(L, rt.n * rt.kk, rt.e + (rt.kk > rt.k ? 1 : 0), rec, table, n_experts,
                 shared_slot);
 }
@@ -292,8 +306,8 @@ int launch_gateup_routed(const GemvArgs& gu, const RouteDev& rt, int max_experts
   } else {
     {
       ProfScope prof_scope(K_ROUTE_SELECT, st);
-      route_record_kernel<EPL><<<1, 1024, 0, st>>>(rt, inds_out, w_out, rec, gu.table,
-                                                   gu.n_experts, gu.shared_slot);
+      route_record_kernel<EPL><<<1, 64 * route_record_waves<EPL>(), 0, st>>>(
+          rt, inds_out, w_out, rec, gu.table, gu.n_experts, gu.shared_slot);
       PMOE_LAUNCH_CHECK("route_record_kernel");
     }
     gateup_routed_kernel<UB, L, G, R, EPL, true><<<grid, 256, 0, st>>>(gu, rt, inds_out, w_out,

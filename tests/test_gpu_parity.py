@@ -187,6 +187,47 @@ def test_qwen3_235b_decode_vs_oracle(n):
     check_close(out.float().cpu().numpy(), O.combine_f64(y, ref_w), f"235B decode n={n}")
 
 
+@pytest.mark.parametrize("n,scoring", [(1, "softmax"), (8, "softmax"), (8, "sigmoid")])
+def test_decode_over_512_experts_vs_oracle(n, scoring):
+    """1000 experts, D1024, I512, top-8, 4-bit.  Softmax takes the decode
+    routing with 16 logits per lane (each block's routing prologue at n=1,
+    the routing launch at n=8); sigmoid group scoring above 512 experts takes
+    the general path (routing launch, dispatch, GEMVs).  Routing bit-exact,
+    outputs within tolerance of the oracle."""
+    K = _k()
+    from pagedmoe_amd.slab import SlabStore
+    from pagedmoe_amd._lib import geom
+    e, ng, tg, scale = 1000, 8, 4, 2.5
+    spec = O.LayerSpec(1024, e, 512, 8)
+    g = geom(spec.hidden, spec.inter, spec.bits)
+    slab = SlabStore(g, e, DEV)
+    fill_slab_gpu(slab, range(e), seed=9)
+    rng = np.random.default_rng(700 + n)
+    gwb = O.bf16_round(rng.standard_normal((e, spec.hidden), dtype=np.float32)
+                       * np.float32(0.02))
+    bias = (rng.standard_normal(e, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+    xb = _x_bits(rng, n, spec.hidden)
+    table = torch.arange(e, dtype=torch.int32, device=DEV)
+    logits = O.router_logits(xb, gwb)
+    if scoring == "softmax":
+        rc = K.route_cfg("softmax", e, spec.top_k)
+        ref_i, ref_w = O.softmax_topk(logits, spec.top_k)
+        kw = {}
+    else:
+        rc = K.route_cfg("sigmoid", e, spec.top_k, True, ng, tg, scale)
+        ref_i, ref_w = O.sigmoid_group_topk(logits, bias, ng, tg, spec.top_k, True, scale)
+        kw = {"score_bias": torch.from_numpy(bias).to(DEV)}
+    out, gi, gwt = K.moe_block(g, rc, slab.buf, table, bits_to_bf16_tensor(gwb, DEV),
+                               bits_to_bf16_tensor(xb, DEV), **kw)
+    assert np.array_equal(gi.cpu().numpy(), ref_i)
+    assert np.array_equal(gwt.cpu().numpy(), ref_w)
+    used = sorted(set(ref_i.reshape(-1).tolist()))
+    experts = {x: slot_to_expert(slab, x) for x in used}
+    y = O.switch_glu_f64(xb, ref_i, experts)
+    check_close(out.float().cpu().numpy(), O.combine_f64(y, ref_w), f"E1000 decode n={n}")
+    slab.release()
+
+
 def test_deepseek_shared_decode_vs_oracle():
     """Config 4 routing (sigmoid+bias, 8 groups/top-4, top-8, scale 2.5) + a
     shared expert, at reduced hidden size so the oracle stays fast."""
