@@ -73,16 +73,6 @@ struct TileInfo {
   int e, p0, m, slot;
 };
 
-__device__ __forceinline__ TileInfo tile_info(const PrefillArgs& a, int t) {
-  const int2 tl = a.tiles[t];
-  TileInfo ti;
-  ti.e = tl.x;
-  const int cnt = a.counts[tl.x];
-  ti.m = min(kTileM, cnt - tl.y);
-  ti.p0 = a.offsets[tl.x] + tl.y;
-  ti.slot = tl.x < a.n_experts ? a.table[tl.x] : a.shared_slot;
-  return ti;
-}
 
 // ---------------------------------------------------------------- dequant
 
@@ -362,19 +352,33 @@ __device__ __forceinline__ void gemm_tile_any(int nmb, int n_groups, const Stage
 }
 
 // Blocks are dealt to the 8 XCDs round-robin by linear id; remap so each XCD
-// gets a contiguous run of (tile, column block) work items: the column blocks
-// of one tile share its activation rows, and consecutive tiles of one expert
-// share weights, in that XCD's L2.  The grid is a multiple of 8 blocks and at
-// least 8 * ceil(total / 8), so every item has a block.  Returns false for
-// blocks with no work.
-__device__ __forceinline__ bool xcd_work(int n_cols, int n_tiles, int& tile, int& cb) {
-  const int total = n_cols * n_tiles;
+// gets a contiguous run of work items, and order an expert's items column
+// block first, tile second: the blocks that read one weight column block
+// for each of the expert's tiles are consecutive, so they run side by side
+// on one XCD and its L2 can serve the weights to all but the first.  The
+// expert's items are the same range [t0 * n_cols, (t0 + nt) * n_cols) in
+// either order, found from the tile that tile-major order puts at the item.
+// The grid is a multiple of 8 blocks and at least 8 * ceil(total / 8), so
+// every item has a block.  Returns false for blocks with no work.
+__device__ __forceinline__ bool xcd_work(const PrefillArgs& a, int n_cols, TileInfo& ti,
+                                         int& cb) {
+  const int total = n_cols * *a.n_tiles;
   const int lin = blockIdx.x + gridDim.x * blockIdx.y;
   const int per = (total + 7) >> 3;
   const int w = (lin & 7) * per + (lin >> 3);
   if ((lin >> 3) >= per || w >= total) return false;
-  tile = w / n_cols;
-  cb = w - tile * n_cols;
+  const int tp = w / n_cols;
+  const int2 tl = a.tiles[tp];
+  const int cnt = a.counts[tl.x];
+  const int t0 = tp - tl.y / kTileM;              // the expert's first tile
+  const int nt = (cnt + kTileM - 1) / kTileM;     // and its tile count
+  const int l = w - t0 * n_cols;
+  cb = l / nt;
+  const int r0 = (l - cb * nt) * kTileM;          // first row of this item's tile
+  ti.e = tl.x;
+  ti.m = min(kTileM, cnt - r0);
+  ti.p0 = a.offsets[tl.x] + r0;
+  ti.slot = tl.x < a.n_experts ? a.table[tl.x] : a.shared_slot;
   return true;
 }
 
@@ -390,9 +394,9 @@ template <int BITS>
 __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(const PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_raw[kLdsBytes];
   uint16_t* lds = reinterpret_cast<uint16_t*>(lds_raw);
-  int t, cb;
-  if (!xcd_work(a.out_cols / kGuCols, *a.n_tiles, t, cb)) return;
-  const TileInfo ti = tile_info(a, t);
+  TileInfo ti;
+  int cb;
+  if (!xcd_work(a, a.out_cols / kGuCols, ti, cb)) return;
   if (ti.slot < 0) return;  // the down kernel writes this tile's zero rows
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -450,9 +454,9 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(const PrefillArgs
 template <int BITS>
 __global__ __launch_bounds__(kThreads) void down_mfma_kernel(const PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kTileM * kLdsRow];
-  int t, cb;
-  if (!xcd_work(a.out_cols / kDnCols, *a.n_tiles, t, cb)) return;
-  const TileInfo ti = tile_info(a, t);
+  TileInfo ti;
+  int cb;
+  if (!xcd_work(a, a.out_cols / kDnCols, ti, cb)) return;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int col = cb * kDnCols + wave * 32 + (lane & 31);
