@@ -144,9 +144,13 @@ size_t pmoe_moe_workspace(const pmoe_geom* g, int n, int k, int shared,
                           int n_experts);
 
 /* Rows per tile of the prefill expert GEMMs (the dispatch's row tiles of one
- * expert).  No reference counterpart (mlx's gather_qmm tiles internally);
- * for callers and tests that reason about tile edges. */
-int pmoe_prefill_tile_rows(void);
+ * expert) for a call of n tokens with kk flat columns per token (top-k plus
+ * the shared column) over n_experts routed experts: 32 when the routed
+ * experts see at most 32 rows each on average, else 128 (the environment
+ * variable PMOE_PREFILL_SMALL=1 / 0 pins 32 / 128).  No reference
+ * counterpart (mlx's gather_qmm tiles internally); for callers and tests
+ * that reason about tile edges. */
+int pmoe_prefill_tile_rows(int n, int kk, int n_experts);
 
 /* A MoE workspace starts with a 673,024-byte synchronisation header (grid
  * barrier counters, launch epoch and per-block flags of the one-launch

@@ -81,7 +81,7 @@ SIGNATURES = {
     "pmoe_moe_workspace": (_SZ, [ctypes.POINTER(Geom), _I, _I, _I, _I]),
     "pmoe_moe_workspace_init": (_I, [_P, _SZ, _P]),
     "pmoe_moe_workspace_status": (_I, [_P, ctypes.POINTER(ctypes.c_uint32), _P]),
-    "pmoe_prefill_tile_rows": (_I, []),
+    "pmoe_prefill_tile_rows": (_I, [_I, _I, _I]),
     "pmoe_moe_workspace_error_async": (_I, [_P, _P, _P]),
     "pmoe_set_barrier_spin": (_I, [ctypes.c_uint64]),
     "pmoe_switch_glu": (_I, [ctypes.POINTER(Geom), _P, _P, _I, _P, _P, _I, _I, _P, _P, _SZ, _P]),

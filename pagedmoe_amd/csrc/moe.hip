@@ -18,9 +18,10 @@ namespace pmoe {
 int prefill_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* table,
                     int n_experts, int shared_slot, const uint16_t* x, int n, int kk,
                     const int32_t* order, const int32_t* counts, const int32_t* offsets,
-                    const int2* tiles, const int32_t* n_tiles, int max_tiles, uint16_t* h,
-                    void* y, int y_f32, hipStream_t st);
-int prefill_tile_m();
+                    const int2* tiles, const int32_t* n_tiles, int tile_m, int max_tiles,
+                    uint16_t* h, void* y, int y_f32, hipStream_t st);
+int prefill_tile_rows(int n, int kk, int n_experts);
+int prefill_min_tile_rows();
 bool prefill_wanted(const pmoe_geom* g, int n, int kk, int n_ids);
 
 namespace {
@@ -75,8 +76,8 @@ size_t carve(const pmoe_geom* g, int n, int k, int shared, int n_experts, void* 
   t.offsets = c.take<int32_t>(n_ids + 1);
   t.active = c.take<int32_t>(n_ids);
   t.n_active = c.take<int32_t>(1);
-  const int tm = prefill_tile_m();
-  t.max_tiles = int(rows / tm) + n_ids + 1;
+  // tile capacity for the shortest prefill tiles
+  t.max_tiles = int(rows / prefill_min_tile_rows()) + n_ids + 1;
   t.tiles = c.take<int2>(t.max_tiles);
   t.n_tiles = c.take<int32_t>(1);
   t.h = c.take<uint16_t>(rows * g->inter);
@@ -198,15 +199,16 @@ int run_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* table, i
   const int rows = n * kk;
   const int n_ids = n_experts + (kk > k ? 1 : 0);
   const bool prefill = prefill_wanted(g, n, kk, n_ids);
+  const int tm = prefill ? prefill_tile_rows(n, kk, n_experts) : 0;
   int rc = PMOE_OK;
   if (!dispatched)
     rc = dispatch_ext(inds, rows, k, kk, n_ids, w.order, w.counts, w.offsets, w.inv, w.active,
-                      w.n_active, prefill ? prefill_tile_m() : 0, w.tiles, w.n_tiles, w.dws,
-                      w.dws_bytes, st);
+                      w.n_active, tm, w.tiles, w.n_tiles, w.dws, w.dws_bytes, st);
   if (rc) return rc;
   if (prefill)
     return prefill_experts(g, slab, table, n_experts, shared_slot, x, n, kk, w.order, w.counts,
-                           w.offsets, w.tiles, w.n_tiles, w.max_tiles, w.h, y, y_f32, st);
+                           w.offsets, w.tiles, w.n_tiles, tm,
+                           std::min(rows / tm + n_ids + 1, w.max_tiles), w.h, y, y_f32, st);
   const int max_experts = rows < n_ids ? rows : n_ids;
   GemvArgs a{};
   a.slab = slab;

@@ -270,16 +270,17 @@ __device__ __forceinline__ void dequant_job(const LaneWords<BITS>& lw, const SBl
 // a time, one block ahead.  The loop is unrolled by 8 so the register rings
 // are indexed statically; loads past the end clamp to the last group (their
 // data is unused).  n_groups is a multiple of 8.
-template <int BITS, int NMB>
+template <int BITS, int NMB, int MB>
 __device__ __forceinline__ void gemm_tile(int n_groups, const StageRows& rows, const LaneRow& lr,
-                                          uint16_t* lds, f32x16 (&acc)[kMB]) {
+                                          uint16_t* lds, f32x16 (&acc)[MB]) {
+  static_assert(NMB <= MB, "row blocks beyond the accumulators");
   const int lane = threadIdx.x & 63;
   const int m = lane & 31;
   const int h = lane >> 5;
   const int last = n_groups - 1;
   const int last_blk = (n_groups >> 3) - 1;
 #pragma unroll
-  for (int mb = 0; mb < kMB; ++mb) acc[mb] = f32x16{};
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x16{};
   LaneWords<BITS> W[4];
   StageRegs X[2];
   SBlk S[2];
@@ -339,16 +340,35 @@ __device__ __forceinline__ void gemm_tile(int n_groups, const StageRows& rows, c
 // Row of accumulator register r of a 32x32 block for lane half h.
 __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 
-template <int BITS>
+template <int BITS, int MB>
 __device__ __forceinline__ void gemm_tile_any(int nmb, int n_groups, const StageRows& rows,
                                               const LaneRow& lr, uint16_t* lds,
-                                              f32x16 (&acc)[kMB]) {
-  switch (nmb) {
-    case 1: gemm_tile<BITS, 1>(n_groups, rows, lr, lds, acc); break;
-    case 2: gemm_tile<BITS, 2>(n_groups, rows, lr, lds, acc); break;
-    case 3: gemm_tile<BITS, 3>(n_groups, rows, lr, lds, acc); break;
-    default: gemm_tile<BITS, kMB>(n_groups, rows, lr, lds, acc); break;
+                                              f32x16 (&acc)[MB]) {
+  if constexpr (MB == 1) {
+    gemm_tile<BITS, 1, 1>(n_groups, rows, lr, lds, acc);
+  } else {
+    switch (nmb) {
+      case 1: gemm_tile<BITS, 1, MB>(n_groups, rows, lr, lds, acc); break;
+      case 2: gemm_tile<BITS, 2, MB>(n_groups, rows, lr, lds, acc); break;
+      case 3: gemm_tile<BITS, 3, MB>(n_groups, rows, lr, lds, acc); break;
+      default: gemm_tile<BITS, MB, MB>(n_groups, rows, lr, lds, acc); break;
+    }
   }
+}
+
+// Staged rows of a tile: rows [p0, p0 + m) of the sorted order, gathered
+// from act row order[p] / kk (gate/up) or read in place (order null: down).
+// Rows past the tile re-load its last row.
+__device__ __forceinline__ StageRows tile_rows(const uint16_t* act, const int32_t* order, int kk,
+                                               int cols, int p0, int m) {
+  StageRows rows;
+  rows.base = act;
+#pragma unroll
+  for (int j = 0; j < kStageSteps; ++j) {
+    const int r = p0 + min((kThreads / 8) * j + int(threadIdx.x >> 3), m - 1);
+    rows.off[j] = uint32_t(order ? order[r] / kk : r) * uint32_t(cols);
+  }
+  return rows;
 }
 
 // Blocks are dealt to the 8 XCDs round-robin by linear id; remap so each XCD
@@ -360,6 +380,7 @@ __device__ __forceinline__ void gemm_tile_any(int nmb, int n_groups, const Stage
 // either order, found from the tile that tile-major order puts at the item.
 // The grid is a multiple of 8 blocks and at least 8 * ceil(total / 8), so
 // every item has a block.  Returns false for blocks with no work.
+template <int TM>
 __device__ __forceinline__ bool xcd_work(const PrefillArgs& a, int n_cols, TileInfo& ti,
                                          int& cb) {
   const int total = n_cols * *a.n_tiles;
@@ -370,13 +391,13 @@ __device__ __forceinline__ bool xcd_work(const PrefillArgs& a, int n_cols, TileI
   const int tp = w / n_cols;
   const int2 tl = a.tiles[tp];
   const int cnt = a.counts[tl.x];
-  const int t0 = tp - tl.y / kTileM;              // the expert's first tile
-  const int nt = (cnt + kTileM - 1) / kTileM;     // and its tile count
+  const int t0 = tp - tl.y / TM;                  // the expert's first tile
+  const int nt = (cnt + TM - 1) / TM;             // and its tile count
   const int l = w - t0 * n_cols;
   cb = l / nt;
-  const int r0 = (l - cb * nt) * kTileM;          // first row of this item's tile
+  const int r0 = (l - cb * nt) * TM;              // first row of this item's tile
   ti.e = tl.x;
-  ti.m = min(kTileM, cnt - r0);
+  ti.m = min(TM, cnt - r0);
   ti.p0 = a.offsets[tl.x] + r0;
   ti.slot = tl.x < a.n_experts ? a.table[tl.x] : a.shared_slot;
   return true;
@@ -384,19 +405,31 @@ __device__ __forceinline__ bool xcd_work(const PrefillArgs& a, int n_cols, TileI
 
 // ---------------------------------------------------------------- kernels
 
+// Tile height.  Tiles of 128 rows (MB = kMB row blocks) run at one block
+// per CU (218 registers a wave, 64 of them accumulators); for layers whose
+// experts see few rows each the dispatch cuts 32-row tiles instead (MB = 1,
+// about 105 registers, two blocks per CU, which hide each other's load
+// latency), so an expert with many rows (a shared expert's, say) spreads
+// over many blocks.  The dispatch's tile height is 32 * MB; a tile is
+// clamped to that height in xcd_work.  Both forms give every row the same
+// MFMA sequence, so the outputs are bit-identical.
+//
 // LDS of one block: the activation staging buffers, reused after the main
 // loop by the gate/up epilogue for the up waves' accumulators.
 constexpr int kStageBytes = 2 * kTileM * kLdsRow * 2;
-constexpr int kUpBytes = 4 * kMB * 16 * 64 * 4;  // 4 up waves x accumulators
-constexpr int kLdsBytes = kStageBytes > kUpBytes ? kStageBytes : kUpBytes;
+template <int MB>
+constexpr int gateup_lds_bytes() {
+  constexpr int up = 4 * MB * 16 * 64 * 4;  // 4 up waves x accumulators
+  return kStageBytes > up ? kStageBytes : up;
+}
 
-template <int BITS>
-__global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(const PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds_raw[kLdsBytes];
+template <int BITS, int MB>
+__global__ __launch_bounds__(kThreads, MB < kMB ? 4 : 1) void gateup_mfma_kernel(const PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds_raw[gateup_lds_bytes<MB>()];
   uint16_t* lds = reinterpret_cast<uint16_t*>(lds_raw);
   TileInfo ti;
   int cb;
-  if (!xcd_work(a, a.out_cols / kGuCols, ti, cb)) return;
+  if (!xcd_work<32 * MB>(a, a.out_cols / kGuCols, ti, cb)) return;
   if (ti.slot < 0) return;  // the down kernel writes this tile's zero rows
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -408,42 +441,36 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(const PrefillArgs
   const int groups = a.cols / 64;
   constexpr int kHalf = 64 * BITS / 16;  // bytes of half a group
   const int h = lane >> 5;
-  StageRows rows;
-  rows.base = a.act;
-#pragma unroll
-  for (int j = 0; j < kStageSteps; ++j) {
-    const int r = min((kThreads / 8) * j + int(threadIdx.x >> 3), ti.m - 1);
-    rows.off[j] = uint32_t(a.order[ti.p0 + r] / a.kk) * uint32_t(a.cols);
-  }
   const int blks = groups / 8;
   LaneRow lr;
   lr.w = base + (up ? a.w1 : a.w0) + col * row_bytes + h * kHalf;
   lr.s = reinterpret_cast<const u32x4*>(base + (up ? a.s1 : a.s0)) + size_t(col) * blks;
   lr.b = reinterpret_cast<const u32x4*>(base + (up ? a.b1 : a.b0)) + size_t(col) * blks;
-  f32x16 acc[kMB];
+  const StageRows rows = tile_rows(a.act, a.order, a.kk, a.cols, ti.p0, ti.m);
+  f32x16 acc[MB];
   const int nmb = (ti.m + 31) >> 5;
-  gemm_tile_any<BITS>(nmb, groups, rows, lr, lds, acc);
+  gemm_tile_any<BITS, MB>(nmb, groups, rows, lr, lds, acc);
   // SwiGLU: up wave wq + 4 hands its accumulators (the same rows and
   // columns, lane for lane) to gate wave wq through LDS (the staging
   // buffers are free: the main loop ended with a block barrier)
   float* ul = reinterpret_cast<float*>(lds_raw);
   if (up) {
 #pragma unroll
-    for (int mb = 0; mb < kMB; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
       if (mb < nmb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ul[((wq * kMB + mb) * 16 + r) * 64 + lane] = acc[mb][r];
+        for (int r = 0; r < 16; ++r) ul[((wq * MB + mb) * 16 + r) * 64 + lane] = acc[mb][r];
   }
   __syncthreads();
   if (up) return;
   uint16_t* hout = static_cast<uint16_t*>(a.out);
 #pragma unroll
-  for (int mb = 0; mb < kMB; ++mb) {
+  for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = mb * 32 + acc_row(r, h);
       if (row < ti.m) {
-        const float u = ul[((wq * kMB + mb) * 16 + r) * 64 + lane];
+        const float u = ul[((wq * MB + mb) * 16 + r) * 64 + lane];
         const float v = silu_fast(acc[mb][r]) * u;
         hout[size_t(ti.p0 + row) * a.out_cols + col] = f2bf(v);
       }
@@ -451,12 +478,12 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(const PrefillArgs
   }
 }
 
-template <int BITS>
-__global__ __launch_bounds__(kThreads) void down_mfma_kernel(const PrefillArgs a) {
+template <int BITS, int MB>
+__global__ __launch_bounds__(kThreads, MB < kMB ? 4 : 1) void down_mfma_kernel(const PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kTileM * kLdsRow];
   TileInfo ti;
   int cb;
-  if (!xcd_work(a, a.out_cols / kDnCols, ti, cb)) return;
+  if (!xcd_work<32 * MB>(a, a.out_cols / kDnCols, ti, cb)) return;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int col = cb * kDnCols + wave * 32 + (lane & 31);
@@ -475,23 +502,17 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(const PrefillArgs a
   const size_t row_bytes = size_t(a.cols) * BITS / 8;
   const int groups = a.cols / 64;
   constexpr int kHalf = 64 * BITS / 16;
-  StageRows rows;
-  rows.base = a.act;
-#pragma unroll
-  for (int j = 0; j < kStageSteps; ++j) {
-    const int r = min((kThreads / 8) * j + int(threadIdx.x >> 3), ti.m - 1);
-    rows.off[j] = uint32_t(ti.p0 + r) * uint32_t(a.cols);
-  }
   const int blks = groups / 8;
   LaneRow lr;
   lr.w = base + a.w0 + col * row_bytes + h * kHalf;
   lr.s = reinterpret_cast<const u32x4*>(base + a.s0) + size_t(col) * blks;
   lr.b = reinterpret_cast<const u32x4*>(base + a.b0) + size_t(col) * blks;
-  f32x16 acc[kMB];
+  const StageRows rows = tile_rows(a.act, nullptr, 1, a.cols, ti.p0, ti.m);
+  f32x16 acc[MB];
   const int nmb = (ti.m + 31) >> 5;
-  gemm_tile_any<BITS>(nmb, groups, rows, lr, lds, acc);
+  gemm_tile_any<BITS, MB>(nmb, groups, rows, lr, lds, acc);
 #pragma unroll
-  for (int mb = 0; mb < kMB; ++mb) {
+  for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = mb * 32 + acc_row(r, h);
@@ -508,11 +529,24 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(const PrefillArgs a
 
 }  // namespace
 
-int prefill_tile_m() { return kTileM; }
+// 32-row tiles at two blocks per CU when the routed experts see at most 32
+// rows each on average (n * kk rows over n_experts); PMOE_PREFILL_SMALL=1 /
+// 0 pins either form (read per call, so the two can be compared).
+int prefill_tile_rows(int n, int kk, int n_experts) {
+  const char* v = getenv("PMOE_PREFILL_SMALL");
+  bool small = long(n) * kk <= 32L * n_experts;
+  if (v && v[0] == '1') small = true;
+  if (v && v[0] == '0') small = false;
+  return small ? 32 : kTileM;
+}
+
+int prefill_min_tile_rows() { return 32; }
 
 }  // namespace pmoe
 
-extern "C" int pmoe_prefill_tile_rows(void) { return pmoe::prefill_tile_m(); }
+extern "C" int pmoe_prefill_tile_rows(int n, int kk, int n_experts) {
+  return pmoe::prefill_tile_rows(n, kk, n_experts);
+}
 
 namespace pmoe {
 
@@ -529,14 +563,16 @@ bool prefill_wanted(const pmoe_geom* g, int n, int kk, int n_ids) {
 int prefill_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* table, int n_experts,
                     int shared_slot, const uint16_t* x, int n, int kk, const int32_t* order,
                     const int32_t* counts, const int32_t* offsets, const int2* tiles,
-                    const int32_t* n_tiles, int max_tiles, uint16_t* h, void* y, int y_f32,
-                    hipStream_t st) {
+                    const int32_t* n_tiles, int tile_m, int max_tiles, uint16_t* h, void* y,
+                    int y_f32, hipStream_t st) {
+  PMOE_REQUIRE(tile_m == 32 || tile_m == kTileM, "prefill: tile height must be 32 or 128");
   PMOE_REQUIRE(g->inter % 512 == 0 && g->hidden % 512 == 0,
                "prefill: hidden and inter must be multiples of 512");
   PMOE_REQUIRE(max_tiles > 0 && max_tiles <= (1 << 20), "prefill: tile count out of range");
   PMOE_REQUIRE(int64_t(n) * g->hidden < (int64_t(1) << 31) &&
                    int64_t(n) * kk * g->inter < (int64_t(1) << 31),
                "prefill: activations exceed 2^31 elements");
+  const bool small = tile_m == 32;
   PrefillArgs a{};
   a.slab = slab;
   a.expert_bytes = g->expert_bytes;
@@ -565,10 +601,14 @@ int prefill_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* tabl
     const int items = g->inter / kGuCols * max_tiles;
     dim3 grid((items + 7) / 8 * 8);  // a multiple of 8: xcd_work deals items per XCD
     ProfScope prof_scope(K_PREFILL_GATEUP, st);
-    if (g->bits == 4)
-      gateup_mfma_kernel<4><<<grid, kThreads, 0, st>>>(a);
+    if (g->bits == 4 && small)
+      gateup_mfma_kernel<4, 1><<<grid, kThreads, 0, st>>>(a);
+    else if (g->bits == 4)
+      gateup_mfma_kernel<4, kMB><<<grid, kThreads, 0, st>>>(a);
+    else if (small)
+      gateup_mfma_kernel<6, 1><<<grid, kThreads, 0, st>>>(a);
     else
-      gateup_mfma_kernel<6><<<grid, kThreads, 0, st>>>(a);
+      gateup_mfma_kernel<6, kMB><<<grid, kThreads, 0, st>>>(a);
     PMOE_LAUNCH_CHECK("gateup_mfma_kernel");
   }
   // down -> y (flat rows)
@@ -585,10 +625,14 @@ int prefill_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* tabl
     const int items = g->hidden / kDnCols * max_tiles;
     dim3 grid((items + 7) / 8 * 8);
     ProfScope prof_scope(K_PREFILL_DOWN, st);
-    if (g->bits == 4)
-      down_mfma_kernel<4><<<grid, kThreads, 0, st>>>(a);
+    if (g->bits == 4 && small)
+      down_mfma_kernel<4, 1><<<grid, kThreads, 0, st>>>(a);
+    else if (g->bits == 4)
+      down_mfma_kernel<4, kMB><<<grid, kThreads, 0, st>>>(a);
+    else if (small)
+      down_mfma_kernel<6, 1><<<grid, kThreads, 0, st>>>(a);
     else
-      down_mfma_kernel<6><<<grid, kThreads, 0, st>>>(a);
+      down_mfma_kernel<6, kMB><<<grid, kThreads, 0, st>>>(a);
     PMOE_LAUNCH_CHECK("down_mfma_kernel");
   }
   return PMOE_OK;

@@ -87,3 +87,19 @@ def test_moe_block_rejects_bad_routing_before_any_launch(n, cfg):
                            dummy, n, -1, None, dummy, dummy, dummy, dummy, 1 << 30, None)
     assert r == -1, lib.pmoe_last_error()
     assert b"routing" in lib.pmoe_last_error()
+
+
+def test_prefill_tile_rows_by_rows_per_expert(monkeypatch):
+    """32-row prefill tiles when the routed experts see at most 32 rows each
+    on average (Qwen3-Next-shaped 1024-token prefill: 11 columns x 1024
+    tokens over 512 experts), 128-row tiles above (Qwen3-235B-shaped 2048-token
+    prefill: 16 rows x 128 per expert); PMOE_PREFILL_SMALL pins either."""
+    f = _lib.lib().pmoe_prefill_tile_rows
+    monkeypatch.delenv("PMOE_PREFILL_SMALL", raising=False)
+    assert f(1024, 11, 512) == 32
+    assert f(2048, 8, 128) == 128
+    assert f(128, 8, 32) == 32 and f(129, 8, 32) == 128   # 1024 rows vs 32 x 32
+    monkeypatch.setenv("PMOE_PREFILL_SMALL", "1")
+    assert f(2048, 8, 128) == 32
+    monkeypatch.setenv("PMOE_PREFILL_SMALL", "0")
+    assert f(1024, 11, 512) == 128

@@ -67,7 +67,7 @@ def test_prefill_moe_block_vs_oracle(bits):
     xb = _x(rng, 512, spec.hidden)
     ref_i, ref_w, _, ref = O.moe_layer_f64(spec, xb, gw, experts, logit_bias=lb)
     counts = np.bincount(ref_i.reshape(-1), minlength=spec.experts)
-    assert counts.max() > _tile_rows(), "skew should give an expert several tiles"
+    assert counts.max() > _tile_rows(512, 4, 32), "skew should give an expert several tiles"
     g, slab = _slab(spec, experts)
     table = torch.arange(spec.experts, dtype=torch.int32, device=DEV)
     rc = K.route_cfg("softmax", spec.experts, spec.top_k)
@@ -121,9 +121,94 @@ def test_prefill_sigmoid_shared_vs_oracle():
     check_close(out.float().cpu().numpy(), ref, "prefill sigmoid + shared")
 
 
-def _tile_rows():
+def _small_layer(bits):
+    """D1024/E64/I512 top-4 plus a shared expert, 256 tokens: 1,280 rows, ~16
+    per routed expert, so the prefill cuts 32-row tiles and runs two blocks
+    per CU.  Skewed routing gives some experts several tiles; the shared
+    expert's 256 rows are eight."""
+    spec = O.LayerSpec(1024, 64, 512, 4, bits=bits, shared=1)
+    gw, experts, _, sh, _ = O.make_layer(spec, seed=70 + bits)
+    rng = np.random.default_rng(71)
+    lb = rng.standard_normal(spec.experts, dtype=np.float32) * np.float32(1.5)
+    xb = _x(rng, 256, spec.hidden)
+    return spec, gw, experts, sh, lb, xb
+
+
+def _small_run(K, spec, gw, experts, sh, lb, xb, table_edit=None):
+    g, slab = _slab(spec, experts, extra=sh)
+    table = torch.arange(spec.experts, dtype=torch.int32, device=DEV)
+    if table_edit is not None:
+        table_edit(table)
+    rc = K.route_cfg("softmax", spec.experts, spec.top_k)
+    out, gi, gwt = K.moe_block(g, rc, slab.buf, table, bits_to_bf16_tensor(gw, DEV),
+                               bits_to_bf16_tensor(xb, DEV), logit_bias=torch.from_numpy(lb).to(DEV),
+                               shared_slot=spec.experts)
+    return out, gi, gwt
+
+
+@pytest.mark.parametrize("bits", [4, 6])
+def test_prefill_small_tiles_vs_oracle(bits, monkeypatch):
+    """The 32-row-tile form (chosen by rows per expert) against the float64
+    oracle on every token, and bit-identical to the 128-row-tile form."""
     from pagedmoe_amd import _lib
-    return int(_lib.lib().pmoe_prefill_tile_rows())
+    K = _k()
+    spec, gw, experts, sh, lb, xb = _small_layer(bits)
+    ref_i, ref_w, _, ref = O.moe_layer_f64(spec, xb, gw, experts, logit_bias=lb, shared=sh)
+    counts = np.bincount(ref_i.reshape(-1), minlength=spec.experts)
+    assert counts.max() > 64, "skew should give an expert three tiles"
+    with _lib.KernelTimer() as kt:
+        out, gi, gwt = _small_run(K, spec, gw, experts, sh, lb, xb)
+    torch.cuda.synchronize()
+    assert "prefill_gateup" in kt.result, "prefill path not taken"
+    assert np.array_equal(gi.cpu().numpy(), ref_i)
+    assert np.array_equal(gwt.cpu().numpy(), ref_w)
+    check_close(out.float().cpu().numpy(), ref, f"prefill small tiles {bits}-bit")
+    monkeypatch.setenv("PMOE_PREFILL_SMALL", "0")
+    big, _, _ = _small_run(K, spec, gw, experts, sh, lb, xb)
+    assert torch.equal(out.view(torch.int16), big.view(torch.int16)), (
+        f"forms differ: max |d| {(out.float() - big.float()).abs().max().item():.3e}")
+
+
+def test_prefill_small_tiles_nonresident_and_forced_on_tall_tiles(monkeypatch):
+    """An expert whose table entry is -1 gives exact zero rows in the
+    32-row-tile form; that form pinned on for the skewed 512-token layer
+    (experts of up to ~200 rows) matches the 128-row-tile form bit for
+    bit."""
+    K = _k()
+    spec, gw, experts, sh, lb, xb = _small_layer(4)
+    ids = O.softmax_topk(O.router_logits(xb, gw, lb), spec.top_k)[0]
+    gone = int(np.bincount(ids.reshape(-1), minlength=spec.experts).argmax())
+
+    def drop(table):
+        table[gone] = -1
+
+    out, gi, _ = _small_run(K, spec, gw, experts, sh, lb, xb, table_edit=drop)
+    ref_i, ref_w = O.softmax_topk(O.router_logits(xb, gw, lb), spec.top_k)
+    assert np.array_equal(gi.cpu().numpy(), ref_i)
+    y = O.switch_glu_f64(xb, ref_i, experts)
+    y[ref_i == gone] = 0.0
+    ref = O.combine_f64(y, ref_w, O.expert_ffn_f64(O.bf16_to_f32(xb), sh[0]))
+    check_close(out.float().cpu().numpy(), ref, "prefill small tiles, expert absent")
+    spec2 = O.LayerSpec(1024, 32, 512, 4)
+    gw2, experts2, _, _, _ = O.make_layer(spec2, seed=24)
+    rng = np.random.default_rng(21)
+    lb2 = rng.standard_normal(spec2.experts, dtype=np.float32)
+    xb2 = _x(rng, 512, spec2.hidden)
+    g2, slab2 = _slab(spec2, experts2)
+    table2 = torch.arange(spec2.experts, dtype=torch.int32, device=DEV)
+    rc2 = K.route_cfg("softmax", spec2.experts, spec2.top_k)
+    outs = []
+    for pin in ("1", "0"):
+        monkeypatch.setenv("PMOE_PREFILL_SMALL", pin)
+        o, _, _ = K.moe_block(g2, rc2, slab2.buf, table2, bits_to_bf16_tensor(gw2, DEV),
+                              bits_to_bf16_tensor(xb2, DEV), logit_bias=torch.from_numpy(lb2).to(DEV))
+        outs.append(o)
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
+def _tile_rows(n, kk, n_experts):
+    from pagedmoe_amd import _lib
+    return int(_lib.lib().pmoe_prefill_tile_rows(n, kk, n_experts))
 
 
 def _tile_boundary_tokens(inds, tile_m):
@@ -171,7 +256,8 @@ def test_prefill_qwen3_235b_2048_tokens_sampled():
     assert np.array_equal(gi.cpu().numpy(), ref_i)
     assert np.array_equal(gwt.cpu().numpy(), ref_w)
     out = out.float().cpu().numpy()
-    sample = _tile_boundary_tokens(ref_i, _tile_rows()) + [int(t) for t in rng.choice(2048, 6, replace=False)]
+    sample = (_tile_boundary_tokens(ref_i, _tile_rows(2048, k, E))
+              + [int(t) for t in rng.choice(2048, 6, replace=False)])
     cache = {}
     for t in sample:
         x = O.bf16_to_f32(xb[t])
@@ -213,7 +299,8 @@ def test_prefill_qwen3_next_1024_tokens_sampled():
     out = out.float().cpu().numpy()
     gate_logit = C.router_logits(xb, sgb)[:, 0].astype(np.float64)
     shared = slot_to_expert(slab, E)
-    sample = _tile_boundary_tokens(ref_i, _tile_rows()) + [int(t) for t in rng.choice(1024, 6, replace=False)]
+    sample = (_tile_boundary_tokens(ref_i, _tile_rows(1024, k + 1, E))
+              + [int(t) for t in rng.choice(1024, 6, replace=False)])
     cache = {}
     for t in sample:
         x = O.bf16_to_f32(xb[t])
