@@ -216,11 +216,10 @@ __device__ __forceinline__ void fma8(float& acc, const uint4& a, const uint4& b)
 // bias is added to routed rows only.  The loads of 8 passes are issued
 // together (one memory round trip for hidden <= 4096).  Every lane returns
 // the logit.
-__device__ float router_dot(const FusedArgs& a, const RouteDev& rt, int e, int t) {
+// Dot of one router row with one token row over d columns, in the router's
+// fixed lane order.
+__device__ float router_row_dot(const uint16_t* wrow, const uint16_t* xrow, int d) {
   const int lane = threadIdx.x & 63;
-  const int d = a.gu.cols;
-  const uint16_t* wrow = e < rt.e ? a.gate_w + size_t(e) * d : a.gate_extra;
-  const uint16_t* xrow = a.x + size_t(t) * d;
   const int passes = (d + 511) / 512;
   float acc = 0.0f;
   for (int p0 = 0; p0 < passes; p0 += 8) {
@@ -239,7 +238,13 @@ __device__ float router_dot(const FusedArgs& a, const RouteDev& rt, int e, int t
       if (p0 + j < passes && col < d) fma8(acc, xv[j], wv[j]);
     }
   }
-  const float sum = wave_sum_bfly(acc);
+  return wave_sum_bfly(acc);
+}
+
+__device__ float router_dot(const FusedArgs& a, const RouteDev& rt, int e, int t) {
+  const int d = a.gu.cols;
+  const uint16_t* wrow = e < rt.e ? a.gate_w + size_t(e) * d : a.gate_extra;
+  const float sum = router_row_dot(wrow, a.x + size_t(t) * d, d);
   return a.logit_bias && e < rt.e ? sum + a.logit_bias[e] : sum;
 }
 
@@ -574,9 +579,16 @@ __device__ __forceinline__ T device_load(const T* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Leading arguments: the pointers and sizes of the launch's first loads
+// (launch counter, slot table, router rows, x), as plain arguments.  This
+// file is built with kernel-argument preload, which puts a kernel's first
+// argument dwords into SGPRs as its waves start, so those loads issue
+// without waiting for the argument segment (a struct argument is not
+// preloaded).
 template <int UG, int LG, int GG, int RG, int UD, int LD, int GD, int RD>
-__global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(const FusedArgs a,
-                                                               const RouteDev rt) {
+__global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(
+    DecodeSync* sync_p, const int32_t* table_p, const uint16_t* x_p, const uint16_t* gate_p,
+    const float* bias_p, int d, int n_experts, const FusedArgs a, const RouteDev rt) {
   constexpr int RPW = 64 / LG;
   constexpr int kRows = RG * RPW;           // gate/up rows per item
   constexpr int kHD = RD > 1 ? RD / 2 : 1;  // down steps per half
@@ -596,7 +608,7 @@ __global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(const FusedArgs a
   const int per_xcd = a.n_blocks / kXcdCount;
   const int lw = (blockIdx.x / kXcdCount) * kFWaves + wave;  // wave index within the group
   const int n_lw = per_xcd * kFWaves;
-  DecodeSync* sy = a.sync;
+  DecodeSync* sy = sync_p;
   uint8_t* hdr = reinterpret_cast<uint8_t*>(sy);
   uint64_t* lgx = reinterpret_cast<uint64_t*>(hdr + kXcdLogitOffset);
   uint32_t* hx = reinterpret_cast<uint32_t*>(hdr + kXcdHOffset) + size_t(xcd) * kXcdMaxInter;
@@ -616,7 +628,7 @@ __global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(const FusedArgs a
     old = __hip_atomic_fetch_add(
         reinterpret_cast<uint32_t*>(hdr + kXcdCounterOffset + xcd * kDecodeFlagStride), 1u,
         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const int32_t tab = int(threadIdx.x) < rt.e ? a.gu.table[threadIdx.x] : -1;
+  const int32_t tab = int(threadIdx.x) < n_experts ? table_p[threadIdx.x] : -1;
 
   // A: logit e by wave 0 of block e.  (Vector loads and stores share one
   // counter, so a wave that waits for a load also waits for the device-scope
@@ -625,15 +637,16 @@ __global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(const FusedArgs a
   trace_mark(sy, 0);
   if (wave == 0) {
     const uint32_t my_tag = __builtin_amdgcn_readfirstlane(old) / uint32_t(per_xcd) + 1u;
-    if (int(threadIdx.x) < rt.e) s_table[threadIdx.x] = tab;
-    for (int e = blockIdx.x; e < rt.e; e += a.n_blocks) {
-      const float v = router_dot(a, rt, e, 0);
+    if (int(threadIdx.x) < n_experts) s_table[threadIdx.x] = tab;
+    for (int e = blockIdx.x; e < n_experts; e += a.n_blocks) {
+      const float sum = router_row_dot(gate_p + size_t(e) * d, x_p, d);
+      const float v = bias_p ? sum + bias_p[e] : sum;
       if (lane == 0)
         __hip_atomic_store(&lgx[e], (uint64_t(my_tag) << 32) | __float_as_uint(v),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (lane == 0) s_tag = my_tag;
-  } else if (int(threadIdx.x) < rt.e) {
+  } else if (int(threadIdx.x) < n_experts) {
     s_table[threadIdx.x] = tab;
   }
   trace_mark(sy, 1);
@@ -867,10 +880,17 @@ struct Variant {
 };
 
 using FusedFn = void (*)(const FusedArgs, const RouteDev);
+using XcdFn = void (*)(DecodeSync*, const int32_t*, const uint16_t*, const uint16_t*,
+                       const float*, int, int, const FusedArgs, const RouteDev);
 
 struct Entry {
   FusedFn fn;
   int sub_rows;  // down rows per wave item
+};
+
+struct XcdEntry {
+  XcdFn fn;
+  int sub_rows;
 };
 
 // Gate/up row steps per wave item and down row steps per down item (~16
@@ -894,7 +914,7 @@ Entry make_entry() {
 }
 
 template <int UG, int LG, int GG, int UD, int LD, int GD>
-Entry make_xcd_entry() {
+XcdEntry make_xcd_entry() {
   constexpr int RG = gateup_steps<UG, GG>(), RD = down_steps<UD, LD, GD>();
   return {&decode_xcd_kernel<UG, LG, GG, RG, UD, LD, GD, RD>, RD * (64 / LD)};
 }
@@ -932,9 +952,9 @@ const std::map<Variant, Entry>& variants() {
 // Expert-per-XCD variants (key epl = 0): the shapes of the grid-wide table
 // except the 6-bit 48-lane-group down rows, whose gate/up + down prefetch
 // registers exceed 256 VGPRs (those shapes keep the grid-wide launch).
-const std::map<Variant, Entry>& xcd_variants() {
-  static const std::map<Variant, Entry> m = [] {
-    std::map<Variant, Entry> v;
+const std::map<Variant, XcdEntry>& xcd_variants() {
+  static const std::map<Variant, XcdEntry> m = [] {
+    std::map<Variant, XcdEntry> v;
 #define PMOE_XV(B, UG, LG, GG, UD, LD, GD) \
   v[{B, UG, LG, GG, UD, LD, GD, 0}] = make_xcd_entry<UG, LG, GG, UD, LD, GD>();
     PMOE_XV(4, 16, 32, 1, 16, 16, 1)
@@ -958,20 +978,19 @@ bool xcd_enabled() {
 
 // Blocks per launch: one per CU, provided the kernel fits one block per CU
 // with this LDS size (checked once per device, kernel and size).
-int fused_blocks(FusedFn fn, size_t lds) {
+int fused_blocks(const void* fn, size_t lds) {
   static std::mutex mu;
   static std::map<std::tuple<int, void*, size_t>, int> cache;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
   std::lock_guard<std::mutex> lk(mu);
-  const auto key = std::make_tuple(dev, reinterpret_cast<void*>(fn), lds);
+  const auto key = std::make_tuple(dev, const_cast<void*>(fn), lds);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
   int cus = 0, nb = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(fn),
-                                                   kFThreads, lds) != hipSuccess)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, kFThreads, lds) != hipSuccess)
     nb = 0;
   const int blocks = nb >= 1 ? cus : 0;
   cache[key] = blocks;
@@ -1023,14 +1042,15 @@ int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int
       dn.cols <= kXcdMaxInter && dn.rows_out <= kXcdMaxHidden && rt.e + 128 <= kFThreads) {
     const auto xt = xcd_variants().find({bits, sg.ub, sg.lpr, sg.gpl, sd.ub, sd.lpr, sd.gpl, 0});
     if (xt != xcd_variants().end()) {
-      const int blocks = fused_blocks(xt->second.fn, 0);
+      const int blocks = fused_blocks(reinterpret_cast<const void*>(xt->second.fn), 0);
       const int per_xcd = blocks / kXcdCount;
       const int n_tiles = (dn.rows_out + xt->second.sub_rows - 1) / xt->second.sub_rows;
       if (blocks > 0 && blocks <= kDecodeMaxBlocks && blocks % kXcdCount == 0 &&
           (per_xcd & (per_xcd - 1)) == 0 && n_tiles <= kXcdMaxTiles) {
         a.n_blocks = blocks;
         ProfScope prof_scope(K_DECODE_XCD, st);
-        xt->second.fn<<<blocks, kFThreads, 0, st>>>(a, rt);
+        xt->second.fn<<<blocks, kFThreads, 0, st>>>(a.sync, a.gu.table, a.x, a.gate_w,
+                                                     a.logit_bias, a.gu.cols, rt.e, a, rt);
         PMOE_LAUNCH_CHECK("decode_xcd_kernel");
         return PMOE_OK;
       }
@@ -1041,13 +1061,13 @@ int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int
   if (it == vs.end()) return kDecodeFusedDeclined;
   const Entry& en = it->second;
   // tile = down rows per block, a whole number of wave items
-  int blocks = fused_blocks(en.fn, 0);
+  int blocks = fused_blocks(reinterpret_cast<const void*>(en.fn), 0);
   if (blocks <= 0) return kDecodeFusedDeclined;
   const int per_block = (dn.rows_out + blocks - 1) / blocks;
   const int tile = (per_block + en.sub_rows - 1) / en.sub_rows * en.sub_rows;
   const size_t lds = size_t(rt.n) * rt.kk * tile * sizeof(float);
   if (lds > 64 * 1024) return kDecodeFusedDeclined;
-  blocks = fused_blocks(en.fn, lds);
+  blocks = fused_blocks(reinterpret_cast<const void*>(en.fn), lds);
   if (blocks <= 0 || blocks > kDecodeMaxBlocks || blocks * tile < dn.rows_out)
     return kDecodeFusedDeclined;
   a.n_blocks = blocks;
