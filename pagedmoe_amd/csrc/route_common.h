@@ -67,15 +67,33 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Maximum of an unsigned key over the wave, wave-uniform: xor exchanges
-// within each row of 16 lanes, then the four row maxima by readlane.
-__device__ __forceinline__ uint32_t wave_max_key(uint32_t v) {
-  v = max(v, __float_as_uint(xor_lane<1>(__uint_as_float(v))));
-  v = max(v, __float_as_uint(xor_lane<2>(__uint_as_float(v))));
-  v = max(v, __float_as_uint(xor_lane<4>(__uint_as_float(v))));
-  v = max(v, __float_as_uint(xor_lane<8>(__uint_as_float(v))));
-  const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
-  const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+// Inverse of order_key (a zero of either sign comes back as +0).
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+template <int D>
+__device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
+  const uint32_t lo = __float_as_uint(xor_lane<D>(__uint_as_float(uint32_t(v))));
+  const uint32_t hi = __float_as_uint(xor_lane<D>(__uint_as_float(uint32_t(v >> 32))));
+  return (uint64_t(hi) << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane(uint32_t(v), l);
+  const uint32_t hi = __builtin_amdgcn_readlane(uint32_t(v >> 32), l);
+  return (uint64_t(hi) << 32) | lo;
+}
+
+// Maximum of a 64-bit key over the wave, wave-uniform: xor exchanges within
+// each row of 16 lanes, then the four row maxima by readlane.
+__device__ __forceinline__ uint64_t wave_max_key64(uint64_t v) {
+  v = max(v, xor_lane64<1>(v));
+  v = max(v, xor_lane64<2>(v));
+  v = max(v, xor_lane64<4>(v));
+  v = max(v, xor_lane64<8>(v));
+  const uint64_t r0 = readlane64(v, 0), r1 = readlane64(v, 16);
+  const uint64_t r2 = readlane64(v, 32), r3 = readlane64(v, 48);
   return max(max(r0, r1), max(r2, r3));
 }
 
@@ -87,41 +105,38 @@ struct Pick {
 };
 
 // Top-k of per-lane values v[i] (id lane + 64*i, valid when id < n_valid,
-// k <= n_valid): k rounds of a wave-wide maximum of order-preserving keys,
-// each taking the lowest id among the entries holding the maximum.  Lane j
-// (< k) returns pick j; picks come out sorted by (value desc, id asc), and
-// extra[i] of each pick is carried along.  Registers and scalar ops only.
-template <int EPL>
+// k <= n_valid): k rounds of a wave-wide maximum of the 64-bit keys
+// order_key(v) << 32 | ~id, so the maximum is the largest value and, among
+// equal values, the lowest id, and it names its own id and value (no search
+// for the holder; invalid and taken entries hold key 0, below every valid
+// key).  Lane j (< k) returns pick j; picks come out sorted by (value desc,
+// id asc), and extra[i] of each pick is carried along when PAYLOAD.
+// Registers and scalar ops only.
+template <int EPL, bool PAYLOAD = true>
 __device__ __forceinline__ Pick wave_topk(const float (&v)[EPL], int n_valid, int k,
                                           const float (&extra)[EPL]) {
   const int lane = threadIdx.x & 63;
-  uint32_t key[EPL];
-  bool avail[EPL];
+  uint64_t key[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
-    avail[i] = lane + 64 * i < n_valid;
-    key[i] = order_key(v[i]);
+    const int id = lane + 64 * i;
+    key[i] = id < n_valid ? (uint64_t(order_key(v[i])) << 32) | uint32_t(~uint32_t(id)) : 0;
   }
   Pick pk{0.0f, 0, 0.0f};
   for (int j = 0; j < k; ++j) {
-    uint32_t best = 0;
+    uint64_t best = 0;
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) best = avail[i] ? max(best, key[i]) : best;
-    const uint32_t top = wave_max_key(best);
-    int sel = -1;  // lowest id holding top: first i with a hit, lowest lane in it
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      const uint64_t hit = wave_ballot(avail[i] && key[i] == top);
-      if (sel < 0 && hit) sel = 64 * i + __builtin_ctzll(hit);
-    }
+    for (int i = 0; i < EPL; ++i) best = max(best, key[i]);
+    const uint64_t top = wave_max_key64(best);
+    const int sel = int(~uint32_t(top));
     const int sl = sel & 63, si = sel >> 6;
-    float pv = 0.0f, px = 0.0f;
+    const float pv = key_value(uint32_t(top >> 32));
+    float px = 0.0f;
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
       if (i == si) {
-        pv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[i]), sl));
-        px = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(extra[i]), sl));
-        if (lane == sl) avail[i] = false;
+        if (PAYLOAD) px = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(extra[i]), sl));
+        if (lane == sl) key[i] = 0;
       }
     }
     if (lane == j) pk = Pick{pv, sel, px};
@@ -160,7 +175,7 @@ __device__ void route_token(const RouteDev& r, int t, RouteLds& L, WaveTmp& W, i
   float wk = 0.0f;
   int ik = 0;
   if (r.scoring == PMOE_SCORE_SOFTMAX) {
-    const Pick pk = wave_topk<EPL>(v, e, k, x);
+    const Pick pk = wave_topk<EPL, false>(v, e, k, x);
     const float m = lane_value(pk.v, 0);
     // lane j < k holds exp(v_j - m); the sum runs in pick order j = 0..k-1
     const float ej = lane < k ? pexp(pk.v - m) : 0.0f;
@@ -210,7 +225,7 @@ __device__ void route_token(const RouteDev& r, int t, RouteLds& L, WaveTmp& W, i
         }
         gscore[0] = t1 + t2;
       }
-      const Pick gp = wave_topk<EPL>(gscore, r.n_group, r.topk_group, x);
+      const Pick gp = wave_topk<EPL, false>(gscore, r.n_group, r.topk_group, x);
       uint64_t keep = 0;
       for (int j = 0; j < r.topk_group; ++j) keep |= 1ull << __builtin_amdgcn_readlane(gp.i, j);
 #pragma unroll
