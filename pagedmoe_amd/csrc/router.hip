@@ -10,6 +10,8 @@
 // element d = 512*t + 8*l + j is owned by lane l; each lane runs
 // acc = fma(x_d, w_d, acc) for t ascending, j ascending (one 16-byte load of
 // x and of w per t); the 64 lane partials are combined by an xor butterfly.
+#include <type_traits>
+
 #include "pmoe_internal.h"
 #include "pmoe_kernels.h"
 
@@ -34,8 +36,11 @@ __device__ __forceinline__ void fma8(float& acc, const uint4& a, const uint4& b)
 
 // One wave computes a TE x TN tile of logits (experts x tokens).
 // Rows e < n_w come from w (+ bias), row n_w (if e > n_w) from w_extra;
-// out has ld = e columns.
-template <int TE, int TN>
+// out has ld = e columns.  Passes of 512 columns are loaded UNR at a time
+// (one memory round trip per group: compiled per pass, a wave waited for
+// one pass's loads before issuing the next pass's); FULL (d a multiple of
+// 512) drops the column guard.
+template <int TE, int TN, int UNR, bool FULL>
 __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const uint16_t* __restrict__ w_extra, const float* __restrict__ bias, int n, int d, int e,
@@ -51,27 +56,38 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = 0.0f;
 
+  // UNR passes at a time: every load of the group is issued before the
+  // first FMA (sched_barrier keeps the compiler from sinking them), then the
+  // FMAs run in pass order.  Passes past the end and columns past d load an
+  // in-bounds address and skip their FMAs.
   const int passes = (d + 511) / 512;
-#pragma unroll 4
-  for (int t = 0; t < passes; ++t) {
-    const int col = t * 512 + lane * 8;
-    if (col < d) {
-      uint4 wv[TE], xv[TN];
+  for (int t0 = 0; t0 < passes; t0 += UNR) {
+    uint4 wv[UNR][TE], xv[UNR][TN];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int col = min(min(t0 + u, passes - 1) * 512 + lane * 8, d - 8);
 #pragma unroll
       for (int i = 0; i < TE; ++i) {
         const int ei = min(e0 + i, e - 1);
         const uint16_t* src = ei < n_w ? w + size_t(ei) * d : w_extra;
-        wv[i] = *reinterpret_cast<const uint4*>(src + col);
+        wv[u][i] = *reinterpret_cast<const uint4*>(src + col);
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int nj = min(n0 + j, n - 1);
-        xv[j] = *reinterpret_cast<const uint4*>(x + size_t(nj) * d + col);
+        xv[u][j] = *reinterpret_cast<const uint4*>(x + size_t(nj) * d + col);
       }
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < TE; ++i)
+    for (int u = 0; u < UNR; ++u) {
+      const int col = (t0 + u) * 512 + lane * 8;
+      if (t0 + u < passes && (FULL || col < d)) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) fma8(acc[i][j], xv[j], wv[i]);
+        for (int i = 0; i < TE; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) fma8(acc[i][j], xv[u][j], wv[u][i]);
+      }
     }
   }
 #pragma unroll
@@ -260,18 +276,31 @@ int router_logits_ext(const uint16_t* x, const uint16_t* w, const uint16_t* w_ex
   if (n == 0) return PMOE_OK;
   const int e = n_w + (w_extra ? 1 : 0);
   ProfScope prof_scope(K_ROUTER_LOGITS, st);
+  const bool full = d % 512 == 0;
+  auto launch = [&](auto te, auto tn, auto unr, dim3 grid) {
+    constexpr int TE = decltype(te)::value, TN = decltype(tn)::value, UNR = decltype(unr)::value;
+    if (full)
+      router_logits_kernel<TE, TN, UNR, true><<<grid, 256, 0, st>>>(x, w, w_extra, bias, n, d, e,
+                                                                   n_w, out);
+    else
+      router_logits_kernel<TE, TN, UNR, false><<<grid, 256, 0, st>>>(x, w, w_extra, bias, n, d,
+                                                                    e, n_w, out);
+  };
+  using I1 = std::integral_constant<int, 1>;
+  using I4 = std::integral_constant<int, 4>;
+  using I8 = std::integral_constant<int, 8>;
   if (n >= 32) {
-    constexpr int TE = 4, TN = 8;
-    dim3 grid((e + kRouterWaves * TE - 1) / (kRouterWaves * TE), (n + TN - 1) / TN);
-    router_logits_kernel<TE, TN><<<grid, 256, 0, st>>>(x, w, w_extra, bias, n, d, e, n_w, out);
+    // one pass per group: the 4 x 8 tile's 12 loads a pass keep three waves
+    // per SIMD; staging 4 passes (256 registers, one wave) took 64 -> 139 us
+    // at 2048 tokens
+    dim3 grid((e + kRouterWaves * 4 - 1) / (kRouterWaves * 4), (n + 8 - 1) / 8);
+    launch(I4{}, I8{}, I1{}, grid);
   } else if (n >= 4) {
-    constexpr int TE = 1, TN = 4;
-    dim3 grid((e + kRouterWaves * TE - 1) / (kRouterWaves * TE), (n + TN - 1) / TN);
-    router_logits_kernel<TE, TN><<<grid, 256, 0, st>>>(x, w, w_extra, bias, n, d, e, n_w, out);
+    dim3 grid((e + kRouterWaves - 1) / kRouterWaves, (n + 4 - 1) / 4);
+    launch(I1{}, I4{}, I8{}, grid);
   } else {
-    constexpr int TE = 1, TN = 1;
-    dim3 grid((e + kRouterWaves * TE - 1) / (kRouterWaves * TE), n);
-    router_logits_kernel<TE, TN><<<grid, 256, 0, st>>>(x, w, w_extra, bias, n, d, e, n_w, out);
+    dim3 grid((e + kRouterWaves - 1) / kRouterWaves, n);
+    launch(I1{}, I1{}, I8{}, grid);
   }
   PMOE_LAUNCH_CHECK("router_logits_kernel");
   return PMOE_OK;
