@@ -217,26 +217,44 @@ __device__ __forceinline__ void fma8(float& acc, const uint4& a, const uint4& b)
 // together (one memory round trip for hidden <= 4096).  Every lane returns
 // the logit.
 // Dot of one router row with one token row over d columns, in the router's
-// fixed lane order.
-__device__ float router_row_dot(const uint16_t* wrow, const uint16_t* xrow, int d) {
+// fixed lane order, 8 passes of 512 columns a group.  A group's loads are
+// unconditional (passes and columns past the end re-read in-bounds data)
+// and only the FMAs are guarded: with a guarded branch per pass, the
+// compiler waited for the first passes' loads before issuing the later
+// ones.
+struct RouterGroup {
+  uint4 w[8], x[8];
+};
+
+__device__ __forceinline__ void router_group_load(RouterGroup& g, const uint16_t* wrow,
+                                                  const uint16_t* xrow, int d, int p0) {
   const int lane = threadIdx.x & 63;
   const int passes = (d + 511) / 512;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int col = min(min(p0 + j, passes - 1) * 512 + lane * 8, d - 8);
+    g.w[j] = *reinterpret_cast<const uint4*>(wrow + col);
+    g.x[j] = *reinterpret_cast<const uint4*>(xrow + col);
+  }
+}
+
+__device__ __forceinline__ void router_group_fma(float& acc, const RouterGroup& g, int d,
+                                                 int p0) {
+  const int lane = threadIdx.x & 63;
+  const int passes = (d + 511) / 512;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int col = (p0 + j) * 512 + lane * 8;
+    if (p0 + j < passes && col < d) fma8(acc, g.x[j], g.w[j]);
+  }
+}
+
+__device__ float router_row_dot(const uint16_t* wrow, const uint16_t* xrow, int d) {
   float acc = 0.0f;
-  for (int p0 = 0; p0 < passes; p0 += 8) {
-    uint4 wv[8], xv[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int col = (p0 + j) * 512 + lane * 8;
-      if (p0 + j < passes && col < d) {
-        wv[j] = *reinterpret_cast<const uint4*>(wrow + col);
-        xv[j] = *reinterpret_cast<const uint4*>(xrow + col);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int col = (p0 + j) * 512 + lane * 8;
-      if (p0 + j < passes && col < d) fma8(acc, xv[j], wv[j]);
-    }
+  for (int p0 = 0; p0 < (d + 511) / 512; p0 += 8) {
+    RouterGroup g;
+    router_group_load(g, wrow, xrow, d, p0);
+    router_group_fma(acc, g, d, p0);
   }
   return wave_sum_bfly(acc);
 }
@@ -621,14 +639,22 @@ __global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(
     g_trace[blockIdx.x * 32 + 25] = __builtin_amdgcn_s_memrealtime();
   }
 #endif
-  // the launch counter and the slot table are requested first; their
-  // values are used after the router, so their round trips overlap it
+  // The slot table, the first group of this block's router row and the
+  // launch counter are requested at once; their values are used after the
+  // router's FMAs, so their round trips overlap.  The row's loads go before
+  // the counter's atomic (sched_barrier keeps that order): issued after it,
+  // the compiler reused the atomic's return register for a row address and
+  // waited for the atomic first.
+  const int32_t tab = int(threadIdx.x) < n_experts ? table_p[threadIdx.x] : -1;
+  RouterGroup rg0;
+  if (wave == 0 && int(blockIdx.x) < n_experts)
+    router_group_load(rg0, gate_p + size_t(blockIdx.x) * d, x_p, d, 0);
+  __builtin_amdgcn_sched_barrier(0);
   uint32_t old = 0;
   if (threadIdx.x == 0)
     old = __hip_atomic_fetch_add(
         reinterpret_cast<uint32_t*>(hdr + kXcdCounterOffset + xcd * kDecodeFlagStride), 1u,
         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const int32_t tab = int(threadIdx.x) < n_experts ? table_p[threadIdx.x] : -1;
 
   // A: logit e by wave 0 of block e.  (Vector loads and stores share one
   // counter, so a wave that waits for a load also waits for the device-scope
@@ -636,16 +662,37 @@ __global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(
   // store, and waves 2-3, which store nothing, poll the logits.)
   trace_mark(sy, 0);
   if (wave == 0) {
-    const uint32_t my_tag = __builtin_amdgcn_readfirstlane(old) / uint32_t(per_xcd) + 1u;
-    if (int(threadIdx.x) < n_experts) s_table[threadIdx.x] = tab;
+    // The table goes to LDS after the dot product (its load is older than
+    // the row's, so it has arrived) and before the logit store (waiting for
+    // it after the store would also wait for the store's acknowledgement).
+    bool table_done = false;
     for (int e = blockIdx.x; e < n_experts; e += a.n_blocks) {
-      const float sum = router_row_dot(gate_p + size_t(e) * d, x_p, d);
+      float acc = 0.0f;
+      for (int p0 = 0; p0 < (d + 511) / 512; p0 += 8) {
+        RouterGroup g;
+        if (e == int(blockIdx.x) && p0 == 0)
+          g = rg0;
+        else
+          router_group_load(g, gate_p + size_t(e) * d, x_p, d, p0);
+        router_group_fma(acc, g, d, p0);
+      }
+      const float sum = wave_sum_bfly(acc);
       const float v = bias_p ? sum + bias_p[e] : sum;
+      if (!table_done && int(threadIdx.x) < n_experts) s_table[threadIdx.x] = tab;
+      table_done = true;
+      // a zero computed from the dot product keeps the counter's use (and
+      // the wait for it) after the router loads; loop-invariant code
+      // motion would hoist it before them
+      uint32_t zero;
+      asm volatile("v_mov_b32 %0, 0" : "=v"(zero) : "v"(v));
+      const uint32_t my_tag =
+          __builtin_amdgcn_readfirstlane(old + zero) / uint32_t(per_xcd) + 1u;
       if (lane == 0)
         __hip_atomic_store(&lgx[e], (uint64_t(my_tag) << 32) | __float_as_uint(v),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (lane == 0) s_tag = my_tag;
+    if (!table_done && int(threadIdx.x) < n_experts) s_table[threadIdx.x] = tab;
+    if (lane == 0) s_tag = __builtin_amdgcn_readfirstlane(old) / uint32_t(per_xcd) + 1u;
   } else if (int(threadIdx.x) < n_experts) {
     s_table[threadIdx.x] = tab;
   }
