@@ -78,12 +78,13 @@ def build_layers(g, spec, n_layers, device, seed=0):
 
 
 # kernel -> the sources its code comes from (the traffic profile is valid
-# only for the build of these files it was measured on)
+# only for the build of these files it was measured on; the Makefile holds
+# per-file compiler flags)
 KERNEL_SOURCES = {
     "decode_fused_kernel": ["decode_fused.hip", "gemv_common.h", "route_common.h",
-                            "pmoe_internal.h", "pmoe_kernels.h"],
+                            "pmoe_internal.h", "pmoe_kernels.h", "Makefile"],
     "decode_xcd_kernel": ["decode_fused.hip", "gemv_common.h", "route_common.h",
-                          "pmoe_internal.h", "pmoe_kernels.h"],
+                          "pmoe_internal.h", "pmoe_kernels.h", "Makefile"],
     "gateup_routed_kernel": ["decode.hip", "gemv_common.h", "route_common.h",
                              "pmoe_internal.h", "pmoe_kernels.h"],
     "prefill": ["prefill.hip", "dispatch.hip", "moe.hip", "pmoe_internal.h", "pmoe_kernels.h"],
