@@ -106,8 +106,7 @@ gateup_routed_kernel(const GemvArgs a, const RouteDev rt, int32_t* inds_out, flo
     const bool publish = blockIdx.x == 0 && blockIdx.y == 0;
     route_block<EPL, 4>(rt, L, W, publish ? inds_out : nullptr, w_out);
     if (publish)
-      publish_route(L, rt.n * rt.kk, rt.e + (rt.kk > rt.k ? 1 : 0), rec, a.table, a.n_experts,
-                    a.shared_slot);
+      publish_route(L, rt.n * rt.kk, rec, a.table, a.n_experts, a.shared_slot);
     if (u >= L.n_active) return;
     e = L.active[u];
     slot = e < a.n_experts ? a.table[e] : a.shared_slot;
@@ -146,8 +145,7 @@ __global__ __launch_bounds__(64 * route_record_waves<EPL>()) void route_record_k
   __shared__ RouteLds L;
   __shared__ WaveTmp W[NW];
   route_block<EPL, NW>(rt, L, W, inds_out, w_out);
-  publish_route(L, rt.n * rt.kk, rt.e + (rt.kk > rt.k ? 1 : 0), rec, table, n_experts,
-                shared_slot);
+  publish_route(L, rt.n * rt.kk, rec, table, n_experts, shared_slot);
 }
 
 // Decode down projection + weighted combine, routing recomputed in the

@@ -392,7 +392,8 @@ __device__ __forceinline__ void route_rank1_weights(const RouteDev& r, const flo
 }
 
 // Routing record in global memory: what block (0, 0) of the gate/up launch
-// publishes for the down launch (same layout as the LDS copy).
+// (or the routing launch) publishes for the later launches: the LDS copy's
+// rows, and its active list with the shared expert moved to the front.
 // It also holds the slab slot of every active expert (slot[u] for
 // active[u]), so a per-expert block of the later launches finds its weights
 // without a dependent slot-table read.
@@ -405,19 +406,26 @@ struct RouteRecord {
 };
 
 // table: expert id -> slot (-1: absent); id n_experts is the shared expert.
-__device__ __forceinline__ void publish_route(const RouteLds& L, int rows, int n_ids,
-                                              RouteRecord* g, const int32_t* table,
-                                              int n_experts, int shared_slot) {
+// The record lists the shared expert (last in L.active) first: its blocks
+// carry a row of every token, the longest work of a per-expert launch, and
+// the dispatcher starts blocks in blockIdx.y order, so they start first
+// instead of running alone at the end.  The routed experts follow in
+// ascending id order.
+__device__ __forceinline__ void publish_route(const RouteLds& L, int rows, RouteRecord* g,
+                                              const int32_t* table, int n_experts,
+                                              int shared_slot) {
   for (int i = threadIdx.x; i < rows; i += blockDim.x) {
     g->ids[i] = L.ids[i];
     g->w[i] = L.w[i];
   }
-  for (int i = threadIdx.x; i < n_ids; i += blockDim.x) g->active[i] = L.active[i];
-  for (int u = threadIdx.x; u < L.n_active; u += blockDim.x) {
-    const int e = L.active[u];
+  const int na = L.n_active;
+  const int rot = na > 0 && L.active[na - 1] >= n_experts ? na - 1 : 0;
+  for (int u = threadIdx.x; u < na; u += blockDim.x) {
+    const int e = L.active[u + rot < na ? u + rot : u + rot - na];
+    g->active[u] = e;
     g->slot[u] = e < n_experts ? table[e] : shared_slot;
   }
-  if (threadIdx.x == 0) g->n_active = L.n_active;
+  if (threadIdx.x == 0) g->n_active = na;
 }
 
 // What a block working on the u-th active expert needs from the record, in
