@@ -104,40 +104,74 @@ struct Pick {
   float x;  // payload carried along
 };
 
+// Compare-exchange: a ends up the larger (DESC) or the smaller key, the
+// payloads following their keys.
+template <bool PAYLOAD>
+__device__ __forceinline__ void key_cas(uint64_t& a, uint64_t& b, float& pa, float& pb,
+                                        bool desc) {
+  const bool sw = desc ? (b > a) : (a > b);
+  const uint64_t ka = a;
+  a = sw ? b : a;
+  b = sw ? ka : b;
+  if (PAYLOAD) {
+    const float qa = pa;
+    pa = sw ? pb : pa;
+    pb = sw ? qa : pb;
+  }
+}
+
+// Bitonic sort of a lane's N keys (N a power of two), largest first;
+// every index is static, so the keys stay in registers.
+template <int N, bool PAYLOAD>
+__device__ __forceinline__ void sort_keys_desc(uint64_t (&key)[N], float (&pay)[N]) {
+#pragma unroll
+  for (int size = 2; size <= N; size <<= 1)
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1)
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int j = i ^ stride;
+        if (j > i) key_cas<PAYLOAD>(key[i], key[j], pay[i], pay[j], (i & size) == 0);
+      }
+}
+
 // Top-k of per-lane values v[i] (id lane + 64*i, valid when id < n_valid,
-// k <= n_valid): k rounds of a wave-wide maximum of the 64-bit keys
-// order_key(v) << 32 | ~id, so the maximum is the largest value and, among
-// equal values, the lowest id, and it names its own id and value (no search
-// for the holder; invalid and taken entries hold key 0, below every valid
-// key).  Lane j (< k) returns pick j; picks come out sorted by (value desc,
-// id asc), and extra[i] of each pick is carried along when PAYLOAD.
-// Registers and scalar ops only.
+// k <= n_valid), by 64-bit keys order_key(v) << 32 | ~id: the larger value
+// first and, among equal values, the lower id (invalid entries hold key 0,
+// below every valid key).  Each lane sorts its keys once, largest first;
+// then k rounds each take the wave-wide maximum of the lanes' first keys,
+// which names its own id and value, and the lane that held it drops it
+// (shifts its list).  Lane j (< k) returns pick j; picks come out sorted by
+// (value desc, id asc), and extra[i] of each pick is carried along when
+// PAYLOAD.  Registers and scalar ops only.
 template <int EPL, bool PAYLOAD = true>
 __device__ __forceinline__ Pick wave_topk(const float (&v)[EPL], int n_valid, int k,
                                           const float (&extra)[EPL]) {
   const int lane = threadIdx.x & 63;
   uint64_t key[EPL];
+  float pay[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     const int id = lane + 64 * i;
     key[i] = id < n_valid ? (uint64_t(order_key(v[i])) << 32) | uint32_t(~uint32_t(id)) : 0;
+    pay[i] = PAYLOAD ? extra[i] : 0.0f;
   }
+  sort_keys_desc<EPL, PAYLOAD>(key, pay);
   Pick pk{0.0f, 0, 0.0f};
   for (int j = 0; j < k; ++j) {
-    uint64_t best = 0;
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) best = max(best, key[i]);
-    const uint64_t top = wave_max_key64(best);
+    const uint64_t top = wave_max_key64(key[0]);
     const int sel = int(~uint32_t(top));
-    const int sl = sel & 63, si = sel >> 6;
+    const int sl = sel & 63;
     const float pv = key_value(uint32_t(top >> 32));
-    float px = 0.0f;
+    const float px =
+        PAYLOAD ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pay[0]), sl)) : 0.0f;
+    if (lane == sl) {
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      if (i == si) {
-        if (PAYLOAD) px = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(extra[i]), sl));
-        if (lane == sl) key[i] = 0;
+      for (int i = 0; i + 1 < EPL; ++i) {
+        key[i] = key[i + 1];
+        if (PAYLOAD) pay[i] = pay[i + 1];
       }
+      key[EPL - 1] = 0;
     }
     if (lane == j) pk = Pick{pv, sel, px};
   }
@@ -209,9 +243,7 @@ __device__ void route_token(const RouteDev& r, int t, RouteLds& L, WaveTmp& W, i
     wave_lds_sync();
     if (r.n_group > 1) {
       const int gs = e / r.n_group;
-      float gscore[EPL];
-#pragma unroll
-      for (int i = 0; i < EPL; ++i) gscore[i] = 0.0f;
+      float gscore[1] = {0.0f}, gnone[1] = {0.0f};  // group `lane` (n_group <= 64)
       if (lane < r.n_group) {
         float t1 = -__builtin_inff(), t2 = -__builtin_inff();
         for (int j = 0; j < gs; ++j) {
@@ -225,7 +257,7 @@ __device__ void route_token(const RouteDev& r, int t, RouteLds& L, WaveTmp& W, i
         }
         gscore[0] = t1 + t2;
       }
-      const Pick gp = wave_topk<EPL, false>(gscore, r.n_group, r.topk_group, x);
+      const Pick gp = wave_topk<1, false>(gscore, r.n_group, r.topk_group, gnone);
       uint64_t keep = 0;
       for (int j = 0; j < r.topk_group; ++j) keep |= 1ull << __builtin_amdgcn_readlane(gp.i, j);
 #pragma unroll
