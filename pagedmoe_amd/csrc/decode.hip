@@ -12,10 +12,13 @@
 // pairs, v_dot2_f32_bf16, xor-butterfly row sums) is in gemv_common.h.  The
 // gate/up launch (DUAL) computes both projections of a row together and
 // writes h = silu(g)*u as bf16.
+#include <type_traits>
+
 #include "gemv_common.h"
 #include "pmoe_internal.h"
 #include "pmoe_kernels.h"
 #include "route_common.h"
+#include "router_tile.h"
 
 namespace pmoe {
 
@@ -129,23 +132,53 @@ gateup_routed_kernel(const GemvArgs a, const RouteDev rt, int32_t* inds_out, flo
   gemv_expert<UB, LPR, GPL, R, true>(a, slot, s_m, s_rows, wrow0, act_row, store);
 }
 
-// Routing of several tokens at once (one wave per token, 16 waves; 8 with
-// more than 8 logits per lane, whose arrays need 256 registers a wave),
-// written to the record and the routing outputs.
-template <int EPL>
-constexpr int route_record_waves() {
-  return EPL > 8 ? 8 : 16;
-}
+// Router launch of a decode call of several tokens whose last block also
+// routes: every block stores its logits at device scope and then arrives at
+// a counter; the block that arrives last (every logit visible) routes the
+// tokens with its 8 waves (one token per wave per round; route_block, logits
+// read at device scope), publishes the routing record (shared expert first)
+// and the routing outputs, and resets the counter for the next launch.  No
+// block waits for another, and the per-expert launches after it find the
+// record ready.  Every block copies the slot table into LDS while its logits
+// load, so the last one's record needs no further dependent read.
+constexpr int kTailWaves = 8;
 
-template <int EPL>
-__global__ __launch_bounds__(64 * route_record_waves<EPL>()) void route_record_kernel(
-    const RouteDev rt, int32_t* inds_out, float* w_out, RouteRecord* rec, const int32_t* table,
-    int n_experts, int shared_slot) {
-  constexpr int NW = route_record_waves<EPL>();
+struct RouteTail {
+  RouteDev rt;
+  RouteRecord* rec;
+  const int32_t* table;
+  int n_experts, shared_slot;
+  int32_t* inds_out;
+  float* w_out;
+  uint32_t* arrive;  // zero between launches
+};
+
+template <int TE, int TN, int UNR, bool FULL, int EPL>
+__global__ __launch_bounds__(64 * kTailWaves) void router_route_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    const uint16_t* __restrict__ w_extra, const float* __restrict__ bias, int n, int d, int e,
+    int n_w, float* __restrict__ out, const RouteTail t) {
   __shared__ RouteLds L;
-  __shared__ WaveTmp W[NW];
-  route_block<EPL, NW>(rt, L, W, inds_out, w_out);
-  publish_route(L, rt.n * rt.kk, rec, table, n_experts, shared_slot);
+  __shared__ WaveTmp W[kTailWaves];
+  __shared__ int32_t s_table[kRouteMaxIds];
+  __shared__ int s_last;
+  for (int i = threadIdx.x; i < t.n_experts; i += 64 * kTailWaves) s_table[i] = t.table[i];
+  const int e0 = (blockIdx.x * kTailWaves + int(threadIdx.x >> 6)) * TE;
+  if (e0 < e)
+    router_tile<TE, TN, UNR, FULL, true>(x, w, w_extra, bias, n, d, e, n_w, out, e0,
+                                         blockIdx.y * TN);
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's logits have reached device scope
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t total = gridDim.x * gridDim.y;
+    s_last = __hip_atomic_fetch_add(t.arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             total - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  if (threadIdx.x == 0) __hip_atomic_store(t.arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  route_block<EPL, kTailWaves, true>(t.rt, L, W, t.inds_out, t.w_out);
+  publish_route(L, t.rt.n * t.rt.kk, t.rec, s_table, t.n_experts, t.shared_slot);
 }
 
 // Decode down projection + weighted combine, routing recomputed in the
@@ -292,25 +325,20 @@ int launch_qgemv(const GemvArgs& a, Shape sh, int max_experts, hipStream_t st) {
   return fail(PMOE_EINVAL, "qgemv: unsupported row shape");
 }
 
+// One token: every block routes it itself.  Several: the router launch
+// (router_route_kernel) has published the record.
 template <int UB, int EPL, int L, int G>
 int launch_gateup_routed(const GemvArgs& gu, const RouteDev& rt, int max_experts,
                          int32_t* inds_out, float* w_out, RouteRecord* rec, hipStream_t st) {
   constexpr int R = rows_r<UB, G, true>();
   constexpr int rows = 4 * R * (64 / L);
   dim3 grid((gu.rows_out + rows - 1) / rows, max_experts);
-  if (rt.n == 1) {
+  if (rt.n == 1)
     gateup_routed_kernel<UB, L, G, R, EPL, false><<<grid, 256, 0, st>>>(gu, rt, inds_out, w_out,
                                                                         rec);
-  } else {
-    {
-      ProfScope prof_scope(K_ROUTE_SELECT, st);
-      route_record_kernel<EPL><<<1, 64 * route_record_waves<EPL>(), 0, st>>>(
-          rt, inds_out, w_out, rec, gu.table, gu.n_experts, gu.shared_slot);
-      PMOE_LAUNCH_CHECK("route_record_kernel");
-    }
+  else
     gateup_routed_kernel<UB, L, G, R, EPL, true><<<grid, 256, 0, st>>>(gu, rt, inds_out, w_out,
                                                                        rec);
-  }
   PMOE_LAUNCH_CHECK("gateup_routed_kernel");
   return PMOE_OK;
 }
@@ -340,6 +368,38 @@ int launch_down_routed(const GemvArgs& dn, const RouteDev& rt, int max_experts, 
   dim3 grid((dn.rows_out + T - 1) / T);
   down_routed_kernel<UB, L, G, R, EPL><<<grid, 256, lds, st>>>(dn, rt, out, rec);
   PMOE_LAUNCH_CHECK("down_routed_kernel");
+  return PMOE_OK;
+}
+
+// The router launch of a decode call: plain logits for one token, logits
+// plus routing (router_route_kernel) for several.
+template <int EPL>
+int launch_router(const RouterIn& ri, const RouteDev& rt, RouteRecord* rec, const GemvArgs& gu,
+                  int32_t* inds_out, float* w_out, hipStream_t st) {
+  if (rt.n == 1)
+    return router_logits_ext(ri.x, ri.w, ri.w_extra, ri.bias, rt.n, ri.d, rt.e, ri.out, st);
+  PMOE_REQUIRE(ri.x && ri.w && ri.out && ri.arrive, "decode: null router input");
+  PMOE_REQUIRE(ri.d % 8 == 0, "router_logits: hidden must be a multiple of 8");
+  const int n = rt.n, n_w = rt.e;
+  const int e = n_w + (ri.w_extra ? 1 : 0);
+  RouteTail t{rt, rec, gu.table, gu.n_experts, gu.shared_slot, inds_out, w_out, ri.arrive};
+  const bool full = ri.d % 512 == 0;
+  ProfScope prof_scope(K_ROUTER_LOGITS, st);
+  auto go = [&](auto tn, dim3 grid) {
+    constexpr int TN = decltype(tn)::value;
+    if (full)
+      router_route_kernel<1, TN, 8, true, EPL><<<grid, 64 * kTailWaves, 0, st>>>(
+          ri.x, ri.w, ri.w_extra, ri.bias, n, ri.d, e, n_w, ri.out, t);
+    else
+      router_route_kernel<1, TN, 8, false, EPL><<<grid, 64 * kTailWaves, 0, st>>>(
+          ri.x, ri.w, ri.w_extra, ri.bias, n, ri.d, e, n_w, ri.out, t);
+  };
+  const int gx = (e + kTailWaves - 1) / kTailWaves;
+  if (n >= 4)
+    go(std::integral_constant<int, 4>{}, dim3(gx, (n + 3) / 4));
+  else
+    go(std::integral_constant<int, 1>{}, dim3(gx, n));
+  PMOE_LAUNCH_CHECK("router_route_kernel");
   return PMOE_OK;
 }
 
@@ -402,7 +462,7 @@ int qgemv(const GemvArgs& a, int bits, bool dual, int max_experts, int, hipStrea
 // gu.out (h), then down + combine into out [n, hidden].
 int decode_routed(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int bits,
                   int32_t* inds_out, float* w_out, uint16_t* out, void* record,
-                  hipStream_t st) {
+                  const RouterIn& ri, hipStream_t st) {
   PMOE_REQUIRE(record != nullptr, "decode: null routing record");
   RouteRecord* rec = static_cast<RouteRecord*>(record);
   PMOE_REQUIRE(rt.n >= 1 && rt.n * rt.kk <= kRouteMaxRows, "decode: too many rows");
@@ -419,11 +479,13 @@ int decode_routed(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, in
   const int n_ids = rt.e + (rt.kk > rt.k ? 1 : 0);
   const int max_experts = rows < n_ids ? rows : n_ids;
   const int epl = (rt.e + 63) / 64;
+  PMOE_REQUIRE(bits == 4 || bits == 6, "decode: bits must be 4 or 6");
 #define PMOE_EPL(EP)                                                                     \
   if (epl <= EP) {                                                                       \
+    const int rr = launch_router<EP>(ri, rt, rec, gu, inds_out, w_out, st);              \
+    if (rr) return rr;                                                                   \
     if (bits == 4) return launch_routed<4, EP>(gu, dn, rt, max_experts, inds_out, w_out, out, rec, st); \
-    if (bits == 6) return launch_routed<6, EP>(gu, dn, rt, max_experts, inds_out, w_out, out, rec, st); \
-    return fail(PMOE_EINVAL, "decode: bits must be 4 or 6");                            \
+    return launch_routed<6, EP>(gu, dn, rt, max_experts, inds_out, w_out, out, rec, st); \
   }
   PMOE_EPL(2)
   PMOE_EPL(4)

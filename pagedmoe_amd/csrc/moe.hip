@@ -262,8 +262,10 @@ bool fused_enabled(int n) {
 }
 
 // Decode block path: the fused one-launch layer (decode_fused.hip) when it
-// covers the shape, else logits (+ shared gate column), then gate/up and
-// down+combine, each recomputing the routing in its prologue.
+// covers the shape, else the router launch (logits + shared gate column;
+// with several tokens its last block also routes and publishes the record),
+// then gate/up and down+combine (one token: each block recomputes the
+// routing in its prologue).
 int decode_block(const pmoe_geom* g, const pmoe_route_cfg* rc, const uint8_t* slab,
                  const int32_t* table, const uint16_t* gate_w, const float* score_bias,
                  const float* logit_bias, const uint16_t* x, int n, int shared_slot,
@@ -273,7 +275,6 @@ int decode_block(const pmoe_geom* g, const pmoe_route_cfg* rc, const uint8_t* sl
   const int shared = shared_slot >= 0 ? 1 : 0;
   const int kk = k + shared;
   const uint16_t* extra = (shared && shared_gate) ? shared_gate : nullptr;
-  int r = PMOE_OK;
   RouteDev rt{};
   rt.logits = w.logits;
   rt.ld = e + (extra ? 1 : 0);
@@ -318,10 +319,11 @@ int decode_block(const pmoe_geom* g, const pmoe_route_cfg* rc, const uint8_t* sl
                                 out, w.sync, st);
     if (r2 != kDecodeFusedDeclined) return r2;
   }
-  r = router_logits_ext(x, gate_w, extra, logit_bias, n, g->hidden, e, w.logits, st);
-  if (r) return r;
   dn.out = w.y;  // fp32 per-slot outputs when the down runs expert-split
-  return decode_routed(gu, dn, rt, g->bits, inds_out, w_out, out, w.record, st);
+  const RouterIn ri{x, gate_w, extra, logit_bias, g->hidden, w.logits,
+                    reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(w.sync) +
+                                                kRouteArriveOffset)};
+  return decode_routed(gu, dn, rt, g->bits, inds_out, w_out, out, w.record, ri, st);
 }
 
 int experts_and_combine(const pmoe_geom* g, const uint8_t* slab, const int32_t* table,

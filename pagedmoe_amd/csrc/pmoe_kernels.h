@@ -64,13 +64,28 @@ struct RouteDev;
 
 int qgemv(const GemvArgs& a, int bits, bool dual, int max_experts, int max_rows_per_expert,
           hipStream_t st);
-// Decode experts with routing recomputed per block (decode.hip).
-// record: scratch for the routing handed from gate/up to down
-// (decode_record_bytes()).  dn.out: fp32 [n*kk, hidden] scratch for the
-// expert-split down (many active experts), or null for the tile-major down
-// only.
+// Router inputs of a decode call (as router_logits_ext takes them; logits
+// into out) and the counter the router blocks of a several-token call
+// arrive at (kRouteArriveOffset in the workspace header; zero between calls).
+struct RouterIn {
+  const uint16_t* x;
+  const uint16_t* w;
+  const uint16_t* w_extra;
+  const float* bias;
+  int d;
+  float* out;
+  uint32_t* arrive;
+};
+
+// Decode experts (decode.hip): the router launch (which also routes when
+// there are several tokens), gate/up, down.  One token: every block
+// recomputes the routing.  record: scratch for the routing handed to the
+// later launches (decode_record_bytes()).  dn.out: fp32 [n*kk, hidden]
+// scratch for the expert-split down (many active experts), or null for the
+// tile-major down only.
 int decode_routed(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int bits,
-                  int32_t* inds_out, float* w_out, uint16_t* out, void* record, hipStream_t st);
+                  int32_t* inds_out, float* w_out, uint16_t* out, void* record,
+                  const RouterIn& ri, hipStream_t st);
 size_t decode_record_bytes();
 
 // Grid-barrier state of the fused decode launch: the first kDecodeSyncBytes
@@ -85,6 +100,9 @@ struct DecodeSync {
   uint32_t epoch;      // launches completed on this workspace
   uint32_t error;      // sticky: bit 0 = a barrier or data wait timed out
 };
+// Router blocks of a several-token decode call arrive here (decode.hip
+// router_route_kernel; its own 128-byte line; the last arriver resets it).
+constexpr size_t kRouteArriveOffset = 128;
 constexpr int kDecodeMaxBlocks = 512;
 constexpr int kDecodeGroup = 16;  // blocks per arrival group
 constexpr int kDecodeMaxGroups = kDecodeMaxBlocks / kDecodeGroup;

@@ -72,28 +72,21 @@ __device__ __forceinline__ float key_value(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
-template <int D>
-__device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
-  const uint32_t lo = __float_as_uint(xor_lane<D>(__uint_as_float(uint32_t(v))));
-  const uint32_t hi = __float_as_uint(xor_lane<D>(__uint_as_float(uint32_t(v >> 32))));
-  return (uint64_t(hi) << 32) | lo;
+// Maximum of v over the wave (all 64 lanes active), wave-uniform: DPP
+// maxima within each row of 16 lanes (quad swaps, half-row and row
+// mirrors), then the four row maxima by readlane.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+  return uint32_t(__builtin_amdgcn_update_dpp(0, int(x), CTRL, 0xF, 0xF, false));
 }
 
-__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
-  const uint32_t lo = __builtin_amdgcn_readlane(uint32_t(v), l);
-  const uint32_t hi = __builtin_amdgcn_readlane(uint32_t(v >> 32), l);
-  return (uint64_t(hi) << 32) | lo;
-}
-
-// Maximum of a 64-bit key over the wave, wave-uniform: xor exchanges within
-// each row of 16 lanes, then the four row maxima by readlane.
-__device__ __forceinline__ uint64_t wave_max_key64(uint64_t v) {
-  v = max(v, xor_lane64<1>(v));
-  v = max(v, xor_lane64<2>(v));
-  v = max(v, xor_lane64<4>(v));
-  v = max(v, xor_lane64<8>(v));
-  const uint64_t r0 = readlane64(v, 0), r1 = readlane64(v, 16);
-  const uint64_t r2 = readlane64(v, 32), r3 = readlane64(v, 48);
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = max(v, dpp_u32<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = max(v, dpp_u32<0x141>(v));  // row_half_mirror
+  v = max(v, dpp_u32<0x140>(v));  // row_mirror
+  const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
   return max(max(r0, r1), max(r2, r3));
 }
 
@@ -136,14 +129,16 @@ __device__ __forceinline__ void sort_keys_desc(uint64_t (&key)[N], float (&pay)[
 }
 
 // Top-k of per-lane values v[i] (id lane + 64*i, valid when id < n_valid,
-// k <= n_valid), by 64-bit keys order_key(v) << 32 | ~id: the larger value
-// first and, among equal values, the lower id (invalid entries hold key 0,
-// below every valid key).  Each lane sorts its keys once, largest first;
-// then k rounds each take the wave-wide maximum of the lanes' first keys,
-// which names its own id and value, and the lane that held it drops it
-// (shifts its list).  Lane j (< k) returns pick j; picks come out sorted by
-// (value desc, id asc), and extra[i] of each pick is carried along when
-// PAYLOAD.  Registers and scalar ops only.
+// k <= n_valid), in the order of the 64-bit keys order_key(v) << 32 | ~id:
+// the larger value first and, among equal values, the lower id (invalid
+// entries hold key 0, below every valid key).  Each lane sorts its keys
+// once, largest first.  A round takes the wave maximum of the lanes' first
+// values (32-bit); when one lane holds it, that lane's first key is the
+// pick, else the lowest id among the lanes holding it (a second 32-bit
+// maximum, of ~id); the lane that held the pick drops it (shifts its
+// list).  Lane j (< k) returns pick j; picks come out sorted by (value
+// desc, id asc), and extra[i] of each pick is carried along when PAYLOAD.
+// Registers and scalar ops only.
 template <int EPL, bool PAYLOAD = true>
 __device__ __forceinline__ Pick wave_topk(const float (&v)[EPL], int n_valid, int k,
                                           const float (&extra)[EPL]) {
@@ -159,10 +154,15 @@ __device__ __forceinline__ Pick wave_topk(const float (&v)[EPL], int n_valid, in
   sort_keys_desc<EPL, PAYLOAD>(key, pay);
   Pick pk{0.0f, 0, 0.0f};
   for (int j = 0; j < k; ++j) {
-    const uint64_t top = wave_max_key64(key[0]);
-    const int sel = int(~uint32_t(top));
+    const uint32_t hv = uint32_t(key[0] >> 32), hl = uint32_t(key[0]);
+    const uint32_t top = wave_max_u32(hv);
+    const uint64_t at = wave_ballot(hv == top);
+    const uint32_t lo = __popcll(at) == 1
+                            ? __builtin_amdgcn_readlane(hl, __builtin_ctzll(at))
+                            : wave_max_u32(hv == top ? hl : 0u);
+    const int sel = int(~lo);
     const int sl = sel & 63;
-    const float pv = key_value(uint32_t(top >> 32));
+    const float pv = key_value(top);
     const float px =
         PAYLOAD ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pay[0]), sl)) : 0.0f;
     if (lane == sl) {
@@ -206,6 +206,10 @@ __device__ void route_token(const RouteDev& r, int t, RouteLds& L, WaveTmp& W, i
     v[i] = ei < e ? load_logit<COHERENT>(row + ei) : 0.0f;
     x[i] = 0.0f;
   }
+  // the shared gate's logit, requested with the routed ones (loaded after
+  // the top-k it would be a second round trip)
+  const bool sg = r.kk > k && r.shared_gate;
+  const float sg_logit = sg ? load_logit<COHERENT>(row + e) : 0.0f;
   float wk = 0.0f;
   int ik = 0;
   if (r.scoring == PMOE_SCORE_SOFTMAX) {
@@ -286,7 +290,7 @@ __device__ void route_token(const RouteDev& r, int t, RouteLds& L, WaveTmp& W, i
   }
   if (r.kk > k && lane == 0) {
     L.ids[t * r.kk + k] = e;  // shared expert column
-    L.w[t * r.kk + k] = r.shared_gate ? psigmoid(load_logit<COHERENT>(row + e)) : 1.0f;
+    L.w[t * r.kk + k] = sg ? psigmoid(sg_logit) : 1.0f;
   }
 }
 

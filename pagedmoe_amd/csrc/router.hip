@@ -6,100 +6,33 @@
 // sigmoid + correction bias + grouped top-k + routed scaling (consumed
 // streaming.py:2424-2442).
 //
-// Summation order of a logit (shared with the CPU oracle, bit for bit):
-// element d = 512*t + 8*l + j is owned by lane l; each lane runs
-// acc = fma(x_d, w_d, acc) for t ascending, j ascending (one 16-byte load of
-// x and of w per t); the 64 lane partials are combined by an xor butterfly.
+// Summation order of a logit (shared with the CPU oracle, bit for bit): see
+// router_tile.h.
 #include <type_traits>
 
 #include "pmoe_internal.h"
 #include "pmoe_kernels.h"
+#include "router_tile.h"
 
 namespace pmoe {
 
 namespace {
 
-constexpr int kRouterWaves = 4;
 constexpr int kMaxEPL = 16;    // experts per lane in the select kernels (E <= 1024)
 constexpr int kMaxK = 16;
 
-__device__ __forceinline__ void fma8(float& acc, const uint4& a, const uint4& b) {
-  acc = __builtin_fmaf(bf16lo(a.x), bf16lo(b.x), acc);
-  acc = __builtin_fmaf(bf16hi(a.x), bf16hi(b.x), acc);
-  acc = __builtin_fmaf(bf16lo(a.y), bf16lo(b.y), acc);
-  acc = __builtin_fmaf(bf16hi(a.y), bf16hi(b.y), acc);
-  acc = __builtin_fmaf(bf16lo(a.z), bf16lo(b.z), acc);
-  acc = __builtin_fmaf(bf16hi(a.z), bf16hi(b.z), acc);
-  acc = __builtin_fmaf(bf16lo(a.w), bf16lo(b.w), acc);
-  acc = __builtin_fmaf(bf16hi(a.w), bf16hi(b.w), acc);
-}
-
-// One wave computes a TE x TN tile of logits (experts x tokens).
-// Rows e < n_w come from w (+ bias), row n_w (if e > n_w) from w_extra;
-// out has ld = e columns.  Passes of 512 columns are loaded UNR at a time
-// (one memory round trip per group: compiled per pass, a wave waited for
-// one pass's loads before issuing the next pass's); FULL (d a multiple of
-// 512) drops the column guard.
+// One wave computes a TE x TN tile of logits (experts x tokens); see
+// router_tile.h for the summation order and the load grouping.
 template <int TE, int TN, int UNR, bool FULL>
 __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const uint16_t* __restrict__ w_extra, const float* __restrict__ bias, int n, int d, int e,
     int n_w, float* __restrict__ out) {
-  const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int e0 = (blockIdx.x * kRouterWaves + wave) * TE;
   const int n0 = blockIdx.y * TN;
   if (e0 >= e) return;
-  float acc[TE][TN];
-#pragma unroll
-  for (int i = 0; i < TE; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = 0.0f;
-
-  // UNR passes at a time: every load of the group is issued before the
-  // first FMA (sched_barrier keeps the compiler from sinking them), then the
-  // FMAs run in pass order.  Passes past the end and columns past d load an
-  // in-bounds address and skip their FMAs.
-  const int passes = (d + 511) / 512;
-  for (int t0 = 0; t0 < passes; t0 += UNR) {
-    uint4 wv[UNR][TE], xv[UNR][TN];
-#pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      const int col = min(min(t0 + u, passes - 1) * 512 + lane * 8, d - 8);
-#pragma unroll
-      for (int i = 0; i < TE; ++i) {
-        const int ei = min(e0 + i, e - 1);
-        const uint16_t* src = ei < n_w ? w + size_t(ei) * d : w_extra;
-        wv[u][i] = *reinterpret_cast<const uint4*>(src + col);
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int nj = min(n0 + j, n - 1);
-        xv[u][j] = *reinterpret_cast<const uint4*>(x + size_t(nj) * d + col);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      const int col = (t0 + u) * 512 + lane * 8;
-      if (t0 + u < passes && (FULL || col < d)) {
-#pragma unroll
-        for (int i = 0; i < TE; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j) fma8(acc[i][j], xv[u][j], wv[u][i]);
-      }
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < TE; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const float s = wave_sum_bfly(acc[i][j]);
-      if (lane == ((i * TN + j) & 63) && e0 + i < e && n0 + j < n) {
-        const bool biased = bias && e0 + i < n_w;
-        out[size_t(n0 + j) * e + e0 + i] = biased ? s + bias[e0 + i] : s;
-      }
-    }
+  router_tile<TE, TN, UNR, FULL, false>(x, w, w_extra, bias, n, d, e, n_w, out, e0, n0);
 }
 
 // (value, index) order used by every top-k here: larger value first, lower
