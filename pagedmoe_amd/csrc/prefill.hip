@@ -264,16 +264,19 @@ __device__ __forceinline__ void dequant_job(const LaneWords<BITS>& lw, const SBl
 
 // acc[mb] = A_tile(mb) . B over the whole reduction, for the tile's first
 // NMB 32-row blocks.  Software pipeline (per quantization group j): weights
-// of group j+3 and activations of group j+2 are in flight, group j+1's
+// of group j+WD (3, or 7 for an 8-group reduction: all of them) and
+// activations of group j+2 are in flight, group j+1's
 // weights are dequantized while group j's MFMAs run, and group j+1's
 // activations go to the other LDS buffer.  Scales/biases arrive 8 groups at
 // a time, one block ahead.  The loop is unrolled by 8 so the register rings
 // are indexed statically; loads past the end clamp to the last group (their
 // data is unused).  n_groups is a multiple of 8.
-template <int BITS, int NMB, int MB>
+template <int BITS, int NMB, int MB, int WD = 3>
 __device__ __forceinline__ void gemm_tile(int n_groups, const StageRows& rows, const LaneRow& lr,
                                           uint16_t* lds, f32x16 (&acc)[MB]) {
   static_assert(NMB <= MB, "row blocks beyond the accumulators");
+  static_assert(WD == 3 || WD == 7, "weight groups in flight: a ring of 4 or 8");
+  constexpr int WR = WD + 1;
   const int lane = threadIdx.x & 63;
   const int m = lane & 31;
   const int h = lane >> 5;
@@ -281,15 +284,14 @@ __device__ __forceinline__ void gemm_tile(int n_groups, const StageRows& rows, c
   const int last_blk = (n_groups >> 3) - 1;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x16{};
-  LaneWords<BITS> W[4];
+  LaneWords<BITS> W[WR];
   StageRegs X[2];
   SBlk S[2];
   bf16x8 B[2][4];
   load_sblk(S[0], lr, 0);
   load_sblk(S[1], lr, min(1, last_blk));
-  load_group<BITS>(W[0], lr, 0);
-  load_group<BITS>(W[1], lr, min(1, last));
-  load_group<BITS>(W[2], lr, min(2, last));
+#pragma unroll
+  for (int i = 0; i < WD; ++i) load_group<BITS>(W[i], lr, min(i, last));
   stage_load<NMB>(rows, 0, X[0]);
   stage_store<NMB>(lds, X[0]);
   stage_load<NMB>(rows, min(1, last), X[1]);
@@ -301,7 +303,7 @@ __device__ __forceinline__ void gemm_tile(int n_groups, const StageRows& rows, c
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int j = j0 + u;
-      load_group<BITS>(W[(u + 3) & 3], lr, min(j + 3, last));
+      load_group<BITS>(W[(u + WD) % WR], lr, min(j + WD, last));
       stage_load<NMB>(rows, min(j + 2, last), X[u & 1]);
       const uint16_t* xs = lds + (u & 1) * (kTileM * kLdsRow) + m * kLdsRow + 32 * h;
       // Fragment f = (mb, st): one MFMA.  The next group's dequant is
@@ -324,7 +326,7 @@ __device__ __forceinline__ void gemm_tile(int n_groups, const StageRows& rows, c
                                                               acc[f >> 2], 0, 0, 0);
 #pragma unroll
         for (int jb = 8 * f / NF; jb < 8 * (f + 1) / NF; ++jb)
-          dequant_job<BITS>(W[(u + 1) & 3], sn, si, jb, B[(u + 1) & 1]);
+          dequant_job<BITS>(W[(u + 1) % WR], sn, si, jb, B[(u + 1) & 1]);
         __builtin_amdgcn_sched_barrier(0);
       }
       stage_store<NMB>(lds + ((u + 1) & 1) * (kTileM * kLdsRow), X[(u + 1) & 1]);
@@ -345,7 +347,12 @@ __device__ __forceinline__ void gemm_tile_any(int nmb, int n_groups, const Stage
                                               const LaneRow& lr, uint16_t* lds,
                                               f32x16 (&acc)[MB]) {
   if constexpr (MB == 1) {
-    gemm_tile<BITS, 1, 1>(n_groups, rows, lr, lds, acc);
+    // a reduction of 8 groups (a 512-wide down): every group's weights are
+    // requested before the first MFMA
+    if (n_groups == 8)
+      gemm_tile<BITS, 1, 1, 7>(n_groups, rows, lr, lds, acc);
+    else
+      gemm_tile<BITS, 1, 1>(n_groups, rows, lr, lds, acc);
   } else {
     switch (nmb) {
       case 1: gemm_tile<BITS, 1, MB>(n_groups, rows, lr, lds, acc); break;
