@@ -222,10 +222,11 @@ int router_logits_ext(const uint16_t* x, const uint16_t* w, const uint16_t* w_ex
   using I1 = std::integral_constant<int, 1>;
   using I4 = std::integral_constant<int, 4>;
   using I8 = std::integral_constant<int, 8>;
-  if (n >= 32) {
+  if (n >= 32 && e >= 16) {
     // one pass per group: the 4 x 8 tile's 12 loads a pass keep three waves
     // per SIMD; staging 4 passes (256 registers, one wave) took 64 -> 139 us
-    // at 2048 tokens
+    // at 2048 tokens.  (A few columns -- a shared expert's gate -- take the
+    // 1 x 4 tile below: a 4 x 8 tile would leave one wave of four busy.)
     dim3 grid((e + kRouterWaves * 4 - 1) / (kRouterWaves * 4), (n + 8 - 1) / 8);
     launch(I4{}, I8{}, I1{}, grid);
   } else if (n >= 4) {
