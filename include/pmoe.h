@@ -155,7 +155,9 @@ int pmoe_prefill_tile_rows(int n, int kk, int n_experts);
 /* A MoE workspace starts with a 673,024-byte synchronisation header (grid
  * barrier counters, launch epoch and per-block flags of the one-launch
  * decode layer; launch and tile counters, tagged logit and h words and the
- * down partials of its expert-per-XCD form).  It must be zero before the
+ * down partials of its expert-per-XCD form; the arrival counter of the
+ * several-token decode's router launch, whose last block routes).  It must
+ * be zero before the
  * first pmoe_moe_block call on that workspace and is kept consistent by
  * every call after that, so it must not be overwritten between calls.  This
  * enqueues the zeroing on stream (a kernel, so it may be captured in a
