@@ -12,6 +12,7 @@
 
 #include "pmoe_internal.h"
 #include "pmoe_kernels.h"
+#include "route_common.h"
 #include "router_tile.h"
 
 namespace pmoe {
@@ -81,38 +82,42 @@ __device__ __forceinline__ void wave_topk(const float (&v)[kMaxEPL], uint32_t sk
   }
 }
 
+// Softmax top-k of one token per wave (rows of logits [n, e]): the picks of
+// pmoe::wave_topk (each lane sorts its logits once; k rounds of a 32-bit
+// wave maximum), which are those of the (value desc, id asc) order, then the
+// weights exp(v - v_max) / s with s the sum over the picks in pick order
+// (norm) or the wave butterfly over all logits.  The same arithmetic as the
+// decode launches' routing (route_common.h route_token).
+template <int EPL>
 __global__ __launch_bounds__(256) void route_softmax_kernel(
     const float* __restrict__ logits, int n, int e, int k, int norm,
     int32_t* __restrict__ inds, float* __restrict__ weights) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= n) return;
-  const int epl = (e + 63) / 64;
-  float v[kMaxEPL];
-  uint32_t skip = 0;
+  float v[EPL], none[EPL];
 #pragma unroll
-  for (int i = 0; i < kMaxEPL; ++i) {
+  for (int i = 0; i < EPL; ++i) {
     const int ei = lane + 64 * i;
-    v[i] = (i < epl && ei < e) ? logits[size_t(row) * e + ei] : 0.0f;
-    if (i < epl && ei >= e) skip |= 1u << i;
+    v[i] = ei < e ? logits[size_t(row) * e + ei] : 0.0f;
+    none[i] = 0.0f;
   }
-  float sv[kMaxK];
-  int si[kMaxK];
-  wave_topk(v, skip, epl, k, sv, si);
-  const float m = sv[0];
+  const Pick pk = pmoe::wave_topk<EPL, false>(v, e, k, none);
+  const float m = lane_value(pk.v, 0);
+  const float ej = lane < k ? pexp(pk.v - m) : 0.0f;
   float s = 0.0f;
   if (norm) {
-    for (int kk = 0; kk < k; ++kk) s = s + pexp(sv[kk] - m);
+    for (int j = 0; j < k; ++j) s = s + lane_value(ej, j);
   } else {
     float acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kMaxEPL; ++i)
-      if (i < epl && lane + 64 * i < e) acc = acc + pexp(v[i] - m);
+    for (int i = 0; i < EPL; ++i)
+      if (lane + 64 * i < e) acc = acc + pexp(v[i] - m);
     s = wave_sum_bfly(acc);
   }
-  for (int kk = lane; kk < k; kk += 64) {
-    inds[size_t(row) * k + kk] = si[kk];
-    weights[size_t(row) * k + kk] = pexp(sv[kk] - m) / s;
+  if (lane < k) {
+    inds[size_t(row) * k + lane] = pk.i;
+    weights[size_t(row) * k + lane] = ej / s;
   }
 }
 
@@ -252,7 +257,18 @@ int route_softmax(const float* logits, int n, int e, int k, int norm, int32_t* i
   PMOE_REQUIRE(k > 0 && k <= kMaxK && k <= e, "route_softmax_topk: k must be 1..min(16, E)");
   if (n <= 0) return PMOE_OK;
   ProfScope prof_scope(K_ROUTE_SELECT, st);
-  route_softmax_kernel<<<(n + 3) / 4, 256, 0, st>>>(logits, n, e, k, norm, inds, weights);
+  const int epl = (e + 63) / 64;
+  const dim3 grid((n + 3) / 4);
+  if (epl <= 1)
+    route_softmax_kernel<1><<<grid, 256, 0, st>>>(logits, n, e, k, norm, inds, weights);
+  else if (epl <= 2)
+    route_softmax_kernel<2><<<grid, 256, 0, st>>>(logits, n, e, k, norm, inds, weights);
+  else if (epl <= 4)
+    route_softmax_kernel<4><<<grid, 256, 0, st>>>(logits, n, e, k, norm, inds, weights);
+  else if (epl <= 8)
+    route_softmax_kernel<8><<<grid, 256, 0, st>>>(logits, n, e, k, norm, inds, weights);
+  else
+    route_softmax_kernel<16><<<grid, 256, 0, st>>>(logits, n, e, k, norm, inds, weights);
   PMOE_LAUNCH_CHECK("route_softmax_kernel");
   return PMOE_OK;
 }
