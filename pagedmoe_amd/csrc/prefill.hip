@@ -94,39 +94,48 @@ __device__ __forceinline__ float ubyte_f(uint32_t v) {
   return f;
 }
 
+// bf16 pair (a in the low half, b in the high half) in one word: one
+// v_cvt_pk_bf16_f32, rounding each to nearest even like a bf16 cast.
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+
 // Half HF (values 4*HF .. 4*HF+3) of one 4-bit word, lo = w & 0x0F0F0F0F
-// (even values), hi = (w >> 4) & 0x0F0F0F0F (odd values), into o[4HF..].
+// (even values), hi = (w >> 4) & 0x0F0F0F0F (odd values), into words
+// o[2HF], o[2HF+1] of the operand (two bf16 each).
 template <int HF>
 __device__ __forceinline__ void deq4_half(uint32_t lo, uint32_t hi, float s, float b,
-                                          bf16x8& o) {
-  o[4 * HF + 0] = (__bf16)__builtin_fmaf(s, ubyte_f<2 * HF>(lo), b);
-  o[4 * HF + 1] = (__bf16)__builtin_fmaf(s, ubyte_f<2 * HF>(hi), b);
-  o[4 * HF + 2] = (__bf16)__builtin_fmaf(s, ubyte_f<2 * HF + 1>(lo), b);
-  o[4 * HF + 3] = (__bf16)__builtin_fmaf(s, ubyte_f<2 * HF + 1>(hi), b);
+                                          u32x4& o) {
+  o[2 * HF] = pk_bf16(__builtin_fmaf(s, ubyte_f<2 * HF>(lo), b),
+                      __builtin_fmaf(s, ubyte_f<2 * HF>(hi), b));
+  o[2 * HF + 1] = pk_bf16(__builtin_fmaf(s, ubyte_f<2 * HF + 1>(lo), b),
+                          __builtin_fmaf(s, ubyte_f<2 * HF + 1>(hi), b));
 }
 
-// 6-bit field j of a little-endian bit stream held in words w[].
+// 6-bit field J of a little-endian bit stream held in words w[], as float:
+// one v_bfe_u32 (or, across a word boundary, v_alignbit_b32 and a mask)
+// and one v_cvt_f32_ubyte0.
 template <int J>
-__device__ __forceinline__ uint32_t field6(const uint32_t* w) {
+__device__ __forceinline__ float field6f(const uint32_t* w) {
   constexpr int bit = 6 * J, wi = bit / 32, sh = bit % 32;
+  uint32_t v;
   if constexpr (sh <= 26)
-    return (w[wi] >> sh) & 63u;
+    v = (w[wi] >> sh) & 63u;
   else
-    return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & 63u;
+    v = __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & 63u;
+  return float(v);
 }
 
-template <int S>
-__device__ __forceinline__ bf16x8 deq8_6(const uint32_t* w, float s, float b) {
-  bf16x8 r;
-  r[0] = (__bf16)__builtin_fmaf(s, float(field6<8 * S + 0>(w)), b);
-  r[1] = (__bf16)__builtin_fmaf(s, float(field6<8 * S + 1>(w)), b);
-  r[2] = (__bf16)__builtin_fmaf(s, float(field6<8 * S + 2>(w)), b);
-  r[3] = (__bf16)__builtin_fmaf(s, float(field6<8 * S + 3>(w)), b);
-  r[4] = (__bf16)__builtin_fmaf(s, float(field6<8 * S + 4>(w)), b);
-  r[5] = (__bf16)__builtin_fmaf(s, float(field6<8 * S + 5>(w)), b);
-  r[6] = (__bf16)__builtin_fmaf(s, float(field6<8 * S + 6>(w)), b);
-  r[7] = (__bf16)__builtin_fmaf(s, float(field6<8 * S + 7>(w)), b);
-  return r;
+// Values 8S + 4HF .. 8S + 4HF + 3 of a 6-bit half group into words
+// o[2HF], o[2HF+1] of the operand.
+template <int S, int HF>
+__device__ __forceinline__ void deq4_6(const uint32_t* w, float s, float b, u32x4& o) {
+  constexpr int J = 8 * S + 4 * HF;
+  o[2 * HF] = pk_bf16(__builtin_fmaf(s, field6f<J>(w), b), __builtin_fmaf(s, field6f<J + 1>(w), b));
+  o[2 * HF + 1] =
+      pk_bf16(__builtin_fmaf(s, field6f<J + 2>(w), b), __builtin_fmaf(s, field6f<J + 3>(w), b));
 }
 
 // One lane's packed words of one group: values [32h, 32h + 32) of a row.
@@ -230,14 +239,15 @@ __device__ __forceinline__ float bf_at(const u32x4& v, int i) {
 
 // Dequant job jb (0..7) of a group: half jb & 1 (4 values) of MFMA step
 // jb >> 1, with the group's scale/bias at entry i of sb.  Eight small jobs
-// per group let the dequant spread evenly between the MFMAs.
+// per group let the dequant spread evenly between the MFMAs.  The operand
+// of step st is o[st]: 8 bf16 as 4 words.
 template <int BITS>
 __device__ __forceinline__ void dequant_job(const LaneWords<BITS>& lw, const SBlk& sb, int i,
-                                            int jb, bf16x8 (&o)[4]) {
+                                            int jb, u32x4 (&o)[4]) {
   const int st = jb >> 1;
   const float s = bf_at(sb.s, i);
   const float b = bf_at(sb.b, i);
-  bf16x8& out = o[st];
+  u32x4& out = o[st];
   if constexpr (BITS == 4) {
     const uint32_t w = lw.w[st];
     const uint32_t lo = w & 0x0F0F0F0Fu;
@@ -247,18 +257,51 @@ __device__ __forceinline__ void dequant_job(const LaneWords<BITS>& lw, const SBl
     else
       deq4_half<0>(lo, hi, s, b, out);
   } else {
-    bf16x8 t;
-    switch (st) {
-      case 0: t = deq8_6<0>(lw.w, s, b); break;
-      case 1: t = deq8_6<1>(lw.w, s, b); break;
-      case 2: t = deq8_6<2>(lw.w, s, b); break;
-      default: t = deq8_6<3>(lw.w, s, b); break;
+    switch (jb) {
+      case 0: deq4_6<0, 0>(lw.w, s, b, out); break;
+      case 1: deq4_6<0, 1>(lw.w, s, b, out); break;
+      case 2: deq4_6<1, 0>(lw.w, s, b, out); break;
+      case 3: deq4_6<1, 1>(lw.w, s, b, out); break;
+      case 4: deq4_6<2, 0>(lw.w, s, b, out); break;
+      case 5: deq4_6<2, 1>(lw.w, s, b, out); break;
+      case 6: deq4_6<3, 0>(lw.w, s, b, out); break;
+      default: deq4_6<3, 1>(lw.w, s, b, out); break;
     }
-    if (jb & 1) {
-      out[4] = t[4]; out[5] = t[5]; out[6] = t[6]; out[7] = t[7];
-    } else {
-      out[0] = t[0]; out[1] = t[1]; out[2] = t[2]; out[3] = t[3];
-    }
+  }
+}
+
+// LDS rows of one activation staging buffer: the tile's rows, and at least
+// the 64 rows one staging step of 512 threads writes.
+template <int MB>
+constexpr int stage_rows() {
+  return 32 * MB > 64 ? 32 * MB : 64;
+}
+
+// One group's MFMAs for the tile's first NMB 32-row blocks (activations at
+// xs in LDS, weights b), with the next group's dequant (words wn, scale and
+// bias entry si of sn, into bn) spread over the fragments.  Fragment
+// f = (mb, st): one MFMA; the LDS reads run two fragments ahead, and
+// sched_barrier keeps that order.  (Step-major order, with consecutive
+// MFMAs on different accumulators, measured slower: the second wave on the
+// SIMD already fills the accumulation latency.)
+template <int BITS, int NMB, int MB>
+__device__ __forceinline__ void group_mfma(const uint16_t* xs, const u32x4 (&b)[4],
+                                           const LaneWords<BITS>& wn, const SBlk& sn, int si,
+                                           u32x4 (&bn)[4], f32x16 (&acc)[MB]) {
+  constexpr int NF = 4 * NMB;
+  bf16x8 A[3];
+  A[0] = *reinterpret_cast<const bf16x8*>(xs);
+  if constexpr (NF > 1) A[1] = *reinterpret_cast<const bf16x8*>(xs + 8);
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    if (f + 2 < NF)
+      A[(f + 2) % 3] = *reinterpret_cast<const bf16x8*>(
+          xs + ((f + 2) >> 2) * 32 * kLdsRow + 8 * ((f + 2) & 3));
+    acc[f >> 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        A[f % 3], __builtin_bit_cast(bf16x8, b[f & 3]), acc[f >> 2], 0, 0, 0);
+#pragma unroll
+    for (int jb = 8 * f / NF; jb < 8 * (f + 1) / NF; ++jb) dequant_job<BITS>(wn, sn, si, jb, bn);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -277,6 +320,7 @@ __device__ __forceinline__ void gemm_tile(int n_groups, const StageRows& rows, c
   static_assert(NMB <= MB, "row blocks beyond the accumulators");
   static_assert(WD == 3 || WD == 7, "weight groups in flight: a ring of 4 or 8");
   constexpr int WR = WD + 1;
+  constexpr int SR = stage_rows<MB>();
   const int lane = threadIdx.x & 63;
   const int m = lane & 31;
   const int h = lane >> 5;
@@ -287,7 +331,7 @@ __device__ __forceinline__ void gemm_tile(int n_groups, const StageRows& rows, c
   LaneWords<BITS> W[WR];
   StageRegs X[2];
   SBlk S[2];
-  bf16x8 B[2][4];
+  u32x4 B[2][4];
   load_sblk(S[0], lr, 0);
   load_sblk(S[1], lr, min(1, last_blk));
 #pragma unroll
@@ -305,31 +349,150 @@ __device__ __forceinline__ void gemm_tile(int n_groups, const StageRows& rows, c
       const int j = j0 + u;
       load_group<BITS>(W[(u + WD) % WR], lr, min(j + WD, last));
       stage_load<NMB>(rows, min(j + 2, last), X[u & 1]);
-      const uint16_t* xs = lds + (u & 1) * (kTileM * kLdsRow) + m * kLdsRow + 32 * h;
-      // Fragment f = (mb, st): one MFMA.  The next group's dequant is
-      // spread over the fragments and the LDS reads run two fragments
-      // ahead; sched_barrier keeps that order.  (Step-major order, with
-      // consecutive MFMAs on different accumulators, measured slower: the
-      // second wave on the SIMD already fills the accumulation latency.)
-      constexpr int NF = 4 * NMB;
-      const SBlk& sn = u < 7 ? S[0] : S[1];
-      const int si = (u + 1) & 7;
-      bf16x8 A[3];
-      A[0] = *reinterpret_cast<const bf16x8*>(xs);
-      if constexpr (NF > 1) A[1] = *reinterpret_cast<const bf16x8*>(xs + 8);
-#pragma unroll
-      for (int f = 0; f < NF; ++f) {
-        if (f + 2 < NF)
-          A[(f + 2) % 3] = *reinterpret_cast<const bf16x8*>(
-              xs + ((f + 2) >> 2) * 32 * kLdsRow + 8 * ((f + 2) & 3));
-        acc[f >> 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[f % 3], B[u & 1][f & 3],
-                                                              acc[f >> 2], 0, 0, 0);
-#pragma unroll
-        for (int jb = 8 * f / NF; jb < 8 * (f + 1) / NF; ++jb)
-          dequant_job<BITS>(W[(u + 1) % WR], sn, si, jb, B[(u + 1) & 1]);
-        __builtin_amdgcn_sched_barrier(0);
+      const uint16_t* xs = lds + (u & 1) * (SR * kLdsRow) + m * kLdsRow + 32 * h;
+      group_mfma<BITS, NMB, MB>(xs, B[u & 1], W[(u + 1) % WR], u < 7 ? S[0] : S[1], (u + 1) & 7,
+                                B[(u + 1) & 1], acc);
+      stage_store<NMB>(lds + ((u + 1) & 1) * (SR * kLdsRow), X[(u + 1) & 1]);
+      if (u == 7) {
+        S[0] = S[1];
+        load_sblk(S[1], lr, min((j0 >> 3) + 2, last_blk));
       }
-      stage_store<NMB>(lds + ((u + 1) & 1) * (kTileM * kLdsRow), X[(u + 1) & 1]);
+      __syncthreads();
+    }
+  }
+}
+
+// 6-bit weights in coalesced units.  A lane's operand is half a group of
+// one row (24 bytes); read straight from HBM, each load instruction would
+// touch 32 rows for 512 bytes.  Instead a wave reads a unit -- 4 groups of
+// its 32 rows, 192 contiguous bytes a row -- as 6 loads of 16 bytes a lane
+// (piece p = 64 i + lane: row p / 12, bytes 16 (p % 12) of the unit), each
+// instruction covering runs of whole rows; copies the unit into its own
+// LDS buffer (row pitch 200 bytes: the 8-byte reads of 16 consecutive rows
+// fall on distinct banks) and reads each group's half rows back in the
+// operand layout.  The words are the same, so the dequant and the MFMAs
+// (and their results) are unchanged.
+constexpr int kUnitPieces = 6;                  // 16-byte pieces a lane per unit
+constexpr int kUnitPitch = 200;                 // LDS bytes per row of a unit
+constexpr int kUnitLds = 32 * kUnitPitch;       // LDS bytes per wave
+static_assert(kUnitPitch == 12 * 16 + 8, "piece p of row r sits at 16 p + 8 r");
+
+struct Unit6 {
+  u32x4 v[kUnitPieces];
+};
+
+// Row of piece p (p < 384): p / 12.
+__device__ __forceinline__ uint32_t unit_row(uint32_t p) { return (p * 43691u) >> 19; }
+
+// Copy the unit held in un to buf, then (if load) load unit k of the
+// wave's 32 rows into un (row 0 at w0, row_bytes apart; w0 is the same in
+// every lane, so each load takes it as a scalar base with a 32-bit lane
+// offset).  The pieces' rows are recomputed here (a few integer ops)
+// rather than held in registers across the loop.
+__device__ __forceinline__ void cycle_unit6(Unit6& un, uint8_t* buf, const uint8_t* w0,
+                                            uint32_t row_bytes, int k, bool load) {
+  uint32_t lane = threadIdx.x & 63;
+  asm volatile("" : "+v"(lane));  // opaque: not hoisted out of the loop
+  uint32_t r[kUnitPieces];
+#pragma unroll
+  for (int i = 0; i < kUnitPieces; ++i) r[i] = unit_row(64 * i + lane);
+  // piece p of row r at 16 p + 8 r = 200 r + 16 (p - 12 r)
+  uint8_t* d = buf + 16 * lane;
+#pragma unroll
+  for (int i = 0; i < kUnitPieces; ++i) {
+    uint32_t* q = reinterpret_cast<uint32_t*>(d + 1024 * i + 8 * r[i]);
+    *reinterpret_cast<u32x2*>(q) = u32x2{un.v[i][0], un.v[i][1]};
+    *reinterpret_cast<u32x2*>(q + 2) = u32x2{un.v[i][2], un.v[i][3]};
+  }
+  __builtin_amdgcn_sched_barrier(0);  // the copy reads un before it is reloaded
+  if (load) {
+    // byte 16 (p - 12 r) of row r: r row_bytes + 16 (p - 12 r)
+    const uint8_t* wk = w0 + 192 * k;
+#pragma unroll
+    for (int i = 0; i < kUnitPieces; ++i)
+      un.v[i] = *reinterpret_cast<const u32x4*>(
+          wk + (16 * (64 * i + lane) + r[i] * (row_bytes - 192)));
+  }
+}
+
+// First unit of the wave's rows into un.
+__device__ __forceinline__ void load_unit6(Unit6& un, const uint8_t* w0, uint32_t row_bytes) {
+  const uint32_t lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < kUnitPieces; ++i)
+    un.v[i] = *reinterpret_cast<const u32x4*>(
+        w0 + (16 * (64 * i + lane) + unit_row(64 * i + lane) * (row_bytes - 192)));
+}
+
+// Group gi (0..3) of the unit at lds + rd, where rd is the lane's half row
+// in the wave's buffer (the same register for every group: the group's
+// place is the instructions' offset field).
+__device__ __forceinline__ void read_group6(LaneWords<6>& lw, const uint8_t* lds, uint32_t rd,
+                                            int gi) {
+  const u32x2* s = reinterpret_cast<const u32x2*>(lds + rd + 48 * gi);
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const u32x2 t = s[j];
+    lw.w[2 * j] = t[0];
+    lw.w[2 * j + 1] = t[1];
+  }
+}
+
+// gemm_tile for 6-bit weights read in units: the same pipeline, with the
+// weights of group j+1 read from the wave's LDS copy of their unit.  One
+// unit is held in registers: when group j+1 opens a unit, that unit is
+// copied to LDS and its registers take the next one (4 groups ahead; a
+// block's 16 waves keep ~96 KB a CU in flight).  n_groups is a multiple
+// of 8.
+template <int NMB, int MB>
+__device__ __forceinline__ void gemm_tile_u6(int n_groups, const StageRows& rows,
+                                             const uint8_t* w0, uint32_t row_bytes,
+                                             const LaneRow& lr, uint16_t* lds, uint8_t* wbuf,
+                                             f32x16 (&acc)[MB]) {
+  static_assert(NMB <= MB, "row blocks beyond the accumulators");
+  constexpr int SR = stage_rows<MB>();
+  const int lane = threadIdx.x & 63;
+  const int m = lane & 31;
+  const int h = lane >> 5;
+  const int last = n_groups - 1;
+  const int last_blk = (n_groups >> 3) - 1;
+  const int last_unit = (n_groups >> 2) - 1;
+  const uint8_t* lds8 = reinterpret_cast<const uint8_t*>(lds);
+  uint32_t rd = uint32_t(wbuf - lds8) + m * kUnitPitch + 24 * h;
+  asm volatile("" : "+v"(rd));  // one base register for every group's reads
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x16{};
+  Unit6 U;
+  LaneWords<6> Wn;
+  StageRegs X[2];
+  SBlk S[2];
+  u32x4 B[2][4];
+  load_sblk(S[0], lr, 0);
+  load_sblk(S[1], lr, min(1, last_blk));
+  load_unit6(U, w0, row_bytes);
+  stage_load<NMB>(rows, 0, X[0]);
+  stage_store<NMB>(lds, X[0]);
+  stage_load<NMB>(rows, min(1, last), X[1]);
+  cycle_unit6(U, wbuf, w0, row_bytes, 1, true);
+  read_group6(Wn, lds8, rd, 0);
+#pragma unroll
+  for (int jb = 0; jb < 8; ++jb) dequant_job<6>(Wn, S[0], 0, jb, B[0]);
+  __syncthreads();
+
+  for (int j0 = 0; j0 < n_groups; j0 += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = j0 + u;
+      // group j+1 opens unit un (held in U)
+      const int un = (j + 1) >> 2;
+      if ((u & 3) == 3 && un <= last_unit)
+        cycle_unit6(U, wbuf, w0, row_bytes, un + 1, un + 1 <= last_unit);
+      read_group6(Wn, lds8, rd, (u + 1) & 3);
+      stage_load<NMB>(rows, min(j + 2, last), X[u & 1]);
+      const uint16_t* xs = lds + (u & 1) * (SR * kLdsRow) + m * kLdsRow + 32 * h;
+      group_mfma<6, NMB, MB>(xs, B[u & 1], Wn, u < 7 ? S[0] : S[1], (u + 1) & 7,
+                             B[(u + 1) & 1], acc);
+      stage_store<NMB>(lds + ((u + 1) & 1) * (SR * kLdsRow), X[(u + 1) & 1]);
       if (u == 7) {
         S[0] = S[1];
         load_sblk(S[1], lr, min((j0 >> 3) + 2, last_blk));
@@ -344,9 +507,12 @@ __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 *
 
 template <int BITS, int MB>
 __device__ __forceinline__ void gemm_tile_any(int nmb, int n_groups, const StageRows& rows,
-                                              const LaneRow& lr, uint16_t* lds,
+                                              const LaneRow& lr, const uint8_t* w0,
+                                              uint32_t row_bytes, uint16_t* lds, uint8_t* wbuf,
                                               f32x16 (&acc)[MB]) {
-  if constexpr (MB == 1) {
+  if constexpr (MB == 1 && BITS == 6) {
+    gemm_tile_u6<1, 1>(n_groups, rows, w0, row_bytes, lr, lds, wbuf, acc);
+  } else if constexpr (MB == 1) {
     // a reduction of 8 groups (a 512-wide down): every group's weights are
     // requested before the first MFMA
     if (n_groups == 8)
@@ -423,22 +589,35 @@ __device__ __forceinline__ bool xcd_work(const PrefillArgs& a, int n_cols, TileI
 //
 // LDS of one block: the activation staging buffers, reused after the main
 // loop by the gate/up epilogue for the up waves' accumulators.
-constexpr int kStageBytes = 2 * kTileM * kLdsRow * 2;
+// 6-bit weights at 32-row tiles go through the 8 waves' unit buffers after
+// that (gemm_tile_u6).
 template <int MB>
+constexpr int stage_bytes() {
+  return 2 * stage_rows<MB>() * kLdsRow * 2;
+}
+template <int BITS, int MB>
+constexpr int unit_lds_bytes() {
+  return BITS == 6 && MB == 1 ? (kThreads / 64) * kUnitLds : 0;
+}
+template <int BITS, int MB>
 constexpr int gateup_lds_bytes() {
   constexpr int up = 4 * MB * 16 * 64 * 4;  // 4 up waves x accumulators
-  return kStageBytes > up ? kStageBytes : up;
+  return (stage_bytes<MB>() > up ? stage_bytes<MB>() : up) + unit_lds_bytes<BITS, MB>();
+}
+template <int BITS, int MB>
+constexpr int down_lds_bytes() {
+  return stage_bytes<MB>() + unit_lds_bytes<BITS, MB>();
 }
 
 template <int BITS, int MB>
 __global__ __launch_bounds__(kThreads, MB < kMB ? 4 : 1) void gateup_mfma_kernel(const PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds_raw[gateup_lds_bytes<MB>()];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_raw[gateup_lds_bytes<BITS, MB>()];
   uint16_t* lds = reinterpret_cast<uint16_t*>(lds_raw);
   TileInfo ti;
   int cb;
   if (!xcd_work<32 * MB>(a, a.out_cols / kGuCols, ti, cb)) return;
   if (ti.slot < 0) return;  // the down kernel writes this tile's zero rows
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int up = wave >> 2;   // waves 0-3: gate rows, 4-7: the same up rows
   const int wq = wave & 3;
@@ -453,10 +632,14 @@ __global__ __launch_bounds__(kThreads, MB < kMB ? 4 : 1) void gateup_mfma_kernel
   lr.w = base + (up ? a.w1 : a.w0) + col * row_bytes + h * kHalf;
   lr.s = reinterpret_cast<const u32x4*>(base + (up ? a.s1 : a.s0)) + size_t(col) * blks;
   lr.b = reinterpret_cast<const u32x4*>(base + (up ? a.b1 : a.b0)) + size_t(col) * blks;
+  const int col0 = cb * kGuCols + wq * 32;  // the wave's first row (uniform)
+  const uint8_t* w0 = base + (up ? a.w1 : a.w0) + size_t(col0) * row_bytes;
+  uint8_t* wbuf = lds_raw + gateup_lds_bytes<BITS, MB>() - unit_lds_bytes<BITS, MB>() +
+                  wave * kUnitLds;
   const StageRows rows = tile_rows(a.act, a.order, a.kk, a.cols, ti.p0, ti.m);
   f32x16 acc[MB];
   const int nmb = (ti.m + 31) >> 5;
-  gemm_tile_any<BITS, MB>(nmb, groups, rows, lr, lds, acc);
+  gemm_tile_any<BITS, MB>(nmb, groups, rows, lr, w0, uint32_t(row_bytes), lds, wbuf, acc);
   // SwiGLU: up wave wq + 4 hands its accumulators (the same rows and
   // columns, lane for lane) to gate wave wq through LDS (the staging
   // buffers are free: the main loop ended with a block barrier)
@@ -487,11 +670,12 @@ __global__ __launch_bounds__(kThreads, MB < kMB ? 4 : 1) void gateup_mfma_kernel
 
 template <int BITS, int MB>
 __global__ __launch_bounds__(kThreads, MB < kMB ? 4 : 1) void down_mfma_kernel(const PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kTileM * kLdsRow];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_raw[down_lds_bytes<BITS, MB>()];
+  uint16_t* lds = reinterpret_cast<uint16_t*>(lds_raw);
   TileInfo ti;
   int cb;
   if (!xcd_work<32 * MB>(a, a.out_cols / kDnCols, ti, cb)) return;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int col = cb * kDnCols + wave * 32 + (lane & 31);
   const int h = lane >> 5;
@@ -514,10 +698,13 @@ __global__ __launch_bounds__(kThreads, MB < kMB ? 4 : 1) void down_mfma_kernel(c
   lr.w = base + a.w0 + col * row_bytes + h * kHalf;
   lr.s = reinterpret_cast<const u32x4*>(base + a.s0) + size_t(col) * blks;
   lr.b = reinterpret_cast<const u32x4*>(base + a.b0) + size_t(col) * blks;
+  const int col0 = cb * kDnCols + wave * 32;  // the wave's first row (uniform)
+  const uint8_t* w0 = base + a.w0 + size_t(col0) * row_bytes;
+  uint8_t* wbuf = lds_raw + stage_bytes<MB>() + wave * kUnitLds;
   const StageRows rows = tile_rows(a.act, nullptr, 1, a.cols, ti.p0, ti.m);
   f32x16 acc[MB];
   const int nmb = (ti.m + 31) >> 5;
-  gemm_tile_any<BITS, MB>(nmb, groups, rows, lr, lds, acc);
+  gemm_tile_any<BITS, MB>(nmb, groups, rows, lr, w0, uint32_t(row_bytes), lds, wbuf, acc);
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
