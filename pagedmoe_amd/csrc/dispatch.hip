@@ -70,12 +70,25 @@ __device__ __forceinline__ int block_excl_scan(int v, int* s_tmp, int* total) {
   return base + incl - v;
 }
 
-// Per-expert totals -> counts, offsets, active list, n_active and (when
-// tile_m > 0) the (expert, first row) list of tile_m-row tiles.  Run by a
-// block of 1024 threads; cnt[] is in LDS, one entry per expert.
+// The prefill GEMMs' tile list (when tile_m > 0): tile t of expert e with
+// c rows is {slot of e, t * tile_m, c, offset of e}, everything a GEMM block
+// needs to find its rows and weights in one load.  Slots come from the slot
+// table (routed ids below n_routed) or are the shared expert's.
+struct TileSink {
+  int4* tiles;
+  int32_t* n_tiles;
+  int tile_m;
+  const int32_t* table;
+  int n_routed, shared_slot;
+};
+
+// Per-expert totals -> counts, offsets, active list, n_active and the tile
+// list.  Run by a block of 1024 threads; cnt[] is in LDS, one entry per
+// expert.
 __device__ void finish_scan(const int* cnt, int n_experts, int32_t* counts, int32_t* offsets,
-                            int32_t* active, int32_t* n_active, int tile_m, int2* tiles,
-                            int32_t* n_tiles, int* s_off, int* s_tmp) {
+                            int32_t* active, int32_t* n_active, const TileSink& ts, int* s_off,
+                            int* s_tmp) {
+  const int tile_m = ts.tile_m;
   const int e = threadIdx.x;
   const int c = e < n_experts ? cnt[e] : 0;
   int total = 0;
@@ -90,12 +103,15 @@ __device__ void finish_scan(const int* cnt, int n_experts, int32_t* counts, int3
     counts[e] = c;
     offsets[e] = off;
     if (c > 0) active[act] = e;
-    for (int t = 0; t < nt; ++t) tiles[toff + t] = make_int2(e, t * tile_m);
+    if (nt > 0) {
+      const int slot = e < ts.n_routed ? ts.table[e] : ts.shared_slot;
+      for (int t = 0; t < nt; ++t) ts.tiles[toff + t] = make_int4(slot, t * tile_m, c, off);
+    }
   }
   if (e == 0) {
     offsets[n_experts] = total;
     *n_active = act_total;
-    if (tile_m > 0) *n_tiles = tiles_total;
+    if (tile_m > 0) *ts.n_tiles = tiles_total;
   }
   __syncthreads();
 }
@@ -104,8 +120,7 @@ __device__ void finish_scan(const int* cnt, int n_experts, int32_t* counts, int3
 __global__ __launch_bounds__(1024) void dispatch_small_kernel(
     const IdSrc src, int rows, int n_experts, int32_t* __restrict__ order,
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ inv,
-    int32_t* __restrict__ active, int32_t* __restrict__ n_active, int tile_m,
-    int2* __restrict__ tiles, int32_t* __restrict__ n_tiles) {
+    int32_t* __restrict__ active, int32_t* __restrict__ n_active, const TileSink ts) {
   __shared__ int s_e[kSmallRows];
   __shared__ int s_cnt[kMaxExperts];
   __shared__ int s_off[kMaxExperts];
@@ -124,8 +139,7 @@ __global__ __launch_bounds__(1024) void dispatch_small_kernel(
     for (int j = 0; j < tid; ++j) rank += (s_e[j] == my_e);
   }
   __syncthreads();
-  finish_scan(s_cnt, n_experts, counts, offsets, active, n_active, tile_m, tiles, n_tiles, s_off,
-              s_tmp);
+  finish_scan(s_cnt, n_experts, counts, offsets, active, n_active, ts, s_off, s_tmp);
   if (my_e >= 0) {
     const int pos = s_off[my_e] + rank;
     order[pos] = tid;
@@ -163,7 +177,7 @@ __global__ __launch_bounds__(kChunk) void dispatch_count_kernel(
 __global__ __launch_bounds__(1024) void dispatch_scan_kernel(
     int32_t* __restrict__ hist, int n_blocks, int n_experts, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ active, int32_t* __restrict__ n_active,
-    int tile_m, int2* __restrict__ tiles, int32_t* __restrict__ n_tiles) {
+    const TileSink ts) {
   __shared__ int s_cnt[kMaxExperts];
   __shared__ int s_off[kMaxExperts];
   __shared__ int s_tmp[16];
@@ -182,8 +196,7 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(
     s_cnt[e] = run;
   }
   __syncthreads();
-  finish_scan(s_cnt, n_experts, counts, offsets, active, n_active, tile_m, tiles, n_tiles, s_off,
-              s_tmp);
+  finish_scan(s_cnt, n_experts, counts, offsets, active, n_active, ts, s_off, s_tmp);
   if (e < n_experts) {
     // each block's base position per expert: expert offset + earlier blocks
     int run = s_off[e];
@@ -225,21 +238,25 @@ size_t dispatch_workspace(int rows, int n_experts) {
   return ((blocks * n_experts + rows) * sizeof(int32_t) + 255) / 256 * 256;
 }
 
-// Internal entry: also builds the prefill tile list when tile_m > 0.  Ids
-// outside their range are dropped: counted nowhere, inv = -1.
+// Internal entry: also builds the prefill tile list when tile_m > 0 (slots
+// from table, the shared pseudo-id's from shared_slot).  Ids outside their
+// range are dropped: counted nowhere, inv = -1.
 int dispatch_ext(const int32_t* inds, int rows, int k_routed, int kk, int n_ids, int32_t* order,
                  int32_t* counts, int32_t* offsets, int32_t* inv, int32_t* active,
-                 int32_t* n_active, int tile_m, int2* tiles, int32_t* n_tiles, void* ws,
-                 size_t ws_bytes, hipStream_t st) {
+                 int32_t* n_active, int tile_m, int4* tiles, int32_t* n_tiles,
+                 const int32_t* table, int shared_slot, void* ws, size_t ws_bytes,
+                 hipStream_t st) {
   PMOE_REQUIRE(n_ids > 0 && n_ids <= kMaxExperts, "dispatch: experts must be 1..1024");
   PMOE_REQUIRE(rows >= 0, "dispatch: negative rows");
   PMOE_REQUIRE(k_routed >= 1 && kk >= k_routed && kk <= k_routed + 1, "dispatch: bad columns");
   PMOE_REQUIRE(rows % kk == 0, "dispatch: rows must be a multiple of the columns");
   const IdSrc src{inds, k_routed, kk, kk > k_routed ? n_ids - 1 : n_ids};
+  PMOE_REQUIRE(tile_m == 0 || (tiles && n_tiles && table), "dispatch: tile list needs the slot table");
+  const TileSink ts{tiles, n_tiles, tile_m, table, src.n_routed, shared_slot};
   ProfScope prof_scope(K_DISPATCH, st);
   if (rows <= kSmallRows) {
     dispatch_small_kernel<<<1, 1024, 0, st>>>(src, rows, n_ids, order, counts, offsets, inv,
-                                              active, n_active, tile_m, tiles, n_tiles);
+                                              active, n_active, ts);
     PMOE_LAUNCH_CHECK("dispatch_small_kernel");
     return PMOE_OK;
   }
@@ -251,7 +268,7 @@ int dispatch_ext(const int32_t* inds, int rows, int k_routed, int kk, int n_ids,
   dispatch_count_kernel<<<blocks, kChunk, 0, st>>>(src, rows, n_ids, hist, rank);
   PMOE_LAUNCH_CHECK("dispatch_count_kernel");
   dispatch_scan_kernel<<<1, 1024, 0, st>>>(hist, blocks, n_ids, counts, offsets, active,
-                                           n_active, tile_m, tiles, n_tiles);
+                                           n_active, ts);
   PMOE_LAUNCH_CHECK("dispatch_scan_kernel");
   dispatch_scatter_kernel<<<blocks, kChunk, 0, st>>>(src, rows, n_ids, hist, rank, order, inv);
   PMOE_LAUNCH_CHECK("dispatch_scatter_kernel");
@@ -269,6 +286,6 @@ extern "C" int pmoe_dispatch(const int32_t* inds, int rows, int n_experts, int32
                              int32_t* n_active, void* ws, size_t ws_bytes, void* stream) {
   pmoe::clear_error();
   return pmoe::dispatch_ext(inds, rows, 1, 1, n_experts, order, counts, offsets, inv, active,
-                            n_active, 0, nullptr, nullptr, ws, ws_bytes,
+                            n_active, 0, nullptr, nullptr, nullptr, -1, ws, ws_bytes,
                             static_cast<hipStream_t>(stream));
 }

@@ -15,11 +15,9 @@
 
 namespace pmoe {
 
-int prefill_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* table,
-                    int n_experts, int shared_slot, const uint16_t* x, int n, int kk,
-                    const int32_t* order, const int32_t* counts, const int32_t* offsets,
-                    const int2* tiles, const int32_t* n_tiles, int tile_m, int max_tiles,
-                    uint16_t* h, void* y, int y_f32, hipStream_t st);
+int prefill_experts(const pmoe_geom* g, const uint8_t* slab, const uint16_t* x, int n, int kk,
+                    const int32_t* order, const int4* tiles, const int32_t* n_tiles, int tile_m,
+                    int max_tiles, uint16_t* h, void* y, int y_f32, hipStream_t st);
 int prefill_tile_rows(int n, int kk, int n_experts);
 int prefill_min_tile_rows();
 bool prefill_wanted(const pmoe_geom* g, int n, int kk, int n_ids);
@@ -39,7 +37,7 @@ struct MoeWs {
   int32_t* offsets = nullptr;     // [n_ids + 1]
   int32_t* active = nullptr;      // [n_ids]
   int32_t* n_active = nullptr;    // [1]
-  int2* tiles = nullptr;          // [max_tiles]
+  int4* tiles = nullptr;          // [max_tiles] {slot, first row, rows, offset}
   int32_t* n_tiles = nullptr;     // [1]
   uint16_t* h = nullptr;          // [rows, inter] bf16
   float* y = nullptr;             // [rows, hidden] (bf16 or f32 per-slot outputs)
@@ -78,7 +76,7 @@ size_t carve(const pmoe_geom* g, int n, int k, int shared, int n_experts, void* 
   t.n_active = c.take<int32_t>(1);
   // tile capacity for the shortest prefill tiles
   t.max_tiles = int(rows / prefill_min_tile_rows()) + n_ids + 1;
-  t.tiles = c.take<int2>(t.max_tiles);
+  t.tiles = c.take<int4>(t.max_tiles);
   t.n_tiles = c.take<int32_t>(1);
   t.h = c.take<uint16_t>(rows * g->inter);
   t.y = c.take<float>(rows * g->hidden);
@@ -194,20 +192,18 @@ int check_route_cfg(const pmoe_route_cfg* rc) {
 // y receives [rows, hidden] (f32 when y_f32, else bf16).
 int run_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* table, int n_experts,
                 int shared_slot, const uint16_t* x, const int32_t* inds, int n, int k, int kk,
-                int max_rows_per_expert, const MoeWs& w, void* y, int y_f32, hipStream_t st,
-                bool dispatched = false) {
+                int max_rows_per_expert, const MoeWs& w, void* y, int y_f32, hipStream_t st) {
   const int rows = n * kk;
   const int n_ids = n_experts + (kk > k ? 1 : 0);
   const bool prefill = prefill_wanted(g, n, kk, n_ids);
   const int tm = prefill ? prefill_tile_rows(n, kk, n_experts) : 0;
-  int rc = PMOE_OK;
-  if (!dispatched)
-    rc = dispatch_ext(inds, rows, k, kk, n_ids, w.order, w.counts, w.offsets, w.inv, w.active,
-                      w.n_active, tm, w.tiles, w.n_tiles, w.dws, w.dws_bytes, st);
+  // the tile list carries the slots of this table
+  int rc = dispatch_ext(inds, rows, k, kk, n_ids, w.order, w.counts, w.offsets, w.inv, w.active,
+                        w.n_active, tm, w.tiles, w.n_tiles, table, shared_slot, w.dws,
+                        w.dws_bytes, st);
   if (rc) return rc;
   if (prefill)
-    return prefill_experts(g, slab, table, n_experts, shared_slot, x, n, kk, w.order, w.counts,
-                           w.offsets, w.tiles, w.n_tiles, tm,
+    return prefill_experts(g, slab, x, n, kk, w.order, w.tiles, w.n_tiles, tm,
                            std::min(rows / tm + n_ids + 1, w.max_tiles), w.h, y, y_f32, st);
   const int max_experts = rows < n_ids ? rows : n_ids;
   GemvArgs a{};
@@ -329,11 +325,11 @@ int decode_block(const pmoe_geom* g, const pmoe_route_cfg* rc, const uint8_t* sl
 int experts_and_combine(const pmoe_geom* g, const uint8_t* slab, const int32_t* table,
                         int n_experts, const uint16_t* x, const int32_t* inds, const float* wts,
                         int n, int k, int shared_slot, const uint16_t* shared_gate, int max_rpe,
-                        uint16_t* out, const MoeWs& w, hipStream_t st, bool dispatched = false) {
+                        uint16_t* out, const MoeWs& w, hipStream_t st) {
   const int shared = shared_slot >= 0 ? 1 : 0;
   const int kk = k + shared;
   int rc = run_experts(g, slab, table, n_experts, shared_slot, x, inds, n, k, kk, max_rpe, w,
-                       w.y, 0, st, dispatched);
+                       w.y, 0, st);
   if (rc) return rc;
   const float* sl = nullptr;
   if (shared && shared_gate) {

@@ -155,11 +155,15 @@ int route_sigmoid(const float* logits, const float* bias, int n, int e, int n_gr
 
 // Dispatch (dispatch.hip).  Flat row r reads id inds[(r / kk) * k_routed +
 // r % kk] when r % kk < k_routed and the shared pseudo-id n_routed otherwise;
-// n_ids = n_routed + (kk > k_routed).
+// n_ids = n_routed + (kk > k_routed).  With tile_m > 0 it also writes the
+// prefill tile list: tile t of id e with c rows is {slot, t * tile_m, c,
+// offset of e}, slot = table[e] for routed ids, shared_slot for the shared
+// pseudo-id.
 size_t dispatch_workspace(int rows, int n_experts);
 int dispatch_ext(const int32_t* inds, int rows, int k_routed, int kk, int n_ids,
                  int32_t* order, int32_t* counts, int32_t* offsets, int32_t* inv,
-                 int32_t* active, int32_t* n_active, int tile_m, int2* tiles, int32_t* n_tiles,
-                 void* ws, size_t ws_bytes, hipStream_t st);
+                 int32_t* active, int32_t* n_active, int tile_m, int4* tiles, int32_t* n_tiles,
+                 const int32_t* table, int shared_slot, void* ws, size_t ws_bytes,
+                 hipStream_t st);
 
 }  // namespace pmoe

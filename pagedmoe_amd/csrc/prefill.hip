@@ -50,13 +50,8 @@ constexpr int kDnCols = 256;         // hidden columns per down block
 struct PrefillArgs {
   const uint8_t* slab;
   int64_t expert_bytes;
-  const int32_t* table;
-  int n_experts;
-  int shared_slot;
   const int32_t* order;
-  const int32_t* counts;
-  const int32_t* offsets;
-  const int2* tiles;
+  const int4* tiles;     // {slot, first row, expert rows, expert offset} per tile
   const int32_t* n_tiles;
   const uint16_t* act;   // gate/up: x [n, hidden]; down: h [rows, inter] in sorted order
   int kk;                // flat rows per token (gate/up activation gather)
@@ -68,9 +63,9 @@ struct PrefillArgs {
   int out_f32;
 };
 
-// Tile of this block: expert, first sorted position, row count, slot.
+// Tile of this block: first sorted position, row count, slot.
 struct TileInfo {
-  int e, p0, m, slot;
+  int p0, m, slot;
 };
 
 
@@ -562,17 +557,16 @@ __device__ __forceinline__ bool xcd_work(const PrefillArgs& a, int n_cols, TileI
   const int w = (lin & 7) * per + (lin >> 3);
   if ((lin >> 3) >= per || w >= total) return false;
   const int tp = w / n_cols;
-  const int2 tl = a.tiles[tp];
-  const int cnt = a.counts[tl.x];
+  const int4 tl = a.tiles[tp];                    // the tile record carries the expert's
+  const int cnt = tl.z;                           // slot, rows and offset
   const int t0 = tp - tl.y / TM;                  // the expert's first tile
   const int nt = (cnt + TM - 1) / TM;             // and its tile count
   const int l = w - t0 * n_cols;
   cb = l / nt;
   const int r0 = (l - cb * nt) * TM;              // first row of this item's tile
-  ti.e = tl.x;
   ti.m = min(TM, cnt - r0);
-  ti.p0 = a.offsets[tl.x] + r0;
-  ti.slot = tl.x < a.n_experts ? a.table[tl.x] : a.shared_slot;
+  ti.p0 = tl.w + r0;
+  ti.slot = tl.x;
   return true;
 }
 
@@ -754,11 +748,9 @@ bool prefill_wanted(const pmoe_geom* g, int n, int kk, int n_ids) {
   return rows >= 1024 && rows >= 16L * n_ids;
 }
 
-int prefill_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* table, int n_experts,
-                    int shared_slot, const uint16_t* x, int n, int kk, const int32_t* order,
-                    const int32_t* counts, const int32_t* offsets, const int2* tiles,
-                    const int32_t* n_tiles, int tile_m, int max_tiles, uint16_t* h, void* y,
-                    int y_f32, hipStream_t st) {
+int prefill_experts(const pmoe_geom* g, const uint8_t* slab, const uint16_t* x, int n, int kk,
+                    const int32_t* order, const int4* tiles, const int32_t* n_tiles, int tile_m,
+                    int max_tiles, uint16_t* h, void* y, int y_f32, hipStream_t st) {
   PMOE_REQUIRE(tile_m == 32 || tile_m == kTileM, "prefill: tile height must be 32 or 128");
   PMOE_REQUIRE(g->inter % 512 == 0 && g->hidden % 512 == 0,
                "prefill: hidden and inter must be multiples of 512");
@@ -770,12 +762,7 @@ int prefill_experts(const pmoe_geom* g, const uint8_t* slab, const int32_t* tabl
   PrefillArgs a{};
   a.slab = slab;
   a.expert_bytes = g->expert_bytes;
-  a.table = table;
-  a.n_experts = n_experts;
-  a.shared_slot = shared_slot;
   a.order = order;
-  a.counts = counts;
-  a.offsets = offsets;
   a.tiles = tiles;
   a.n_tiles = n_tiles;
   // gate + up -> h (sorted rows)
