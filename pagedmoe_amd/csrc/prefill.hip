@@ -360,63 +360,78 @@ __device__ __forceinline__ void gemm_tile(int n_groups, const StageRows& rows, c
 // 6-bit weights in coalesced units.  A lane's operand is half a group of
 // one row (24 bytes); read straight from HBM, each load instruction would
 // touch 32 rows for 512 bytes.  Instead a wave reads a unit -- 4 groups of
-// its 32 rows, 192 contiguous bytes a row -- as 6 loads of 16 bytes a lane
-// (piece p = 64 i + lane: row p / 12, bytes 16 (p % 12) of the unit), each
-// instruction covering runs of whole rows; copies the unit into its own
-// LDS buffer (row pitch 200 bytes: the 8-byte reads of 16 consecutive rows
-// fall on distinct banks) and reads each group's half rows back in the
-// operand layout.  The words are the same, so the dequant and the MFMAs
-// (and their results) are unchanged.
+// its 32 rows, 192 contiguous bytes a row -- as 6 loads of 16 bytes a lane,
+// copies it into its own LDS buffer (row pitch 200 bytes: the 8-byte reads
+// of 16 consecutive rows fall on distinct banks) and reads each group's
+// half rows back in the operand layout.  The words are the same, so the
+// dequant and the MFMAs (and their results) are unchanged.
+//
+// Rows are whole 128-byte lines (their length is a multiple of 384 bytes),
+// so units k and k + 1 (k even) of a row share the line of bytes
+// [192 k + 128, 192 k + 256).  The pieces a row owns outright (8 of its
+// 12: the unit's whole line) are loaded by 4 instructions of 8 rows x 128
+// bytes, non-temporal; the shared half line (4 pieces) by 2 instructions
+// of 16 rows x 64 bytes, cached, so that the unit 4 groups later can find
+// it in L2 instead of reading the line from HBM a second time.
 constexpr int kUnitPieces = 6;                  // 16-byte pieces a lane per unit
 constexpr int kUnitPitch = 200;                 // LDS bytes per row of a unit
 constexpr int kUnitLds = 32 * kUnitPitch;       // LDS bytes per wave
-static_assert(kUnitPitch == 12 * 16 + 8, "piece p of row r sits at 16 p + 8 r");
 
 struct Unit6 {
   u32x4 v[kUnitPieces];
 };
 
-// Row of piece p (p < 384): p / 12.
-__device__ __forceinline__ uint32_t unit_row(uint32_t p) { return (p * 43691u) >> 19; }
+// Piece i (0..5) of a lane in a unit of parity P: its row r and 16-byte
+// column c (0..11) within the row's 192 bytes.  Pieces 0-3: the unit's own
+// line (columns 0-7, or 4-11 for odd units); 4-5: the shared half line
+// (columns 8-11, or 0-3).
+template <int P>
+__device__ __forceinline__ void unit_piece(int i, uint32_t lane, uint32_t& r, uint32_t& c) {
+  if (i < 4) {
+    r = 8 * i + (lane >> 3);
+    c = (lane & 7) + 4 * P;
+  } else {
+    r = 16 * (i - 4) + (lane >> 2);
+    c = (lane & 3) + 8 * (1 - P);
+  }
+}
 
-// Copy the unit held in un to buf, then (if load) load unit k of the
-// wave's 32 rows into un (row 0 at w0, row_bytes apart; w0 is the same in
-// every lane, so each load takes it as a scalar base with a 32-bit lane
-// offset).  The pieces' rows are recomputed here (a few integer ops)
-// rather than held in registers across the loop.
+// Unit k (parity P) of the wave's 32 rows into un (row 0 at w0, row_bytes
+// apart; w0 is the same in every lane, so each load takes it as a scalar
+// base with a 32-bit lane offset).
+template <int P>
+__device__ __forceinline__ void load_unit6(Unit6& un, const uint8_t* w0, uint32_t row_bytes,
+                                           int k, uint32_t lane) {
+  const uint8_t* wk = w0 + 192 * k;
+#pragma unroll
+  for (int i = 0; i < kUnitPieces; ++i) {
+    uint32_t r, c;
+    unit_piece<P>(i, lane, r, c);
+    const u32x4* src = reinterpret_cast<const u32x4*>(wk + (r * row_bytes + 16 * c));
+    if (i < 4)
+      un.v[i] = __builtin_nontemporal_load(src);
+    else
+      un.v[i] = *src;
+  }
+}
+
+// Copy the unit held in un (parity P) to buf, then (if load) load unit k
+// (parity 1 - P) into un.
+template <int P>
 __device__ __forceinline__ void cycle_unit6(Unit6& un, uint8_t* buf, const uint8_t* w0,
                                             uint32_t row_bytes, int k, bool load) {
   uint32_t lane = threadIdx.x & 63;
-  asm volatile("" : "+v"(lane));  // opaque: not hoisted out of the loop
-  uint32_t r[kUnitPieces];
-#pragma unroll
-  for (int i = 0; i < kUnitPieces; ++i) r[i] = unit_row(64 * i + lane);
-  // piece p of row r at 16 p + 8 r = 200 r + 16 (p - 12 r)
-  uint8_t* d = buf + 16 * lane;
+  asm volatile("" : "+v"(lane));  // opaque: addresses recomputed here, not held across the loop
 #pragma unroll
   for (int i = 0; i < kUnitPieces; ++i) {
-    uint32_t* q = reinterpret_cast<uint32_t*>(d + 1024 * i + 8 * r[i]);
+    uint32_t r, c;
+    unit_piece<P>(i, lane, r, c);
+    uint32_t* q = reinterpret_cast<uint32_t*>(buf + r * kUnitPitch + 16 * c);
     *reinterpret_cast<u32x2*>(q) = u32x2{un.v[i][0], un.v[i][1]};
     *reinterpret_cast<u32x2*>(q + 2) = u32x2{un.v[i][2], un.v[i][3]};
   }
   __builtin_amdgcn_sched_barrier(0);  // the copy reads un before it is reloaded
-  if (load) {
-    // byte 16 (p - 12 r) of row r: r row_bytes + 16 (p - 12 r)
-    const uint8_t* wk = w0 + 192 * k;
-#pragma unroll
-    for (int i = 0; i < kUnitPieces; ++i)
-      un.v[i] = *reinterpret_cast<const u32x4*>(
-          wk + (16 * (64 * i + lane) + r[i] * (row_bytes - 192)));
-  }
-}
-
-// First unit of the wave's rows into un.
-__device__ __forceinline__ void load_unit6(Unit6& un, const uint8_t* w0, uint32_t row_bytes) {
-  const uint32_t lane = threadIdx.x & 63;
-#pragma unroll
-  for (int i = 0; i < kUnitPieces; ++i)
-    un.v[i] = *reinterpret_cast<const u32x4*>(
-        w0 + (16 * (64 * i + lane) + unit_row(64 * i + lane) * (row_bytes - 192)));
+  if (load) load_unit6<1 - P>(un, w0, row_bytes, k, lane);
 }
 
 // Group gi (0..3) of the unit at lds + rd, where rd is the lane's half row
@@ -464,11 +479,11 @@ __device__ __forceinline__ void gemm_tile_u6(int n_groups, const StageRows& rows
   u32x4 B[2][4];
   load_sblk(S[0], lr, 0);
   load_sblk(S[1], lr, min(1, last_blk));
-  load_unit6(U, w0, row_bytes);
+  load_unit6<0>(U, w0, row_bytes, 0, threadIdx.x & 63);
   stage_load<NMB>(rows, 0, X[0]);
   stage_store<NMB>(lds, X[0]);
   stage_load<NMB>(rows, min(1, last), X[1]);
-  cycle_unit6(U, wbuf, w0, row_bytes, 1, true);
+  cycle_unit6<0>(U, wbuf, w0, row_bytes, 1, true);
   read_group6(Wn, lds8, rd, 0);
 #pragma unroll
   for (int jb = 0; jb < 8; ++jb) dequant_job<6>(Wn, S[0], 0, jb, B[0]);
@@ -478,10 +493,12 @@ __device__ __forceinline__ void gemm_tile_u6(int n_groups, const StageRows& rows
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int j = j0 + u;
-      // group j+1 opens unit un (held in U)
+      // group j+1 opens unit un (held in U; odd at u = 3, even at u = 7)
       const int un = (j + 1) >> 2;
-      if ((u & 3) == 3 && un <= last_unit)
-        cycle_unit6(U, wbuf, w0, row_bytes, un + 1, un + 1 <= last_unit);
+      if (u == 3 && un <= last_unit)
+        cycle_unit6<1>(U, wbuf, w0, row_bytes, un + 1, un + 1 <= last_unit);
+      if (u == 7 && un <= last_unit)
+        cycle_unit6<0>(U, wbuf, w0, row_bytes, un + 1, un + 1 <= last_unit);
       read_group6(Wn, lds8, rd, (u + 1) & 3);
       stage_load<NMB>(rows, min(j + 2, last), X[u & 1]);
       const uint16_t* xs = lds + (u & 1) * (SR * kLdsRow) + m * kLdsRow + 32 * h;
