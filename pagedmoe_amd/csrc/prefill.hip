@@ -517,6 +517,115 @@ __device__ __forceinline__ void gemm_tile_u6(int n_groups, const StageRows& rows
 // Row of accumulator register r of a 32x32 block for lane half h.
 __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 
+// 4-bit weights in units of 4 groups: one 128-byte line of each of the
+// wave's 32 rows.  A unit is loaded as 4 instructions of 8 rows x 128
+// bytes (lane l: row 8 i + l / 8, 16-byte column l % 8), non-temporal
+// since no line is read again, copied to the wave's LDS buffer (row pitch
+// 144 bytes: the 16-byte reads of 16 consecutive rows fall on distinct
+// banks), and each group's half row is read back in the operand layout
+// (16 bytes a lane, where the direct form loaded them from HBM with each
+// instruction touching 32 rows).  Same words, same results.
+constexpr int kUnit4Pitch = 144;
+constexpr int kUnit4Lds = 32 * kUnit4Pitch;  // LDS bytes per wave
+
+struct Unit4 {
+  u32x4 v[4];
+};
+
+__device__ __forceinline__ void load_unit4(Unit4& un, const uint8_t* w0, uint32_t row_bytes, int k,
+                                           uint32_t lane) {
+  const uint8_t* wk = w0 + 128 * k;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    un.v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+        wk + ((8 * i + (lane >> 3)) * row_bytes + 16 * (lane & 7))));
+}
+
+// Copy the unit held in un to buf, then (if load) load unit k into un.
+__device__ __forceinline__ void cycle_unit4(Unit4& un, uint8_t* buf, const uint8_t* w0,
+                                            uint32_t row_bytes, int k, bool load) {
+  uint32_t lane = threadIdx.x & 63;
+  asm volatile("" : "+v"(lane));  // opaque: addresses recomputed here, not held across the loop
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    *reinterpret_cast<u32x4*>(buf + (8 * i + (lane >> 3)) * kUnit4Pitch + 16 * (lane & 7)) =
+        un.v[i];
+  __builtin_amdgcn_sched_barrier(0);  // the copy reads un before it is reloaded
+  if (load) load_unit4(un, w0, row_bytes, k, lane);
+}
+
+// Group gi (0..3) of the unit at lds + rd (rd: the lane's half row).
+__device__ __forceinline__ void read_group4(LaneWords<4>& lw, const uint8_t* lds, uint32_t rd,
+                                            int gi) {
+  const u32x4 t = *reinterpret_cast<const u32x4*>(lds + rd + 32 * gi);
+  lw.w[0] = t[0];
+  lw.w[1] = t[1];
+  lw.w[2] = t[2];
+  lw.w[3] = t[3];
+}
+
+// gemm_tile for 4-bit weights read in units (128-row tiles): the same
+// pipeline, the weights of group j+1 read from the wave's LDS copy of
+// their unit; one unit in registers, loaded when the previous one is
+// copied (4 groups ahead).  n_groups is a multiple of 8.
+template <int NMB, int MB>
+__device__ __forceinline__ void gemm_tile_u4(int n_groups, const StageRows& rows,
+                                             const uint8_t* w0, uint32_t row_bytes,
+                                             const LaneRow& lr, uint16_t* lds, uint8_t* wbuf,
+                                             f32x16 (&acc)[MB]) {
+  static_assert(NMB <= MB, "row blocks beyond the accumulators");
+  constexpr int SR = stage_rows<MB>();
+  const int lane = threadIdx.x & 63;
+  const int m = lane & 31;
+  const int h = lane >> 5;
+  const int last = n_groups - 1;
+  const int last_blk = (n_groups >> 3) - 1;
+  const int last_unit = (n_groups >> 2) - 1;
+  const uint8_t* lds8 = reinterpret_cast<const uint8_t*>(lds);
+  uint32_t rd = uint32_t(wbuf - lds8) + m * kUnit4Pitch + 16 * h;
+  asm volatile("" : "+v"(rd));  // one base register for every group's reads
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x16{};
+  Unit4 U;
+  LaneWords<4> Wn;
+  StageRegs X[2];
+  SBlk S[2];
+  u32x4 B[2][4];
+  load_sblk(S[0], lr, 0);
+  load_sblk(S[1], lr, min(1, last_blk));
+  load_unit4(U, w0, row_bytes, 0, threadIdx.x & 63);
+  stage_load<NMB>(rows, 0, X[0]);
+  stage_store<NMB>(lds, X[0]);
+  stage_load<NMB>(rows, min(1, last), X[1]);
+  cycle_unit4(U, wbuf, w0, row_bytes, 1, true);
+  read_group4(Wn, lds8, rd, 0);
+#pragma unroll
+  for (int jb = 0; jb < 8; ++jb) dequant_job<4>(Wn, S[0], 0, jb, B[0]);
+  __syncthreads();
+
+  for (int j0 = 0; j0 < n_groups; j0 += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = j0 + u;
+      // group j+1 opens unit un (held in U)
+      const int un = (j + 1) >> 2;
+      if ((u & 3) == 3 && un <= last_unit)
+        cycle_unit4(U, wbuf, w0, row_bytes, un + 1, un + 1 <= last_unit);
+      read_group4(Wn, lds8, rd, (u + 1) & 3);
+      stage_load<NMB>(rows, min(j + 2, last), X[u & 1]);
+      const uint16_t* xs = lds + (u & 1) * (SR * kLdsRow) + m * kLdsRow + 32 * h;
+      group_mfma<4, NMB, MB>(xs, B[u & 1], Wn, u < 7 ? S[0] : S[1], (u + 1) & 7,
+                             B[(u + 1) & 1], acc);
+      stage_store<NMB>(lds + ((u + 1) & 1) * (SR * kLdsRow), X[(u + 1) & 1]);
+      if (u == 7) {
+        S[0] = S[1];
+        load_sblk(S[1], lr, min((j0 >> 3) + 2, last_blk));
+      }
+      __syncthreads();
+    }
+  }
+}
+
 template <int BITS, int MB>
 __device__ __forceinline__ void gemm_tile_any(int nmb, int n_groups, const StageRows& rows,
                                               const LaneRow& lr, const uint8_t* w0,
@@ -531,6 +640,13 @@ __device__ __forceinline__ void gemm_tile_any(int nmb, int n_groups, const Stage
       gemm_tile<BITS, 1, 1, 7>(n_groups, rows, lr, lds, acc);
     else
       gemm_tile<BITS, 1, 1>(n_groups, rows, lr, lds, acc);
+  } else if constexpr (BITS == 4) {
+    switch (nmb) {
+      case 1: gemm_tile_u4<1, MB>(n_groups, rows, w0, row_bytes, lr, lds, wbuf, acc); break;
+      case 2: gemm_tile_u4<2, MB>(n_groups, rows, w0, row_bytes, lr, lds, wbuf, acc); break;
+      case 3: gemm_tile_u4<3, MB>(n_groups, rows, w0, row_bytes, lr, lds, wbuf, acc); break;
+      default: gemm_tile_u4<MB, MB>(n_groups, rows, w0, row_bytes, lr, lds, wbuf, acc); break;
+    }
   } else {
     switch (nmb) {
       case 1: gemm_tile<BITS, 1, MB>(n_groups, rows, lr, lds, acc); break;
@@ -607,8 +723,12 @@ constexpr int stage_bytes() {
   return 2 * stage_rows<MB>() * kLdsRow * 2;
 }
 template <int BITS, int MB>
+constexpr int unit_wave_bytes() {
+  return BITS == 6 && MB == 1 ? kUnitLds : BITS == 4 && MB > 1 ? kUnit4Lds : 0;
+}
+template <int BITS, int MB>
 constexpr int unit_lds_bytes() {
-  return BITS == 6 && MB == 1 ? (kThreads / 64) * kUnitLds : 0;
+  return (kThreads / 64) * unit_wave_bytes<BITS, MB>();
 }
 template <int BITS, int MB>
 constexpr int gateup_lds_bytes() {
@@ -646,7 +766,7 @@ __global__ __launch_bounds__(kThreads, MB < kMB ? 4 : 1) void gateup_mfma_kernel
   const int col0 = cb * kGuCols + wq * 32;  // the wave's first row (uniform)
   const uint8_t* w0 = base + (up ? a.w1 : a.w0) + size_t(col0) * row_bytes;
   uint8_t* wbuf = lds_raw + gateup_lds_bytes<BITS, MB>() - unit_lds_bytes<BITS, MB>() +
-                  wave * kUnitLds;
+                  wave * unit_wave_bytes<BITS, MB>();
   const StageRows rows = tile_rows(a.act, a.order, a.kk, a.cols, ti.p0, ti.m);
   f32x16 acc[MB];
   const int nmb = (ti.m + 31) >> 5;
@@ -711,7 +831,7 @@ __global__ __launch_bounds__(kThreads, MB < kMB ? 4 : 1) void down_mfma_kernel(c
   lr.b = reinterpret_cast<const u32x4*>(base + a.b0) + size_t(col) * blks;
   const int col0 = cb * kDnCols + wave * 32;  // the wave's first row (uniform)
   const uint8_t* w0 = base + a.w0 + size_t(col0) * row_bytes;
-  uint8_t* wbuf = lds_raw + stage_bytes<MB>() + wave * kUnitLds;
+  uint8_t* wbuf = lds_raw + stage_bytes<MB>() + wave * unit_wave_bytes<BITS, MB>();
   const StageRows rows = tile_rows(a.act, nullptr, 1, a.cols, ti.p0, ti.m);
   f32x16 acc[MB];
   const int nmb = (ti.m + 31) >> 5;
