@@ -833,6 +833,10 @@ __global__ __launch_bounds__(kThreads, MB < kMB ? 4 : 1) void down_mfma_kernel(c
   const uint8_t* w0 = base + a.w0 + size_t(col0) * row_bytes;
   uint8_t* wbuf = lds_raw + stage_bytes<MB>() + wave * unit_wave_bytes<BITS, MB>();
   const StageRows rows = tile_rows(a.act, nullptr, 1, a.cols, ti.p0, ti.m);
+  // the tile's output rows, read while the weights stream (the main loop's
+  // barriers publish them), not one dependent load per row at the end
+  __shared__ int32_t s_ord[32 * MB];
+  if (int(threadIdx.x) < ti.m) s_ord[threadIdx.x] = a.order[ti.p0 + threadIdx.x];
   f32x16 acc[MB];
   const int nmb = (ti.m + 31) >> 5;
   gemm_tile_any<BITS, MB>(nmb, groups, rows, lr, w0, uint32_t(row_bytes), lds, wbuf, acc);
@@ -842,7 +846,7 @@ __global__ __launch_bounds__(kThreads, MB < kMB ? 4 : 1) void down_mfma_kernel(c
     for (int r = 0; r < 16; ++r) {
       const int row = mb * 32 + acc_row(r, h);
       if (row < ti.m) {
-        const size_t o = size_t(a.order[ti.p0 + row]) * a.out_cols;
+        const size_t o = size_t(s_ord[row]) * a.out_cols;
         if (a.out_f32)
           static_cast<float*>(a.out)[o + col] = acc[mb][r];
         else
