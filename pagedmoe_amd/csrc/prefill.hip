@@ -771,28 +771,32 @@ __global__ __launch_bounds__(kThreads, MB < kMB ? 4 : 1) void gateup_mfma_kernel
   f32x16 acc[MB];
   const int nmb = (ti.m + 31) >> 5;
   gemm_tile_any<BITS, MB>(nmb, groups, rows, lr, w0, uint32_t(row_bytes), lds, wbuf, acc);
-  // SwiGLU: up wave wq + 4 hands its accumulators (the same rows and
-  // columns, lane for lane) to gate wave wq through LDS (the staging
-  // buffers are free: the main loop ended with a block barrier)
+  // SwiGLU: gate wave wq and up wave wq + 4 hold the same rows and columns,
+  // lane for lane, and swap halves through LDS (the staging buffers are
+  // free: the main loop ended with a block barrier).  With several row
+  // blocks each computes half of them (the up wave hands over the first
+  // half, the gate wave the second); with one, the gate wave computes it.
+  // h = silu(gate) * up either way.
   float* ul = reinterpret_cast<float*>(lds_raw);
-  if (up) {
+  constexpr int kSplit = MB > 1 ? MB / 2 : MB;  // row blocks the gate wave computes
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-      if (mb < nmb)
+  for (int mb = 0; mb < MB; ++mb)
+    if (mb < nmb && (up ? mb < kSplit : mb >= kSplit))
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ul[((wq * MB + mb) * 16 + r) * 64 + lane] = acc[mb][r];
-  }
+      for (int r = 0; r < 16; ++r) ul[((wq * MB + mb) * 16 + r) * 64 + lane] = acc[mb][r];
   __syncthreads();
-  if (up) return;
   uint16_t* hout = static_cast<uint16_t*>(a.out);
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
+    if (up ? mb < kSplit : mb >= kSplit) continue;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = mb * 32 + acc_row(r, h);
       if (row < ti.m) {
-        const float u = ul[((wq * MB + mb) * 16 + r) * 64 + lane];
-        const float v = silu_fast(acc[mb][r]) * u;
+        const float o = ul[((wq * MB + mb) * 16 + r) * 64 + lane];
+        const float g = up ? o : acc[mb][r];
+        const float u = up ? acc[mb][r] : o;
+        const float v = silu_fast(g) * u;
         hout[size_t(ti.p0 + row) * a.out_cols + col] = f2bf(v);
       }
     }
