@@ -22,13 +22,10 @@ one layer later (streaming.py:2002).  PREFETCH_DEPTH adds the previous-token
 heuristic: the next layers' last routed ids (streaming.py:2283-2299).
 
 Whether prediction pays is measured, not modelled (streaming.py:1790-1970):
-with predict mode "auto", windows of PREDICT_WINDOW decode tokens alternate
-prediction on and off, tokens/s is pooled per state, and once each side has
-PREDICT_MIN_TOKENS the faster state wins if the gap clears both
-PREDICT_MARGIN and PREDICT_Z error bars; the decision holds PREDICT_HOLD
-windows, then half the evidence is kept and the probe resumes.  Wrong
-guesses cost copy bandwidth, so on a link-bound workload with guesses that
-are often wrong the governor settles on off.
+with predict mode "auto", governor.PredictGovernor compares adjacent
+windows of decode tokens run with prediction on and off.  Wrong guesses
+cost copy bandwidth, so on a link-bound workload with guesses that are
+often wrong it settles on off.
 
 Flow decode.  The slot table is already on the GPU and the expert kernels
 read it directly, computing an exact zero row for every routed expert that
@@ -60,11 +57,10 @@ layers can be captured in one HIP graph and replayed after each
 
 from __future__ import annotations
 
-import time
-
 import torch
 
 from . import config
+from .governor import PredictGovernor
 
 
 class PrefetchRing:
@@ -265,99 +261,3 @@ class PrefetchRing:
                 "pred_issued": self.pred_issued, "pred_used": self.pred_used,
                 "pred_precision": self.pred_used / self.pred_issued if self.pred_issued else None,
                 "spec_reads": self.spec_reads}
-
-
-class PredictGovernor:
-    """A/B governor of route prediction (mode "auto"); "on" and "off" pin
-    the depth.  ``token()`` is called at every decode token boundary."""
-
-    def __init__(self, ring: PrefetchRing, mode: str):
-        self.ring = ring
-        self.depth = ring.predict_depth
-        self.mode = mode if mode in ("on", "off", "auto") else "auto"
-        if self.mode == "off":
-            ring.predict_depth = 0
-        self.decision = None
-        self.probing = True
-        self.hold_left = 0
-        self.last_t = None
-        self.win_tokens = 0
-        self.win_time = 0.0
-        self.acc = {True: [0.0, 0.0, 0.0, 0.0], False: [0.0, 0.0, 0.0, 0.0]}  # n, sum, sumsq, tokens
-        self.log: list = []
-
-    def set_mode(self, mode: str) -> None:
-        self.mode = mode
-        self.ring.predict_depth = 0 if mode == "off" else self.depth
-        self.probing, self.decision = mode == "auto", None
-
-    def describe(self) -> dict:
-        return {"mode": self.mode, "decision": self.decision, "probing": self.probing,
-                "depth": self.ring.predict_depth}
-
-    def token(self) -> None:
-        if self.mode != "auto" or self.depth <= 0:
-            return
-        now = time.perf_counter()
-        prev, self.last_t = self.last_t, now
-        if prev is None or now - prev > 1.0:    # a gap between requests, not a step
-            return
-        self.win_time += now - prev
-        self.win_tokens += 1
-        if self.win_tokens < max(4, int(config.PREDICT_WINDOW)):
-            return
-        tokens, seconds = self.win_tokens, self.win_time
-        self.win_tokens, self.win_time = 0, 0.0
-        self._window(tokens, seconds)
-
-    def _settle(self, on: bool, reason: str, hold: int) -> None:
-        self.ring.predict_depth = self.depth if on else 0
-        self.probing = False
-        self.hold_left = hold
-        self.decision = on
-        self.log.append(reason)
-
-    def _window(self, tokens: int, seconds: float) -> None:
-        active = self.ring.predict_depth > 0
-        if not self.probing:
-            self.hold_left -= 1
-            if self.hold_left <= 0:
-                for a in self.acc.values():
-                    for i in range(4):
-                        a[i] *= 0.5
-                self.probing = True
-                self.ring.predict_depth = self.depth
-            return
-        rate = tokens / seconds
-        a = self.acc[active]
-        a[0] += 1.0
-        a[1] += rate
-        a[2] += rate * rate
-        a[3] += tokens
-        self.ring.predict_depth = 0 if active else self.depth   # alternate
-        floor = max(int(config.PREDICT_WINDOW), int(config.PREDICT_MIN_TOKENS))
-        if min(self.acc[True][3], self.acc[False][3]) < floor:
-            return
-        (on_r, on_v, on_n), (off_r, off_v, off_n) = (self._stats(self.acc[True]),
-                                                     self._stats(self.acc[False]))
-        if on_n < 2 or off_n < 2:
-            return
-        err = (on_v / on_n + off_v / off_n) ** 0.5
-        gap = on_r - off_r
-        need = max((float(config.PREDICT_MARGIN) - 1.0) * off_r, float(config.PREDICT_Z) * err)
-        what = f"{on_r:.1f} tok/s with prediction, {off_r:.1f} without (+/-{config.PREDICT_Z * err:.1f})"
-        hold = int(config.PREDICT_HOLD)
-        if gap > need:
-            self._settle(True, "on: " + what, hold)
-        elif -gap > need:
-            self._settle(False, "off: " + what, hold)
-        elif min(self.acc[True][3], self.acc[False][3]) >= floor * int(config.PREDICT_MAX_PROBE):
-            self._settle(False, "off, no measurable difference: " + what, 4 * hold)
-
-    @staticmethod
-    def _stats(a):
-        n, total, total_sq = a[0], a[1], a[2]
-        if n < 2:
-            return (total / n if n else 0.0), float("inf"), n
-        mean = total / n
-        return mean, max(0.0, (total_sq - total * mean) / (n - 1)), n
