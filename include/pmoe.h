@@ -468,6 +468,44 @@ int pmoe_slab_fetch_prefill(pmoe_slab* s, pmoe_copy_engine* ce,
                             const int32_t* ids, int n_ids, int* n_miss,
                             int* n_unplaced, int* ticket);
 
+/* ---- slot-safety ledger (replaces PAGED_MOE_SLAB_VERIFY's per-slot
+ *      write-in-flight counters and check_slots, cache.py:554-556,
+ *      :1171-1206) ----------------------------------------------------------
+ * A debug log of every event that orders slot writes against compute: the
+ * copy engines record fences, queued copies (dst, src, bytes), issues,
+ * joins and host-observed completions; the slab records each row it
+ * publishes (a PUBLISH, then one ROW per resident expert); the caller notes
+ * each compute it enqueues (pmoe_ledger_note with PMOE_LEDGER_COMPUTE).
+ * Off by default; when off nothing is recorded.  One log for the process,
+ * in call order; `who` is the engine or slab handle.  A checker replays it
+ * and flags a copy issued while an earlier compute may still read its slot,
+ * a compute reading a slot whose copy it did not wait for, and a row that
+ * maps an expert to a slot holding another. */
+enum {
+  PMOE_LEDGER_FENCE = 1,      /* who=engine */
+  PMOE_LEDGER_SUBMIT = 2,     /* who=engine, a=dst, b=src, c=bytes */
+  PMOE_LEDGER_ISSUE = 3,      /* who=engine, a=batch (-1: none) */
+  PMOE_LEDGER_JOIN = 4,       /* who=engine: stream waits for every issued copy */
+  PMOE_LEDGER_BATCH_JOIN = 5, /* who=engine, a=batch */
+  PMOE_LEDGER_HOST_DONE = 6,  /* who=engine, a=batch: the host saw it complete */
+  PMOE_LEDGER_HOST_SYNC = 7,  /* who=engine: the host waited for every copy */
+  PMOE_LEDGER_PUBLISH = 8,    /* who=slab, a=layer: the row below replaces it */
+  PMOE_LEDGER_ROW = 9,        /* who=slab, a=layer, b=expert, c=slot */
+  PMOE_LEDGER_COMPUTE = 10    /* who=slab, a=layer: a compute reading the row */
+};
+
+typedef struct {
+  int64_t kind, who, a, b, c;
+} pmoe_ledger_rec;
+
+/* Turn recording on (clearing the log) or off. */
+int pmoe_ledger_enable(int on);
+/* Append a caller event (PMOE_LEDGER_COMPUTE); ignored while off. */
+int pmoe_ledger_note(int64_t kind, const void* who, int64_t a, int64_t b, int64_t c);
+/* Move up to cap records, oldest first, into out; *n receives the count.
+ * Returns the number of records dropped because the log was full (0). */
+int pmoe_ledger_drain(pmoe_ledger_rec* out, int cap, int* n);
+
 /* ---- measurement probes ---------------------------------------------------
  * No reference counterpart.  Kernels of known HBM traffic that bench.py runs
  * next to the kernels it measures: a streaming read with the expert

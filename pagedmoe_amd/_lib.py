@@ -60,6 +60,10 @@ class SlabStats(ctypes.Structure):
         "spec_started", "spec_claims", "spec_claims_late", "spec_dropped")]
 
 
+class LedgerRec(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int64) for n in ("kind", "who", "a", "b", "c")]
+
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
@@ -135,6 +139,10 @@ SIGNATURES = {
     "pmoe_slab_fetch_prefill": (_I, [_P, _P, ctypes.POINTER(Geom), _P, _P, _I, _I32P, _I,
                                      ctypes.POINTER(_I), ctypes.POINTER(_I),
                                      ctypes.POINTER(_I)]),
+    "pmoe_ledger_enable": (_I, [_I]),
+    "pmoe_ledger_note": (_I, [ctypes.c_int64, _P, ctypes.c_int64, ctypes.c_int64,
+                              ctypes.c_int64]),
+    "pmoe_ledger_drain": (_I, [ctypes.POINTER(LedgerRec), _I, ctypes.POINTER(_I)]),
     "pmoe_probe_sink_bytes": (_SZ, []),
     "pmoe_probe_read": (_I, [_P, _SZ, _P, _SZ, _P]),
     "pmoe_probe_copy": (_I, [_P, _P, _SZ, _P]),

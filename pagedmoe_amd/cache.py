@@ -175,6 +175,50 @@ class ExpertCache:
         self.stitched = False
         self.group_passes = 0
         self.spec_log = None     # a list records fetch / speculate calls (tests replay them)
+        self.ledger = None       # slot-safety ledger (config.SLAB_VERIFY)
+        if config.SLAB_VERIFY:
+            self.verify_slots(True)
+
+    # ------------------------------------------------------------- slot safety
+
+    def _locate(self, dst: int, src: int, nbytes: int):
+        """(slot, (layer index, expert)) of a whole-expert copy into this
+        slab, or None for other copies."""
+        eb = int(self.geom.expert_bytes)
+        off = dst - self.slab.data_ptr
+        if nbytes != eb or off < 0 or off % eb or off // eb >= self.slab.slots:
+            return None
+        owner = None
+        if self.host_store is not None:
+            key, rem = divmod(src - self.host_store.address, eb)
+            if rem == 0 and 0 <= key < self.host_store.n_layers * self.n_experts:
+                owner = divmod(key, self.n_experts)
+        return off // eb, owner
+
+    def verify_slots(self, on: bool = True):
+        """Start (or stop) replaying this cache's copy and compute ordering
+        through a ``verify.SlotLedger`` (the reference's
+        PAGED_MOE_SLAB_VERIFY).  Returns the ledger."""
+        from . import verify
+
+        if on and self.ledger is None:
+            engines = [e.value for e in (self._ce, self._ce_spec) if e.value]
+            self.ledger = verify.SlotLedger(self._h.value, engines, self._locate)
+            verify.attach(self.ledger)
+        elif not on and self.ledger is not None:
+            verify.detach(self.ledger)
+        return self.ledger
+
+    def note_compute(self, layer_key) -> None:
+        """A compute reading the layer's uploaded row has just been
+        enqueued (a no-op unless the slot ledger is on)."""
+        if self.ledger is None:
+            return
+        from . import verify
+
+        check(lib().pmoe_ledger_note(verify.COMPUTE, self._h, self.layer_index(layer_key), 0, 0),
+              "pmoe_ledger_note")
+        verify.drain()
 
     @classmethod
     def from_budget(cls, budget_bytes: int, g: Geom, layer_keys, n_experts: int, **kw):
@@ -505,9 +549,12 @@ class ExpertCache:
             "stage_slots": st.stage_slots, "flow_admits": st.flow_admits,
             "spec_started": st.spec_started, "spec_claims": st.spec_claims,
             "spec_claims_late": st.spec_claims_late, "spec_dropped": st.spec_dropped,
+            "slab_conflicts": None if self.ledger is None else len(self.ledger.conflicts),
         }
 
     def close(self) -> None:
+        if self.ledger is not None:
+            self.verify_slots(False)
         if self._ce_spec.value:
             lib().pmoe_copy_sync(self._ce_spec)
             lib().pmoe_slab_drop_staged(self._h)

@@ -9,7 +9,8 @@ fused prefill pass; FLOW / FLOW_WARMUP / FLOW_WARM_HIT :1218-1237 for flow
 decode; PREDICT_DEPTH :747, PREDICT_SLACK :761 and PREFETCH_DEPTH :722 for
 speculative prefetch (PREFETCH_DEPTH defaults to 0 here: the previous-token
 heuristic pays off with the reference's SSD queue, not a PCIe copy engine);
-PREDICT and the governor knobs :735-741.
+PREDICT and the governor knobs :735-741; SLAB_VERIFY :1467 for the
+slot-safety ledger.
 DECODE_MAX_TOKENS is the reference's _DECODE_MAX_TOKENS
 (streaming.py:69): calls of more tokens take the prefill residency policy.
 """
@@ -59,6 +60,7 @@ PREDICT_MAX_PROBE = 6     # governor: inconclusive after this many times the evi
 PREDICT_HOLD = 128        # governor: windows a decision is kept before re-probing
 ATTN_SUB_CHUNK = 2048     # rows per attention sub-chunk, at most
 ATTN_SCORE_MB = 1024      # fp32 score matrix (heads x rows x keys) of one sub-chunk, at most
+SLAB_VERIFY = False       # replay copy/compute ordering per slot and flag races (debug)
 
 
 def sync_from_environ() -> None:
@@ -67,6 +69,7 @@ def sync_from_environ() -> None:
     global FUSED_PREFILL, ATTN_SUB_CHUNK, ATTN_SCORE_MB, FLOW, FLOW_WARMUP, FLOW_WARM_HIT
     global PREDICT_DEPTH, PREDICT_SLACK, PREFETCH_DEPTH, PREDICT, PREDICT_WINDOW
     global PREDICT_MIN_TOKENS, PREDICT_MARGIN, PREDICT_Z, PREDICT_MAX_PROBE, PREDICT_HOLD
+    global SLAB_VERIFY
     SLAB_RESERVE_FRAC = _env("SLAB_RESERVE_FRAC", 0.1, float)
     LFRU = _env("LFRU", True, _bool)
     LFRU_SCAN = _env("LFRU_SCAN", 8, int)
@@ -93,6 +96,7 @@ def sync_from_environ() -> None:
     PREDICT_Z = _env("PREDICT_Z", 2.0, float)
     PREDICT_MAX_PROBE = _env("PREDICT_MAX_PROBE", 6, int)
     PREDICT_HOLD = _env("PREDICT_HOLD", 128, int)
+    SLAB_VERIFY = _env("SLAB_VERIFY", False, _bool)
 
 
 sync_from_environ()

@@ -17,6 +17,7 @@
 // for group i+1 are already in flight").  All streams have default priority.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <deque>
 #include <mutex>
 #include <vector>
@@ -24,6 +25,59 @@
 #include "pmoe_internal.h"
 
 constexpr int kMaxBatches = 64;
+
+// ---------------------------------------------------------------- ledger
+// The slot-safety log: one vector for the process, in call order, capped so
+// a forgotten drain cannot grow without bound (drops are counted).
+namespace {
+constexpr size_t kLedgerCap = size_t(1) << 22;
+std::atomic<bool> g_ledger_on{false};
+std::mutex g_ledger_mu;
+std::vector<pmoe_ledger_rec> g_ledger;
+int64_t g_ledger_dropped = 0;
+}  // namespace
+
+namespace pmoe {
+bool ledger_on() { return g_ledger_on.load(std::memory_order_relaxed); }
+void ledger_put(int64_t kind, const void* who, int64_t a, int64_t b, int64_t c) {
+  if (!ledger_on()) return;
+  std::lock_guard<std::mutex> lk(g_ledger_mu);
+  if (g_ledger.size() >= kLedgerCap) {
+    ++g_ledger_dropped;
+    return;
+  }
+  g_ledger.push_back({kind, int64_t(reinterpret_cast<uintptr_t>(who)), a, b, c});
+}
+}  // namespace pmoe
+
+extern "C" int pmoe_ledger_enable(int on) {
+  pmoe::clear_error();
+  std::lock_guard<std::mutex> lk(g_ledger_mu);
+  g_ledger.clear();
+  g_ledger_dropped = 0;
+  g_ledger_on.store(on != 0);
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_ledger_note(int64_t kind, const void* who, int64_t a, int64_t b, int64_t c) {
+  pmoe::clear_error();
+  if (kind != PMOE_LEDGER_COMPUTE) return pmoe::fail(PMOE_EINVAL, "ledger_note: caller events are COMPUTE");
+  pmoe::ledger_put(kind, who, a, b, c);
+  return PMOE_OK;
+}
+
+extern "C" int pmoe_ledger_drain(pmoe_ledger_rec* out, int cap, int* n) {
+  pmoe::clear_error();
+  if (!n || cap < 0 || (cap > 0 && !out)) return pmoe::fail(PMOE_EINVAL, "ledger_drain: bad argument");
+  std::lock_guard<std::mutex> lk(g_ledger_mu);
+  const size_t take = std::min(g_ledger.size(), size_t(cap));
+  std::copy_n(g_ledger.begin(), take, out);
+  g_ledger.erase(g_ledger.begin(), g_ledger.begin() + take);
+  *n = int(take);
+  const int64_t dropped = g_ledger_dropped;
+  g_ledger_dropped = 0;
+  return int(std::min<int64_t>(dropped, 1 << 30));
+}
 
 struct pmoe_copy_engine {
   struct Job {
@@ -123,6 +177,8 @@ extern "C" int pmoe_copy_submit(pmoe_copy_engine* ce, void* dst, const void* src
   if (!bytes) return PMOE_OK;
   std::lock_guard<std::mutex> lk(ce->mu);
   (urgent ? ce->urgent : ce->normal).push_back({dst, src, bytes});
+  pmoe::ledger_put(PMOE_LEDGER_SUBMIT, ce, int64_t(reinterpret_cast<uintptr_t>(dst)),
+                   int64_t(reinterpret_cast<uintptr_t>(src)), int64_t(bytes));
   return PMOE_OK;
 }
 
@@ -132,12 +188,15 @@ extern "C" int pmoe_copy_fence(pmoe_copy_engine* ce, void* stream) {
   std::lock_guard<std::mutex> lk(ce->mu);
   PMOE_HIP(hipEventRecord(ce->fence, static_cast<hipStream_t>(stream)));
   ce->fenced = true;
+  pmoe::ledger_put(PMOE_LEDGER_FENCE, ce);
   return PMOE_OK;
 }
 
-// Caller holds mu.
-static int issue_locked(pmoe_copy_engine* ce) {
+// Caller holds mu.  batch: the batch record the copies form (-1: none),
+// for the ledger.
+static int issue_locked(pmoe_copy_engine* ce, int batch) {
   if (ce->urgent.empty() && ce->normal.empty()) return PMOE_OK;
+  pmoe::ledger_put(PMOE_LEDGER_ISSUE, ce, batch);
   if (ce->fenced)
     for (hipStream_t s : ce->streams) PMOE_HIP(hipStreamWaitEvent(s, ce->fence, 0));
   int first_err = PMOE_OK;
@@ -176,7 +235,7 @@ extern "C" int pmoe_copy_issue(pmoe_copy_engine* ce, int* batch) {
       if (!ce->batches[i].live) b = i;
     if (b < 0) return pmoe::fail(PMOE_EINVAL, "copy_issue: every batch record is in use");
   }
-  const int rc = issue_locked(ce);
+  const int rc = issue_locked(ce, b);
   if (rc) return rc;
   if (batch) {
     for (size_t i = 0; i < ce->streams.size(); ++i)
@@ -194,6 +253,7 @@ static pmoe_copy_engine::Batch* live_batch(pmoe_copy_engine* ce, int b) {
 
 extern "C" int pmoe_copy_batch_done(pmoe_copy_engine* ce, int batch) {
   pmoe::clear_error();
+  if (!ce) return pmoe::fail(PMOE_EINVAL, "copy_batch_done: null engine");
   std::lock_guard<std::mutex> lk(ce->mu);
   auto* b = live_batch(ce, batch);
   if (!b) return pmoe::fail(PMOE_EINVAL, "copy_batch_done: no such batch");
@@ -202,20 +262,24 @@ extern "C" int pmoe_copy_batch_done(pmoe_copy_engine* ce, int batch) {
     if (e == hipErrorNotReady) return 0;
     if (e != hipSuccess) return pmoe::hip_fail(e, "copy_batch_done: hipEventQuery");
   }
+  pmoe::ledger_put(PMOE_LEDGER_HOST_DONE, ce, batch);
   return 1;
 }
 
 extern "C" int pmoe_copy_batch_join(pmoe_copy_engine* ce, int batch, void* stream) {
   pmoe::clear_error();
+  if (!ce) return pmoe::fail(PMOE_EINVAL, "copy_batch_join: null engine");
   std::lock_guard<std::mutex> lk(ce->mu);
   auto* b = live_batch(ce, batch);
   if (!b) return pmoe::fail(PMOE_EINVAL, "copy_batch_join: no such batch");
   for (hipEvent_t ev : b->ev) PMOE_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(stream), ev, 0));
+  pmoe::ledger_put(PMOE_LEDGER_BATCH_JOIN, ce, batch);
   return PMOE_OK;
 }
 
 extern "C" int pmoe_copy_batch_wait(pmoe_copy_engine* ce, int batch) {
   pmoe::clear_error();
+  if (!ce) return pmoe::fail(PMOE_EINVAL, "copy_batch_wait: null engine");
   std::vector<hipEvent_t> evs;
   {
     std::lock_guard<std::mutex> lk(ce->mu);
@@ -224,11 +288,13 @@ extern "C" int pmoe_copy_batch_wait(pmoe_copy_engine* ce, int batch) {
     evs = b->ev;
   }
   for (hipEvent_t ev : evs) PMOE_HIP(hipEventSynchronize(ev));
+  pmoe::ledger_put(PMOE_LEDGER_HOST_DONE, ce, batch);
   return PMOE_OK;
 }
 
 extern "C" int pmoe_copy_batch_release(pmoe_copy_engine* ce, int batch) {
   pmoe::clear_error();
+  if (!ce) return pmoe::fail(PMOE_EINVAL, "copy_batch_release: null engine");
   std::lock_guard<std::mutex> lk(ce->mu);
   auto* b = live_batch(ce, batch);
   if (!b) return pmoe::fail(PMOE_EINVAL, "copy_batch_release: no such batch");
@@ -242,6 +308,7 @@ extern "C" int pmoe_copy_join(pmoe_copy_engine* ce, void* stream) {
   std::lock_guard<std::mutex> lk(ce->mu);
   for (hipEvent_t ev : ce->done)
     PMOE_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(stream), ev, 0));
+  pmoe::ledger_put(PMOE_LEDGER_JOIN, ce);
   return PMOE_OK;
 }
 
@@ -253,8 +320,10 @@ extern "C" int pmoe_copy_flush(pmoe_copy_engine* ce, void* stream) {
   if (ce->urgent.empty() && ce->normal.empty()) return PMOE_OK;
   PMOE_HIP(hipEventRecord(ce->fence, compute));
   ce->fenced = true;
-  const int rc = issue_locked(ce);
+  pmoe::ledger_put(PMOE_LEDGER_FENCE, ce);
+  const int rc = issue_locked(ce, -1);
   for (hipEvent_t ev : ce->done) PMOE_HIP(hipStreamWaitEvent(compute, ev, 0));
+  pmoe::ledger_put(PMOE_LEDGER_JOIN, ce);
   return rc;
 }
 
@@ -266,6 +335,7 @@ extern "C" int pmoe_copy_sync(pmoe_copy_engine* ce) {
     hipError_t e = hipStreamSynchronize(s);
     if (e != hipSuccess && first_err == PMOE_OK) first_err = pmoe::hip_fail(e, "copy_sync");
   }
+  if (first_err == PMOE_OK) pmoe::ledger_put(PMOE_LEDGER_HOST_SYNC, ce);
   return first_err;
 }
 

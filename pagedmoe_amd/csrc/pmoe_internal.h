@@ -15,6 +15,10 @@ namespace pmoe {
 void set_error(const std::string& msg);
 void clear_error();
 
+// Slot-safety ledger (copy_engine.cpp): true while recording.
+bool ledger_on();
+void ledger_put(int64_t kind, const void* who, int64_t a = 0, int64_t b = 0, int64_t c = 0);
+
 inline int fail(int code, const std::string& msg) {
   set_error(msg);
   return code;

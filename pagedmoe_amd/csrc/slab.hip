@@ -299,6 +299,11 @@ static int publish_row(pmoe_slab* s, int layer, const Ticket* overlay, hipStream
         if (es.first >= off && es.first < off + cnt) c.v[es.first - off] = es.second;
     publish_kernel<<<(cnt + 255) / 256, 256, 0, st>>>(c, cnt, dst + off);
     PMOE_LAUNCH_CHECK("publish_kernel");
+    if (pmoe::ledger_on()) {
+      if (off == 0) pmoe::ledger_put(PMOE_LEDGER_PUBLISH, s, layer);
+      for (int i = 0; i < cnt; ++i)
+        if (c.v[i] >= 0) pmoe::ledger_put(PMOE_LEDGER_ROW, s, layer, off + i, c.v[i]);
+    }
   }
   s->dirty[layer] = overlay ? 1 : 0;  // an overlay row differs from the host row
   return PMOE_OK;

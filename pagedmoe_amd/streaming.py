@@ -229,9 +229,11 @@ class StreamedSwitchGLU(nn.Module):
         for member, table in self.passes(ind2):
             if member is None:
                 y = compute(ind2, table)
+                self.cache.note_compute(self.layer_key)
                 continue
             keep = torch.isin(ind2, torch.tensor(member, dtype=torch.int32, device=ind2.device))
             y_g = compute(torch.where(keep, ind2, torch.full_like(ind2, -1)), table)
+            self.cache.note_compute(self.layer_key)
             y = y_g if y is None else torch.where(keep[..., None], y_g, y)
         return y
 
@@ -239,22 +241,31 @@ class StreamedSwitchGLU(nn.Module):
         """Enter this layer's call on the ring; True for a flow token."""
         return self.ring is not None and self.ring.layer_call(self.ring_index, n_tokens)
 
+    def call(self, x2: torch.Tensor, ind2: torch.Tensor, compute) -> torch.Tensor:
+        """One seam call over flat rows x2 [N, D] and routing ind2 [N, K]:
+        a flow token computes once against the device table published at
+        the token's start (no host round trip; non-resident experts give
+        zero rows); otherwise every fetch pass of ``run_passes``, then
+        speculation for the layers ahead.  ``compute(ids, table)`` enqueues
+        the expert kernels of one pass."""
+        c = self.cache
+        if not c.stitched and self.flow_call(ind2.shape[0]):
+            y = compute(ind2, c.table_ptr(self.layer_key))
+            c.note_compute(self.layer_key)
+            self.ring.note(self.ring_index, ind2)
+            return y
+        y = self.run_passes(ind2, compute)
+        if self.ring is not None and ind2.shape[0] <= config.DECODE_MAX_TOKENS:
+            self.ring.speculate(self.ring_index, x2)
+        return y
+
     def forward(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         lead = indices.shape
         x2 = x.reshape(-1, self.hidden).to(torch.bfloat16).contiguous()
         ind2 = indices.reshape(-1, lead[-1]).to(torch.int32).contiguous()
         c = self.cache
-        if not c.stitched and self.flow_call(ind2.shape[0]):
-            # flow token: the device table as published at the token's start,
-            # no host round trip; non-resident experts give zero rows
-            y = K.switch_glu(c.geom, c.slab.buf, c.table_ptr(self.layer_key), self.n_experts,
-                             x2, ind2)
-            self.ring.note(self.ring_index, ind2)
-            return y.reshape(*lead, self.hidden)
-        y = self.run_passes(ind2, lambda ids, table: K.switch_glu(
+        y = self.call(x2, ind2, lambda ids, table: K.switch_glu(
             c.geom, c.slab.buf, table, self.n_experts, x2, ids))
-        if self.ring is not None and ind2.shape[0] <= config.DECODE_MAX_TOKENS:
-            self.ring.speculate(self.ring_index, x2)
         return y.reshape(*lead, self.hidden)
 
 
@@ -294,6 +305,7 @@ class _MoEBlock(nn.Module):
                                        self.gate_weight, x2, score_bias=self._score_bias(),
                                        logit_bias=self.logit_bias, shared_slot=shared_slot,
                                        shared_gate=sg)
+            sm.cache.note_compute(sm.layer_key)
             sm.ring.note(sm.ring_index, inds)
             self.last_routing = (inds, w)
             return out.reshape(shape)
@@ -311,10 +323,12 @@ class _MoEBlock(nn.Module):
             for member, tab in sm.passes(inds):
                 if member is None:
                     out = K.moe_experts(g, slab, tab, n_exp, x2, inds, w, shared_slot, sg)
+                    sm.cache.note_compute(sm.layer_key)
                     continue
                 keep = torch.isin(inds, torch.tensor(member, dtype=torch.int32, device=x2.device))
                 y_g = K.switch_glu(g, slab, tab, n_exp, x2,
                                    torch.where(keep, inds, torch.full_like(inds, -1)))
+                sm.cache.note_compute(sm.layer_key)
                 y = y_g if y is None else torch.where(keep[..., None], y_g, y)
             if out is None:
                 shared_y = shared_logit = None

@@ -802,3 +802,83 @@ def test_route_prediction_speculates_without_changing_outputs():
     assert st["misses"] < twin_cache.stats()["misses"]     # claimed guesses were misses there
     cache.close()
     twin_cache.close()
+
+
+# ---------------------------------------------------------------- slot-safety ledger
+
+def test_speculation_overlapping_compute_is_bit_identical_and_race_free():
+    """Route prediction with nothing waited for between layers (no device
+    synchronise, no wait for the guesses): guesses read into free slots
+    while later layers compute, and are claimed by their targets.  Outputs
+    stay bit-identical to a prediction-off twin, and the native slot ledger
+    (copy engines + slab + computes) replayed by verify.SlotLedger shows no
+    write racing a read."""
+    _, S = _mods()
+    spec = O.LayerSpec(1024, 32, 512, 4)
+    model, _ = _softmax_model(spec, 4, seed=170)
+    twin, _ = _softmax_model(spec, 4, seed=170)
+    cache = S.build_cache_for(model, slots=24)
+    ring = S.patch_model(model, cache, predict_mode="on")
+    twin_cache = S.build_cache_for(twin, slots=24)
+    S.patch_model(twin, twin_cache, predict_mode="off")
+    led = cache.verify_slots(True)
+    rng = np.random.default_rng(172)
+    outs, refs = [], []
+    for t in range(12):
+        h = torch.from_numpy(rng.standard_normal((1, spec.hidden), dtype=np.float32)).to(DEV)
+        for li, layer in enumerate(model.layers):
+            xb = h.to(torch.bfloat16)
+            outs.append(layer.mlp(xb))
+            refs.append(twin.layers[li].mlp(xb))
+            h = h + 0.05 * torch.from_numpy(rng.standard_normal(
+                (1, spec.hidden), dtype=np.float32)).to(DEV)
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(outs, refs)):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), i
+    st = cache.stats()
+    print(f"[ledger spec] {led.report()} started {st['spec_started']} claims "
+          f"{st['spec_claims']} late {st['spec_claims_late']}", flush=True)
+    assert st["spec_started"] > 0 and st["spec_claims"] > 0
+    assert led.counts["BATCH_JOIN"] > 0 and led.counts["COMPUTE"] == 48
+    assert led.conflicts == [], led.conflicts[:3]
+    assert st["slab_conflicts"] == 0
+    cache.close()
+    twin_cache.close()
+
+
+def test_prefill_groups_and_flow_under_the_slot_ledger(monkeypatch):
+    """The native event stream of prefill fetch groups (copies under the
+    previous group's compute, stage slots) and of flow decode (admit behind
+    a fence, install once landed, rows republished) replayed through the
+    slot ledger: no conflicts, and the prefill outputs match the oracle."""
+    from pagedmoe_amd import config
+
+    _, S = _mods()
+    spec = O.LayerSpec(1024, 32, 512, 4)
+    model, ol = _softmax_model(spec, 2, seed=180)
+    cache = S.build_cache_for(model, slots=16, stage_slots=4)   # 20 slots a group: several
+    ring = S.patch_model(model, cache)
+    led = cache.verify_slots(True)
+    rng = np.random.default_rng(181)
+    xb = O.bf16_round(rng.standard_normal((96, spec.hidden), dtype=np.float32))
+    for li, layer in enumerate(model.layers):
+        out = layer.mlp(bits_to_bf16_tensor(xb, DEV))
+        torch.cuda.synchronize()
+        gw, experts, _, _ = ol[li]
+        _, _, _, ref = O.moe_layer_f64(spec, xb, gw, experts)
+        check_close(out.float().cpu().numpy(), ref, f"ledger prefill layer {li}")
+    groups = [len(s.last_groups) for s in ring]
+    monkeypatch.setattr(config, "FLOW_WARMUP", 1)
+    monkeypatch.setattr(config, "FLOW_WARM_HIT", 0.0)
+    ring.flow = True
+    for t in range(10):
+        xt = O.bf16_round(rng.standard_normal((1, spec.hidden), dtype=np.float32))
+        for layer in model.layers:
+            layer.mlp(bits_to_bf16_tensor(xt, DEV))
+    torch.cuda.synchronize()
+    print(f"[ledger prefill+flow] groups per layer {groups}, {led.report()}, "
+          f"flow tokens {ring.flow_tokens}", flush=True)
+    assert max(groups) >= 2 and ring.flow_tokens >= 8
+    assert led.counts["ISSUE"] > 0 and led.counts["BATCH_JOIN"] > 0
+    assert led.conflicts == [], led.conflicts[:3]
+    cache.close()
