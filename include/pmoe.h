@@ -249,6 +249,15 @@ int pmoe_combine(const void* y, const float* weights, int n, int k, int hidden,
                  const void* shared_y, const float* shared_logit, void* out,
                  void* stream);
 
+/* Closed-stitch miss count (replaces the per-layer miss sum of
+ * _closed_forward, streaming.py:905-935, and the token wrapper's one read of
+ * it, _closed_call :2843-2870): *counter += the number of ids[0..n) with
+ * 0 <= id < n_experts and table[id] < 0, i.e. routed experts the live table
+ * does not hold.  One small kernel on stream, no host sync, capturable in a
+ * graph; dropped ids (-1) are not counted.  counter is device int32. */
+int pmoe_count_missing(const int32_t* table, const int32_t* ids, int n, int n_experts,
+                       int32_t* counter, void* stream);
+
 /* ---- slab slot table (replaces ExpertCache's slot policy, cache.py:410:
  *      _alloc_slot :1118-1159, _begin :2327-2453, _finish :2455-2523,
  *      _evict_to_budget :2236-2291, stitch :717-787, flow table :791-859) -- */
@@ -270,6 +279,9 @@ typedef struct {
   /* speculative reads started, claimed by their layer's fetch (of which
    * not yet landed at the claim), and handed back unclaimed */
   int64_t spec_started, spec_claims, spec_claims_late, spec_dropped;
+  /* prefill-ahead reads started (prefill_ahead_reads, cache.py:2644) and
+   * claimed by the next layer's prefill groups (prefill_ahead_used :2694) */
+  int64_t ahead_started, ahead_claims;
 } pmoe_slab_stats;
 
 /* Slot policy + device table [n_layers, n_experts] int32 (-1 = absent).
@@ -350,6 +362,20 @@ int pmoe_slab_set_spec_engine(pmoe_slab* s, pmoe_copy_engine* ce);
 int pmoe_slab_speculate(pmoe_slab* s, const pmoe_geom* g, void* slab,
                         const void* host_store, int layer, const int32_t* ids,
                         int n_ids, int max_staged, int* n_started);
+
+/* Prefill-time prediction (ExpertCache.prefill_ahead, cache.py:2580-2650):
+ * a later prefill layer's predicted ids, in priority order, skipping
+ * resident, pending and staged ones, take a free routed slot while more than
+ * free_floor are free, else a prefill stage slot while more than stage_floor
+ * are free (never an eviction), and their reads start through the
+ * speculation engine as one copy batch, behind that engine's latest fence.
+ * The layer's next pmoe_slab_prefill_request claims the ones it routes (a
+ * hit with no new read; the group's row upload joins the batch first) and
+ * hands back the rest, whose slots return once the batch has landed.
+ * *n_started receives the reads started. */
+int pmoe_slab_prefill_ahead(pmoe_slab* s, const pmoe_geom* g, void* slab,
+                            const void* host_store, int layer, const int32_t* ids,
+                            int n_ids, int free_floor, int stage_floor, int* n_started);
 
 /* Hand back every outstanding guess (flow decode and prefill do not claim
  * them). */

@@ -574,7 +574,9 @@ class SlotPolicy:
                 self.freq[key] = min(self.freq_max, self.freq.get(key, 0) + 1)
                 self.pinned.add(self.slot_of[key])
                 hits.append(e)
-            elif key in staged:
+            elif key in staged and staged[key] < self.slots:
+                # a guess in a prefill stage slot is never made resident
+                # there; it is a miss and handed back below
                 self.hits += 1
                 slot = staged.pop(key)
                 self.pinned.add(slot)
@@ -634,10 +636,40 @@ class SlotPolicy:
         self.settle()
 
     def settle(self):
-        """Handed-back guesses' reads have landed: their slots are free."""
+        """Handed-back guesses' reads have landed: their slots are free (a
+        prefill stage slot goes back to the stage)."""
         drain = self.__dict__.setdefault("draining", [])
-        self.free.extend(drain)
+        for slot in drain:
+            (self.stage_free if slot >= self.slots else self.free).append(slot)
         drain.clear()
+
+    def prefill_ahead(self, layer, ids, free_floor, stage_floor):
+        """Prefill-time prediction (cache.py:2580-2650): ids in priority
+        order, skipping resident, pending and staged ones, take a free slot
+        while more than ``free_floor`` are free, else a stage slot while more
+        than ``stage_floor`` are free; never an eviction; the first id that
+        finds neither stops the pass.  Returns [(id, slot)] started."""
+        self.settle()
+        if not hasattr(self, "stage_free"):
+            self.set_stage(self.slots, 0)
+        staged = self.__dict__.setdefault("staged", OrderedDict())
+        pending = getattr(self, "pending", {})
+        got, seen = [], set()
+        for e in ids:
+            key = (layer, int(e))
+            if key in seen or key in self.lru or key in pending or key in staged:
+                continue
+            seen.add(key)
+            if len(self.free) > free_floor:
+                slot = self.free.pop()
+            elif len(self.stage_free) > stage_floor:
+                slot = self.stage_free.pop()
+            else:
+                break
+            got.append((key, slot))
+        for key, slot in got:
+            staged[key] = slot
+        return [(key[1], slot) for key, slot in got]
 
     # ---- prefill fetch groups (cache.py:2347-2453 with prefill=True,
     # PREFILL_TOUCH=0, PREFILL_SLAB=1; _install(..., "soft") :2306-2312;
@@ -656,12 +688,24 @@ class SlotPolicy:
         if not hasattr(self, "stage_free"):
             self.set_stage(self.slots, 0)
         ticket = next(t for t in range(64) if t not in self.groups)
-        held = {"layer": layer, "temp": [], "free": [], "stage": []}
+        held = {"layer": layer, "temp": [], "free": [], "stage": [], "claimed": []}
+        staged = self.__dict__.setdefault("staged", OrderedDict())
         placed, unplaced = [], 0
         for e in sorted({int(i) for i in ids}):
             key = (layer, e)
             if key in self.lru:
                 self.hits += 1
+                continue
+            if key in staged:             # its read already started: claimed
+                slot = staged.pop(key)
+                self.hits += 1
+                held["claimed"].append((e, slot))
+                if slot < self.slots and len(self.lru) < self.budget:
+                    self.slot_of[key] = slot
+                    self.lru[key] = slot
+                else:
+                    held["temp"].append((e, slot))
+                    held["free" if slot < self.slots else "stage"].append(slot)
                 continue
             self.misses += 1
             if self.free:
@@ -681,6 +725,7 @@ class SlotPolicy:
                 continue
             placed.append((e, slot))
         self.groups[ticket] = held
+        self._drop_staged(lambda key: key[0] == layer)
         return ticket, placed, unplaced
 
     def compute_row(self, ticket, n_experts) -> np.ndarray:

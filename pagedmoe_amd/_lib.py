@@ -57,7 +57,8 @@ class SlabStats(ctypes.Structure):
         "hits", "misses", "evictions", "starved", "installs", "resident", "slots",
         "budget", "reserve", "stitched", "bytes_copied", "prefill_slot_reads",
         "prefill_installs", "stage_reads", "prefill_starved", "stage_slots", "flow_admits",
-        "spec_started", "spec_claims", "spec_claims_late", "spec_dropped")]
+        "spec_started", "spec_claims", "spec_claims_late", "spec_dropped",
+        "ahead_started", "ahead_claims")]
 
 
 class LedgerRec(ctypes.Structure):
@@ -96,6 +97,7 @@ SIGNATURES = {
     "pmoe_moe_block_noalloc": (_I, [ctypes.POINTER(Geom), ctypes.POINTER(RouteCfg), _P, _P, _P,
                                     _P, _P, _P, _I, _I, _P, _P, _P, _P, _P]),
     "pmoe_combine": (_I, [_P, _P, _I, _I, _I, _P, _P, _P, _P]),
+    "pmoe_count_missing": (_I, [_P, _P, _I, _I, _P, _P]),
     "pmoe_slab_create": (_I, [ctypes.POINTER(_P), _I, _I, _I, _F, _I, _I]),
     "pmoe_slab_destroy": (_I, [_P]),
     "pmoe_slab_device_table": (_P, [_P, _I]),
@@ -112,6 +114,8 @@ SIGNATURES = {
     "pmoe_slab_speculate": (_I, [_P, ctypes.POINTER(Geom), _P, _P, _I, _I32P, _I, _I,
                                  ctypes.POINTER(_I)]),
     "pmoe_slab_drop_staged": (_I, [_P]),
+    "pmoe_slab_prefill_ahead": (_I, [_P, ctypes.POINTER(Geom), _P, _P, _I, _I32P, _I, _I, _I,
+                                     ctypes.POINTER(_I)]),
     "pmoe_slab_set_stage": (_I, [_P, _I, _I]),
     "pmoe_slab_capacity": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "pmoe_slab_prefill_request": (_I, [_P, _I, _I32P, _I, _I32P, _I32P, ctypes.POINTER(_I),

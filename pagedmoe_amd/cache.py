@@ -89,6 +89,13 @@ class HostExpertStore:
             pass
 
 
+# prefill-ahead stands down while the share of its reads the next layer
+# routed stays under AHEAD_MIN_PRECISION (cache.py:237-243)
+AHEAD_MIN_PRECISION = 0.5
+AHEAD_MIN_SAMPLE = 512
+AHEAD_DECAY = 0.98
+
+
 def default_stage_slots(g: Geom, n_experts: int) -> int:
     """The prefill stage's size: four groups of PREFILL_STAGE_GROUP_MB (at
     least 8 experts a group) and at least 32 slots, as ensure_stage sizes it
@@ -176,6 +183,9 @@ class ExpertCache:
         self.group_passes = 0
         self.spec_log = None     # a list records fetch / speculate calls (tests replay them)
         self.ledger = None       # slot-safety ledger (config.SLAB_VERIFY)
+        self._ahead_n = 0.0      # prefill-ahead reads started / used, decayed
+        self._ahead_u = 0.0
+        self.ahead_skipped = 0
         if config.SLAB_VERIFY:
             self.verify_slots(True)
 
@@ -411,6 +421,53 @@ class ExpertCache:
                                         ctypes.byref(n)), "pmoe_slab_speculate")
         return n.value
 
+    def prefill_group_experts(self) -> int:
+        """Experts in one prefill fetch group (the stage's group size, at
+        least 8 experts, at most GROUP_BYTES)."""
+        per = int(self.geom.expert_bytes)
+        return max(1, min(config.GROUP_BYTES,
+                          max(config.PREFILL_STAGE_GROUP_MB << 20, 8 * per)) // per)
+
+    def prefill_ahead(self, layer_key, expert_ids, free_floor: int | None = None,
+                      stage_floor: int | None = None) -> int:
+        """Start a later prefill layer's predicted reads (cache.py:2580-2650):
+        ids in priority order into free routed slots while more than
+        ``free_floor`` (default max(8, slots // 50)) stay free, then into
+        prefill stage slots while more than ``stage_floor`` stay free for
+        that layer's unpredicted misses (default one fetch group's worth, at
+        most a quarter of the stage: the reference's stage holds four groups
+        and keeps one back); never an eviction.  The reads run on the speculation engine behind its latest
+        fence; that layer's prefill groups claim the ids they route and hand
+        back the rest.  Stands down while fewer than half of the recent
+        guesses were used (after AHEAD_MIN_SAMPLE of them).  Returns the reads
+        started."""
+        if not self._ce_spec.value or self.stitched:
+            return 0
+        if self._ahead_n >= AHEAD_MIN_SAMPLE and self._ahead_u < AHEAD_MIN_PRECISION * self._ahead_n:
+            self.ahead_skipped += 1
+            self._ahead_n *= AHEAD_DECAY
+            self._ahead_u *= AHEAD_DECAY
+            return 0
+        if free_floor is None:
+            free_floor = max(8, self.routed_slots // 50)
+        if stage_floor is None:
+            stage_floor = min(self.stage_slots // 4, self.prefill_group_experts())
+        ids = [int(e) for e in expert_ids]
+        arr = (ctypes.c_int32 * max(1, len(ids)))(*ids)
+        n = ctypes.c_int()
+        check(lib().pmoe_slab_prefill_ahead(self._h, ctypes.byref(self.geom),
+                                            ctypes.c_void_p(self.slab.data_ptr),
+                                            ctypes.c_void_p(self.host_store.address),
+                                            self.layer_index(layer_key), arr, len(ids),
+                                            int(free_floor), int(stage_floor), ctypes.byref(n)),
+              "pmoe_slab_prefill_ahead")
+        return n.value
+
+    def note_ahead(self, started: int, used: int) -> None:
+        """Precision bookkeeping of one prefill-ahead set (cache.py:2694-2696)."""
+        self._ahead_n = self._ahead_n * AHEAD_DECAY + started
+        self._ahead_u = self._ahead_u * AHEAD_DECAY + used
+
     def drop_staged(self) -> None:
         """Hand back every outstanding guess (flow decode, prefill)."""
         check(lib().pmoe_slab_drop_staged(self._h), "pmoe_slab_drop_staged")
@@ -549,6 +606,8 @@ class ExpertCache:
             "stage_slots": st.stage_slots, "flow_admits": st.flow_admits,
             "spec_started": st.spec_started, "spec_claims": st.spec_claims,
             "spec_claims_late": st.spec_claims_late, "spec_dropped": st.spec_dropped,
+            "prefill_ahead_reads": st.ahead_started, "prefill_ahead_used": st.ahead_claims,
+            "prefill_ahead_skipped": self.ahead_skipped,
             "slab_conflicts": None if self.ledger is None else len(self.ledger.conflicts),
         }
 

@@ -1,18 +1,19 @@
 """Hot-path knobs, read from the environment once at import.
 
 Names and defaults follow the reference's PAGED_MOE_* knobs that touch this
-path (config.py: SLAB_RESERVE_FRAC :718, LFRU/LFRU_SCAN :1477-1478, STITCH
-:1186, PREFILL_TOUCH :617, PREFILL_STAGE / PREFILL_STAGE_GROUP_MB
-:1603-1608, GROUP_BYTES :1531); ``sync_from_environ()`` re-reads them
-(config.py:853); FUSED_PREFILL :1633 and ATTN_SUB_CHUNK :1562 for the
-fused prefill pass; FLOW / FLOW_WARMUP / FLOW_WARM_HIT :1218-1237 for flow
-decode; PREDICT_DEPTH :747, PREDICT_SLACK :761 and PREFETCH_DEPTH :722 for
-speculative prefetch (PREFETCH_DEPTH defaults to 0 here: the previous-token
-heuristic pays off with the reference's SSD queue, not a PCIe copy engine);
-PREDICT and the governor knobs :735-741; SLAB_VERIFY :1467 for the
-slot-safety ledger.
-DECODE_MAX_TOKENS is the reference's _DECODE_MAX_TOKENS
-(streaming.py:69): calls of more tokens take the prefill residency policy.
+path (config.py): SLAB_RESERVE_FRAC :718, LFRU / LFRU_SCAN :1477-1478,
+STITCH :1186 and STITCH_PARTIAL :1187 (closed stitch), PREFILL_TOUCH :617,
+PREFILL_STAGE / PREFILL_STAGE_GROUP_MB :1603-1608, GROUP_BYTES :1531;
+``sync_from_environ()`` re-reads them (config.py:853).  FUSED_PREFILL
+:1633 and ATTN_SUB_CHUNK :1562 for the fused prefill pass; PREFILL_AHEAD
+:1583 for prefill-time prediction; FLOW / FLOW_WARMUP / FLOW_WARM_HIT
+:1218-1237 for flow decode; PREDICT_DEPTH :747, PREDICT_SLACK :761 and
+PREFETCH_DEPTH :722 for speculative prefetch (PREFETCH_DEPTH defaults to 0
+here: the previous-token heuristic pays off with the reference's SSD queue,
+not a PCIe copy engine); PREDICT and the governor knobs :735-741;
+SLAB_VERIFY :1467 for the slot-safety ledger.  DECODE_MAX_TOKENS is the
+reference's _DECODE_MAX_TOKENS (streaming.py:69): calls of more tokens take
+the prefill residency policy.
 """
 
 from __future__ import annotations
@@ -38,6 +39,7 @@ SLAB_RESERVE_FRAC = 0.1   # slots held back from the resident budget
 LFRU = True               # second-chance eviction for reused experts
 LFRU_SCAN = 8             # entries scanned per eviction
 STITCH = True             # pin every expert in a fixed slot when the slab holds them all
+STITCH_PARTIAL = False    # closed stitch: one-pass decode over the live table, replayed on a miss
 COPY_SPLIT_BYTES = 64 << 20  # H2D copy piece size (an expert of up to 64 MiB is one copy)
 COPY_STREAMS = 2          # copy streams of the engine
 DECODE_MAX_TOKENS = 20    # calls of more tokens are prefill (no touch, no eviction)
@@ -45,6 +47,7 @@ PREFILL_STAGE = True      # stage slots for prefill misses that find no free slo
 PREFILL_STAGE_GROUP_MB = 384  # prefill fetch group size; the stage holds four groups
 GROUP_BYTES = 1024 << 20  # ceiling on one prefill fetch group
 FUSED_PREFILL = True      # long calls sub-chunk attention, run the MoE once
+PREFILL_AHEAD = True      # a prefill layer starts the next layer's predicted reads
 FLOW = False              # decode tokens with no host sync inside (residency once per token)
 FLOW_WARMUP = 2           # tokens after a prefill that take the per-layer path first
 FLOW_WARM_HIT = 0.9       # hit-rate EMA the per-layer path must reach before flow resumes
@@ -64,9 +67,11 @@ SLAB_VERIFY = False       # replay copy/compute ordering per slot and flag races
 
 
 def sync_from_environ() -> None:
-    global SLAB_RESERVE_FRAC, LFRU, LFRU_SCAN, STITCH, COPY_SPLIT_BYTES, COPY_STREAMS
+    global SLAB_RESERVE_FRAC, LFRU, LFRU_SCAN, STITCH, STITCH_PARTIAL, COPY_SPLIT_BYTES
+    global COPY_STREAMS
     global DECODE_MAX_TOKENS, PREFILL_STAGE, PREFILL_STAGE_GROUP_MB, GROUP_BYTES
     global FUSED_PREFILL, ATTN_SUB_CHUNK, ATTN_SCORE_MB, FLOW, FLOW_WARMUP, FLOW_WARM_HIT
+    global PREFILL_AHEAD
     global PREDICT_DEPTH, PREDICT_SLACK, PREFETCH_DEPTH, PREDICT, PREDICT_WINDOW
     global PREDICT_MIN_TOKENS, PREDICT_MARGIN, PREDICT_Z, PREDICT_MAX_PROBE, PREDICT_HOLD
     global SLAB_VERIFY
@@ -74,6 +79,7 @@ def sync_from_environ() -> None:
     LFRU = _env("LFRU", True, _bool)
     LFRU_SCAN = _env("LFRU_SCAN", 8, int)
     STITCH = _env("STITCH", True, _bool)
+    STITCH_PARTIAL = _env("STITCH_PARTIAL", False, _bool)
     COPY_SPLIT_BYTES = _env("COPY_SPLIT_KB", 65536, int) * 1024
     COPY_STREAMS = _env("COPY_STREAMS", 2, int)
     DECODE_MAX_TOKENS = _env("DECODE_MAX_TOKENS", 20, int)
@@ -81,6 +87,7 @@ def sync_from_environ() -> None:
     PREFILL_STAGE_GROUP_MB = _env("PREFILL_STAGE_GROUP_MB", 384, int)
     GROUP_BYTES = _env("GROUP_MB", 1024, int) << 20
     FUSED_PREFILL = _env("FUSED_PREFILL", True, _bool)
+    PREFILL_AHEAD = _env("PREFILL_AHEAD", True, _bool)
     ATTN_SUB_CHUNK = _env("ATTN_SUB_CHUNK", 2048, int)
     ATTN_SCORE_MB = _env("ATTN_SCORE_MB", 1024, int)
     FLOW = _env("FLOW", False, _bool)

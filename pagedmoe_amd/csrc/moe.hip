@@ -565,6 +565,40 @@ extern "C" int pmoe_moe_block_noalloc(const pmoe_geom* g, const pmoe_route_cfg* 
                         shared_gate, out, inds_out, weights_out, ws, kStaticScratchBytes, stream);
 }
 
+namespace pmoe {
+namespace {
+
+// One block: each thread counts its strided ids, a wave sum, then one
+// atomic per wave (vector atomics only).
+__global__ __launch_bounds__(256) void count_missing_kernel(const int32_t* __restrict__ table,
+                                                            const int32_t* __restrict__ ids,
+                                                            int n, int n_experts,
+                                                            int32_t* __restrict__ counter) {
+  int c = 0;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const int e = ids[i];
+    c += (e >= 0 && e < n_experts && table[e] < 0) ? 1 : 0;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+  if ((threadIdx.x & 63) == 0 && c) atomicAdd(counter, c);
+}
+
+}  // namespace
+}  // namespace pmoe
+
+extern "C" int pmoe_count_missing(const int32_t* table, const int32_t* ids, int n, int n_experts,
+                                  int32_t* counter, void* stream) {
+  pmoe::clear_error();
+  PMOE_REQUIRE(table && counter && (n == 0 || ids), "count_missing: null pointer");
+  PMOE_REQUIRE(n >= 0 && n_experts > 0, "count_missing: bad shape");
+  if (n == 0) return PMOE_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  pmoe::count_missing_kernel<<<1, 256, 0, st>>>(table, ids, n, n_experts, counter);
+  PMOE_LAUNCH_CHECK("count_missing_kernel");
+  return PMOE_OK;
+}
+
 extern "C" int pmoe_combine(const void* y, const float* weights, int n, int k, int hidden,
                             const void* shared_y, const float* shared_logit, void* out,
                             void* stream) {

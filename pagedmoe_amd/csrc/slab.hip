@@ -64,6 +64,7 @@ struct Ticket {
   int layer = -1;
   std::vector<std::pair<int, int>> temp;  // (expert, slot) not installed as resident
   std::vector<int> from_free, from_stage;
+  std::vector<int> claims;                // speculation batches of claimed prefill-ahead reads
 };
 
 }  // namespace
@@ -158,17 +159,18 @@ struct pmoe_slab {
     }
     // nothing evictable: give up an unclaimed guess, the latest staged first
     // (cache.py:1149-1157); its read must land before the slot is reused
-    if (!staged_keys.empty() && spec_ce) {
-      const int k = staged_keys.back();
+    // (a guess in a prefill stage slot is never taken for a resident entry)
+    for (size_t i = staged_keys.size(); spec_ce && i-- > 0;) {
+      const int k = staged_keys[i];
       const int slot = staged_slot[k], b = staged_batch[k];
-      if (pmoe_copy_batch_wait(spec_ce, b) == PMOE_OK) {
-        staged_slot[k] = -1;
-        staged_batch[k] = -1;
-        staged_keys.pop_back();
-        ++st.spec_dropped;
-        if (--batch_refs[b] == 0) (void)pmoe_copy_batch_release(spec_ce, b);
-        return slot;
-      }
+      if (slot >= slots) continue;
+      if (pmoe_copy_batch_wait(spec_ce, b) != PMOE_OK) break;
+      staged_slot[k] = -1;
+      staged_batch[k] = -1;
+      staged_keys.erase(staged_keys.begin() + long(i));
+      ++st.spec_dropped;
+      if (--batch_refs[b] == 0) (void)pmoe_copy_batch_release(spec_ce, b);
+      return slot;
     }
     ++st.starved;
     return -1;
@@ -365,7 +367,9 @@ extern "C" int pmoe_slab_request(pmoe_slab* s, int layer, const int32_t* ids, in
       s->move_to_end(k);
       s->freq[k] = std::min(kFreqMax, s->freq[k] + 1);
       s->pin(s->slot_of[k]);
-    } else if (s->staged_slot[k] >= 0) {  // a guess claimed: no new read
+    } else if (s->staged_slot[k] >= 0 && s->staged_slot[k] < s->slots) {
+      // a guess claimed: no new read (a prefill-ahead read in a stage slot is
+      // not made resident there; it is handed back below)
       ++s->st.hits;
       ++s->st.spec_claims;
       const int slot = s->staged_slot[k];
@@ -487,7 +491,10 @@ static int settle_spec(pmoe_slab* s) {
       keep.push_back(sb);
       continue;
     }
-    s->free_slots.push_back(sb.first);
+    if (sb.first >= s->slots)
+      s->stage_free.push_back(sb.first);
+    else
+      s->free_slots.push_back(sb.first);
     if (--s->batch_refs[sb.second] == 0) {
       const int rc = pmoe_copy_batch_release(s->spec_ce, sb.second);
       if (rc) return rc;
@@ -550,6 +557,67 @@ extern "C" int pmoe_slab_speculate(pmoe_slab* s, const pmoe_geom* g, void* slab,
   return PMOE_OK;
 }
 
+extern "C" int pmoe_slab_prefill_ahead(pmoe_slab* s, const pmoe_geom* g, void* slab,
+                                       const void* host_store, int layer, const int32_t* ids,
+                                       int n_ids, int free_floor, int stage_floor,
+                                       int* n_started) {
+  pmoe::clear_error();
+  if (!s || !g || !slab || !host_store || (n_ids > 0 && !ids) || !n_started || layer < 0 ||
+      layer >= s->n_layers || n_ids < 0 || free_floor < 0 || stage_floor < 0)
+    return pmoe::fail(PMOE_EINVAL, "slab_prefill_ahead: bad argument");
+  *n_started = 0;
+  std::lock_guard<std::mutex> lk(s->mu);
+  if (!s->spec_ce) return pmoe::fail(PMOE_EINVAL, "slab_prefill_ahead: no speculation engine");
+  int rc = settle_spec(s);
+  if (rc) return rc;
+  const int base = layer * s->n_experts;
+  std::vector<std::pair<int, int>> got;  // (key, slot)
+  std::vector<char> seen(size_t(s->n_experts), 0);
+  for (int i = 0; i < n_ids; ++i) {
+    const int e = ids[i];
+    if (e < 0 || e >= s->n_experts) return pmoe::fail(PMOE_EINVAL, "slab_prefill_ahead: id out of range");
+    const int k = base + e;
+    if (seen[e] || s->in_lru[k] || s->pending[k] || s->staged_slot[k] >= 0) continue;
+    seen[e] = 1;
+    int slot = -1;
+    if (int(s->free_slots.size()) > free_floor) {
+      slot = s->free_slots.back();
+      s->free_slots.pop_back();
+    } else if (int(s->stage_free.size()) > stage_floor) {
+      slot = s->stage_free.back();
+      s->stage_free.pop_back();
+    } else {
+      break;
+    }
+    got.emplace_back(k, slot);
+  }
+  if (got.empty()) return PMOE_OK;
+  // one copy batch for the whole set: the next layer's groups want most of it
+  const size_t eb = size_t(g->expert_bytes);
+  for (const auto& ks : got) {
+    rc = pmoe_copy_submit(s->spec_ce, static_cast<uint8_t*>(slab) + size_t(ks.second) * eb,
+                          static_cast<const uint8_t*>(host_store) + size_t(ks.first) * eb, eb, 0);
+    if (rc) break;
+  }
+  int b = -1;
+  if (!rc) rc = pmoe_copy_issue(s->spec_ce, &b);
+  if (rc) {  // nothing was issued: the slots go back where they came from
+    for (size_t i = got.size(); i-- > 0;)
+      (got[i].second >= s->slots ? s->stage_free : s->free_slots).push_back(got[i].second);
+    return rc;
+  }
+  for (const auto& ks : got) {
+    s->staged_slot[ks.first] = ks.second;
+    s->staged_batch[ks.first] = b;
+    s->staged_keys.push_back(ks.first);
+  }
+  s->batch_refs[b] = int(got.size());
+  s->st.ahead_started += int64_t(got.size());
+  s->st.bytes_copied += int64_t(got.size()) * int64_t(eb);
+  *n_started = int(got.size());
+  return PMOE_OK;
+}
+
 extern "C" int pmoe_slab_drop_staged(pmoe_slab* s) {
   pmoe::clear_error();
   if (!s) return pmoe::fail(PMOE_EINVAL, "slab_drop_staged: null slab");
@@ -603,7 +671,6 @@ extern "C" int pmoe_slab_prefill_request(pmoe_slab* s, int layer, const int32_t*
     if (s->pending[base + e])
       return pmoe::fail(PMOE_EINVAL,
                         "slab_prefill_request: an admitted expert's copy is not installed");
-  s->drop_layer_staged(layer);
   Ticket& tk = s->tickets[t];
   tk = Ticket();
   tk.live = true;
@@ -613,6 +680,23 @@ extern "C" int pmoe_slab_prefill_request(pmoe_slab* s, int layer, const int32_t*
     const int k = base + e;
     if (s->in_lru[k]) {  // hit: recency and frequency untouched
       ++s->st.hits;
+      continue;
+    }
+    if (s->staged_slot[k] >= 0) {  // a prefill-ahead read already issued: claimed
+      const int slot = s->staged_slot[k];
+      tk.claims.push_back(s->staged_batch[k]);
+      s->staged_slot[k] = -1;
+      s->staged_batch[k] = -1;
+      s->staged_keys.erase(std::find(s->staged_keys.begin(), s->staged_keys.end(), k));
+      ++s->st.hits;
+      ++s->st.ahead_claims;
+      if (slot < s->slots && s->lru_size < s->budget) {
+        s->install(k, slot);
+        ++s->st.prefill_installs;
+      } else {
+        tk.temp.emplace_back(e, slot);
+        (slot < s->slots ? tk.from_free : tk.from_stage).push_back(slot);
+      }
       continue;
     }
     ++s->st.misses;
@@ -641,6 +725,7 @@ extern "C" int pmoe_slab_prefill_request(pmoe_slab* s, int layer, const int32_t*
     if (miss_slots) miss_slots[placed] = slot;
     ++placed;
   }
+  s->drop_layer_staged(layer);  // this layer's guesses it did not route
   *n_miss = placed;
   if (n_unplaced) *n_unplaced = unplaced;
   *ticket = t;
@@ -658,6 +743,13 @@ extern "C" int pmoe_slab_prefill_publish(pmoe_slab* s, int ticket, void* stream)
   std::lock_guard<std::mutex> lk(s->mu);
   Ticket* tk = live_ticket(s, ticket);
   if (!tk) return pmoe::fail(PMOE_EINVAL, "slab_prefill_publish: no such open prefill group");
+  // the group computes on claimed prefill-ahead reads: wait for their batches
+  for (int b : tk->claims) {
+    int rc = pmoe_copy_batch_join(s->spec_ce, b, stream);
+    if (!rc && --s->batch_refs[b] == 0) rc = pmoe_copy_batch_release(s->spec_ce, b);
+    if (rc) return rc;
+  }
+  tk->claims.clear();
   return publish_row(s, tk->layer, tk, static_cast<hipStream_t>(stream));
 }
 
@@ -667,6 +759,9 @@ extern "C" int pmoe_slab_prefill_done(pmoe_slab* s, int ticket) {
   std::lock_guard<std::mutex> lk(s->mu);
   Ticket* tk = live_ticket(s, ticket);
   if (!tk) return pmoe::fail(PMOE_EINVAL, "slab_prefill_done: no such open prefill group");
+  for (int b : tk->claims)  // never published: the host waits for those reads
+    if (pmoe_copy_batch_wait(s->spec_ce, b) == PMOE_OK && --s->batch_refs[b] == 0)
+      (void)pmoe_copy_batch_release(s->spec_ce, b);
   for (int slot : tk->from_free) s->free_slots.push_back(slot);
   for (int slot : tk->from_stage) s->stage_free.push_back(slot);
   if (!tk->temp.empty()) s->dirty[tk->layer] = 1;

@@ -286,6 +286,15 @@ def switch_glu(g: Geom, slab: torch.Tensor, table, n_experts: int, x: torch.Tens
     return y
 
 
+def count_missing(table, ids: torch.Tensor, n_experts: int, counter: torch.Tensor) -> None:
+    """counter (device int32 [1]) += routed ids of ``ids`` that ``table``
+    (device int32 [E], a tensor or a device address) maps to no slot."""
+    _need(ids, torch.int32, "ids")
+    _need(counter, torch.int32, "counter", 1)
+    check(lib().pmoe_count_missing(_table_ptr(table), _ptr(ids), ids.numel(), n_experts,
+                                   _ptr(counter), _stream()), "pmoe_count_missing")
+
+
 def moe_experts(g: Geom, slab, table, n_experts: int, x, inds, weights, shared_slot: int = -1,
                 shared_gate=None) -> torch.Tensor:
     """out [N, D] bf16 = sum_k w[n,k] FFN_{inds[n,k]}(x[n]) (+ shared)."""

@@ -97,6 +97,21 @@ class PrefetchRing:
         self.pred_used = 0
         self.spec_reads = 0
         self.governor = PredictGovernor(self, str(config.PREDICT))
+        # prefill-time prediction (cache.py:2580-2650): the next layer's
+        # router on this layer's MoE input, its reads started behind demand
+        self._ahead_gpu = None         # (target index, device ids [N, k])
+        self._ahead_host = None        # (target index, ids by predicted rows, desc)
+        self._ahead_open = {}          # target index -> (reads started, claims before)
+        # closed stitch (closed.py): a decode token run as one pass over the
+        # live tables, kept only when no routed expert was missing
+        self.closed_live = False       # closed.install ran for this model
+        self.closed_armed = False      # warm enough to attempt closed tokens
+        self.closed_active = False     # the current token is a closed attempt
+        self.warm_streak = 0           # per-layer decode tokens in a row with no miss
+        self.closed_cooldown = 0       # tokens to sit out after a replay
+        self.closed_ok = 0
+        self.closed_replay = 0
+        self._missing = None           # device int32 [1]: missing routed experts
 
     # ---- sequence protocol over the layers
     def __len__(self):
@@ -113,15 +128,18 @@ class PrefetchRing:
         return (self.flow and self._since_prefill >= int(config.FLOW_WARMUP)
                 and self._hit_ema >= float(config.FLOW_WARM_HIT))
 
-    def layer_call(self, index: int, n_tokens: int) -> bool:
-        """Called by each layer on entry; returns True when this call runs
-        as part of a flow token.  Layer 0 opens the token."""
+    def layer_call(self, index: int, n_tokens: int):
+        """Called by each layer on entry: "closed" inside a closed-stitch
+        attempt, "flow" when this call runs as part of a flow token, else
+        None (the per-layer path).  Layer 0 opens the token."""
+        if self.closed_active and n_tokens <= config.DECODE_MAX_TOKENS:
+            return "closed"
         if n_tokens > config.DECODE_MAX_TOKENS:
             if index == 0:
                 self.flow_drop()
                 self._since_prefill = 0
                 self._hit_ema = 0.0
-            return False
+            return None
         if index == 0:
             self._close_token_stats()
             self.token_flow = self._flow_ready()
@@ -136,7 +154,34 @@ class PrefetchRing:
                 self.flow_tokens += 1
             else:
                 self.sync_tokens += 1
-        return self.token_flow
+        return "flow" if self.token_flow else None
+
+    # ---- closed stitch
+    def begin_closed(self) -> None:
+        """Open a closed-stitch attempt: every changed table row is
+        republished (the attempt reads the live residency), and the device
+        miss counter is zeroed with a fill kernel (no memset, so the token
+        may be captured)."""
+        c = self.cache
+        for layer in self.layers:
+            c.sync_table(layer.layer_key)
+        if self._missing is None:
+            self._missing = torch.zeros(1, dtype=torch.int32, device=c.slab.buf.device)
+        else:
+            self._missing.zero_()
+        self.closed_active = True
+
+    def count_missing(self, table, ids) -> None:
+        """Add the layer's routed experts that ``table`` does not hold to the
+        attempt's device counter (no sync)."""
+        from . import kernels as K
+        K.count_missing(table, ids.reshape(-1).contiguous(), self.cache.n_experts, self._missing)
+
+    def end_closed(self) -> int:
+        """Close the attempt; the one host read of a closed token: the number
+        of routed experts that were not resident."""
+        self.closed_active = False
+        return int(self._missing.item())
 
     def _close_token_stats(self):
         if self._token_stats is None:
@@ -212,6 +257,48 @@ class PrefetchRing:
         for tgt, ids in self._pred_gpu:
             self._pred_host.append((tgt, sorted({int(e) for e in ids.reshape(-1).tolist()})))
         self._pred_gpu = []
+        if self._ahead_gpu is not None:
+            tgt, ids = self._ahead_gpu
+            self._ahead_gpu = None
+            counts = torch.bincount(ids.reshape(-1).long().clamp_min(0),
+                                    minlength=self.cache.n_experts).cpu()
+            order = sorted(range(len(counts)), key=lambda e: (-int(counts[e]), e))
+            self._ahead_host = (tgt, [e for e in order if counts[e] > 0])
+
+    # ---- prefill-time prediction
+    def predict_prefill(self, index: int, x2: torch.Tensor) -> None:
+        """Before layer ``index``'s routed-id sync in a prefill call: route
+        the call's rows through the next layer's router (device ids; they
+        ride that sync to the host)."""
+        self._ahead_gpu = self._ahead_host = None
+        if not config.PREFILL_AHEAD or x2 is None or index + 1 >= len(self.layers):
+            return
+        blk = self._router_of(index + 1)
+        if blk is not None and not self.cache.stitched:
+            self._ahead_gpu = (index + 1, blk.predict_ids(x2, 0))
+
+    def issue_prefill_ahead(self, index: int) -> int:
+        """Layer ``index``'s own reads are all queued: start the predicted
+        reads of the next layer, behind a fence at the stream's tail.
+        Returns the reads started."""
+        if self._ahead_host is None or self._ahead_host[0] != index + 1:
+            return 0
+        tgt, ids = self._ahead_host
+        self._ahead_host = None
+        c = self.cache
+        c.spec_fence()
+        before = c.raw_stats().ahead_claims
+        n = c.prefill_ahead(self.layers[tgt].layer_key, ids)
+        if n:
+            self._ahead_open[tgt] = (n, before)
+        return n
+
+    def settle_prefill_ahead(self, index: int) -> None:
+        """Layer ``index``'s prefill groups are done: score its guesses."""
+        got = self._ahead_open.pop(index, None)
+        if got is not None:
+            n, before = got
+            self.cache.note_ahead(n, self.cache.raw_stats().ahead_claims - before)
 
     def note_demand(self, index: int, ids) -> None:
         """A layer's fetch: score its prediction (pred_issued / pred_used)."""
@@ -255,6 +342,8 @@ class PrefetchRing:
 
     def stats(self) -> dict:
         return {"flow": self.flow, "flow_tokens": self.flow_tokens,
+                "closed_armed": self.closed_armed, "closed_ok": self.closed_ok,
+                "closed_replay": self.closed_replay,
                 "predict": self.governor.describe(),
                 "sync_tokens": self.sync_tokens, "pending_batches": len(self._pending),
                 "hit_ema": self._hit_ema, "predict_depth": self.predict_depth,

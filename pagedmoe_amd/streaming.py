@@ -129,11 +129,12 @@ class StreamedSwitchGLU(nn.Module):
         ordered = [e for e in ids if table[e] >= 0] + [e for e in ids if table[e] < 0]
         return [sorted(ordered[i:i + cap]) for i in range(0, len(ordered), cap)]
 
-    def passes(self, indices: torch.Tensor):
+    def passes(self, indices: torch.Tensor, x2: torch.Tensor | None = None):
         """Make the routed experts resident, one fetch group at a time.
         Yields (member ids, or None when this pass covers every routed id;
         device table pointer); the caller enqueues the pass's compute before
-        resuming the generator, and must run it to the end."""
+        resuming the generator, and must run it to the end.  ``x2`` (the
+        call's rows) feeds prefill-time prediction of the next layer."""
         c, lk = self.cache, self.layer_key
         if c.stitched:
             yield None, c.table_ptr(lk)
@@ -142,7 +143,11 @@ class StreamedSwitchGLU(nn.Module):
         if n_tokens <= config.DECODE_MAX_TOKENS:
             yield from self._decode_passes(self.plan_groups(indices))
         else:
+            if self.ring is not None:
+                self.ring.predict_prefill(self.ring_index, x2)
             yield from self._prefill_passes(self.routed_ids(indices))
+            if self.ring is not None:
+                self.ring.settle_prefill_ahead(self.ring_index)
 
     def _decode_passes(self, groups):
         c, lk = self.cache, self.layer_key
@@ -188,6 +193,8 @@ class StreamedSwitchGLU(nn.Module):
         cur = c.fetch_prefill(lk, first)
         self.last_groups = [cur.ids]
         single = not pending
+        if single and self.ring is not None:
+            self.ring.issue_prefill_ahead(self.ring_index)   # every read of this layer is queued
         n_pass = 0
         while cur is not None:
             c.publish_group(cur)
@@ -208,6 +215,8 @@ class StreamedSwitchGLU(nn.Module):
                 if grp:
                     nxt = c.fetch_prefill(lk, grp)
                     self.last_groups.append(("after_done" if cur is None else "open", nxt.ids))
+                    if not pending and self.ring is not None:
+                        self.ring.issue_prefill_ahead(self.ring_index)
             if cur is not None:
                 c.prefill_done(cur)
             cur = nxt
@@ -219,14 +228,14 @@ class StreamedSwitchGLU(nn.Module):
         cap = self.cache.routed_slots
         return [ids[i:i + cap] for i in range(0, len(ids), cap)]
 
-    def run_passes(self, ind2: torch.Tensor, compute) -> torch.Tensor:
+    def run_passes(self, ind2: torch.Tensor, compute, x2: torch.Tensor | None = None) -> torch.Tensor:
         """Per-slot outputs [N, K, D] over every pass of ``passes``:
         ``compute(ids, table)`` runs one pass.  A pass over a subset of the
         routed ids sees the others dropped to -1 (zero rows), and its rows are
         merged by selection, so every row is bit-identical to a single pass
         over a slab that holds every routed expert."""
         y = None
-        for member, table in self.passes(ind2):
+        for member, table in self.passes(ind2, x2):
             if member is None:
                 y = compute(ind2, table)
                 self.cache.note_compute(self.layer_key)
@@ -237,24 +246,33 @@ class StreamedSwitchGLU(nn.Module):
             y = y_g if y is None else torch.where(keep[..., None], y_g, y)
         return y
 
-    def flow_call(self, n_tokens: int) -> bool:
-        """Enter this layer's call on the ring; True for a flow token."""
-        return self.ring is not None and self.ring.layer_call(self.ring_index, n_tokens)
+    def graph_mode(self, n_tokens: int):
+        """Enter this layer's call on the ring: "flow" (a flow token),
+        "closed" (a closed-stitch attempt) or None (the per-layer path)."""
+        if self.ring is None:
+            return None
+        return self.ring.layer_call(self.ring_index, n_tokens)
 
     def call(self, x2: torch.Tensor, ind2: torch.Tensor, compute) -> torch.Tensor:
         """One seam call over flat rows x2 [N, D] and routing ind2 [N, K]:
-        a flow token computes once against the device table published at
-        the token's start (no host round trip; non-resident experts give
-        zero rows); otherwise every fetch pass of ``run_passes``, then
-        speculation for the layers ahead.  ``compute(ids, table)`` enqueues
-        the expert kernels of one pass."""
+        a flow token or a closed-stitch attempt computes once against the
+        device table published at the token's start (no host round trip;
+        non-resident experts give zero rows -- a closed attempt also counts
+        them on the device); otherwise every fetch pass of ``run_passes``,
+        then speculation for the layers ahead.  ``compute(ids, table)``
+        enqueues the expert kernels of one pass."""
         c = self.cache
-        if not c.stitched and self.flow_call(ind2.shape[0]):
-            y = compute(ind2, c.table_ptr(self.layer_key))
+        mode = None if c.stitched else self.graph_mode(ind2.shape[0])
+        if mode is not None:
+            table = c.table_ptr(self.layer_key)
+            y = compute(ind2, table)
             c.note_compute(self.layer_key)
-            self.ring.note(self.ring_index, ind2)
+            if mode == "flow":
+                self.ring.note(self.ring_index, ind2)
+            else:
+                self.ring.count_missing(table, ind2)
             return y
-        y = self.run_passes(ind2, compute)
+        y = self.run_passes(ind2, compute, x2)
         if self.ring is not None and ind2.shape[0] <= config.DECODE_MAX_TOKENS:
             self.ring.speculate(self.ring_index, x2)
         return y
@@ -297,16 +315,21 @@ class _MoEBlock(nn.Module):
         rc = self._route_cfg()
         sg = self.shared_expert_gate if self.use_shared else None
         sm = self.switch_mlp
-        if (isinstance(sm, StreamedSwitchGLU) and not sm.cache.stitched
-                and sm.flow_call(x2.shape[0])):
-            # flow token: the whole block on the GPU against the device table
-            # published at the token's start (streaming.py:675-724)
-            out, inds, w = K.moe_block(g, rc, slab, sm.cache.table_ptr(sm.layer_key),
-                                       self.gate_weight, x2, score_bias=self._score_bias(),
-                                       logit_bias=self.logit_bias, shared_slot=shared_slot,
-                                       shared_gate=sg)
+        mode = (sm.graph_mode(x2.shape[0])
+                if isinstance(sm, StreamedSwitchGLU) and not sm.cache.stitched else None)
+        if mode is not None:
+            # flow token or closed-stitch attempt: the whole block on the GPU
+            # against the device table published at the token's start
+            # (streaming.py:675-724, :905-935)
+            tab = sm.cache.table_ptr(sm.layer_key)
+            out, inds, w = K.moe_block(g, rc, slab, tab, self.gate_weight, x2,
+                                       score_bias=self._score_bias(), logit_bias=self.logit_bias,
+                                       shared_slot=shared_slot, shared_gate=sg)
             sm.cache.note_compute(sm.layer_key)
-            sm.ring.note(sm.ring_index, inds)
+            if mode == "flow":
+                sm.ring.note(sm.ring_index, inds)
+            else:
+                sm.ring.count_missing(tab, inds)
             self.last_routing = (inds, w)
             return out.reshape(shape)
         if isinstance(sm, StreamedSwitchGLU) and not sm.cache.stitched:
@@ -320,7 +343,17 @@ class _MoEBlock(nn.Module):
                                                      self.norm_topk_prob, self.routed_scale)
             out = None
             y = None
-            for member, tab in sm.passes(inds):
+            decode = x2.shape[0] <= config.DECODE_MAX_TOKENS
+            for member, tab in sm.passes(inds, x2):
+                if member is None and decode:
+                    # every routed expert is resident: the one-launch block
+                    # (it routes again, to the same bits), the same arithmetic
+                    # as a flow token or a closed-stitch attempt
+                    out = K.moe_block(g, rc, slab, tab, self.gate_weight, x2,
+                                      score_bias=self._score_bias(), logit_bias=self.logit_bias,
+                                      shared_slot=shared_slot, shared_gate=sg)[0]
+                    sm.cache.note_compute(sm.layer_key)
+                    continue
                 if member is None:
                     out = K.moe_experts(g, slab, tab, n_exp, x2, inds, w, shared_slot, sg)
                     sm.cache.note_compute(sm.layer_key)

@@ -188,3 +188,31 @@ def run_prefill_kat(policy, kat):
     assert placed == kat["then_placed"], placed
     assert sorted(before - set(policy.table())) == kat["then_evicted"]
     return policy
+
+
+# Prefill-time prediction (cache.py:2580-2650), 16 routed slots (budget 12)
+# and a 6-slot stage at 16..21.  Decode makes layer 0's 0..9 resident (slots
+# 0..9; free list [15, 14, 13, 12, 11, 10]).  prefill_ahead for layer 1,
+# priority order [5, 3, 9, 1, 7, 2, 8], floors 2 and 2: 5, 3, 9, 1 take free
+# slots 10..13 while more than 2 stay free; 7, 2, 8 take stage slots 16, 17,
+# 18 while more than 2 stay in the stage.  Layer 1's prefill group over
+# {1..6}: 1, 2, 3, 5 are claimed (hits, no read); 1 and 3 (routed slots) are
+# installed while the table is under budget (10 -> 12), 2 (stage slot 17)
+# and 5 (routed slot 10, table at budget) are held for the group; 4 and 6
+# miss into free slots 14 and 15, held.  The unclaimed guesses 9, 7, 8 are
+# handed back: once landed, slot 12 returns to the free list and 16, 18 to
+# the stage; the group's own slots come back after it: free [12, 14, 10, 15].
+PREFILL_AHEAD = dict(
+    slots=16,
+    stage=(16, 6),
+    warm=list(range(10)),
+    ahead=[5, 3, 9, 1, 7, 2, 8], free_floor=2, stage_floor=2,
+    started=[(5, 10), (3, 11), (9, 12), (1, 13), (7, 16), (2, 17), (8, 18)],
+    prefill=[1, 2, 3, 4, 5, 6],
+    prefill_placed=[(4, 14), (6, 15)],
+    compute_row={1: 13, 3: 11, 2: 17, 4: 14, 5: 10, 6: 15},
+    after={1: 13, 3: 11},
+    hits=4, misses=10 + 2, evictions=0,
+    free_after=[12, 14, 10, 15],
+    stage_after=[21, 20, 19, 16, 18, 17],
+)

@@ -882,3 +882,232 @@ def test_prefill_groups_and_flow_under_the_slot_ledger(monkeypatch):
     assert led.counts["ISSUE"] > 0 and led.counts["BATCH_JOIN"] > 0
     assert led.conflicts == [], led.conflicts[:3]
     cache.close()
+
+
+# ---------------------------------------------------------------- closed stitch
+
+class _TrimKV:
+    """KV cache with mlx-lm's interface: offset, update_and_fetch, trim(n)."""
+
+    def __init__(self):
+        self.k = self.v = None
+
+    @property
+    def offset(self):
+        return 0 if self.k is None else self.k.shape[2]
+
+    def update_and_fetch(self, k, v):
+        self.k = k if self.k is None else torch.cat([self.k, k], 2)
+        self.v = v if self.v is None else torch.cat([self.v, v], 2)
+        return self.k, self.v
+
+    def trim(self, n):
+        n = min(n, self.offset)
+        self.k, self.v = self.k[:, :, :self.offset - n], self.v[:, :, :self.offset - n]
+        return n
+
+
+def _closed_decoder(spec, seed, slots):
+    """A 2-layer pre-norm decoder (attention with a trimmable KV cache, MoE
+    blocks paged through ``slots`` routed slots) and its ring."""
+    import math
+
+    _, S = _mods()
+    moe_model, ol = _softmax_model(spec, 2, seed=seed)
+    cache = S.build_cache_for(moe_model, slots=slots)
+    ring = S.patch_model(moe_model, cache, predict_mode="off")
+
+    class Attn(nn.Module):
+        def __init__(self, s):
+            super().__init__()
+            g = torch.Generator(device=DEV).manual_seed(s)
+            self.w = [torch.randn(spec.hidden, spec.hidden, generator=g, device=DEV)
+                      / spec.hidden ** 0.5 for _ in range(4)]
+
+        def forward(self, x, cache):
+            b, t, d = x.shape
+            q, k, v = (z.reshape(b, t, 4, d // 4).transpose(1, 2).contiguous()
+                       for z in (x @ self.w[0], x @ self.w[1], x @ self.w[2]))
+            k, v = cache.update_and_fetch(k, v)
+            s = q @ k.transpose(-1, -2).contiguous() / math.sqrt(d // 4)
+            o = (torch.softmax(s, -1) @ v).transpose(1, 2).reshape(b, t, d)
+            return 0.05 * (o @ self.w[3])          # small: the residual keeps routing steady
+
+    class Decoder(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.attn = nn.ModuleList([Attn(seed + 10 + i) for i in range(2)])
+            self.moe = nn.ModuleList([moe_model.layers[i].mlp for i in range(2)])
+
+        def forward(self, x, cache=None):
+            for a, m, c in zip(self.attn, self.moe, cache):
+                x = x + a(x, c)
+                x = x + m(x).float()
+            return x
+
+    dec = Decoder()
+    dec._pagedmoe_ring, dec._pagedmoe_cache = ring, cache
+    return dec, cache, ring, ol
+
+
+def test_closed_stitch_keeps_exact_tokens_and_replays_misses(monkeypatch):
+    """Closed stitch (streaming.py:2691-2870): after warm per-layer tokens
+    the decode token runs both MoE layers against the live tables with no
+    routed-id sync; its device miss count decides.  Every token -- kept or
+    replayed after a forced miss -- is bit-identical to a per-layer twin,
+    and the KV caches end in the same state."""
+    from pagedmoe_amd import closed as C, config
+
+    _, S = _mods()
+    monkeypatch.setattr(config, "STITCH_PARTIAL", True)
+    spec = O.LayerSpec(1024, 32, 512, 4)
+    dec, cache, ring, _ = _closed_decoder(spec, 190, slots=24)
+    ref, ref_cache, _, _ = _closed_decoder(spec, 190, slots=24)
+    assert not cache.stitched and C.install(dec)
+    rng = np.random.default_rng(191)
+    hot = [torch.from_numpy(rng.standard_normal((1, 1, spec.hidden), dtype=np.float32)).to(DEV)
+           for _ in range(2)]
+    cold = [torch.from_numpy(rng.standard_normal((1, 1, spec.hidden), dtype=np.float32)).to(DEV)
+            for _ in range(3)]
+    kv, kv_ref = [_TrimKV(), _TrimKV()], [_TrimKV(), _TrimKV()]
+    syncs = {"n": 0}
+    orig = S.StreamedSwitchGLU.routed_ids
+
+    def counted(self, indices):
+        if self.cache is cache:            # the closed-stitch model's layers only
+            syncs["n"] += 1
+        return orig(self, indices)
+
+    monkeypatch.setattr(S.StreamedSwitchGLU, "routed_ids", counted)
+    seq = [hot[t % 2] for t in range(12)] + [cold[0]] + [hot[t % 2] for t in range(4)]
+    seq += [cold[1], cold[2]]
+    log = []
+    for t, x in enumerate(seq):
+        ok, rep, n0 = ring.closed_ok, ring.closed_replay, syncs["n"]
+        with torch.no_grad():
+            y = dec(x, cache=kv)
+            y_ref = ref(x, cache=kv_ref)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_ref), f"token {t}: closed-stitch output differs from per-layer"
+        kind = ("kept" if ring.closed_ok > ok else "replayed" if ring.closed_replay > rep
+                else "per-layer")
+        if kind == "kept":
+            assert syncs["n"] == n0, f"token {t}: a kept closed token synced per layer"
+        log.append(kind)
+    print(f"[closed] {log} ok={ring.closed_ok} replay={ring.closed_replay}", flush=True)
+    assert ring.closed_ok >= 3 and ring.closed_replay >= 1
+    assert "replayed" in log[12:13] or "replayed" in log[17:]
+    for a, b in zip(kv, kv_ref):
+        assert a.offset == b.offset == len(seq)
+        assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
+    assert get_stats_ring(dec)["closed_ok"] == ring.closed_ok
+    cache.close()
+    ref_cache.close()
+
+
+def get_stats_ring(model):
+    _, S = _mods()
+    return S.get_stats(model)["ring"]
+
+
+# ---------------------------------------------------------------- prefill-time prediction
+
+def test_native_prefill_ahead_known_answer():
+    """The native policy on the hand-worked PREFILL_AHEAD trace
+    (tests/slot_kats.py, from cache.py:2580-2650), with real reads: guesses
+    take free slots above the floor then stage slots above its floor; the
+    next layer's prefill group claims four of them (no read), misses two,
+    hands back the rest; the claimed slots hold the host store's bytes."""
+    from pagedmoe_amd.cache import ExpertCache, HostExpertStore
+    from tests import slot_kats
+
+    kat = slot_kats.PREFILL_AHEAD
+    _, S = _mods()
+    spec = O.LayerSpec(1024, 32, 512, 4)
+    model, _ = _softmax_model(spec, 2, seed=200)
+    glus = S.find_switch_glus(model)
+    g = glus[0][1].geom
+    store = HostExpertStore(g, 2, spec.experts)
+    for li, (_, m) in enumerate(glus):
+        for e in range(spec.experts):
+            store.write_from_slot(li, e, m.slab, e)
+    keys = [p for p, _ in glus]
+    cache = ExpertCache(g, kat["slots"], keys, spec.experts, host_store=store,
+                        stage_slots=kat["stage"][1])
+    assert cache.stage_first == kat["stage"][0]
+    led = cache.verify_slots(True)
+    cache.fetch(keys[0], kat["warm"])
+    cache.spec_fence()
+    n = cache.prefill_ahead(keys[1], kat["ahead"], kat["free_floor"], kat["stage_floor"])
+    assert n == len(kat["started"])
+    grp = cache.fetch_prefill(keys[1], kat["prefill"])
+    assert grp.n_miss == len(kat["prefill_placed"]) and grp.n_unplaced == 0
+    cache.publish_group(grp)
+    cache.join()
+    cache.note_compute(keys[1])
+    row = cache.device_table(keys[1])
+    assert {e: int(row[e]) for e in kat["prefill"]} == kat["compute_row"]
+    for e, slot in kat["compute_row"].items():
+        assert np.array_equal(cache.slab.slot_bytes(slot).cpu().numpy(),
+                              store.expert_view(1, e)), (e, slot)
+    cache.sync_spec()
+    cache.drop_staged()
+    cache.prefill_done(grp)
+    t1 = cache.host_table(keys[1])
+    assert {e: int(s) for e, s in enumerate(t1) if s >= 0} == kat["after"]
+    st = cache.stats()
+    assert (st["hits"], st["misses"], st["evictions"]) == (kat["hits"], kat["misses"],
+                                                           kat["evictions"])
+    assert st["prefill_ahead_reads"] == 7 and st["prefill_ahead_used"] == 4
+    assert cache.capacity()[:2] == (len(kat["free_after"]), len(kat["stage_after"]))
+    assert led.conflicts == [], led.conflicts[:3]
+    cache.close()
+    store.close()
+
+
+def test_prefill_ahead_keeps_outputs_and_claims_reads(monkeypatch):
+    """A 4-layer, 96-token prefill through a 20-slot cache (48 stage slots) on a residual
+    stream: with prefill-time prediction each layer starts the next one's
+    predicted reads after its own; the next layer claims the ones it routes.
+    Outputs are bit-identical to a prediction-off twin, the native ledger
+    shows no race, and fewer demand reads wait at the layer boundaries."""
+    from pagedmoe_amd import config
+
+    _, S = _mods()
+    spec = O.LayerSpec(1024, 32, 512, 4)
+
+    def build(ahead):
+        model, _ = _softmax_model(spec, 4, seed=210)
+        cache = S.build_cache_for(model, slots=20, stage_slots=48)
+        S.patch_model(model, cache, predict_mode="off")
+        return model, cache
+
+    model, cache = build(True)
+    twin, twin_cache = build(False)
+    led = cache.verify_slots(True)
+    rng = np.random.default_rng(211)
+    h0 = rng.standard_normal((96, spec.hidden), dtype=np.float32)
+    steps = [0.05 * rng.standard_normal((96, spec.hidden), dtype=np.float32) for _ in range(4)]
+    for m, on in ((model, True), (twin, False)):
+        monkeypatch.setattr(config, "PREFILL_AHEAD", on)
+        h = torch.from_numpy(h0).to(DEV)
+        outs = []
+        for li, layer in enumerate(m.layers):
+            outs.append(layer.mlp(h.to(torch.bfloat16)))
+            h = h + torch.from_numpy(steps[li]).to(DEV)
+        torch.cuda.synchronize()
+        if on:
+            got = outs
+        else:
+            ref = outs
+    for li, (a, b) in enumerate(zip(got, ref)):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), li
+    st, st_ref = cache.stats(), twin_cache.stats()
+    print(f"[prefill ahead] reads {st['prefill_ahead_reads']} used {st['prefill_ahead_used']} "
+          f"skipped {st['prefill_ahead_skipped']}; demand misses {st['misses']} vs "
+          f"{st_ref['misses']} without; ledger {led.report()}", flush=True)
+    assert st["prefill_ahead_reads"] > 0 and st["prefill_ahead_used"] > 0
+    assert st["misses"] < st_ref["misses"]
+    assert led.conflicts == [], led.conflicts[:3]
+    cache.close()
+    twin_cache.close()

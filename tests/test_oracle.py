@@ -650,3 +650,39 @@ def test_lfru_matches_list_implementation(seed, slots, experts, k):
         assert {e: pol.freq.get((0, e), 0) for (_, e) in pol.lru} == ref.count
     assert pol.evictions == ref.evicted
     assert ref.reprieves > 50      # the second-chance branch is exercised
+
+
+def test_prefill_ahead_known_answer():
+    """Prefill-time prediction (cache.py:2580-2650): free slots above a
+    floor, then stage slots above a floor, never an eviction; the next
+    layer's prefill group claims what it routes and the rest is handed back
+    (hand-worked trace in tests/slot_kats.py)."""
+    from tests import slot_kats
+    kat = slot_kats.PREFILL_AHEAD
+    pol = O.SlotPolicy(kat["slots"])
+    pol.set_stage(*kat["stage"])
+    pol.step(0, kat["warm"])
+    assert pol.prefill_ahead(1, kat["ahead"], kat["free_floor"], kat["stage_floor"]) == \
+        kat["started"]
+    ticket, placed, unplaced = pol.step_prefill(1, kat["prefill"])
+    assert placed == kat["prefill_placed"] and unplaced == 0
+    row = pol.compute_row(ticket, 64)
+    assert {e: int(s) for e, s in enumerate(row) if s >= 0 and e in kat["prefill"]} == \
+        kat["compute_row"]
+    pol.settle()
+    pol.prefill_done(ticket)
+    assert {e: int(s) for e, s in enumerate(pol.table(1, 64)) if s >= 0} == kat["after"]
+    assert (pol.hits, pol.misses, pol.evictions) == (kat["hits"], kat["misses"],
+                                                     kat["evictions"])
+    assert pol.free == kat["free_after"] and pol.stage_free == kat["stage_after"]
+
+
+def test_prefill_ahead_floors_and_skips():
+    """Resident, staged and repeated ids are skipped; nothing is started
+    when both lists are at their floors."""
+    pol = O.SlotPolicy(16)
+    pol.set_stage(16, 4)
+    pol.step(0, list(range(12)))                  # free [15, 14, 13, 12]
+    assert pol.prefill_ahead(0, [3, 20, 20, 21], 2, 4) == [(20, 12), (21, 13)]
+    assert pol.prefill_ahead(0, [20, 22], 2, 4) == []   # 20 staged; free at the floor
+    assert pol.prefill_ahead(0, [22, 23], 2, 3) == [(22, 16)]
