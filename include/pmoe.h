@@ -186,6 +186,13 @@ int pmoe_moe_workspace_error_async(const void* ws, uint32_t* host_dst, void* str
  * normally.  Applies to launches issued after the call. */
 int pmoe_set_barrier_spin(uint64_t ticks);
 
+/* Debug: with on != 0, block 0 of the expert-per-XCD decode launch reports
+ * an XCD other than its own, so its group looks split across two XCDs: the
+ * placement check must then set error bit 1 and poison the layer output at
+ * once (tests force the failure this way; every block still exits
+ * normally).  Applies to launches issued after the call. */
+int pmoe_set_split_probe(int on);
+
 /* The seam: y[n, k, :] = FFN_{inds[n,k]}(x[n, :]) as bf16 [n, k, hidden],
  * uncombined, in (token, k) order.  Expert e lives in slab slot table[e]
  * (slab base + slot * expert_bytes).  Replaces

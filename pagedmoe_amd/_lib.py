@@ -89,6 +89,7 @@ SIGNATURES = {
     "pmoe_prefill_tile_rows": (_I, [_I, _I, _I]),
     "pmoe_moe_workspace_error_async": (_I, [_P, _P, _P]),
     "pmoe_set_barrier_spin": (_I, [ctypes.c_uint64]),
+    "pmoe_set_split_probe": (_I, [_I]),
     "pmoe_switch_glu": (_I, [ctypes.POINTER(Geom), _P, _P, _I, _P, _P, _I, _I, _P, _P, _SZ, _P]),
     "pmoe_moe_experts": (_I, [ctypes.POINTER(Geom), _P, _P, _I, _P, _P, _P, _I, _I, _I, _P,
                               _P, _P, _SZ, _P]),

@@ -7,7 +7,7 @@ PREFILL_STAGE / PREFILL_STAGE_GROUP_MB :1603-1608, GROUP_BYTES :1531;
 ``sync_from_environ()`` re-reads them (config.py:853).  FUSED_PREFILL
 :1633 and ATTN_SUB_CHUNK :1562 for the fused prefill pass; PREFILL_AHEAD
 :1583 for prefill-time prediction; FLOW / FLOW_WARMUP / FLOW_WARM_HIT
-:1218-1237 for flow decode; PREDICT_DEPTH :747, PREDICT_SLACK :761 and
+:1218-1237 and FLOW_MAX_CRIT :1253 for flow decode; PREDICT_DEPTH :747, PREDICT_SLACK :761 and
 PREFETCH_DEPTH :722 for speculative prefetch (PREFETCH_DEPTH defaults to 0
 here: the previous-token heuristic pays off with the reference's SSD queue,
 not a PCIe copy engine); PREDICT and the governor knobs :735-741;
@@ -51,6 +51,7 @@ PREFILL_AHEAD = True      # a prefill layer starts the next layer's predicted re
 FLOW = False              # decode tokens with no host sync inside (residency once per token)
 FLOW_WARMUP = 2           # tokens after a prefill that take the per-layer path first
 FLOW_WARM_HIT = 0.9       # hit-rate EMA the per-layer path must reach before flow resumes
+FLOW_MAX_CRIT = 5.0       # flow stops above this many missing routed experts per token (EMA)
 PREDICT_DEPTH = 3         # route prediction: layers predicted ahead per stride
 PREDICT_SLACK = 2         # extra experts per predicted layer beyond its top-k
 PREFETCH_DEPTH = 0        # previous-token heuristic: next layers' last ids (0 = off)
@@ -71,7 +72,7 @@ def sync_from_environ() -> None:
     global COPY_STREAMS
     global DECODE_MAX_TOKENS, PREFILL_STAGE, PREFILL_STAGE_GROUP_MB, GROUP_BYTES
     global FUSED_PREFILL, ATTN_SUB_CHUNK, ATTN_SCORE_MB, FLOW, FLOW_WARMUP, FLOW_WARM_HIT
-    global PREFILL_AHEAD
+    global PREFILL_AHEAD, FLOW_MAX_CRIT
     global PREDICT_DEPTH, PREDICT_SLACK, PREFETCH_DEPTH, PREDICT, PREDICT_WINDOW
     global PREDICT_MIN_TOKENS, PREDICT_MARGIN, PREDICT_Z, PREDICT_MAX_PROBE, PREDICT_HOLD
     global SLAB_VERIFY
@@ -93,6 +94,7 @@ def sync_from_environ() -> None:
     FLOW = _env("FLOW", False, _bool)
     FLOW_WARMUP = _env("FLOW_WARMUP", 2, int)
     FLOW_WARM_HIT = _env("FLOW_WARM_HIT", 0.9, float)
+    FLOW_MAX_CRIT = _env("FLOW_MAX_CRIT", 5.0, float)
     PREDICT_DEPTH = _env("PREDICT_DEPTH", 3, int)
     PREDICT_SLACK = _env("PREDICT_SLACK", 2, int)
     PREFETCH_DEPTH = _env("PREFETCH_DEPTH", 0, int)

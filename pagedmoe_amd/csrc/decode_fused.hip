@@ -82,6 +82,7 @@ constexpr int kFMaxH = 20480;          // bf16 h values staged in LDS in phase D
 #endif
 constexpr uint64_t kSpinTicks = 50000000ull;  // 0.5 s at 100 MHz
 uint64_t g_spin_ticks = kSpinTicks;           // host: limit passed to every launch
+uint32_t g_split_probe = 0;                   // host: pmoe_set_split_probe
 #ifndef PMOE_RANK1
 #define PMOE_RANK1 1  // single-token routing by rank counts over the block
 #endif
@@ -104,6 +105,7 @@ struct FusedArgs {
   float* w_out;
   DecodeSync* sync;
   uint64_t spin;               // barrier poll limit, realtime-clock ticks
+  uint32_t split_probe;        // debug: block 0 reports another XCD (placement check test)
   int n_blocks;
   int tile;                    // hidden rows per block in phase D
 };
@@ -557,7 +559,15 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
 // group: the blocks with b % 8 == x (group x) run pick x, the x-th expert of
 // the top-8 list.  The dispatcher deals blocks round robin over the 8 XCDs
 // (from wherever the previous dispatch left off), so a group shares one XCD
-// and its L2; correctness does not depend on that, only speed does.
+// and its L2.  Correctness depends on that: h travels through the group's L2
+// (phase C).  Each block therefore checks its placement as it starts: it
+// ORs the bit of its XCC_ID into its group's mask for this launch (a
+// device-scope atomic; two masks alternate by launch parity, and the
+// group's last arrival clears the other one for the next launch), and a
+// block that finds another XCD's bit there sets error bit 1 at once and
+// poisons its outputs; every h poll also gives up as soon as any error bit
+// is set, so a split group fails loudly within microseconds instead of
+// waiting out the spin limit.
 //
 // No phase waits at a barrier.  Everything one block needs from another
 // travels as tagged data at device scope and is polled until the tag of
@@ -591,6 +601,8 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
 // block goes on poisoned: its h words and partial rows are NaN, which every
 // output that depends on them inherits through the combine.
 constexpr int kXcdPollSleep = 1;
+// s_getreg operand of HW_REG_XCC_ID (hwreg 20), bits [3:0]: this wave's XCD.
+constexpr int kHwRegXccId = 20 | (0 << 6) | ((4 - 1) << 11);
 
 template <class T>
 __device__ __forceinline__ T device_load(const T* p) {
@@ -619,6 +631,7 @@ __global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(
   __shared__ __align__(16) uint16_t s_h[kXcdMaxInter];
   __shared__ __align__(16) float s_y[kFWaves][kXcdCount][16];  // per wave: partial rows
   __shared__ uint32_t s_tag;
+  __shared__ bool s_last, s_split;
   __shared__ int s_slot;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -692,13 +705,32 @@ __global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (!table_done && int(threadIdx.x) < n_experts) s_table[threadIdx.x] = tab;
-    if (lane == 0) s_tag = __builtin_amdgcn_readfirstlane(old) / uint32_t(per_xcd) + 1u;
+    if (lane == 0) {
+      s_tag = __builtin_amdgcn_readfirstlane(old) / uint32_t(per_xcd) + 1u;
+      s_last = old % uint32_t(per_xcd) == uint32_t(per_xcd) - 1u;
+    }
   } else if (int(threadIdx.x) < n_experts) {
     s_table[threadIdx.x] = tab;
   }
   trace_mark(sy, 1);
   __syncthreads();
   const uint32_t tag = s_tag;
+
+  // placement: this block's XCD into the group's mask of this launch (the
+  // atomic's answer is read after routing, so its round trip overlaps it)
+  uint32_t xseen = 0, xbit = 0;
+  if (threadIdx.x == 64) {
+    uint32_t xcc = __builtin_amdgcn_s_getreg(kHwRegXccId) & 15u;
+    if (a.split_probe && blockIdx.x == 0) xcc ^= 1u;
+    xbit = 1u << xcc;
+    uint32_t* masks = reinterpret_cast<uint32_t*>(hdr + kXcdCounterOffset +
+                                                  xcd * kDecodeFlagStride) + 1;
+    xseen = __hip_atomic_fetch_or(&masks[tag & 1u], xbit, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+    if (s_last)
+      __hip_atomic_store(&masks[(tag & 1u) ^ 1u], 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
 
   // B: every logit of this launch into LDS (threads 128.. poll), then routing
   bool late = false;
@@ -729,9 +761,15 @@ __global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(
     const int e = L.ids[xcd];  // always < rt.e: the ranks are a permutation
     s_slot = e >= 0 && e < rt.e ? s_table[e] : -1;
   }
+  if (threadIdx.x == 64) {
+    s_split = (xseen & ~xbit) != 0u;  // another XCD already ran a block of this group
+    if (s_split)  // error bit 1: the group is split
+      __hip_atomic_fetch_or(&sy->error, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   __syncthreads();
   trace_mark(sy, 3);
   const int slot = s_slot;
+  const bool bad = bad_logits || s_split;
 
   // C: gate/up rows of the pick, two row steps in flight per wave (as in the
   // grid-wide launch's single-row items); h words carry the tag
@@ -755,7 +793,7 @@ __global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(
     // h stays in the group's XCD: a plain store lands in its L2 (and is
     // acknowledged there), where the group's device-scope reads find it
     auto put_h = [&](int o, float hv) {
-      const uint32_t bits = bad_logits ? 0x7fc0u : (slot < 0 ? 0u : uint32_t(f2bf(hv)));
+      const uint32_t bits = bad ? 0x7fc0u : (slot < 0 ? 0u : uint32_t(f2bf(hv)));
       hx[o] = htag | bits;
     };
     GroupAct<UG> act[GG];
@@ -797,7 +835,7 @@ __global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(
 
   // D: the group's h row into LDS (every word of this launch), then the down
   // tiles of the pick and the combine
-  bool poison = bad_logits;
+  bool poison = bad;
   if (slot >= 0) {
     // 4 words a thread per poll (one 16-byte load, two 8-byte device-scope
     // reads); a chunk is kept once all 4 carry this launch's tag
@@ -814,7 +852,8 @@ __global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(
                          (uint32_t(w1) & 0xFFFFu) | (uint32_t(w1 >> 32) << 16));
           break;
         }
-        if (__builtin_amdgcn_s_memrealtime() - t_entry > a.spin) {
+        if (__builtin_amdgcn_s_memrealtime() - t_entry > a.spin ||
+            device_load(&sy->error) != 0u) {  // timed out, or another block failed
           h_late = true;
           break;
         }
@@ -1052,6 +1091,12 @@ extern "C" int pmoe_set_barrier_spin(uint64_t ticks) {
   return PMOE_OK;
 }
 
+extern "C" int pmoe_set_split_probe(int on) {
+  pmoe::clear_error();
+  g_split_probe = on ? 1u : 0u;
+  return PMOE_OK;
+}
+
 #ifdef PMOE_FUSED_TRACE
 extern "C" int pmoe_debug_trace(uint64_t* out, int n) {
   return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_trace), size_t(n) * sizeof(uint64_t)) == hipSuccess
@@ -1083,6 +1128,7 @@ int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int
   a.w_out = w_out;
   a.sync = sync;
   a.spin = g_spin_ticks;
+  a.split_probe = g_split_probe;
   // One token, top-8 softmax, no shared expert: the expert-per-XCD launch
   // when the grid splits into 8 groups of a power-of-two block count.
   if (xcd_enabled() && rank1_route_ok(rt) && rt.k == kXcdCount && rt.kk == rt.k && !gate_extra &&

@@ -98,7 +98,8 @@ size_t decode_record_bytes();
 struct DecodeSync {
   uint32_t arrive[2];  // groups arrived at barrier 1 / barrier 2
   uint32_t epoch;      // launches completed on this workspace
-  uint32_t error;      // sticky: bit 0 = a barrier or data wait timed out
+  uint32_t error;      // sticky: bit 0 = a barrier or data wait timed out,
+                       // bit 1 = an expert-per-XCD block group spanned two XCDs
 };
 // Router blocks of a several-token decode call arrive here (decode.hip
 // router_route_kernel; its own 128-byte line; the last arriver resets it).
@@ -110,12 +111,14 @@ constexpr size_t kDecodeFlagStride = 128;  // bytes between two blocks' flags
 constexpr size_t kDecodeGroupOffset = 256 + kDecodeMaxBlocks * kDecodeFlagStride;
 // Expert-per-XCD launch (decode_fused.hip): one launch counter per block
 // group (its own 128-byte line; each of the group's blocks adds 1 per
-// launch, so counter / blocks-per-group numbers the launch), one arrival
+// launch, so counter / blocks-per-group numbers the launch; the line's next
+// two words are the group's masks of XCDs seen, one per launch parity, each
+// cleared by the group's last arrival of the launch before), one arrival
 // counter per down tile (64 bytes apart; 8 arrivals per launch), the router
 // logits as tagged 64-bit words (launch tag << 32 | fp32 bits), each group's
 // h as tagged 32-bit words (tag & 0xFFFF << 16 | bf16), and each group's
 // fp32 down partials.  Counters only grow and tags name the launch, so
-// nothing is cleared between launches.
+// nothing else is cleared between launches.
 constexpr int kXcdCount = 8;
 constexpr int kXcdMaxHidden = 8192;
 constexpr int kXcdMaxInter = 8192;

@@ -249,6 +249,12 @@ def check_workspace_errors() -> None:
     raise_workspace_errors()
 
 
+def set_split_probe(on: bool) -> None:
+    """Debug: make the expert-per-XCD decode's group 0 look split across two
+    XCDs (pmoe_set_split_probe), so its placement check fires."""
+    check(lib().pmoe_set_split_probe(int(bool(on))), "pmoe_set_split_probe")
+
+
 def set_barrier_spin(ticks: int) -> None:
     """Debug: grid-barrier poll limit of later one-launch decode calls in
     100 MHz ticks (0 = the default 0.5 s); see pmoe_set_barrier_spin."""

@@ -83,6 +83,8 @@ class PrefetchRing:
         self._fenced = False
         self._since_prefill = 0
         self._hit_ema = 0.0
+        self._miss_ema = None          # routed experts missing per token (all layers)
+        self._flow_backoff = False     # flow left because the table stopped holding the routing
         self._token_stats = None
         self.flow_tokens = 0
         self.sync_tokens = 0
@@ -125,8 +127,28 @@ class PrefetchRing:
 
     # ---- token boundaries
     def _flow_ready(self) -> bool:
-        return (self.flow and self._since_prefill >= int(config.FLOW_WARMUP)
-                and self._hit_ema >= float(config.FLOW_WARM_HIT))
+        """Whether the next token runs as a flow token.  In flow, stay while
+        the missing routed experts per token (EMA over every layer, the
+        reference's critical misses, streaming.py:1585-1613) stay at or
+        under FLOW_MAX_CRIT: above it the table has stopped holding what the
+        router wants, and flow would be dropping experts the per-layer path
+        waits for.  Out of flow, enter after FLOW_WARMUP tokens once the hit
+        EMA reaches FLOW_WARM_HIT, and after such an exit only once the
+        misses are back under half the bar."""
+        if not self.flow:
+            return False
+        bar = float(config.FLOW_MAX_CRIT)
+        miss = self._miss_ema
+        if self.token_flow:
+            if bar > 0 and miss is not None and miss > bar:
+                self._flow_backoff = True
+                return False
+            return True
+        if self._since_prefill < int(config.FLOW_WARMUP) or self._hit_ema < float(config.FLOW_WARM_HIT):
+            return False
+        if bar > 0 and self._flow_backoff and miss is not None and miss > bar / 2:
+            return False
+        return True
 
     def layer_call(self, index: int, n_tokens: int):
         """Called by each layer on entry: "closed" inside a closed-stitch
@@ -137,12 +159,15 @@ class PrefetchRing:
         if n_tokens > config.DECODE_MAX_TOKENS:
             if index == 0:
                 self.flow_drop()
+                self.token_flow = False
                 self._since_prefill = 0
                 self._hit_ema = 0.0
             return None
         if index == 0:
             self._close_token_stats()
-            self.token_flow = self._flow_ready()
+            was_flow, self.token_flow = self.token_flow, self._flow_ready()
+            if was_flow and not self.token_flow:
+                self.flow_drop()           # land and install what flow admitted
             if self.token_flow and self.auto_pump:
                 self.begin_token()
             self._since_prefill += 1
@@ -190,6 +215,7 @@ class PrefetchRing:
         h, m = st.hits - self._token_stats[0], st.misses - self._token_stats[1]
         if h + m:
             self._hit_ema = 0.5 * self._hit_ema + 0.5 * (h / (h + m))
+            self._miss_ema = m if self._miss_ema is None else 0.7 * self._miss_ema + 0.3 * m
         self._token_stats = None
 
     def begin_token(self, replayed: bool = False) -> None:
@@ -346,7 +372,8 @@ class PrefetchRing:
                 "closed_replay": self.closed_replay,
                 "predict": self.governor.describe(),
                 "sync_tokens": self.sync_tokens, "pending_batches": len(self._pending),
-                "hit_ema": self._hit_ema, "predict_depth": self.predict_depth,
+                "hit_ema": self._hit_ema, "miss_ema": self._miss_ema,
+                "predict_depth": self.predict_depth,
                 "pred_issued": self.pred_issued, "pred_used": self.pred_used,
                 "pred_precision": self.pred_used / self.pred_issued if self.pred_issued else None,
                 "spec_reads": self.spec_reads}

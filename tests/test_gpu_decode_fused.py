@@ -418,3 +418,42 @@ def test_graph_on_cached_workspace_survives_a_larger_call(monkeypatch):
     monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
     with pytest.raises(PmoeError, match="during graph capture"):
         K.moe_workspace(layer.g, 4096, 4, 0, 32, DEV)
+
+
+def test_split_group_is_reported_at_once(monkeypatch):
+    """The expert-per-XCD launch checks that each block group shares one
+    XCD (its h words travel through that XCD's L2).  Forced from the host
+    (block 0 reports another XCD; every block still exits normally): error
+    bit 1 is set and the layer output is NaN within the launch -- no block
+    waits out the 0.5 s spin limit -- PmoeError is raised at the next sync
+    point, and the next call is bit-exact again."""
+    import time
+
+    from pagedmoe_amd._lib import PmoeError
+    K = _k()
+    monkeypatch.setenv("PMOE_DECODE_XCD", "1")
+    layer = _Layer(4096, 128, 1536, 8, seed=9)
+    ws = K.moe_workspace(layer.g, 1, 8, 0, 128, DEV)
+    x = layer.x(1, seed=901)
+    assert "decode_xcd" in _fused_launches(layer, x)
+    good, _, _ = layer.run(x, ws=ws)
+    torch.cuda.synchronize()
+    assert K.workspace_error(ws) == 0
+    print("[fused] split probe on", flush=True)
+    K.set_split_probe(True)
+    try:
+        t0 = time.perf_counter()
+        bad, _, _ = layer.run(x, ws=ws)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+    finally:
+        K.set_split_probe(False)
+    assert K.workspace_error(ws) & 2
+    assert torch.isnan(bad.float()).any(), "a split group wrote only finite outputs"
+    assert dt < 0.2, f"the split launch took {dt:.3f} s: a poll waited out its limit"
+    with pytest.raises(PmoeError, match="different XCDs"):
+        K.check_workspace_errors()
+    again, _, _ = layer.run(x, ws=ws)
+    torch.cuda.synchronize()
+    assert K.workspace_error(ws) == 0
+    assert torch.equal(again.view(torch.int16), good.view(torch.int16))

@@ -640,6 +640,7 @@ def _flow_model(monkeypatch, seed, slots=16):
     ring = S.patch_model(model, cache)
     monkeypatch.setattr(config, "FLOW_WARMUP", 1)
     monkeypatch.setattr(config, "FLOW_WARM_HIT", 0.0)
+    monkeypatch.setattr(config, "FLOW_MAX_CRIT", 0.0)     # these tests want flow to stay on
     ring.flow = True
     return spec, model, ol, cache, ring
 
@@ -870,6 +871,7 @@ def test_prefill_groups_and_flow_under_the_slot_ledger(monkeypatch):
     groups = [len(s.last_groups) for s in ring]
     monkeypatch.setattr(config, "FLOW_WARMUP", 1)
     monkeypatch.setattr(config, "FLOW_WARM_HIT", 0.0)
+    monkeypatch.setattr(config, "FLOW_MAX_CRIT", 0.0)
     ring.flow = True
     for t in range(10):
         xt = O.bf16_round(rng.standard_normal((1, spec.hidden), dtype=np.float32))

@@ -224,6 +224,7 @@ def test_flow_schedule_is_race_free(cpu_seam, monkeypatch):
     host round trip."""
     monkeypatch.setattr(config, "FLOW_WARMUP", 1)
     monkeypatch.setattr(config, "FLOW_WARM_HIT", 0.0)
+    monkeypatch.setattr(config, "FLOW_MAX_CRIT", 0.0)      # no miss-rate exit here
     twin, layers, ring = build(3, 16, lag=2)
     ring.flow = True
     rng = np.random.default_rng(2)
@@ -244,6 +245,7 @@ def test_planted_stale_flow_rows_are_caught(cpu_seam, monkeypatch):
     holding another."""
     monkeypatch.setattr(config, "FLOW_WARMUP", 1)
     monkeypatch.setattr(config, "FLOW_WARM_HIT", 0.0)
+    monkeypatch.setattr(config, "FLOW_MAX_CRIT", 0.0)
     twin, layers, ring = build(3, 16, lag=2)
     ring.flow = True
     rng = np.random.default_rng(2)
@@ -256,3 +258,28 @@ def test_planted_stale_flow_rows_are_caught(cpu_seam, monkeypatch):
         for s in layers:
             s.call(x2, routing(rng, 1), fake_compute(8))
     assert {"OWNER-MISMATCH", "READ-BEFORE-LANDED"} & set(kinds(twin.ledger))
+
+
+def test_flow_leaves_when_tokens_keep_missing_and_returns_when_warm(cpu_seam, monkeypatch):
+    """Flow's exit (streaming.py:1585-1613 behaviour): tokens whose routing
+    keeps missing push the missing-experts EMA over FLOW_MAX_CRIT, flow ends
+    (its admitted copies installed, flow_drop), per-layer tokens follow; a
+    hot routing brings the misses under half the bar and flow resumes.  The
+    ledger stays clean throughout."""
+    monkeypatch.setattr(config, "FLOW_WARMUP", 1)
+    monkeypatch.setattr(config, "FLOW_WARM_HIT", 0.0)
+    monkeypatch.setattr(config, "FLOW_MAX_CRIT", 5.0)
+    twin, layers, ring = build(3, 16, lag=2)
+    ring.flow = True
+    rng = np.random.default_rng(3)
+    x2 = torch.zeros(1, 8)
+    hot = [routing(rng, 1) for _ in layers]
+    modes = []
+    for t in range(40):
+        cold = 4 <= t < 16
+        for i, s in enumerate(layers):
+            s.call(x2, routing(rng, 1) if cold else hot[i], fake_compute(8))
+        modes.append(ring.token_flow)
+    assert any(modes[:4]) and not all(modes[4:20])          # flow on, then off under misses
+    assert modes[-1] and ring._flow_backoff                  # and back once hot again
+    assert twin.ledger.conflicts == [], twin.ledger.conflicts[:3]
