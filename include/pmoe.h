@@ -233,7 +233,9 @@ int pmoe_moe_block(const pmoe_geom* g, const pmoe_route_cfg* rc,
  * workspace is a static 32 MiB device array of the library, one per GPU,
  * held until the process ends; its address is looked up on the first call
  * on each device, which also zeroes its synchronisation header with a
- * kernel.  Nothing is allocated.  Calls whose workspace would exceed 32 MiB
+ * kernel -- so that first call must run outside graph capture (under
+ * capture it returns PMOE_ESTATE and launches nothing); later calls may be
+ * captured.  Nothing is allocated.  Calls whose workspace would exceed 32 MiB
  * (prefill-sized batches: pmoe_moe_workspace(g, n, k, shared, E) > 32 MiB)
  * return PMOE_ESPACE before anything is launched.  Every call on a GPU
  * shares that GPU's array, so calls that overlap on one GPU (several

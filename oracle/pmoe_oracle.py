@@ -54,7 +54,12 @@ PINNING = {
     "slot_policy": "reference KATs: full stitch set unevictable (test_stitch.py:53-58), "
                    "admit installs+MRU+hit count (test_flow.py:88-118), every slot "
                    "accounted once (test_prefill_slab.py:79-99); brute-force LRU on "
-                   "tiny traces with LFRU off",
+                   "tiny traces with LFRU off; hand-worked traces from the text of "
+                   "cache.py (tests/slot_kats.py): the LFRU second chance, plain LRU, "
+                   "pins over budget, prefill after a warm decode and into a cold slab, "
+                   "flow admission, speculation (claims, hand-back) and prefill-time "
+                   "prediction (floors, free then stage slots, claims); an independent "
+                   "list-plus-counter LFRU over Zipf traces",
     "unit_mass": "KAT test_moe_gate_routing.py:28-34",
 }
 

@@ -503,7 +503,8 @@ extern "C" int pmoe_moe_block(const pmoe_geom* g, const pmoe_route_cfg* rc_cfg, 
 // code `scratch` only names the symbol: its device address is looked up with
 // hipGetSymbolAddress once per device (with that device current) and kept in
 // g_scratch_ptr[device]; only that address is ever passed to kernels.  The
-// same first call zeroes the array's synchronisation header with a kernel;
+// same first call zeroes the array's synchronisation header with a kernel
+// (so it must not be made under graph capture: it returns PMOE_ESTATE);
 // every later call leaves the header consistent, as pmoe_moe_block does for
 // a caller's workspace.  All calls on one GPU share the array, so calls that
 // overlap on one GPU (two streams, two threads) race.
@@ -525,6 +526,14 @@ static int scratch_for_device(void** out, hipStream_t st) {
   PMOE_REQUIRE(dev >= 0 && dev < kMaxDevices, "moe_block_noalloc: device index out of range");
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    // the header's zeroing must run once, eagerly: captured into a graph it
+    // would run again at every replay and wipe the counters the calls keep
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    PMOE_HIP(hipStreamIsCapturing(st, &cap));
+    if (cap != hipStreamCaptureStatusNone)
+      return pmoe::fail(PMOE_ESTATE,
+                        "moe_block_noalloc: the first call on a device sets up its static "
+                        "scratch and must run outside graph capture");
     void* p = nullptr;
     PMOE_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
     workspace_init_kernel<<<64, 256, 0, st>>>(static_cast<uint32_t*>(p),
