@@ -573,10 +573,13 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
 // travels as tagged data at device scope and is polled until the tag of
 // this launch appears, so each block goes on the moment its own inputs
 // exist:
-//   A  logit e is computed once, by wave 0 of block e (router_dot, the
-//      order of router_logits_kernel), and published as a 64-bit word
-//      (tag << 32 | fp32 bits);
-//   B  every block polls the E logit words into LDS and routes
+//   A  every group computes all E logits, logit e by its wave e (the order
+//      of router_logits_kernel, so every group gets the same bits), and
+//      publishes each as a 64-bit word (tag << 32 | fp32 bits) into the
+//      group's own logit array with a plain store, which stays in the
+//      group's L2 (a device-scope store would first have to reach memory,
+//      ~2 us at launch);
+//   B  every block polls its group's E logit words into LDS and routes
 //      (route_rank1_select: the same bits everywhere); slot of pick x;
 //   C  the gate/up rows of pick x are dealt over the group's waves; h is
 //      published as 32-bit words (tag & 0xFFFF << 16 | bf16) into the
@@ -601,6 +604,8 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
 // block goes on poisoned: its h words and partial rows are NaN, which every
 // output that depends on them inherits through the combine.
 constexpr int kXcdPollSleep = 1;
+// Router rows per wave in the group-local router: E <= this x waves per group.
+constexpr int kXcdLogitsPerWave = 2;
 // s_getreg operand of HW_REG_XCC_ID (hwreg 20), bits [3:0]: this wave's XCD.
 constexpr int kHwRegXccId = 20 | (0 << 6) | ((4 - 1) << 11);
 
@@ -652,7 +657,7 @@ __global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(
     g_trace[blockIdx.x * 32 + 25] = __builtin_amdgcn_s_memrealtime();
   }
 #endif
-  // The slot table, the first group of this block's router row and the
+  // The slot table, the first group of this wave's router row and the
   // launch counter are requested at once; their values are used after the
   // router's FMAs, so their round trips overlap.  The row's loads go before
   // the counter's atomic (sched_barrier keeps that order): issued after it,
@@ -660,8 +665,7 @@ __global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(
   // waited for the atomic first.
   const int32_t tab = int(threadIdx.x) < n_experts ? table_p[threadIdx.x] : -1;
   RouterGroup rg0;
-  if (wave == 0 && int(blockIdx.x) < n_experts)
-    router_group_load(rg0, gate_p + size_t(blockIdx.x) * d, x_p, d, 0);
+  if (lw < n_experts) router_group_load(rg0, gate_p + size_t(lw) * d, x_p, d, 0);
   __builtin_amdgcn_sched_barrier(0);
   uint32_t old = 0;
   if (threadIdx.x == 0)
@@ -669,52 +673,49 @@ __global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(
         reinterpret_cast<uint32_t*>(hdr + kXcdCounterOffset + xcd * kDecodeFlagStride), 1u,
         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  // A: logit e by wave 0 of block e.  (Vector loads and stores share one
-  // counter, so a wave that waits for a load also waits for the device-scope
-  // stores it issued before: the slot table goes to LDS before the logit
-  // store, and waves 2-3, which store nothing, poll the logits.)
+  // A: every group computes all E logits (the router's fixed order, so each
+  // group gets the same bits): the group's wave lw takes rows lw, lw + n_lw.
+  // They are published after the barrier below into the group's own logit
+  // words with plain stores, which land in the group's L2 where its polls
+  // find them -- a device-scope store would have to reach memory before a
+  // block on another XCD could see it, ~2 us at launch.
   trace_mark(sy, 0);
-  if (wave == 0) {
-    // The table goes to LDS after the dot product (its load is older than
-    // the row's, so it has arrived) and before the logit store (waiting for
-    // it after the store would also wait for the store's acknowledgement).
-    bool table_done = false;
-    for (int e = blockIdx.x; e < n_experts; e += a.n_blocks) {
-      float acc = 0.0f;
-      for (int p0 = 0; p0 < (d + 511) / 512; p0 += 8) {
-        RouterGroup g;
-        if (e == int(blockIdx.x) && p0 == 0)
-          g = rg0;
-        else
-          router_group_load(g, gate_p + size_t(e) * d, x_p, d, p0);
-        router_group_fma(acc, g, d, p0);
-      }
-      const float sum = wave_sum_bfly(acc);
-      const float v = bias_p ? sum + bias_p[e] : sum;
-      if (!table_done && int(threadIdx.x) < n_experts) s_table[threadIdx.x] = tab;
-      table_done = true;
-      // a zero computed from the dot product keeps the counter's use (and
-      // the wait for it) after the router loads; loop-invariant code
-      // motion would hoist it before them
-      uint32_t zero;
-      asm volatile("v_mov_b32 %0, 0" : "=v"(zero) : "v"(v));
-      const uint32_t my_tag =
-          __builtin_amdgcn_readfirstlane(old + zero) / uint32_t(per_xcd) + 1u;
-      if (lane == 0)
-        __hip_atomic_store(&lgx[e], (uint64_t(my_tag) << 32) | __float_as_uint(v),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (int(threadIdx.x) < n_experts) s_table[threadIdx.x] = tab;  // the oldest load
+  float lv[kXcdLogitsPerWave];
+#pragma unroll
+  for (int j = 0; j < kXcdLogitsPerWave; ++j) {
+    const int e = lw + j * n_lw;
+    lv[j] = 0.0f;
+    if (e >= n_experts) break;
+    float acc = 0.0f;
+    for (int p0 = 0; p0 < (d + 511) / 512; p0 += 8) {
+      RouterGroup g;
+      if (j == 0 && p0 == 0)
+        g = rg0;
+      else
+        router_group_load(g, gate_p + size_t(e) * d, x_p, d, p0);
+      router_group_fma(acc, g, d, p0);
     }
-    if (!table_done && int(threadIdx.x) < n_experts) s_table[threadIdx.x] = tab;
-    if (lane == 0) {
-      s_tag = __builtin_amdgcn_readfirstlane(old) / uint32_t(per_xcd) + 1u;
-      s_last = old % uint32_t(per_xcd) == uint32_t(per_xcd) - 1u;
-    }
-  } else if (int(threadIdx.x) < n_experts) {
-    s_table[threadIdx.x] = tab;
+    const float sum = wave_sum_bfly(acc);
+    lv[j] = bias_p ? sum + bias_p[e] : sum;
+  }
+  if (threadIdx.x == 0) {
+    s_tag = old / uint32_t(per_xcd) + 1u;
+    s_last = old % uint32_t(per_xcd) == uint32_t(per_xcd) - 1u;
   }
   trace_mark(sy, 1);
-  __syncthreads();
+  // only LDS crosses this barrier (slot table, tag): wave 0 does not wait
+  // here for its logit store's device-scope acknowledgement (~1.2 us)
+  block_lds_sync();
   const uint32_t tag = s_tag;
+  uint64_t* lgx_g = lgx + size_t(xcd) * kXcdLogitStride;  // the group's logit words
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < kXcdLogitsPerWave; ++j) {
+      const int e = lw + j * n_lw;
+      if (e < n_experts) lgx_g[e] = (uint64_t(tag) << 32) | __float_as_uint(lv[j]);
+    }
+  }
 
   // placement: this block's XCD into the group's mask of this launch (the
   // atomic's answer is read after routing, so its round trip overlaps it)
@@ -737,7 +738,7 @@ __global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(
   const int li = int(threadIdx.x) - 128;
   if (li >= 0 && li < rt.e) {
     while (true) {
-      const uint64_t w = device_load(&lgx[li]);
+      const uint64_t w = device_load(&lgx_g[li]);
       if (uint32_t(w >> 32) == tag) {
         s_logit[li] = __uint_as_float(uint32_t(w));
         break;
@@ -1132,14 +1133,16 @@ int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int
   // One token, top-8 softmax, no shared expert: the expert-per-XCD launch
   // when the grid splits into 8 groups of a power-of-two block count.
   if (xcd_enabled() && rank1_route_ok(rt) && rt.k == kXcdCount && rt.kk == rt.k && !gate_extra &&
-      dn.cols <= kXcdMaxInter && dn.rows_out <= kXcdMaxHidden && rt.e + 128 <= kFThreads) {
+      dn.cols <= kXcdMaxInter && dn.rows_out <= kXcdMaxHidden && rt.e + 128 <= kFThreads &&
+      rt.e <= int(kXcdLogitStride)) {
     const auto xt = xcd_variants().find({bits, sg.ub, sg.lpr, sg.gpl, sd.ub, sd.lpr, sd.gpl, 0});
     if (xt != xcd_variants().end()) {
       const int blocks = fused_blocks(reinterpret_cast<const void*>(xt->second.fn), 0);
       const int per_xcd = blocks / kXcdCount;
       const int n_tiles = (dn.rows_out + xt->second.sub_rows - 1) / xt->second.sub_rows;
       if (blocks > 0 && blocks <= kDecodeMaxBlocks && blocks % kXcdCount == 0 &&
-          (per_xcd & (per_xcd - 1)) == 0 && n_tiles <= kXcdMaxTiles) {
+          (per_xcd & (per_xcd - 1)) == 0 && n_tiles <= kXcdMaxTiles &&
+          rt.e <= kXcdLogitsPerWave * per_xcd * kFWaves) {
         a.n_blocks = blocks;
         ProfScope prof_scope(K_DECODE_XCD, st);
         xt->second.fn<<<blocks, kFThreads, 0, st>>>(a.sync, a.gu.table, a.x, a.gate_w,

@@ -114,8 +114,9 @@ constexpr size_t kDecodeGroupOffset = 256 + kDecodeMaxBlocks * kDecodeFlagStride
 // launch, so counter / blocks-per-group numbers the launch; the line's next
 // two words are the group's masks of XCDs seen, one per launch parity, each
 // cleared by the group's last arrival of the launch before), one arrival
-// counter per down tile (64 bytes apart; 8 arrivals per launch), the router
-// logits as tagged 64-bit words (launch tag << 32 | fp32 bits), each group's
+// counter per down tile (64 bytes apart; 8 arrivals per launch), each
+// group's router logits as tagged 64-bit words (launch tag << 32 | fp32
+// bits; every group computes all of them), each group's
 // h as tagged 32-bit words (tag & 0xFFFF << 16 | bf16), and each group's
 // fp32 down partials.  Counters only grow and tags name the launch, so
 // nothing else is cleared between launches.
@@ -127,7 +128,8 @@ constexpr size_t kXcdTileStride = 64;
 constexpr size_t kXcdCounterOffset = kDecodeGroupOffset + 2 * kDecodeMaxGroups * kDecodeFlagStride;
 constexpr size_t kXcdTileOffset = kXcdCounterOffset + kXcdCount * kDecodeFlagStride;
 constexpr size_t kXcdLogitOffset = kXcdTileOffset + kXcdMaxTiles * kXcdTileStride;
-constexpr size_t kXcdHOffset = kXcdLogitOffset + 1024 * sizeof(uint64_t);
+constexpr size_t kXcdLogitStride = 512;  // logit words per group (routed experts, at most)
+constexpr size_t kXcdHOffset = kXcdLogitOffset + kXcdCount * kXcdLogitStride * sizeof(uint64_t);
 constexpr size_t kXcdPartOffset =
     kXcdHOffset + size_t(kXcdCount) * kXcdMaxInter * sizeof(uint32_t);
 constexpr size_t kDecodeSyncBytes =

@@ -67,6 +67,15 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Block barrier that orders LDS only: waits for this wave's LDS operations
+// (lgkmcnt), not for its global stores, so a device-scope store issued just
+// before does not hold the whole block until it is acknowledged.
+__device__ __forceinline__ void block_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Inverse of order_key (a zero of either sign comes back as +0).
 __device__ __forceinline__ float key_value(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
