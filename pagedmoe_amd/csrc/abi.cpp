@@ -36,7 +36,7 @@ Profiler& prof() {
 
 const char* kNames[K_COUNT] = {"router_logits", "route_select", "dispatch",  "qgemv_gateup",
                                "qgemv_down",    "combine",      "prefill_gateup", "prefill_down",
-                               "decode_fused",  "decode_xcd"};
+                               "decode_fused",  "decode_xcd",   "experts_xcd"};
 
 }  // namespace
 

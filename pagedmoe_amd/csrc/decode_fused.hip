@@ -604,6 +604,7 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(const FusedArgs
 // block goes on poisoned: its h words and partial rows are NaN, which every
 // output that depends on them inherits through the combine.
 constexpr int kXcdPollSleep = 1;
+
 // Router rows per wave in the group-local router: E <= this x waves per group.
 constexpr int kXcdLogitsPerWave = 2;
 // s_getreg operand of HW_REG_XCC_ID (hwreg 20), bits [3:0]: this wave's XCD.
@@ -946,6 +947,344 @@ __global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(
 #endif
 }
 
+// The experts of one token given its 8 ids and weights (pmoe_moe_experts),
+// expert per XCD as above without the router: group x = blockIdx % 8 runs
+// column x (ids[x], slot table[ids[x]]; an id outside [0, E) is dropped,
+// a non-resident one gives zero rows) -- gate/up + SwiGLU, h exchanged in
+// the group's L2, down rows.  A shared expert is split over the groups:
+// group x computes gate/up rows [x*R, x*R + R) of it first (h as
+// launch-tagged 64-bit words at device scope, which every group reads) and
+// its down tiles t with t % 8 == x (launch-tagged 64-bit words at device
+// scope).  Each column's down rows are rounded to bf16, as the three-launch
+// path's per-slot outputs are; the last of a tile's 8 group arrivals
+// combines it in column order with fp32 fmas, the shared expert last with
+// weight 1 -- the three-launch path's outputs bit for bit.
+//
+// The launch tag comes from the group's launch counter (thread 0); it is
+// needed from the first h store on, so the block waits for it once, after
+// its first item's weights are requested.  A CU's vector memory requests
+// return in order: the h polls are answered once the down weights requested
+// during the last gate/up item have landed, and that request overlaps the
+// exchange.
+template <int UG, int LG, int GG, int RG, int UD, int LD, int GD, int RD>
+__global__ __launch_bounds__(kFThreads) void experts_xcd_kernel(
+    DecodeSync* sync_p, const int32_t* ids_p, const float* w_p, int n_experts, int shared_slot,
+    const FusedArgs a) {
+  constexpr int RPW = 64 / LG;
+  constexpr int kRows = RG * RPW;           // gate/up rows per item
+  constexpr int kHD = RD > 1 ? RD / 2 : 1;  // down steps per half
+  constexpr int kSub = RD * (64 / LD);      // down rows per tile
+  static_assert(kSub == 8 || kSub == 16, "down tiles of 8 or 16 rows");
+  __shared__ __align__(16) uint16_t s_h[kXcdMaxInter];   // the column's h
+  __shared__ __align__(16) uint16_t s_hs[kXcdMaxInter];  // the shared expert's h
+  __shared__ __align__(16) float s_y[kFWaves][kXcdCount + 1][16];
+  __shared__ uint32_t s_tag;
+  __shared__ bool s_last;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int xcd = blockIdx.x % kXcdCount;
+  const int per_xcd = a.n_blocks / kXcdCount;
+  const int lw = (blockIdx.x / kXcdCount) * kFWaves + wave;
+  const int n_lw = per_xcd * kFWaves;
+  DecodeSync* sy = sync_p;
+  uint8_t* hdr = reinterpret_cast<uint8_t*>(sy);
+  // the column's h: (tag & 0xFFFF) << 16 | bf16 words in the group's L2
+  uint32_t* hx = reinterpret_cast<uint32_t*>(hdr + kXcdEHOffset) + size_t(xcd) * kXcdMaxInter;
+  uint64_t* hs = reinterpret_cast<uint64_t*>(hdr + kXcdSharedHOffset);
+  float* part = reinterpret_cast<float*>(hdr + kXcdEPartOffset);
+  uint64_t* ps = reinterpret_cast<uint64_t*>(hdr + kXcdSharedPartOffset);
+  uint32_t* line = reinterpret_cast<uint32_t*>(hdr + kXcdCounterOffset + xcd * kDecodeFlagStride);
+  const uint64_t t_entry = __builtin_amdgcn_s_memrealtime();
+  trace_mark(sy, 16);
+  // the launch counter first: its answer (the tag) is waited for after the
+  // first item's weight loads are issued
+  uint32_t old = 0;
+  if (threadIdx.x == 0)
+    old = __hip_atomic_fetch_add(&line[kXcdECounterWord], 1u, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_sched_barrier(0);
+  const bool has_shared = shared_slot >= 0;
+  // the column's slot, read where a branch needs it (a wave whose first
+  // item is a shared one does not wait for these two dependent loads)
+  auto load_slot = [&]() {
+    const int id = ids_p[xcd];
+    return id >= 0 && id < n_experts ? a.gu.table[id] : -1;
+  };
+
+  const int inter = a.gu.rows_out;
+  const int sh_rows =
+      has_shared ? ((inter + kXcdCount - 1) / kXcdCount + kRows - 1) / kRows * kRows : 0;
+  const int sr0 = xcd * sh_rows, sr1 = min(inter, sr0 + sh_rows);
+  const int n_sh = sr1 > sr0 ? (sr1 - sr0 + kRows - 1) / kRows : 0;  // shared items, first
+  const int items = n_sh + (inter + kRows - 1) / kRows;
+  const int n_tiles = (a.dn.rows_out + kSub - 1) / kSub;
+  // down items: this group's shared tiles (t % 8 == xcd) first, then every tile
+  const int n_sh_t = has_shared ? (n_tiles - xcd + kXcdCount - 1) / kXcdCount : 0;
+  const int n_dt = n_sh_t + n_tiles;
+  auto d_tile = [&](int j) { return j < n_sh_t ? j * kXcdCount + xcd : j - n_sh_t; };
+
+  uint32_t tag = 0, htag = 0, xseen = 0, xbit = 0;
+  auto sync_tag = [&]() {
+    if (threadIdx.x == 0) {
+      s_tag = old / uint32_t(per_xcd) + 1u;
+      s_last = old % uint32_t(per_xcd) == uint32_t(per_xcd) - 1u;
+    }
+    block_lds_sync();
+    tag = s_tag;
+    htag = (tag & 0xFFFFu) << 16;
+    trace_mark(sy, 0);
+    // placement: this block's XCD into the group's mask of this launch (its
+    // answer is read after the h polls); the group's last block clears the
+    // other mask for the next launch
+    if (threadIdx.x == 64) {
+      uint32_t xcc = __builtin_amdgcn_s_getreg(kHwRegXccId) & 15u;
+      if (a.split_probe && blockIdx.x == 0) xcc ^= 1u;
+      xbit = 1u << xcc;
+      xseen = __hip_atomic_fetch_or(&line[kXcdECounterWord + 1 + int(tag & 1u)], xbit,
+                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (s_last)
+        __hip_atomic_store(&line[kXcdECounterWord + 1 + int((tag & 1u) ^ 1u)], 0u,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
+
+  // the wave's first down item, requested during its last gate/up item
+  GemvRegs<UD, LD, GD, kHD, false> qd1, qd2;
+  auto prefetch_down = [&](int half) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (lw < n_dt) {
+      int pslot;
+      if (lw < n_sh_t)
+        pslot = shared_slot;
+      else
+        pslot = load_slot();
+      const int prow = d_tile(lw) * kSub;
+      if (pslot >= 0) {
+        if (half == 0) gemv_load<UD, LD, GD, kHD, false>(a.dn, pslot, prow, qd1);
+        if (half == 1 && RD > 1)
+          gemv_load<UD, LD, GD, kHD, false>(a.dn, pslot, prow + kHD * (64 / LD), qd2);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  {
+    const int g_sub = lane % LG, g_rsub = lane / LG;
+    GroupAct<UG> act[GG];
+    if (lw < items) gemv_load_act<UG, LG, GG>(a.gu.act, a.gu.cols, act);
+    auto item = [&](int it, bool first, auto last_tag) {
+      constexpr bool LAST = decltype(last_tag)::value;
+      const bool sh = it < n_sh;
+      const int wrow0 = sh ? sr0 + it * kRows : (it - n_sh) * kRows;
+      const int rlim = sh ? sr1 : inter;
+      int islot;
+      if (sh)
+        islot = shared_slot;
+      else
+        islot = load_slot();
+      const int o = wrow0 + g_sub * RPW + g_rsub;
+      if (islot < 0) {  // a column that is not resident: zero h words
+        if (first) sync_tag();
+        if (g_sub < RG && o < rlim) hx[o] = htag;
+        if (LAST) {
+          prefetch_down(0);
+          prefetch_down(1);
+        }
+        return;
+      }
+      GemvRegs<UG, LG, GG, 1, true> q[2];
+      gemv_load<UG, LG, GG, 1, true>(a.gu, islot, wrow0, q[0]);
+      gemv_load<UG, LG, GG, 1, true>(a.gu, islot, wrow0 + RPW, q[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (first) sync_tag();
+      float hv = 0.0f;
+#pragma unroll
+      for (int st = 0; st < RG; ++st) {
+        __builtin_amdgcn_sched_barrier(0);
+        gemv_rows<UG, LG, GG, 1, true, Collect, true>(a.gu, q[st & 1], act, wrow0 + st * RPW,
+                                                      collect_fn(hv, g_sub - st));
+        __builtin_amdgcn_sched_barrier(0);
+        if (st + 2 < RG)
+          gemv_load<UG, LG, GG, 1, true>(a.gu, islot, wrow0 + (st + 2) * RPW, q[st & 1]);
+        if (LAST && st == RG / 2 - 1) prefetch_down(0);
+      }
+      if (first) trace_mark(sy, 21);
+      if (g_sub < RG && o < rlim) {
+        const uint32_t bits = uint32_t(f2bf(hv));
+        if (sh)  // every group reads the shared expert's h
+          __hip_atomic_store(&hs[o], (uint64_t(tag) << 32) | bits, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        else  // the column's h stays in the group's L2
+          hx[o] = htag | bits;
+      }
+      if (LAST) prefetch_down(1);
+    };
+    const int mine = lw < items ? (items - 1 - lw) / n_lw + 1 : 0;
+    for (int j = 0; j + 1 < mine; ++j) item(lw + j * n_lw, j == 0, std::false_type{});
+    if (mine > 0) {
+      item(lw + (mine - 1) * n_lw, mine == 1, std::true_type{});
+    } else {
+      sync_tag();
+      prefetch_down(0);
+      prefetch_down(1);
+    }
+  }
+  trace_mark(sy, 7);
+
+  // D: h rows into LDS -- the column's (the group's L2) and, for blocks with
+  // a shared tile, the shared expert's (device scope)
+  bool h_late = false;
+  auto timed_out = [&]() {
+    return __builtin_amdgcn_s_memrealtime() - t_entry > a.spin || device_load(&sy->error) != 0u;
+  };
+  const int slot = load_slot();
+  if (slot >= 0) {
+    for (int c = threadIdx.x; c < a.dn.cols / 4 && !h_late; c += kFThreads) {
+      const uint64_t* src = reinterpret_cast<const uint64_t*>(hx) + 2 * c;
+      while (true) {
+        const uint64_t w0 = device_load(src), w1 = device_load(src + 1);
+        const uint32_t t = uint32_t(w0) & uint32_t(w0 >> 32) & uint32_t(w1) & uint32_t(w1 >> 32);
+        const uint32_t u = uint32_t(w0) | uint32_t(w0 >> 32) | uint32_t(w1) | uint32_t(w1 >> 32);
+        if ((t & 0xFFFF0000u) == htag && (u & 0xFFFF0000u) == htag) {
+          *reinterpret_cast<uint2*>(&s_h[4 * c]) =
+              make_uint2((uint32_t(w0) & 0xFFFFu) | (uint32_t(w0 >> 32) << 16),
+                         (uint32_t(w1) & 0xFFFFu) | (uint32_t(w1 >> 32) << 16));
+          break;
+        }
+        if (timed_out()) {
+          h_late = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(kXcdPollSleep);
+      }
+    }
+  }
+  if (has_shared && (blockIdx.x / kXcdCount) * kFWaves < n_sh_t) {
+    for (int c = threadIdx.x; c < a.dn.cols / 2 && !h_late; c += kFThreads) {
+      while (true) {
+        const uint64_t w0 = device_load(&hs[2 * c]), w1 = device_load(&hs[2 * c + 1]);
+        if (uint32_t(w0 >> 32) == tag && uint32_t(w1 >> 32) == tag) {
+          *reinterpret_cast<uint32_t*>(&s_hs[2 * c]) =
+              (uint32_t(w0) & 0xFFFFu) | (uint32_t(w1) << 16);
+          break;
+        }
+        if (timed_out()) {
+          h_late = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(kXcdPollSleep);
+      }
+    }
+  }
+  bool split = false;
+  if (threadIdx.x == 64 && (xseen & ~xbit) != 0u) {  // another XCD ran a block of this group
+    split = true;
+    __hip_atomic_fetch_or(&sy->error, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  bool poison = false;
+  if (__syncthreads_or(h_late || split)) {
+    poison = true;
+    if (threadIdx.x == 0)
+      __hip_atomic_fetch_or(&sy->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  trace_mark(sy, 8);
+
+  const float kNaN = __uint_as_float(0x7fc00000u);
+  float* yx = part + size_t(xcd) * kXcdMaxHidden;
+  constexpr int kQ = kSub / 4;  // 16-byte chunks of a tile
+  // the combine's inputs: column weights and which columns count
+  const int idc = lane < kXcdCount ? ids_p[lane] : -1;
+  const float wc = lane < kXcdCount ? w_p[lane] : 0.0f;
+  const uint64_t kept = wave_ballot(idc >= 0 && idc < n_experts);
+  for (int j = lw; j < n_dt; j += n_lw) {
+    const bool sh = j < n_sh_t;
+    const int tl = d_tile(j);
+    const int row0 = tl * kSub;
+    const int dslot = sh ? shared_slot : slot;
+    float* own = s_y[wave][xcd];
+    if (dslot < 0) {  // not resident: exact zero rows
+      if (lane < kSub) own[lane] = poison ? kNaN : 0.0f;
+    } else {
+      if (j != lw) {
+        gemv_load<UD, LD, GD, kHD, false>(a.dn, dslot, row0, qd1);
+        if (RD > 1) gemv_load<UD, LD, GD, kHD, false>(a.dn, dslot, row0 + kHD * (64 / LD), qd2);
+      }
+      GroupAct<UD> act[GD];
+      gemv_load_act<UD, LD, GD>(sh ? s_hs : s_h, a.dn.cols, act);
+      // each column's output as the bf16 the per-slot outputs hold
+      auto to_own = [&](int, int o, float v) {
+        own[o - row0] = poison ? kNaN : bf16f(f2bf(v));
+      };
+      gemv_rows<UD, LD, GD, kHD, false>(a.dn, qd1, act, row0, to_own);
+      if (RD > 1) gemv_rows<UD, LD, GD, kHD, false>(a.dn, qd2, act, row0 + kHD * (64 / LD), to_own);
+    }
+    wave_lds_sync();
+    trace_mark(sy, 11);
+    if (sh) {  // the shared rows of this tile, for whichever group combines it
+      if (lane < kSub)
+        __hip_atomic_store(&ps[row0 + lane], (uint64_t(tag) << 32) | __float_as_uint(own[lane]),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      continue;
+    }
+    // rows past rows_out are never read: a tile's partial is stored whole
+    if (lane < kQ)
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(yx + row0) + 2 * lane,
+                         *reinterpret_cast<const uint64_t*>(own + 4 * lane), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT),
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(yx + row0) + 2 * lane + 1,
+                         *reinterpret_cast<const uint64_t*>(own + 4 * lane + 2), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // the partial has reached device scope
+    uint32_t prev = 0;
+    if (lane == 0)
+      prev = __hip_atomic_fetch_add(
+          reinterpret_cast<uint32_t*>(hdr + kXcdTileOffset + size_t(tl) * kXcdTileStride), 1u,
+          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __builtin_amdgcn_readfirstlane(prev);
+    trace_mark(sy, 19);
+    if (prev % kXcdCount != kXcdCount - 1) continue;
+    // last of the 8: the other groups' rows of the tile (and the shared
+    // rows) into LDS
+    if (lane < kXcdCount * kQ) {
+      const int x = lane / kQ, c = lane % kQ;
+      if (x != xcd) {
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(
+            part + size_t(x) * kXcdMaxHidden + row0 + 4 * c);
+        *reinterpret_cast<uint64_t*>(&s_y[wave][x][4 * c]) = device_load(src);
+        *reinterpret_cast<uint64_t*>(&s_y[wave][x][4 * c + 2]) = device_load(src + 1);
+      }
+    }
+    bool s_bad = false;
+    if (has_shared && lane < kSub) {
+      while (true) {
+        const uint64_t w = device_load(&ps[row0 + lane]);
+        if (uint32_t(w >> 32) == tag) {
+          s_y[wave][kXcdCount][lane] = __uint_as_float(uint32_t(w));
+          break;
+        }
+        if (timed_out()) {
+          s_bad = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(kXcdPollSleep);
+      }
+    }
+    if (wave_ballot(s_bad) != 0ull && lane == 0)
+      __hip_atomic_fetch_or(&sy->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wave_lds_sync();
+    trace_mark(sy, 20);
+    const int o = row0 + lane;
+    if (lane < kSub && o < a.dn.rows_out) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int x = 0; x < kXcdCount; ++x)
+        if ((kept >> x) & 1ull) acc = __builtin_fmaf(lane_value(wc, x), s_y[wave][x][lane], acc);
+      if (has_shared) acc = __builtin_fmaf(1.0f, s_y[wave][kXcdCount][lane], acc);
+      a.out[o] = s_bad ? f2bf(kNaN) : f2bf(acc);
+    }
+  }
+  trace_mark(sy, 6);
+}
+
 // ---------------------------------------------------------------- host side
 
 // Row steps per wave item: weights of one item stay in registers next to the
@@ -1006,6 +1345,18 @@ XcdEntry make_xcd_entry() {
   return {&decode_xcd_kernel<UG, LG, GG, RG, UD, LD, GD, RD>, RD * (64 / LD)};
 }
 
+using ExpertsFn = void (*)(DecodeSync*, const int32_t*, const float*, int, int, const FusedArgs);
+struct ExpertsEntry {
+  ExpertsFn fn;
+  int sub_rows;
+};
+
+template <int UG, int LG, int GG, int UD, int LD, int GD>
+ExpertsEntry make_experts_entry() {
+  constexpr int RG = gateup_steps<UG, GG>(), RD = down_steps<UD, LD, GD>();
+  return {&experts_xcd_kernel<UG, LG, GG, RG, UD, LD, GD, RD>, RD * (64 / LD)};
+}
+
 // Supported (gate/up row shape, down row shape) pairs, from gateup_shape and
 // pick_shape:
 // 4-bit hidden 1024/inter 512, 4096/1536, 4096/2048, 7168/2048, 2048/512,
@@ -1053,6 +1404,26 @@ const std::map<Variant, XcdEntry>& xcd_variants() {
     PMOE_XV(6, 48, 16, 1, 48, 8, 1)
     PMOE_XV(6, 48, 32, 1, 48, 8, 1)
 #undef PMOE_XV
+    return v;
+  }();
+  return m;
+}
+
+// Given-ids expert-per-XCD variants: the same shapes.
+const std::map<Variant, ExpertsEntry>& experts_variants() {
+  static const std::map<Variant, ExpertsEntry> m = [] {
+    std::map<Variant, ExpertsEntry> v;
+#define PMOE_EV(B, UG, LG, GG, UD, LD, GD) \
+  v[{B, UG, LG, GG, UD, LD, GD, 0}] = make_experts_entry<UG, LG, GG, UD, LD, GD>();
+    PMOE_EV(4, 16, 32, 1, 16, 16, 1)
+    PMOE_EV(4, 32, 64, 2, 16, 64, 1)
+    PMOE_EV(4, 16, 64, 2, 16, 16, 3)
+    PMOE_EV(4, 16, 64, 2, 16, 64, 1)
+    PMOE_EV(4, 16, 64, 1, 16, 16, 1)
+    PMOE_EV(4, 16, 64, 1, 16, 8, 3)
+    PMOE_EV(6, 48, 16, 1, 48, 8, 1)
+    PMOE_EV(6, 48, 32, 1, 48, 8, 1)
+#undef PMOE_EV
     return v;
   }();
   return m;
@@ -1171,6 +1542,36 @@ int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int
   ProfScope prof_scope(K_DECODE_FUSED, st);
   en.fn<<<blocks, kFThreads, lds, st>>>(a, rt);
   PMOE_LAUNCH_CHECK("decode_fused_kernel");
+  return PMOE_OK;
+}
+
+int experts_xcd(const GemvArgs& gu, const GemvArgs& dn, int bits, int n_experts,
+                const int32_t* ids, const float* wts, int shared_slot, uint16_t* out,
+                DecodeSync* sync, hipStream_t st) {
+  const char* v = getenv("PMOE_EXPERTS_XCD");
+  if ((v && v[0] == '0') || !xcd_enabled() || !sync) return kDecodeFusedDeclined;
+  if (dn.cols > kXcdMaxInter || dn.rows_out > kXcdMaxHidden) return kDecodeFusedDeclined;
+  const Shape sg = gateup_shape(bits, gu, kXcdCount + 1), sd = pick_shape(bits, dn.cols);
+  if (sg.lpr == 0 || sd.lpr == 0) return kDecodeFusedDeclined;
+  const auto et = experts_variants().find({bits, sg.ub, sg.lpr, sg.gpl, sd.ub, sd.lpr, sd.gpl, 0});
+  if (et == experts_variants().end()) return kDecodeFusedDeclined;
+  const int blocks = fused_blocks(reinterpret_cast<const void*>(et->second.fn), 0);
+  const int per_xcd = blocks / kXcdCount;
+  const int n_tiles = (dn.rows_out + et->second.sub_rows - 1) / et->second.sub_rows;
+  if (blocks <= 0 || blocks > kDecodeMaxBlocks || blocks % kXcdCount != 0 ||
+      (per_xcd & (per_xcd - 1)) != 0 || n_tiles > kXcdMaxTiles)
+    return kDecodeFusedDeclined;
+  FusedArgs a{};
+  a.gu = gu;
+  a.dn = dn;
+  a.out = out;
+  a.sync = sync;
+  a.spin = g_spin_ticks;
+  a.split_probe = g_split_probe;
+  a.n_blocks = blocks;
+  ProfScope prof_scope(K_EXPERTS_XCD, st);
+  et->second.fn<<<blocks, kFThreads, 0, st>>>(sync, ids, wts, n_experts, shared_slot, a);
+  PMOE_LAUNCH_CHECK("experts_xcd_kernel");
   return PMOE_OK;
 }
 

@@ -328,6 +328,30 @@ int experts_and_combine(const pmoe_geom* g, const uint8_t* slab, const int32_t* 
                         uint16_t* out, const MoeWs& w, hipStream_t st) {
   const int shared = shared_slot >= 0 ? 1 : 0;
   const int kk = k + shared;
+  if (n == 1 && k == kXcdCount && !(shared && shared_gate)) {
+    // one token, eight columns: the expert-per-XCD launch (same outputs)
+    GemvArgs gu{};
+    gu.slab = slab;
+    gu.expert_bytes = g->expert_bytes;
+    gu.table = table;
+    gu.n_experts = n_experts;
+    gu.shared_slot = shared_slot;
+    gu.kk = kk;
+    gu.p0 = {g->off[PMOE_GATE_W], g->off[PMOE_GATE_S], g->off[PMOE_GATE_B]};
+    gu.p1 = {g->off[PMOE_UP_W], g->off[PMOE_UP_S], g->off[PMOE_UP_B]};
+    gu.rows_out = g->inter;
+    gu.cols = g->hidden;
+    gu.act = x;
+    gu.act_stride = g->hidden;
+    gu.act_by_token = 1;
+    GemvArgs dn = gu;
+    dn.p0 = {g->off[PMOE_DOWN_W], g->off[PMOE_DOWN_S], g->off[PMOE_DOWN_B]};
+    dn.p1 = dn.p0;
+    dn.rows_out = g->hidden;
+    dn.cols = g->inter;
+    const int r = experts_xcd(gu, dn, g->bits, n_experts, inds, wts, shared_slot, out, w.sync, st);
+    if (r != kDecodeFusedDeclined) return r;
+  }
   int rc = run_experts(g, slab, table, n_experts, shared_slot, x, inds, n, k, kk, max_rpe, w,
                        w.y, 0, st);
   if (rc) return rc;

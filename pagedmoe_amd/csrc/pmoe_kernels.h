@@ -17,6 +17,7 @@ enum KernelId {
   K_PREFILL_DOWN,
   K_DECODE_FUSED,
   K_DECODE_XCD,
+  K_EXPERTS_XCD,
   K_COUNT
 };
 
@@ -118,7 +119,13 @@ constexpr size_t kDecodeGroupOffset = 256 + kDecodeMaxBlocks * kDecodeFlagStride
 // group's router logits as tagged 64-bit words (launch tag << 32 | fp32
 // bits; every group computes all of them), each group's
 // h as tagged 32-bit words (tag & 0xFFFF << 16 | bf16), and each group's
-// fp32 down partials.  Counters only grow and tags name the launch, so
+// fp32 down partials.  The given-ids form of that launch (experts_xcd)
+// keeps its own launch count in word 4 of each group's counter line (each
+// block of the group adds 1 per launch) and its XCD masks in words 5-6, and
+// its own regions: the shared expert's h and down rows as 64-bit words
+// (launch tag << 32 | bf16 or fp32 bits; every group writes its share, the
+// groups read them all), each group's h as tagged 32-bit words and each
+// group's fp32 down rows.  Counters only grow and tags name the launch, so
 // nothing else is cleared between launches.
 constexpr int kXcdCount = 8;
 constexpr int kXcdMaxHidden = 8192;
@@ -132,8 +139,15 @@ constexpr size_t kXcdLogitStride = 512;  // logit words per group (routed expert
 constexpr size_t kXcdHOffset = kXcdLogitOffset + kXcdCount * kXcdLogitStride * sizeof(uint64_t);
 constexpr size_t kXcdPartOffset =
     kXcdHOffset + size_t(kXcdCount) * kXcdMaxInter * sizeof(uint32_t);
-constexpr size_t kDecodeSyncBytes =
+constexpr int kXcdECounterWord = 4;  // given-ids launch count, then its 2 XCD masks
+constexpr size_t kXcdSharedHOffset =
     kXcdPartOffset + size_t(kXcdCount) * kXcdMaxHidden * sizeof(float);
+constexpr size_t kXcdSharedPartOffset = kXcdSharedHOffset + size_t(kXcdMaxInter) * sizeof(uint64_t);
+constexpr size_t kXcdEHOffset = kXcdSharedPartOffset + size_t(kXcdMaxHidden) * sizeof(uint64_t);
+constexpr size_t kXcdEPartOffset =
+    kXcdEHOffset + size_t(kXcdCount) * kXcdMaxInter * sizeof(uint32_t);
+constexpr size_t kDecodeSyncBytes =
+    kXcdEPartOffset + size_t(kXcdCount) * kXcdMaxHidden * sizeof(float);
 constexpr int kDecodeFusedDeclined = 1;  // shape not covered: use decode_routed
 
 // Whole decode layer in one persistent launch (decode_fused.hip): router
@@ -145,6 +159,16 @@ int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int
                  const uint16_t* x, const uint16_t* gate_w, const uint16_t* gate_extra,
                  const float* logit_bias, int32_t* inds_out, float* w_out, uint16_t* out,
                  DecodeSync* sync, hipStream_t st);
+
+// The experts of ONE token given its ids and weights (pmoe_moe_experts'
+// arithmetic: each column's output rounded to bf16, combined in column
+// order, shared expert last with weight 1, ids outside [0, n_experts) left
+// out) in one expert-per-XCD launch: exactly kXcdCount ids, optionally a
+// shared expert (no shared gate).  Returns kDecodeFusedDeclined (nothing
+// launched) for shapes it does not cover.
+int experts_xcd(const GemvArgs& gu, const GemvArgs& dn, int bits, int n_experts,
+                const int32_t* ids, const float* wts, int shared_slot, uint16_t* out,
+                DecodeSync* sync, hipStream_t st);
 
 // Routing (router.hip)
 int router_logits(const uint16_t* x, const uint16_t* w, const float* bias, int n, int d, int e,
