@@ -460,6 +460,46 @@ int qgemv(const GemvArgs& a, int bits, bool dual, int max_experts, int, hipStrea
 
 // Decode MoE experts with routing fused into both projections: gate/up into
 // gu.out (h), then down + combine into out [n, hidden].
+int decode_route(const GemvArgs& gu, const RouteDev& rt, int32_t* inds_out, float* w_out,
+                 void* record, const RouterIn& ri, hipStream_t st) {
+  PMOE_REQUIRE(record != nullptr && inds_out != nullptr && w_out != nullptr,
+               "decode: null routing outputs");
+  PMOE_REQUIRE(rt.n >= 1 && rt.n * rt.kk <= kRouteMaxRows && rt.e + 1 <= kRouteMaxIds &&
+                   rt.k <= kRouteMaxK && rt.k <= rt.e,
+               "decode: bad routing shape");
+  PMOE_REQUIRE(ri.x && ri.w && ri.out && ri.arrive, "decode: null router input");
+  PMOE_REQUIRE(ri.d % 8 == 0, "router_logits: hidden must be a multiple of 8");
+  RouteRecord* rec = static_cast<RouteRecord*>(record);
+  const int epl = (rt.e + 63) / 64;
+  const int n = rt.n, n_w = rt.e;
+  const int e = n_w + (ri.w_extra ? 1 : 0);
+  RouteTail t{rt, rec, gu.table, gu.n_experts, gu.shared_slot, inds_out, w_out, ri.arrive};
+  const bool full = ri.d % 512 == 0;
+  const int gx = (e + kTailWaves - 1) / kTailWaves;
+  ProfScope prof_scope(K_ROUTER_LOGITS, st);
+  auto go = [&](auto ep) {
+    constexpr int EP = decltype(ep)::value;
+    if (full)
+      router_route_kernel<1, 1, 8, true, EP><<<dim3(gx, n), 64 * kTailWaves, 0, st>>>(
+          ri.x, ri.w, ri.w_extra, ri.bias, n, ri.d, e, n_w, ri.out, t);
+    else
+      router_route_kernel<1, 1, 8, false, EP><<<dim3(gx, n), 64 * kTailWaves, 0, st>>>(
+          ri.x, ri.w, ri.w_extra, ri.bias, n, ri.d, e, n_w, ri.out, t);
+  };
+  if (epl <= 2)
+    go(std::integral_constant<int, 2>{});
+  else if (epl <= 4)
+    go(std::integral_constant<int, 4>{});
+  else if (epl <= 8)
+    go(std::integral_constant<int, 8>{});
+  else if (epl <= 16)
+    go(std::integral_constant<int, 16>{});
+  else
+    return fail(PMOE_EINVAL, "decode: too many experts");
+  PMOE_LAUNCH_CHECK("router_route_kernel");
+  return PMOE_OK;
+}
+
 int decode_routed(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int bits,
                   int32_t* inds_out, float* w_out, uint16_t* out, void* record,
                   const RouterIn& ri, hipStream_t st) {

@@ -106,6 +106,7 @@ struct FusedArgs {
   DecodeSync* sync;
   uint64_t spin;               // barrier poll limit, realtime-clock ticks
   uint32_t split_probe;        // debug: block 0 reports another XCD (placement check test)
+  uint32_t round_y;            // given-ids launch: columns rounded to bf16 before the combine
   int n_blocks;
   int tile;                    // hidden rows per block in phase D
 };
@@ -956,9 +957,10 @@ __global__ __launch_bounds__(kFThreads) void decode_xcd_kernel(
 // launch-tagged 64-bit words at device scope, which every group reads) and
 // its down tiles t with t % 8 == x (launch-tagged 64-bit words at device
 // scope).  Each column's down rows are rounded to bf16, as the three-launch
-// path's per-slot outputs are; the last of a tile's 8 group arrivals
-// combines it in column order with fp32 fmas, the shared expert last with
-// weight 1 -- the three-launch path's outputs bit for bit.
+// path's per-slot outputs are (round_y; the decode block combines fp32 rows);
+// the last of a tile's 8 group arrivals combines it in column order with
+// fp32 fmas, the shared expert last with weight 1 -- the three-launch path's
+// outputs bit for bit.
 //
 // The launch tag comes from the group's launch counter (thread 0); it is
 // needed from the first h store on, so the block waits for it once, after
@@ -1210,9 +1212,10 @@ __global__ __launch_bounds__(kFThreads) void experts_xcd_kernel(
       }
       GroupAct<UD> act[GD];
       gemv_load_act<UD, LD, GD>(sh ? s_hs : s_h, a.dn.cols, act);
-      // each column's output as the bf16 the per-slot outputs hold
+      // each column's output as the bf16 the per-slot outputs hold (or the
+      // fp32 value, for the decode block's combine)
       auto to_own = [&](int, int o, float v) {
-        own[o - row0] = poison ? kNaN : bf16f(f2bf(v));
+        own[o - row0] = poison ? kNaN : (a.round_y ? bf16f(f2bf(v)) : v);
       };
       gemv_rows<UD, LD, GD, kHD, false>(a.dn, qd1, act, row0, to_own);
       if (RD > 1) gemv_rows<UD, LD, GD, kHD, false>(a.dn, qd2, act, row0 + kHD * (64 / LD), to_own);
@@ -1476,6 +1479,33 @@ extern "C" int pmoe_debug_trace(uint64_t* out, int n) {
 }
 #endif
 
+// The expert-per-XCD variant of a one-token layer and its grid, or nullptr.
+static const XcdEntry* xcd_plan(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt,
+                                int bits, bool gate_extra, int* blocks_out) {
+  if (!(xcd_enabled() && rank1_route_ok(rt) && rt.k == kXcdCount && rt.kk == rt.k &&
+        !gate_extra && dn.cols <= kXcdMaxInter && dn.rows_out <= kXcdMaxHidden &&
+        rt.e + 128 <= kFThreads && rt.e <= int(kXcdLogitStride)))
+    return nullptr;
+  const Shape sg = gateup_shape(bits, gu, kXcdCount), sd = pick_shape(bits, dn.cols);
+  const auto xt = xcd_variants().find({bits, sg.ub, sg.lpr, sg.gpl, sd.ub, sd.lpr, sd.gpl, 0});
+  if (xt == xcd_variants().end()) return nullptr;
+  const int blocks = fused_blocks(reinterpret_cast<const void*>(xt->second.fn), 0);
+  const int per_xcd = blocks / kXcdCount;
+  const int n_tiles = (dn.rows_out + xt->second.sub_rows - 1) / xt->second.sub_rows;
+  if (!(blocks > 0 && blocks <= kDecodeMaxBlocks && blocks % kXcdCount == 0 &&
+        (per_xcd & (per_xcd - 1)) == 0 && n_tiles <= kXcdMaxTiles &&
+        rt.e <= kXcdLogitsPerWave * per_xcd * kFWaves))
+    return nullptr;
+  *blocks_out = blocks;
+  return &xt->second;
+}
+
+bool decode_xcd_covers(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int bits,
+                       bool gate_extra) {
+  int blocks = 0;
+  return xcd_plan(gu, dn, rt, bits, gate_extra, &blocks) != nullptr;
+}
+
 int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int bits,
                  const uint16_t* x, const uint16_t* gate_w, const uint16_t* gate_extra,
                  const float* logit_bias, int32_t* inds_out, float* w_out, uint16_t* out,
@@ -1503,25 +1533,14 @@ int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int
   a.split_probe = g_split_probe;
   // One token, top-8 softmax, no shared expert: the expert-per-XCD launch
   // when the grid splits into 8 groups of a power-of-two block count.
-  if (xcd_enabled() && rank1_route_ok(rt) && rt.k == kXcdCount && rt.kk == rt.k && !gate_extra &&
-      dn.cols <= kXcdMaxInter && dn.rows_out <= kXcdMaxHidden && rt.e + 128 <= kFThreads &&
-      rt.e <= int(kXcdLogitStride)) {
-    const auto xt = xcd_variants().find({bits, sg.ub, sg.lpr, sg.gpl, sd.ub, sd.lpr, sd.gpl, 0});
-    if (xt != xcd_variants().end()) {
-      const int blocks = fused_blocks(reinterpret_cast<const void*>(xt->second.fn), 0);
-      const int per_xcd = blocks / kXcdCount;
-      const int n_tiles = (dn.rows_out + xt->second.sub_rows - 1) / xt->second.sub_rows;
-      if (blocks > 0 && blocks <= kDecodeMaxBlocks && blocks % kXcdCount == 0 &&
-          (per_xcd & (per_xcd - 1)) == 0 && n_tiles <= kXcdMaxTiles &&
-          rt.e <= kXcdLogitsPerWave * per_xcd * kFWaves) {
-        a.n_blocks = blocks;
-        ProfScope prof_scope(K_DECODE_XCD, st);
-        xt->second.fn<<<blocks, kFThreads, 0, st>>>(a.sync, a.gu.table, a.x, a.gate_w,
-                                                     a.logit_bias, a.gu.cols, rt.e, a, rt);
-        PMOE_LAUNCH_CHECK("decode_xcd_kernel");
-        return PMOE_OK;
-      }
-    }
+  int xblocks = 0;
+  if (const XcdEntry* xe = xcd_plan(gu, dn, rt, bits, gate_extra != nullptr, &xblocks)) {
+    a.n_blocks = xblocks;
+    ProfScope prof_scope(K_DECODE_XCD, st);
+    xe->fn<<<xblocks, kFThreads, 0, st>>>(a.sync, a.gu.table, a.x, a.gate_w, a.logit_bias,
+                                          a.gu.cols, rt.e, a, rt);
+    PMOE_LAUNCH_CHECK("decode_xcd_kernel");
+    return PMOE_OK;
   }
   const auto& vs = variants();
   const auto it = vs.find({bits, sg.ub, sg.lpr, sg.gpl, sd.ub, sd.lpr, sd.gpl, epl_t});
@@ -1545,22 +1564,37 @@ int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int
   return PMOE_OK;
 }
 
-int experts_xcd(const GemvArgs& gu, const GemvArgs& dn, int bits, int n_experts,
-                const int32_t* ids, const float* wts, int shared_slot, uint16_t* out,
-                DecodeSync* sync, hipStream_t st) {
+// The given-ids variant of a shape and its grid, or nullptr (nothing launched).
+static const ExpertsEntry* experts_plan(const GemvArgs& gu, const GemvArgs& dn, int bits,
+                                        int* blocks_out) {
   const char* v = getenv("PMOE_EXPERTS_XCD");
-  if ((v && v[0] == '0') || !xcd_enabled() || !sync) return kDecodeFusedDeclined;
-  if (dn.cols > kXcdMaxInter || dn.rows_out > kXcdMaxHidden) return kDecodeFusedDeclined;
+  if ((v && v[0] == '0') || !xcd_enabled()) return nullptr;
+  if (dn.cols > kXcdMaxInter || dn.rows_out > kXcdMaxHidden) return nullptr;
   const Shape sg = gateup_shape(bits, gu, kXcdCount + 1), sd = pick_shape(bits, dn.cols);
-  if (sg.lpr == 0 || sd.lpr == 0) return kDecodeFusedDeclined;
+  if (sg.lpr == 0 || sd.lpr == 0) return nullptr;
   const auto et = experts_variants().find({bits, sg.ub, sg.lpr, sg.gpl, sd.ub, sd.lpr, sd.gpl, 0});
-  if (et == experts_variants().end()) return kDecodeFusedDeclined;
+  if (et == experts_variants().end()) return nullptr;
   const int blocks = fused_blocks(reinterpret_cast<const void*>(et->second.fn), 0);
   const int per_xcd = blocks / kXcdCount;
   const int n_tiles = (dn.rows_out + et->second.sub_rows - 1) / et->second.sub_rows;
   if (blocks <= 0 || blocks > kDecodeMaxBlocks || blocks % kXcdCount != 0 ||
       (per_xcd & (per_xcd - 1)) != 0 || n_tiles > kXcdMaxTiles)
-    return kDecodeFusedDeclined;
+    return nullptr;
+  *blocks_out = blocks;
+  return &et->second;
+}
+
+bool experts_xcd_covers(const GemvArgs& gu, const GemvArgs& dn, int bits, int) {
+  int blocks = 0;
+  return experts_plan(gu, dn, bits, &blocks) != nullptr;
+}
+
+int experts_xcd(const GemvArgs& gu, const GemvArgs& dn, int bits, int n_experts,
+                const int32_t* ids, const float* wts, int shared_slot, uint16_t* out,
+                DecodeSync* sync, hipStream_t st, bool round_y) {
+  int blocks = 0;
+  const ExpertsEntry* en = sync ? experts_plan(gu, dn, bits, &blocks) : nullptr;
+  if (!en) return kDecodeFusedDeclined;
   FusedArgs a{};
   a.gu = gu;
   a.dn = dn;
@@ -1568,9 +1602,10 @@ int experts_xcd(const GemvArgs& gu, const GemvArgs& dn, int bits, int n_experts,
   a.sync = sync;
   a.spin = g_spin_ticks;
   a.split_probe = g_split_probe;
+  a.round_y = round_y ? 1u : 0u;
   a.n_blocks = blocks;
   ProfScope prof_scope(K_EXPERTS_XCD, st);
-  et->second.fn<<<blocks, kFThreads, 0, st>>>(sync, ids, wts, n_experts, shared_slot, a);
+  en->fn<<<blocks, kFThreads, 0, st>>>(sync, ids, wts, n_experts, shared_slot, a);
   PMOE_LAUNCH_CHECK("experts_xcd_kernel");
   return PMOE_OK;
 }

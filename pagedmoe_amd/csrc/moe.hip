@@ -310,15 +310,29 @@ int decode_block(const pmoe_geom* g, const pmoe_route_cfg* rc, const uint8_t* sl
   dn.act_stride = g->inter;
   dn.act_by_token = 0;
   dn.out = nullptr;
+  const RouterIn ri{x, gate_w, extra, logit_bias, g->hidden, w.logits,
+                    reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(w.sync) +
+                                                kRouteArriveOffset)};
   if (fused_enabled(n)) {
+    // one token with 8 picks that the expert-per-XCD layer does not route
+    // (sigmoid or grouped scoring, a shared expert): the router launch,
+    // then the given-ids expert-per-XCD launch on its picks, combining fp32
+    // columns as the expert-split down does
+    if (n == 1 && k == kXcdCount && !extra &&
+        !decode_xcd_covers(gu, dn, rt, g->bits, false) &&
+        experts_xcd_covers(gu, dn, g->bits, shared_slot)) {
+      const int r1 = decode_route(gu, rt, inds_out, w_out, w.record, ri, st);
+      if (r1) return r1;
+      const int r3 = experts_xcd(gu, dn, g->bits, e, inds_out, w_out, shared_slot, out, w.sync,
+                                 st, false);
+      if (r3 != kDecodeFusedDeclined) return r3;
+      return fail(PMOE_ESTATE, "decode: the given-ids launch declined a shape it covers");
+    }
     const int r2 = decode_fused(gu, dn, rt, g->bits, x, gate_w, extra, logit_bias, inds_out, w_out,
                                 out, w.sync, st);
     if (r2 != kDecodeFusedDeclined) return r2;
   }
   dn.out = w.y;  // fp32 per-slot outputs when the down runs expert-split
-  const RouterIn ri{x, gate_w, extra, logit_bias, g->hidden, w.logits,
-                    reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(w.sync) +
-                                                kRouteArriveOffset)};
   return decode_routed(gu, dn, rt, g->bits, inds_out, w_out, out, w.record, ri, st);
 }
 

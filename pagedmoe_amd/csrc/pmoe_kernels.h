@@ -88,6 +88,10 @@ int decode_routed(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, in
                   int32_t* inds_out, float* w_out, uint16_t* out, void* record,
                   const RouterIn& ri, hipStream_t st);
 size_t decode_record_bytes();
+// The router launch alone, for any token count (its last block routes and
+// writes inds_out / w_out and the record).
+int decode_route(const GemvArgs& gu, const RouteDev& rt, int32_t* inds_out, float* w_out,
+                 void* record, const RouterIn& ri, hipStream_t st);
 
 // Grid-barrier state of the fused decode launch: the first kDecodeSyncBytes
 // of the MoE workspace, zero before the first call.  Blocks arrive in groups
@@ -166,9 +170,17 @@ int decode_fused(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int
 // out) in one expert-per-XCD launch: exactly kXcdCount ids, optionally a
 // shared expert (no shared gate).  Returns kDecodeFusedDeclined (nothing
 // launched) for shapes it does not cover.
+// round_y: each column's output rounded to bf16 before the combine
+// (pmoe_moe_experts' per-slot outputs); without it the columns combine in
+// fp32, as the decode block's expert-split down does.
 int experts_xcd(const GemvArgs& gu, const GemvArgs& dn, int bits, int n_experts,
                 const int32_t* ids, const float* wts, int shared_slot, uint16_t* out,
-                DecodeSync* sync, hipStream_t st);
+                DecodeSync* sync, hipStream_t st, bool round_y = true);
+// Whether experts_xcd / the expert-per-XCD form of decode_fused take a shape
+// (nothing is launched).
+bool experts_xcd_covers(const GemvArgs& gu, const GemvArgs& dn, int bits, int shared_slot);
+bool decode_xcd_covers(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, int bits,
+                       bool gate_extra);
 
 // Routing (router.hip)
 int router_logits(const uint16_t* x, const uint16_t* w, const float* bias, int n, int d, int e,

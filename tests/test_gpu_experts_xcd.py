@@ -11,6 +11,12 @@ down, combine) bit for bit -- with non-resident columns (zero rows), dropped
 ids (outside [0, E): left out), repeated ids, across shapes on one
 workspace and under HIP-graph replay.  The tiny shape is also checked
 against the oracle's float64 FFN and combine.
+
+A one-token decode block with 8 picks that the expert-per-XCD layer does
+not route (sigmoid grouped scoring, a shared expert) runs the router launch
+and then this launch on its picks, combining fp32 columns: its outputs,
+picks and weights must equal the grid-wide one-launch layer's and the
+three-launch decode's bit for bit.
 """
 
 import os
@@ -220,3 +226,55 @@ def test_experts_xcd_split_group_is_reported_at_once():
     again = _run(ex, x, ids, w, True, xcd=True)
     assert K.workspace_error(ws) == 0
     _same(again, good, "after the split probe")
+
+
+def test_decode_block_routes_then_takes_the_given_ids_launch():
+    """DeepSeek-V3-shaped block at batch 1 (384 experts, sigmoid + bias, 8
+    groups / top-4 / top-8, scale 2.5, a shared expert): moe_block launches
+    the router (routing in its last block) and the given-ids launch; equal
+    to the grid-wide one-launch layer and the three-launch decode."""
+    from pagedmoe_amd._lib import KernelTimer, geom
+    from pagedmoe_amd.slab import SlabStore
+    K = _k()
+    D, E, I = 7168, 384, 2048
+    g = geom(D, I, 4)
+    n_res = 12
+    slab = SlabStore(g, n_res + 1, DEV)
+    fill_slab_gpu(slab, range(n_res + 1), seed=31)
+    rng = np.random.default_rng(31)
+    gate = bits_to_bf16_tensor(O.bf16_round(rng.standard_normal((E, D), dtype=np.float32)
+                                            * np.float32(0.02)), DEV)
+    bias = torch.from_numpy((rng.standard_normal(E) * 0.1).astype(np.float32)).to(DEV)
+    table = torch.from_numpy((np.arange(E) % n_res).astype(np.int32)).to(DEV)
+    rc = K.route_cfg("sigmoid", E, 8, True, 8, 4, 2.5)
+
+    def run(fused, xcd, x):
+        saved = {v: os.environ.get(v) for v in ("PMOE_DECODE_FUSED", "PMOE_EXPERTS_XCD")}
+        os.environ["PMOE_DECODE_FUSED"] = fused
+        os.environ["PMOE_EXPERTS_XCD"] = xcd
+        try:
+            with KernelTimer() as kt:
+                out, inds, w = K.moe_block(g, rc, slab.buf, table, gate, x, score_bias=bias,
+                                           shared_slot=n_res)
+                torch.cuda.synchronize()
+        finally:
+            for v, old in saved.items():
+                if old is None:
+                    del os.environ[v]
+                else:
+                    os.environ[v] = old
+        return out.clone(), inds.clone(), w.clone(), kt.result
+
+    for j in range(3):
+        x = bits_to_bf16_tensor(O.bf16_round(rng.standard_normal((1, D), dtype=np.float32)), DEV)
+        print(f"[experts_xcd] decode block, token {j}", flush=True)
+        a = run("1", "1", x)
+        assert "experts_xcd" in a[3] and "router_logits" in a[3], a[3]
+        b = run("1", "0", x)
+        assert "decode_fused" in b[3], b[3]
+        c = run("0", "1", x)
+        for other, name in ((b, "grid-wide one-launch"), (c, "three-launch")):
+            assert torch.equal(a[1], other[1]), f"picks differ from the {name} layer"
+            assert torch.equal(a[2], other[2]), f"weights differ from the {name} layer"
+            _same(a[0], other[0], name)
+    assert K.workspace_error(K.moe_workspace(g, 1, 8, 1, E, DEV)) == 0
