@@ -143,6 +143,19 @@ gateup_routed_kernel(const GemvArgs a, const RouteDev rt, int32_t* inds_out, flo
 // load, so the last one's record needs no further dependent read.
 constexpr int kTailWaves = 8;
 
+#ifdef PMOE_FUSED_TRACE
+// Debug builds: realtime stamps of the router launch's phases, per block.
+__device__ uint64_t g_rtrace[1024 * 8];
+#define PMOE_RT_MARK(i)                                                              \
+  do {                                                                               \
+    if (threadIdx.x == 0)                                                            \
+      g_rtrace[(blockIdx.y * gridDim.x + blockIdx.x) * 8 + (i)] =                   \
+          __builtin_amdgcn_s_memrealtime();                                          \
+  } while (0)
+#else
+#define PMOE_RT_MARK(i)
+#endif
+
 struct RouteTail {
   RouteDev rt;
   RouteRecord* rec;
@@ -162,23 +175,29 @@ __global__ __launch_bounds__(64 * kTailWaves) void router_route_kernel(
   __shared__ WaveTmp W[kTailWaves];
   __shared__ int32_t s_table[kRouteMaxIds];
   __shared__ int s_last;
+  PMOE_RT_MARK(0);
   for (int i = threadIdx.x; i < t.n_experts; i += 64 * kTailWaves) s_table[i] = t.table[i];
   const int e0 = (blockIdx.x * kTailWaves + int(threadIdx.x >> 6)) * TE;
   if (e0 < e)
     router_tile<TE, TN, UNR, FULL, true>(x, w, w_extra, bias, n, d, e, n_w, out, e0,
                                          blockIdx.y * TN);
+  PMOE_RT_MARK(1);
   __builtin_amdgcn_s_waitcnt(0);  // this wave's logits have reached device scope
   __syncthreads();
+  PMOE_RT_MARK(2);
   if (threadIdx.x == 0) {
     const uint32_t total = gridDim.x * gridDim.y;
     s_last = __hip_atomic_fetch_add(t.arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
              total - 1;
   }
   __syncthreads();
+  PMOE_RT_MARK(3);
   if (!s_last) return;
   if (threadIdx.x == 0) __hip_atomic_store(t.arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   route_block<EPL, kTailWaves, true>(t.rt, L, W, t.inds_out, t.w_out);
+  PMOE_RT_MARK(4);
   publish_route(L, t.rt.n * t.rt.kk, t.rec, s_table, t.n_experts, t.shared_slot);
+  PMOE_RT_MARK(5);
 }
 
 // Decode down projection + weighted combine, routing recomputed in the
@@ -536,3 +555,11 @@ int decode_routed(const GemvArgs& gu, const GemvArgs& dn, const RouteDev& rt, in
 }
 
 }  // namespace pmoe
+
+#ifdef PMOE_FUSED_TRACE
+extern "C" int pmoe_debug_rtrace(uint64_t* out, int n) {
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(pmoe::g_rtrace), size_t(n) * sizeof(uint64_t)) ==
+                 hipSuccess
+             ? 0 : -2;
+}
+#endif

@@ -303,6 +303,126 @@ __device__ void route_token(const RouteDev& r, int t, RouteLds& L, WaveTmp& W, i
   }
 }
 
+// One token with sigmoid scoring, by all NW waves of the block, bit for bit
+// route_token's (and so the oracle's) picks and weights: wave w takes the
+// experts [w*cs, w*cs + cs), cs = ceil(E / NW) <= 64, which are routing
+// group w when there are groups (n_group == NW).  Each wave forms its
+// sigmoids and biased scores; with groups, its group's score is the sum of
+// its two largest biased scores (wave maxima, a repeated maximum counting
+// twice) and wave 0 keeps the top groups exactly as route_token does; the
+// other groups' scores become 0.  Scores are ordered by 64-bit keys
+// (order_key(score) << 32 | ~id: larger score first, lower id among
+// equals).  Each wave ranks its own keys (a lane's rank = the wave's keys
+// above its own) and its top k -- the global top k is among them -- go to
+// LDS; wave 0 ranks those NW*k candidates: pick j is the one with j greater
+// keys.  The weights are route_token's: sigmoid / (sum over the
+// picks in pick order) * scale.
+__host__ __device__ __forceinline__ bool sigmoid_one_ok(const RouteDev& r, int nw) {
+  const int cs = (r.e + nw - 1) / nw;
+  return r.n == 1 && r.scoring == PMOE_SCORE_SIGMOID && cs <= 64 && r.k <= kRouteMaxK &&
+         nw * r.k <= 128 && (r.n_group == 1 || (r.n_group == nw && r.e % nw == 0));
+}
+
+template <int NW, bool COHERENT>
+__device__ void route_sigmoid_one(const RouteDev& r, RouteLds& L, int32_t* inds_out,
+                                  float* w_out) {
+  __shared__ float s_gscore[NW];
+  __shared__ uint64_t s_keep;
+  __shared__ uint64_t s_key[NW][64];
+  __shared__ uint64_t s_ck[NW * kRouteMaxK];
+  __shared__ float s_cx[NW * kRouteMaxK];
+  __shared__ float s_px[kRouteMaxK];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int e = r.e, k = r.k;
+  const int cs = (e + NW - 1) / NW;
+  const int base = wv * cs;
+  const int nv = max(0, min(cs, e - base));  // experts of this wave
+  const int ei = base + lane;
+  const bool mine = lane < nv;
+  float x = 0.0f, c = 0.0f;
+  if (mine) {
+    x = psigmoid(load_logit<COHERENT>(r.logits + ei));
+    c = x + r.bias[ei];
+  }
+  if (r.n_group > 1) {
+    const uint32_t kc = mine ? order_key(c) : 0u;
+    const uint32_t k1 = wave_max_u32(kc);
+    const uint64_t at = wave_ballot(mine && kc == k1);
+    float t2;
+    if (__popcll(at) >= 2) {
+      t2 = key_value(k1);
+    } else {
+      const uint32_t k2 = wave_max_u32(lane == int(__builtin_ctzll(at)) ? 0u : kc);
+      t2 = k2 == 0u ? -__builtin_inff() : key_value(k2);
+    }
+    if (lane == 0) s_gscore[wv] = key_value(k1) + t2;
+    block_lds_sync();
+    if (wv == 0) {
+      float gscore[1] = {lane < r.n_group ? s_gscore[lane] : 0.0f}, gnone[1] = {0.0f};
+      const Pick gp = wave_topk<1, false>(gscore, r.n_group, r.topk_group, gnone);
+      uint64_t keep = 0;
+      for (int j = 0; j < r.topk_group; ++j) keep |= 1ull << __builtin_amdgcn_readlane(gp.i, j);
+      if (lane == 0) s_keep = keep;
+    }
+    block_lds_sync();
+    if (mine && !((s_keep >> wv) & 1ull)) c = 0.0f;  // group wv is not kept
+  }
+  {
+    // this wave's top k by rank counts over its keys (each lane compares
+    // its key with every key of the wave); rank j goes to candidate slot j
+    const uint64_t K = mine ? (uint64_t(order_key(c)) << 32) | uint32_t(~uint32_t(ei)) : 0ull;
+    s_key[wv][lane] = K;
+    if (lane < k) s_ck[wv * k + lane] = 0ull;  // slots past the wave's experts
+    wave_lds_sync();
+    int rk = 0;
+    for (int m = 0; m < nv; ++m) rk += s_key[wv][m] > K ? 1 : 0;
+    if (mine && rk < k) {
+      s_ck[wv * k + rk] = K;
+      s_cx[wv * k + rk] = x;
+    }
+  }
+  block_lds_sync();
+  if (wv == 0) {
+    const int nc = NW * k;
+    const uint64_t K0 = lane < nc ? s_ck[lane] : 0ull;
+    const uint64_t K1 = lane + 64 < nc ? s_ck[lane + 64] : 0ull;
+    int r0 = 0, r1 = 0;
+    for (int m = 0; m < nc; ++m) {
+      const uint64_t km = s_ck[m];
+      r0 += km > K0 ? 1 : 0;
+      r1 += km > K1 ? 1 : 0;
+    }
+    int ik = 0;
+    if (lane < nc && r0 < k) {
+      s_px[r0] = s_cx[lane];
+      L.ids[r0] = int(~uint32_t(K0));
+    }
+    if (lane + 64 < nc && r1 < k) {
+      s_px[r1] = s_cx[lane + 64];
+      L.ids[r1] = int(~uint32_t(K1));
+    }
+    wave_lds_sync();
+    const float px = lane < k ? s_px[lane] : 0.0f;
+    if (lane < k) ik = L.ids[lane];
+    float sum = 0.0f;
+    for (int j = 0; j < k; ++j) sum = sum + lane_value(px, j);
+    if (lane < k) {
+      float w = px;
+      if (r.norm) w = w / sum;
+      const float wk = w * r.scale;
+      L.w[lane] = wk;
+      if (inds_out) {
+        inds_out[lane] = ik;
+        w_out[lane] = wk;
+      }
+    }
+    if (r.kk > k && lane == 0) {
+      L.ids[k] = e;  // shared expert column
+      L.w[k] = r.shared_gate ? psigmoid(load_logit<COHERENT>(r.logits + e)) : 1.0f;
+    }
+  }
+}
+
 // Route all tokens (waves take tokens round robin), then list the active
 // experts in ascending id order.  Ends with a block barrier.
 template <int EPL, int NW, bool COHERENT = false>
@@ -312,8 +432,12 @@ __device__ void route_block(const RouteDev& r, RouteLds& L, WaveTmp* W, int32_t*
   const int wv = tid >> 6;
   const int n_ids = r.e + (r.kk > r.k ? 1 : 0);
   for (int i = tid; i < kRouteMaxIds / 64; i += NW * 64) L.bits[i] = 0;
-  for (int t = wv; t < r.n; t += NW)
-    route_token<EPL, COHERENT>(r, t, L, W[wv], inds_out, w_out);
+  if (sigmoid_one_ok(r, NW)) {
+    route_sigmoid_one<NW, COHERENT>(r, L, inds_out, w_out);
+  } else {
+    for (int t = wv; t < r.n; t += NW)
+      route_token<EPL, COHERENT>(r, t, L, W[wv], inds_out, w_out);
+  }
   __syncthreads();
   const int rows = r.n * r.kk;
   for (int i = tid; i < rows; i += NW * 64) {

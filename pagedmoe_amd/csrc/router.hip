@@ -121,6 +121,14 @@ __global__ __launch_bounds__(256) void route_softmax_kernel(
   }
 }
 
+// One token: the block-parallel sigmoid routing of the decode launches
+// (route_common.h route_sigmoid_one, 8 waves), the same picks and weights.
+__global__ __launch_bounds__(512) void route_sigmoid_one_kernel(const RouteDev r, int32_t* inds,
+                                                                float* weights) {
+  __shared__ RouteLds L;
+  route_sigmoid_one<8, false>(r, L, inds, weights);
+}
+
 __global__ __launch_bounds__(256) void route_sigmoid_kernel(
     const float* __restrict__ logits, const float* __restrict__ bias, int n, int e,
     int n_group, int topk_group, int k, int norm, float scale, int32_t* __restrict__ inds,
@@ -289,6 +297,24 @@ int route_sigmoid(const float* logits, const float* bias, int n, int e, int n_gr
                "route_sigmoid_group_topk: k exceeds the experts of the kept groups");
   if (n <= 0) return PMOE_OK;
   ProfScope prof_scope(K_ROUTE_SELECT, st);
+  RouteDev r{};
+  r.logits = logits;
+  r.ld = e;
+  r.bias = bias;
+  r.scoring = PMOE_SCORE_SIGMOID;
+  r.n = n;
+  r.e = e;
+  r.k = k;
+  r.kk = k;
+  r.norm = norm;
+  r.n_group = n_group;
+  r.topk_group = topk_group;
+  r.scale = scale;
+  if (sigmoid_one_ok(r, 8)) {  // one token: every wave of a block on it
+    route_sigmoid_one_kernel<<<1, 512, 0, st>>>(r, inds, weights);
+    PMOE_LAUNCH_CHECK("route_sigmoid_one_kernel");
+    return PMOE_OK;
+  }
   route_sigmoid_kernel<<<(n + 3) / 4, 256, 0, st>>>(logits, bias, n, e, n_group, topk_group, k,
                                                     norm, scale, inds, weights);
   PMOE_LAUNCH_CHECK("route_sigmoid_kernel");

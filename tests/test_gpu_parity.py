@@ -56,7 +56,9 @@ def test_softmax_topk_bit_exact(n, e, k, norm):
 
 
 @pytest.mark.parametrize("n,e,ng,tg,k,scale", [(1, 384, 8, 4, 8, 2.5), (16, 256, 8, 4, 8, 2.5),
-                                               (4, 64, 1, 1, 6, 1.0), (3, 96, 4, 4, 8, 1.5)])
+                                               (4, 64, 1, 1, 6, 1.0), (3, 96, 4, 4, 8, 1.5),
+                                               (1, 64, 1, 1, 6, 1.0), (1, 384, 1, 1, 8, 2.5),
+                                               (1, 256, 8, 2, 8, 2.5), (1, 96, 4, 4, 8, 1.5)])
 def test_sigmoid_group_topk_bit_exact(n, e, ng, tg, k, scale):
     K = _k()
     rng = np.random.default_rng(e + n)
@@ -67,6 +69,37 @@ def test_sigmoid_group_topk_bit_exact(n, e, ng, tg, k, scale):
                                         torch.from_numpy(bias).to(DEV), ng, tg, k, True, scale)
     assert np.array_equal(gi.cpu().numpy(), ref_i)
     assert np.array_equal(gw.cpu().numpy(), ref_w)
+
+
+@pytest.mark.parametrize("ng,tg", [(8, 4), (1, 1)])
+def test_sigmoid_one_token_ties_bit_exact(ng, tg):
+    """One token (the block-parallel routing): equal biased scores inside a
+    group, across groups and at a group's top two, a group score tie, and a
+    kept group whose scores are all negative (the masked experts' zeros
+    then win) -- lower id first among equals, as the oracle."""
+    K = _k()
+    e, k = 384, 8
+    rng = np.random.default_rng(7)
+    for case in range(4):
+        logits = rng.standard_normal((1, e), dtype=np.float32)
+        bias = (rng.standard_normal(e, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+        if case == 0:    # equal scores: 3 in group 0, 2 more in groups 5 and 7
+            for i in (3, 9, 17, 5 * 48 + 1, 7 * 48 + 40):
+                logits[0, i], bias[i] = np.float32(2.5), np.float32(0.3)
+        elif case == 1:  # two groups with the same top two (same group score)
+            for g, off in ((2, 0), (6, 0)):
+                logits[0, g * 48 + 10 + off], bias[g * 48 + 10 + off] = np.float32(3.0), np.float32(0.2)
+                logits[0, g * 48 + 20 + off], bias[g * 48 + 20 + off] = np.float32(2.0), np.float32(0.2)
+        elif case == 2:  # a group's maximum repeated (counts twice in its score)
+            for i in (4 * 48 + 1, 4 * 48 + 2):
+                logits[0, i], bias[i] = np.float32(4.0), np.float32(0.5)
+        else:            # scores below zero: masked experts (0.0) outrank kept ones
+            bias[:] = np.float32(-2.0)
+        ref_i, ref_w = O.sigmoid_group_topk(logits, bias, ng, tg, k, True, 2.5)
+        gi, gw = K.route_sigmoid_group_topk(torch.from_numpy(logits).to(DEV),
+                                            torch.from_numpy(bias).to(DEV), ng, tg, k, True, 2.5)
+        assert np.array_equal(gi.cpu().numpy(), ref_i), (case, gi.cpu().numpy(), ref_i)
+        assert np.array_equal(gw.cpu().numpy(), ref_w), case
 
 
 @pytest.mark.parametrize("rows,e", [(0, 8), (1, 8), (64, 128), (1000, 32), (1024, 512),
