@@ -152,10 +152,11 @@ size_t pmoe_moe_workspace(const pmoe_geom* g, int n, int k, int shared,
  * that reason about tile edges. */
 int pmoe_prefill_tile_rows(int n, int kk, int n_experts);
 
-/* A MoE workspace starts with a 673,024-byte synchronisation header (grid
+/* A MoE workspace starts with a 1,352,960-byte synchronisation header (grid
  * barrier counters, launch epoch and per-block flags of the one-launch
  * decode layer; launch and tile counters, tagged logit and h words and the
- * down partials of its expert-per-XCD form; the arrival counter of the
+ * down partials of its expert-per-XCD form and of the one-token given-ids
+ * pmoe_moe_experts launch; the arrival counter of the
  * several-token decode's router launch, whose last block routes).  It must
  * be zero before the
  * first pmoe_moe_block call on that workspace and is kept consistent by
@@ -218,7 +219,8 @@ int pmoe_moe_experts(const pmoe_geom* g, const void* slab, const int32_t* table,
  * gate_w bf16 [E, hidden]; score_bias fp32 [E] (sigmoid scoring; NULL
  * otherwise); logit_bias fp32 [E] or NULL.  inds_out/weights_out (device,
  * [n, k]) receive the routing.  Replaces the mlx-lm MoE block call around
- * StreamedSwitchGLU (SURVEY call stack B). */
+ * StreamedSwitchGLU: its router (tapped at streaming.py:165-195), top-k,
+ * the switch_mlp call (streaming.py:946) and the weighted sum. */
 int pmoe_moe_block(const pmoe_geom* g, const pmoe_route_cfg* rc,
                    const void* slab, const int32_t* table, const void* gate_w,
                    const float* score_bias, const float* logit_bias,
