@@ -378,16 +378,21 @@ def _replay_prefill(pol, layer, groups):
 
 
 @pytest.mark.parametrize("stage", [6, 64])
-def test_prefill_groups_keep_the_decode_hot_set(stage):
+def test_prefill_groups_keep_the_decode_hot_set(stage, monkeypatch):
     """32-token calls take the prefill policy (cache.py:2347-2453 with
     prefill=True): hits are not touched, misses never evict, and groups whose
     copies run under the previous group's compute give rows bit-identical to
     the resident module.  With a 6-slot stage a call needs several groups
     that reuse stage slots; with 64, one group.  Tables and counters follow
     the oracle policy replayed over the same groups, and the decode hot set
-    survives the prefill."""
+    survives the prefill.  Prefill-ahead is off here: the replay covers the
+    group policy only (a claimed prefill-ahead read counts as a hit, where
+    the replay sees a miss); its own tests are the PREFILL_AHEAD trace and
+    test_prefill_ahead_keeps_outputs_and_claims_reads."""
+    from pagedmoe_amd import config
     from pagedmoe_amd.cache import ExpertCache, HostExpertStore
 
+    monkeypatch.setattr(config, "PREFILL_AHEAD", False)
     _, S = _mods()
     spec = O.LayerSpec(1024, 32, 512, 4)
     model, _ = _softmax_model(spec, 2, seed=120)
