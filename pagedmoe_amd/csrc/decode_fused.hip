@@ -1005,13 +1005,22 @@ __global__ __launch_bounds__(kFThreads) void experts_xcd_kernel(
     old = __hip_atomic_fetch_add(&line[kXcdECounterWord], 1u, __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
   __builtin_amdgcn_sched_barrier(0);
+#ifdef PMOE_FUSED_TRACE
+  if (threadIdx.x == 0) {
+    asm volatile("" ::"v"(old));
+    trace_mark(sy, 22);  // the launch count is back
+  }
+#endif
   const bool has_shared = shared_slot >= 0;
-  // the column's slot, read where a branch needs it (a wave whose first
-  // item is a shared one does not wait for these two dependent loads)
-  auto load_slot = [&]() {
-    const int id = ids_p[xcd];
-    return id >= 0 && id < n_experts ? a.gu.table[id] : -1;
-  };
+  // the column's id and slot, the same for the whole block, read once
+  // through the scalar cache (as constant memory: neither is written during
+  // the launch): as vector loads the two dependent reads queued behind
+  // every wave's activation loads and the slot was known 5-7 us into the
+  // launch
+  typedef const __attribute__((address_space(4))) int32_t ConstI32;
+  const int col_id = *(ConstI32*)(ids_p + xcd);
+  const int col_slot = col_id >= 0 && col_id < n_experts ? *(ConstI32*)(a.gu.table + col_id) : -1;
+  auto load_slot = [&]() { return col_slot; };
 
   const int inter = a.gu.rows_out;
   const int sh_rows =
@@ -1028,6 +1037,10 @@ __global__ __launch_bounds__(kFThreads) void experts_xcd_kernel(
   uint32_t tag = 0, htag = 0, xseen = 0, xbit = 0;
   auto sync_tag = [&]() {
     if (threadIdx.x == 0) {
+      // opaque: the division stays here, after the first item's weight
+      // loads, instead of being hoisted to the kernel's head, where its wait
+      // for the count also waited for the activation loads
+      asm volatile("" : "+v"(old));
       s_tag = old / uint32_t(per_xcd) + 1u;
       s_last = old % uint32_t(per_xcd) == uint32_t(per_xcd) - 1u;
     }
@@ -1071,8 +1084,10 @@ __global__ __launch_bounds__(kFThreads) void experts_xcd_kernel(
   };
   {
     const int g_sub = lane % LG, g_rsub = lane / LG;
+    // the token's activations, loaded by the wave's first item after its
+    // weights are requested (waiting for them first would hold the weights
+    // back by a round trip)
     GroupAct<UG> act[GG];
-    if (lw < items) gemv_load_act<UG, LG, GG>(a.gu.act, a.gu.cols, act);
     auto item = [&](int it, bool first, auto last_tag) {
       constexpr bool LAST = decltype(last_tag)::value;
       const bool sh = it < n_sh;
@@ -1093,11 +1108,22 @@ __global__ __launch_bounds__(kFThreads) void experts_xcd_kernel(
         }
         return;
       }
+#ifdef PMOE_FUSED_TRACE
+      if (first && threadIdx.x == 0) {
+        asm volatile("" ::"v"(islot));
+        trace_mark(sy, 23);  // the first item's slot is known
+      }
+#endif
       GemvRegs<UG, LG, GG, 1, true> q[2];
       gemv_load<UG, LG, GG, 1, true>(a.gu, islot, wrow0, q[0]);
       gemv_load<UG, LG, GG, 1, true>(a.gu, islot, wrow0 + RPW, q[1]);
       __builtin_amdgcn_sched_barrier(0);
-      if (first) sync_tag();
+      if (first) {
+        trace_mark(sy, 24);  // its weights are requested
+        gemv_load_act<UG, LG, GG>(a.gu.act, a.gu.cols, act);
+        __builtin_amdgcn_sched_barrier(0);
+        sync_tag();
+      }
       float hv = 0.0f;
 #pragma unroll
       for (int st = 0; st < RG; ++st) {
