@@ -98,6 +98,10 @@ CONFIGS = {
     # DeepSeek-style routing with a shared expert at small dims: 6 tokens, then 2
     "sigmoid-shared": (dict(hidden=1024, experts=64, inter=512, top_k=6, scoring="sigmoid",
                             shared=True, n_group=8, topk_group=4, scale=2.5), (6, 2)),
+    # DeepSeek-V3-style top-8 with a shared expert: 2 tokens (three-launch decode),
+    # then 1 (router launch, then the given-ids expert-per-XCD launch)
+    "sigmoid-shared-top8": (dict(hidden=1024, experts=64, inter=512, top_k=8, scoring="sigmoid",
+                                 shared=True, n_group=8, topk_group=4, scale=2.5), (2, 1)),
     # Qwen3-Next-style: 6-bit, top-10 of 512 plus a gated shared expert: 8, then 1
     "qwen3-next-6bit": (dict(hidden=2048, experts=512, inter=512, top_k=10, bits=6, shared=True,
                              shared_gate=True), (8, 1)),
