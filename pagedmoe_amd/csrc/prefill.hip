@@ -42,6 +42,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kTileM = 128;          // rows per dispatch tile
 constexpr int kMB = kTileM / 32;     // 32-row MFMA blocks per tile
 constexpr int kLdsRow = 72;          // bf16 per staged row (64 + 8 pad: 144 B)
+constexpr int kLdsRow2 = 136;        // two groups a row (128 + 8 pad: 272 B)
 constexpr int kThreads = 512;
 constexpr int kStageSteps = kTileM * 8 / kThreads;  // 16-byte pieces per thread per group
 constexpr int kGuCols = 128;         // moe_intermediate columns per gate/up block
@@ -191,13 +192,13 @@ __device__ __forceinline__ void stage_load(const StageRows& sr, int g, StageRegs
     x.v[j] = *reinterpret_cast<const u32x4*>(sr.base + sr.off[j] + g * 64 + c * 8);
 }
 
-template <int NMB>
+template <int NMB, int PITCH = kLdsRow>
 __device__ __forceinline__ void stage_store(uint16_t* lds, const StageRegs& x) {
   const int c = threadIdx.x & 7;
   const int r0 = threadIdx.x >> 3;
 #pragma unroll
   for (int j = 0; j < stage_steps<NMB>(); ++j)
-    *reinterpret_cast<u32x4*>(lds + ((kThreads / 8) * j + r0) * kLdsRow + c * 8) = x.v[j];
+    *reinterpret_cast<u32x4*>(lds + ((kThreads / 8) * j + r0) * PITCH + c * 8) = x.v[j];
 }
 
 // ---------------------------------------------------------------- main loop
@@ -279,7 +280,7 @@ constexpr int stage_rows() {
 // sched_barrier keeps that order.  (Step-major order, with consecutive
 // MFMAs on different accumulators, measured slower: the second wave on the
 // SIMD already fills the accumulation latency.)
-template <int BITS, int NMB, int MB>
+template <int BITS, int NMB, int MB, int PITCH = kLdsRow>
 __device__ __forceinline__ void group_mfma(const uint16_t* xs, const u32x4 (&b)[4],
                                            const LaneWords<BITS>& wn, const SBlk& sn, int si,
                                            u32x4 (&bn)[4], f32x16 (&acc)[MB]) {
@@ -291,7 +292,7 @@ __device__ __forceinline__ void group_mfma(const uint16_t* xs, const u32x4 (&b)[
   for (int f = 0; f < NF; ++f) {
     if (f + 2 < NF)
       A[(f + 2) % 3] = *reinterpret_cast<const bf16x8*>(
-          xs + ((f + 2) >> 2) * 32 * kLdsRow + 8 * ((f + 2) & 3));
+          xs + ((f + 2) >> 2) * 32 * PITCH + 8 * ((f + 2) & 3));
     acc[f >> 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
         A[f % 3], __builtin_bit_cast(bf16x8, b[f & 3]), acc[f >> 2], 0, 0, 0);
 #pragma unroll
@@ -567,14 +568,21 @@ __device__ __forceinline__ void read_group4(LaneWords<4>& lw, const uint8_t* lds
 // gemm_tile for 4-bit weights read in units (128-row tiles): the same
 // pipeline, the weights of group j+1 read from the wave's LDS copy of
 // their unit; one unit in registers, loaded when the previous one is
-// copied (4 groups ahead).  n_groups is a multiple of 8.
+// copied (4 groups ahead).  The activations are staged two groups at a time
+// (rows of 272 bytes: both groups and 16 bytes of pad, conflict-free for the
+// 16-byte fragment reads), so one block barrier serves two groups: pair p
+// of groups sits in buffer p & 1, the pair after next is requested at the
+// start of a pair and the next pair stored at its end (one group a barrier
+// measured 1.5% slower over the 2048-token layer).  n_groups is a multiple
+// of 8.
 template <int NMB, int MB>
 __device__ __forceinline__ void gemm_tile_u4(int n_groups, const StageRows& rows,
-                                             const uint8_t* w0, uint32_t row_bytes,
-                                             const LaneRow& lr, uint16_t* lds, uint8_t* wbuf,
-                                             f32x16 (&acc)[MB]) {
+                                              const uint8_t* w0, uint32_t row_bytes,
+                                              const LaneRow& lr, uint16_t* lds, uint8_t* wbuf,
+                                              f32x16 (&acc)[MB]) {
   static_assert(NMB <= MB, "row blocks beyond the accumulators");
   constexpr int SR = stage_rows<MB>();
+  constexpr int P = kLdsRow2;
   const int lane = threadIdx.x & 63;
   const int m = lane & 31;
   const int h = lane >> 5;
@@ -588,15 +596,18 @@ __device__ __forceinline__ void gemm_tile_u4(int n_groups, const StageRows& rows
   for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x16{};
   Unit4 U;
   LaneWords<4> Wn;
-  StageRegs X[2];
+  StageRegs X[2][2];
   SBlk S[2];
   u32x4 B[2][4];
   load_sblk(S[0], lr, 0);
   load_sblk(S[1], lr, min(1, last_blk));
   load_unit4(U, w0, row_bytes, 0, threadIdx.x & 63);
-  stage_load<NMB>(rows, 0, X[0]);
-  stage_store<NMB>(lds, X[0]);
-  stage_load<NMB>(rows, min(1, last), X[1]);
+  stage_load<NMB>(rows, 0, X[0][0]);
+  stage_load<NMB>(rows, min(1, last), X[0][1]);
+  stage_store<NMB, P>(lds, X[0][0]);
+  stage_store<NMB, P>(lds + 64, X[0][1]);
+  stage_load<NMB>(rows, min(2, last), X[1][0]);
+  stage_load<NMB>(rows, min(3, last), X[1][1]);
   cycle_unit4(U, wbuf, w0, row_bytes, 1, true);
   read_group4(Wn, lds8, rd, 0);
 #pragma unroll
@@ -605,22 +616,29 @@ __device__ __forceinline__ void gemm_tile_u4(int n_groups, const StageRows& rows
 
   for (int j0 = 0; j0 < n_groups; j0 += 8) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int j = j0 + u;
-      // group j+1 opens unit un (held in U)
-      const int un = (j + 1) >> 2;
-      if ((u & 3) == 3 && un <= last_unit)
-        cycle_unit4(U, wbuf, w0, row_bytes, un + 1, un + 1 <= last_unit);
-      read_group4(Wn, lds8, rd, (u + 1) & 3);
-      stage_load<NMB>(rows, min(j + 2, last), X[u & 1]);
-      const uint16_t* xs = lds + (u & 1) * (SR * kLdsRow) + m * kLdsRow + 32 * h;
-      group_mfma<4, NMB, MB>(xs, B[u & 1], Wn, u < 7 ? S[0] : S[1], (u + 1) & 7,
-                             B[(u + 1) & 1], acc);
-      stage_store<NMB>(lds + ((u + 1) & 1) * (SR * kLdsRow), X[(u + 1) & 1]);
-      if (u == 7) {
-        S[0] = S[1];
-        load_sblk(S[1], lr, min((j0 >> 3) + 2, last_blk));
+    for (int q = 0; q < 4; ++q) {
+      // pair q of this 8-group trip: groups j0 + 2q, j0 + 2q + 1 in buffer q & 1
+      stage_load<NMB>(rows, min(j0 + 2 * q + 4, last), X[q & 1][0]);
+      stage_load<NMB>(rows, min(j0 + 2 * q + 5, last), X[q & 1][1]);
+      const uint16_t* xs = lds + (q & 1) * (SR * P) + m * P + 32 * h;
+#pragma unroll
+      for (int v = 0; v < 2; ++v) {
+        const int u = 2 * q + v;
+        const int j = j0 + u;
+        // group j+1 opens unit un (held in U)
+        const int un = (j + 1) >> 2;
+        if ((u & 3) == 3 && un <= last_unit)
+          cycle_unit4(U, wbuf, w0, row_bytes, un + 1, un + 1 <= last_unit);
+        read_group4(Wn, lds8, rd, (u + 1) & 3);
+        group_mfma<4, NMB, MB, P>(xs + 64 * v, B[u & 1], Wn, u < 7 ? S[0] : S[1], (u + 1) & 7,
+                                  B[(u + 1) & 1], acc);
+        if (u == 7) {
+          S[0] = S[1];
+          load_sblk(S[1], lr, min((j0 >> 3) + 2, last_blk));
+        }
       }
+      stage_store<NMB, P>(lds + ((q + 1) & 1) * (SR * P), X[(q + 1) & 1][0]);
+      stage_store<NMB, P>(lds + ((q + 1) & 1) * (SR * P) + 64, X[(q + 1) & 1][1]);
       __syncthreads();
     }
   }
@@ -718,9 +736,9 @@ __device__ __forceinline__ bool xcd_work(const PrefillArgs& a, int n_cols, TileI
 // loop by the gate/up epilogue for the up waves' accumulators.
 // 6-bit weights at 32-row tiles go through the 8 waves' unit buffers after
 // that (gemm_tile_u6).
-template <int MB>
+template <int BITS, int MB>
 constexpr int stage_bytes() {
-  return 2 * stage_rows<MB>() * kLdsRow * 2;
+  return 2 * stage_rows<MB>() * (BITS == 4 && MB > 1 ? kLdsRow2 : kLdsRow) * 2;
 }
 template <int BITS, int MB>
 constexpr int unit_wave_bytes() {
@@ -733,11 +751,11 @@ constexpr int unit_lds_bytes() {
 template <int BITS, int MB>
 constexpr int gateup_lds_bytes() {
   constexpr int up = 4 * MB * 16 * 64 * 4;  // 4 up waves x accumulators
-  return (stage_bytes<MB>() > up ? stage_bytes<MB>() : up) + unit_lds_bytes<BITS, MB>();
+  return (stage_bytes<BITS, MB>() > up ? stage_bytes<BITS, MB>() : up) + unit_lds_bytes<BITS, MB>();
 }
 template <int BITS, int MB>
 constexpr int down_lds_bytes() {
-  return stage_bytes<MB>() + unit_lds_bytes<BITS, MB>();
+  return stage_bytes<BITS, MB>() + unit_lds_bytes<BITS, MB>();
 }
 
 template <int BITS, int MB>
@@ -835,7 +853,7 @@ __global__ __launch_bounds__(kThreads, MB < kMB ? 4 : 1) void down_mfma_kernel(c
   lr.b = reinterpret_cast<const u32x4*>(base + a.b0) + size_t(col) * blks;
   const int col0 = cb * kDnCols + wave * 32;  // the wave's first row (uniform)
   const uint8_t* w0 = base + a.w0 + size_t(col0) * row_bytes;
-  uint8_t* wbuf = lds_raw + stage_bytes<MB>() + wave * unit_wave_bytes<BITS, MB>();
+  uint8_t* wbuf = lds_raw + stage_bytes<BITS, MB>() + wave * unit_wave_bytes<BITS, MB>();
   const StageRows rows = tile_rows(a.act, nullptr, 1, a.cols, ti.p0, ti.m);
   // the tile's output rows, read while the weights stream (the main loop's
   // barriers publish them), not one dependent load per row at the end
