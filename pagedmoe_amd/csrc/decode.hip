@@ -100,8 +100,7 @@ gateup_routed_kernel(const GemvArgs a, const RouteDev rt, int32_t* inds_out, flo
   const int u = blockIdx.y;
   int e, slot;
   if (PRE) {
-    __shared__ RouteOne one;
-    load_route_one(rec, rt.n * rt.kk, u, L, one);
+    const RouteOne one = load_route_one(rec, rt.n * rt.kk, u, L);
     if (u >= one.n_active) return;
     e = one.e;
     slot = one.slot;
@@ -258,10 +257,9 @@ down_split_kernel(const GemvArgs a, const RouteDev rt, float* y, const RouteReco
   __shared__ RouteLds L;
   __shared__ int32_t s_rows[kRouteMaxRows];
   __shared__ int s_m;
-  __shared__ RouteOne one;
   const int rows = rt.n * rt.kk;
   const int u = blockIdx.y;
-  load_route_one(rec, rows, u, L, one);
+  const RouteOne one = load_route_one(rec, rows, u, L);
   if (u >= one.n_active) return;
   const int e = one.e;
   if (threadIdx.x < 64) {

@@ -597,22 +597,29 @@ __device__ __forceinline__ void publish_route(const RouteLds& L, int rows, Route
   if (threadIdx.x == 0) g->n_active = na;
 }
 
-// What a block working on the u-th active expert needs from the record, in
-// one round of independent loads: the flat rows' ids (for wave_rows_of), the
-// expert's id and slot, and the active count.  Ends with a block barrier.
+// What a block working on the u-th active expert needs from the record: the
+// flat rows' ids (for wave_rows_of) go to LDS, ending with a block barrier;
+// the active count and the expert's id and slot, uniform over the block, are
+// read through the scalar cache (invalidated at every dispatch, and the
+// record was written by an earlier launch).  A scalar load does not queue
+// behind the vector loads that the CU's other blocks have in flight, so the
+// block knows its weights' address before its first vector load returns.
+// u may exceed the active count (the launch's grid covers the most experts a
+// call can route); those entries are in bounds and unused.
 struct RouteOne {
   int n_active, e, slot;
 };
 
-__device__ __forceinline__ void load_route_one(const RouteRecord* g, int rows, int u,
-                                               RouteLds& L, RouteOne& o) {
+__device__ __forceinline__ RouteOne load_route_one(const RouteRecord* g, int rows, int u,
+                                                   RouteLds& L) {
+  typedef const __attribute__((address_space(4))) int32_t ConstI32;
+  RouteOne o;
+  o.n_active = *(ConstI32*)(&g->n_active);
+  o.e = *(ConstI32*)(g->active + u);
+  o.slot = *(ConstI32*)(g->slot + u);
   for (int i = threadIdx.x; i < rows; i += blockDim.x) L.ids[i] = g->ids[i];
-  if (threadIdx.x == 0) {
-    o.n_active = g->n_active;
-    o.e = g->active[u];
-    o.slot = g->slot[u];
-  }
   __syncthreads();
+  return o;
 }
 
 __device__ __forceinline__ void load_route(const RouteRecord* g, int rows, int n_ids, RouteLds& L) {
