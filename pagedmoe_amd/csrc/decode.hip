@@ -77,9 +77,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PMOE_MIN_WA
 // Decode gate/up with the routing computed in the block's prologue (see
 // route_common.h): blockIdx.y = u-th active expert in ascending id order.
 // Block (0, 0) also publishes the routing (inds_out, w_out).
-// PRE: the routing record was written by route_record_kernel (several
-// tokens); otherwise every block routes its one token itself and block (0, 0)
-// publishes the record.
+// PRE: the routing record was written by the router launch (several
+// tokens; router_route_kernel); otherwise every block routes its one token
+// itself and block (0, 0) publishes the record.  (Gathering the rows per
+// wave straight from the record, as the expert-split down does, made the
+// Qwen3-235B-shaped batch-8 gate/up slower, 74.8 -> 78.3 us in rocprof.)
 // More than 8 logits per lane (over 512 experts): the routing prologue's
 // per-lane logit, key and payload arrays need more registers than the GEMV's
 // occupancy floor leaves, so those variants run with two waves per SIMD.
@@ -100,7 +102,8 @@ gateup_routed_kernel(const GemvArgs a, const RouteDev rt, int32_t* inds_out, flo
   const int u = blockIdx.y;
   int e, slot;
   if (PRE) {
-    const RouteOne one = load_route_one(rec, rt.n * rt.kk, u, L);
+    const RouteOne one = load_route_one(rec, u);
+    load_route_ids(rec, rt.n * rt.kk, L);
     if (u >= one.n_active) return;
     e = one.e;
     slot = one.slot;
@@ -254,32 +257,26 @@ template <int UB, int LPR, int GPL, int R, int EPL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PMOE_MIN_WAVES, 8))) void
 down_split_kernel(const GemvArgs a, const RouteDev rt, float* y, const RouteRecord* rec) {
   constexpr int RPW = 64 / LPR;
-  __shared__ RouteLds L;
-  __shared__ int32_t s_rows[kRouteMaxRows];
-  __shared__ int s_m;
-  const int rows = rt.n * rt.kk;
+  __shared__ int32_t s_rows[4][kRouteMaxRows];  // each wave's own list (the same rows)
+  const int wave = threadIdx.x >> 6;
   const int u = blockIdx.y;
-  const RouteOne one = load_route_one(rec, rows, u, L);
+  const RouteOne one = load_route_one(rec, u);
+  // rows first: their loads need not wait for the active count
+  const int m = wave_rows_of_record(rec, rt.n * rt.kk, one.e, s_rows[wave]);
   if (u >= one.n_active) return;
-  const int e = one.e;
-  if (threadIdx.x < 64) {
-    const int m = wave_rows_of(L, rows, e, s_rows);
-    if (threadIdx.x == 0) s_m = m;
-  }
   const int slot = one.slot;
-  __syncthreads();
   const int row0 = blockIdx.x * (4 * R * RPW);
   if (slot < 0) {  // exact zero rows (streaming.py:715-719)
-    for (int i = threadIdx.x; i < s_m * 4 * R * RPW; i += 256) {
+    for (int i = threadIdx.x; i < m * 4 * R * RPW; i += 256) {
       const int o = row0 + i % (4 * R * RPW);
-      if (o < a.rows_out) y[size_t(s_rows[i / (4 * R * RPW)]) * a.rows_out + o] = 0.0f;
+      if (o < a.rows_out) y[size_t(s_rows[wave][i / (4 * R * RPW)]) * a.rows_out + o] = 0.0f;
     }
     return;
   }
-  const int wrow0 = row0 + (threadIdx.x >> 6) * (R * RPW);
+  const int wrow0 = row0 + wave * (R * RPW);
   auto act_row = [&](int r) { return a.act + size_t(r) * a.act_stride; };
   auto store = [&](int r, int, int o, float v) { y[size_t(r) * a.rows_out + o] = v; };
-  gemv_expert<UB, LPR, GPL, R, false>(a, slot, s_m, s_rows, wrow0, act_row, store);
+  gemv_expert<UB, LPR, GPL, R, false>(a, slot, m, s_rows[wave], wrow0, act_row, store);
 }
 
 // out[n, o] = sum_c w[n, c] * y[n*kk + c, o] in c order (fma chain from 0,

@@ -598,28 +598,58 @@ __device__ __forceinline__ void publish_route(const RouteLds& L, int rows, Route
 }
 
 // What a block working on the u-th active expert needs from the record: the
-// flat rows' ids (for wave_rows_of) go to LDS, ending with a block barrier;
-// the active count and the expert's id and slot, uniform over the block, are
-// read through the scalar cache (invalidated at every dispatch, and the
-// record was written by an earlier launch).  A scalar load does not queue
-// behind the vector loads that the CU's other blocks have in flight, so the
-// block knows its weights' address before its first vector load returns.
-// u may exceed the active count (the launch's grid covers the most experts a
-// call can route); those entries are in bounds and unused.
+// active count and the expert's id and slot, uniform over the block, read
+// through the scalar cache (invalidated at every dispatch, and the record was
+// written by an earlier launch).  A scalar load does not queue behind the
+// vector loads that the CU's other blocks have in flight, so the block knows
+// its weights' address before its first vector load returns.  u may exceed
+// the active count (the launch's grid covers the most experts a call can
+// route); those entries are in bounds and unused.
 struct RouteOne {
   int n_active, e, slot;
 };
 
-__device__ __forceinline__ RouteOne load_route_one(const RouteRecord* g, int rows, int u,
-                                                   RouteLds& L) {
+__device__ __forceinline__ RouteOne load_route_one(const RouteRecord* g, int u) {
   typedef const __attribute__((address_space(4))) int32_t ConstI32;
   RouteOne o;
   o.n_active = *(ConstI32*)(&g->n_active);
   o.e = *(ConstI32*)(g->active + u);
   o.slot = *(ConstI32*)(g->slot + u);
+  return o;
+}
+
+// The record's flat row ids into L.ids, for wave_rows_of.  Ends with a block
+// barrier.
+__device__ __forceinline__ void load_route_ids(const RouteRecord* g, int rows, RouteLds& L) {
   for (int i = threadIdx.x; i < rows; i += blockDim.x) L.ids[i] = g->ids[i];
   __syncthreads();
-  return o;
+}
+
+// Flat rows (ascending) of the record whose id is `id`, gathered by one wave
+// straight from the record into its own list out[]: every wave of a block
+// builds the same list, so no LDS staging and no block barrier stand between
+// the record and the weight loads.  Returns the count.
+__device__ __forceinline__ int wave_rows_of_record(const RouteRecord* g, int rows, int id,
+                                                   int32_t* out) {
+  static_assert(kRouteMaxRows == 256, "four ids a lane");
+  const int lane = threadIdx.x & 63;
+  int v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 64 * i + lane;
+    v[i] = r < rows ? g->ids[r] : -1;
+  }
+  int m = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (64 * i >= rows) break;
+    const bool hit = v[i] == id;
+    const uint64_t mask = wave_ballot(hit);
+    if (hit) out[m + lanes_below(mask)] = 64 * i + lane;
+    m += __popcll(mask);
+  }
+  wave_lds_sync();
+  return m;
 }
 
 __device__ __forceinline__ void load_route(const RouteRecord* g, int rows, int n_ids, RouteLds& L) {
