@@ -38,36 +38,54 @@ __device__ __forceinline__ int load_id(const IdSrc& src, int r) {
   return (e >= 0 && e < src.n_routed) ? e : -1;
 }
 
-// Exclusive scan of one int per thread over a block of NT threads.  s_tmp
-// holds NT/64 ints.  Returns the exclusive prefix; *total gets the sum.
+// Exclusive scans of three ints per thread over a block of NT threads, side
+// by side (their shuffles overlap and they share the barriers).  s_tmp holds
+// 3 * NT/64 ints.  v[i] becomes the exclusive prefix of v[i]; total[i] gets
+// the sum.
 template <int NT>
-__device__ __forceinline__ int block_excl_scan(int v, int* s_tmp, int* total) {
+__device__ __forceinline__ void block_excl_scan3(int (&v)[3], int* s_tmp, int (&total)[3]) {
+  constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  int incl = v;
+  int incl[3] = {v[0], v[1], v[2]};
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
-    const int o = __shfl_up(incl, off, kWave);
-    if (lane >= off) incl += o;
+    int o[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) o[i] = __shfl_up(incl[i], off, kWave);
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      if (lane >= off) incl[i] += o[i];
   }
-  if (lane == 63) s_tmp[wave] = incl;
+  if (lane == 63)
+#pragma unroll
+    for (int i = 0; i < 3; ++i) s_tmp[i * NW + wave] = incl[i];
   __syncthreads();
   if (wave == 0) {
-    int wvv = lane < NT / 64 ? s_tmp[lane] : 0;
-    int wi = wvv;
+    int wi[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) wi[i] = lane < NW ? s_tmp[i * NW + lane] : 0;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
-      const int o = __shfl_up(wi, off, kWave);
-      if (lane >= off) wi += o;
+      int o[3];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) o[i] = __shfl_up(wi[i], off, kWave);
+#pragma unroll
+      for (int i = 0; i < 3; ++i)
+        if (lane >= off) wi[i] += o[i];
     }
-    if (lane < NT / 64) s_tmp[lane] = wi;  // inclusive wave totals
+    if (lane < NW)
+#pragma unroll
+      for (int i = 0; i < 3; ++i) s_tmp[i * NW + lane] = wi[i];  // inclusive wave totals
   }
   __syncthreads();
-  const int base = wave > 0 ? s_tmp[wave - 1] : 0;
-  const int t = s_tmp[NT / 64 - 1];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const int base = wave > 0 ? s_tmp[i * NW + wave - 1] : 0;
+    total[i] = s_tmp[i * NW + NW - 1];
+    v[i] = base + incl[i] - v[i];
+  }
   __syncthreads();
-  if (total) *total = t;
-  return base + incl - v;
 }
 
 // The prefill GEMMs' tile list (when tile_m > 0): tile t of expert e with
@@ -91,13 +109,12 @@ __device__ void finish_scan(const int* cnt, int n_experts, int32_t* counts, int3
   const int tile_m = ts.tile_m;
   const int e = threadIdx.x;
   const int c = e < n_experts ? cnt[e] : 0;
-  int total = 0;
-  const int off = block_excl_scan<1024>(c, s_tmp, &total);
-  int act_total = 0;
-  const int act = block_excl_scan<1024>(c > 0 ? 1 : 0, s_tmp, &act_total);
-  int tiles_total = 0;
   const int nt = tile_m > 0 ? (c + tile_m - 1) / tile_m : 0;
-  const int toff = block_excl_scan<1024>(nt, s_tmp, &tiles_total);
+  int sc[3] = {c, c > 0 ? 1 : 0, nt};  // rows, active experts, tiles
+  int tot[3];
+  block_excl_scan3<1024>(sc, s_tmp, tot);
+  const int off = sc[0], act = sc[1], toff = sc[2];
+  const int total = tot[0], act_total = tot[1], tiles_total = tot[2];
   if (e < n_experts) {
     s_off[e] = off;
     counts[e] = c;
@@ -124,7 +141,7 @@ __global__ __launch_bounds__(1024) void dispatch_small_kernel(
   __shared__ int s_e[kSmallRows];
   __shared__ int s_cnt[kMaxExperts];
   __shared__ int s_off[kMaxExperts];
-  __shared__ int s_tmp[16];
+  __shared__ int s_tmp[48];
   const int tid = threadIdx.x;
   for (int e = tid; e < n_experts; e += 1024) s_cnt[e] = 0;
   int my_e = -1;
@@ -173,19 +190,34 @@ __global__ __launch_bounds__(kChunk) void dispatch_count_kernel(
 }
 
 // Phase 2 (one block): turn hist[b][e] into each block's base position per
-// expert and produce counts/offsets/active/tiles.
+// expert and produce counts/offsets/active/tiles.  Thread e walks column e of
+// hist; its first kKeep entries are loaded in one round (all in flight) and
+// kept in registers for the second pass, so up to kKeep blocks (16,384 rows)
+// cost one round of loads instead of two passes of dependent rounds.
 __global__ __launch_bounds__(1024) void dispatch_scan_kernel(
     int32_t* __restrict__ hist, int n_blocks, int n_experts, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ active, int32_t* __restrict__ n_active,
     const TileSink ts) {
   __shared__ int s_cnt[kMaxExperts];
   __shared__ int s_off[kMaxExperts];
-  __shared__ int s_tmp[16];
-  constexpr int kBatch = 16;  // block histograms read per round, all in flight
+  __shared__ int s_tmp[48];
+  constexpr int kKeep = 64;   // block histograms held in registers
+  constexpr int kBatch = 16;  // further block histograms read per round, all in flight
   const int e = threadIdx.x;
+  int hk[kKeep];
   if (e < n_experts) {
+    // clamped index: straight-line loads, no branch per entry (n_blocks >= 1),
+    // every load issued before the first is used
+#pragma unroll
+    for (int j = 0; j < kKeep; ++j)
+      hk[j] = hist[size_t(j < n_blocks ? j : n_blocks - 1) * n_experts + e];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < kKeep; ++j) hk[j] = j < n_blocks ? hk[j] : 0;
     int run = 0;
-    for (int b0 = 0; b0 < n_blocks; b0 += kBatch) {
+#pragma unroll
+    for (int j = 0; j < kKeep; ++j) run += hk[j];
+    for (int b0 = kKeep; b0 < n_blocks; b0 += kBatch) {
       int h[kBatch];
 #pragma unroll
       for (int j = 0; j < kBatch; ++j)
@@ -200,7 +232,12 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(
   if (e < n_experts) {
     // each block's base position per expert: expert offset + earlier blocks
     int run = s_off[e];
-    for (int b0 = 0; b0 < n_blocks; b0 += kBatch) {
+#pragma unroll
+    for (int j = 0; j < kKeep; ++j) {
+      if (j < n_blocks) hist[size_t(j) * n_experts + e] = run;
+      run += hk[j];
+    }
+    for (int b0 = kKeep; b0 < n_blocks; b0 += kBatch) {
       int h[kBatch];
 #pragma unroll
       for (int j = 0; j < kBatch; ++j)
