@@ -78,10 +78,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PMOE_MIN_WA
 // route_common.h): blockIdx.y = u-th active expert in ascending id order.
 // Block (0, 0) also publishes the routing (inds_out, w_out).
 // PRE: the routing record was written by the router launch (several
-// tokens; router_route_kernel); otherwise every block routes its one token
-// itself and block (0, 0) publishes the record.  (Gathering the rows per
-// wave straight from the record, as the expert-split down does, made the
-// Qwen3-235B-shaped batch-8 gate/up slower, 74.8 -> 78.3 us in rocprof.)
+// tokens; router_route_kernel) and wave 0 gathers the expert's rows from it
+// for the block; otherwise every block routes its one token itself and block
+// (0, 0) publishes the record.  (Every wave gathering its own list, as the
+// expert-split down does, made the Qwen3-235B-shaped batch-8 gate/up slower,
+// 74.8 -> 78.3 us in rocprof.)
 // More than 8 logits per lane (over 512 experts): the routing prologue's
 // per-lane logit, key and payload arrays need more registers than the GEMV's
 // occupancy floor leaves, so those variants run with two waves per SIMD.
@@ -100,25 +101,27 @@ gateup_routed_kernel(const GemvArgs a, const RouteDev rt, int32_t* inds_out, flo
   __shared__ int32_t s_rows[kRouteMaxRows];
   __shared__ int s_m;
   const int u = blockIdx.y;
-  int e, slot;
+  int slot;
   if (PRE) {
     const RouteOne one = load_route_one(rec, u);
-    load_route_ids(rec, rt.n * rt.kk, L);
     if (u >= one.n_active) return;
-    e = one.e;
     slot = one.slot;
+    if (threadIdx.x < 64) {
+      const int m = wave_rows_of_record(rec, rt.n * rt.kk, one.e, s_rows);
+      if (threadIdx.x == 0) s_m = m;
+    }
   } else {
     const bool publish = blockIdx.x == 0 && blockIdx.y == 0;
     route_block<EPL, 4>(rt, L, W, publish ? inds_out : nullptr, w_out);
     if (publish)
       publish_route(L, rt.n * rt.kk, rec, a.table, a.n_experts, a.shared_slot);
     if (u >= L.n_active) return;
-    e = L.active[u];
+    const int e = L.active[u];
     slot = e < a.n_experts ? a.table[e] : a.shared_slot;
-  }
-  if (threadIdx.x < 64) {
-    const int m = wave_rows_of(L, rt.n * rt.kk, e, s_rows);
-    if (threadIdx.x == 0) s_m = m;
+    if (threadIdx.x < 64) {
+      const int m = wave_rows_of(L, rt.n * rt.kk, e, s_rows);
+      if (threadIdx.x == 0) s_m = m;
+    }
   }
   __syncthreads();
   const int row0 = blockIdx.x * (4 * R * RPW);

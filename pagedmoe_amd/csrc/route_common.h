@@ -618,17 +618,10 @@ __device__ __forceinline__ RouteOne load_route_one(const RouteRecord* g, int u) 
   return o;
 }
 
-// The record's flat row ids into L.ids, for wave_rows_of.  Ends with a block
-// barrier.
-__device__ __forceinline__ void load_route_ids(const RouteRecord* g, int rows, RouteLds& L) {
-  for (int i = threadIdx.x; i < rows; i += blockDim.x) L.ids[i] = g->ids[i];
-  __syncthreads();
-}
-
 // Flat rows (ascending) of the record whose id is `id`, gathered by one wave
-// straight from the record into its own list out[]: every wave of a block
-// builds the same list, so no LDS staging and no block barrier stand between
-// the record and the weight loads.  Returns the count.
+// straight from the record into out[] (no LDS staging of the ids; a wave
+// that gathers its own list needs no block barrier either).  Returns the
+// count.
 __device__ __forceinline__ int wave_rows_of_record(const RouteRecord* g, int rows, int id,
                                                    int32_t* out) {
   static_assert(kRouteMaxRows == 256, "four ids a lane");
