@@ -62,6 +62,7 @@ struct PrefillArgs {
   int out_cols;          // inter (h) or hidden (y)
   void* out;
   int out_f32;
+  int out_vec;           // out is 16-byte aligned: bf16 rows may go out as 16-byte pieces
 };
 
 // Tile of this block: first sorted position, row count, slot.
@@ -819,6 +820,10 @@ __global__ __launch_bounds__(kThreads, MB < kMB ? 4 : 1) void gateup_mfma_kernel
       }
     }
   }
+  // (Staging h through an LDS tile after the exchange area and storing
+  // 16-byte row pieces, as the down does, made gate/up slower at 128-row
+  // tiles: 738 -> 748 us for the 2048-token layer in rocprof; the extra
+  // block barrier costs more than 32 KB of short stores.)
 }
 
 template <int BITS, int MB>
@@ -862,19 +867,44 @@ __global__ __launch_bounds__(kThreads, MB < kMB ? 4 : 1) void down_mfma_kernel(c
   f32x16 acc[MB];
   const int nmb = (ti.m + 31) >> 5;
   gemm_tile_any<BITS, MB>(nmb, groups, rows, lr, w0, uint32_t(row_bytes), lds, wbuf, acc);
+  // bf16 rows go out through LDS (free: the main loop ended with a block
+  // barrier) as 16-byte row pieces, 32 threads a row: 2-byte stores straight
+  // from the accumulators, each instruction covering half a line of two
+  // rows, took a fifth of a block's life.  Row pitch kDnCols + 8 values
+  // (528 bytes): the rows the two lane halves write fall on other banks.
+  // Forms whose LDS cannot hold the tile (6-bit, 128 rows) store directly.
+  constexpr int kEp = kDnCols + 8;
+  constexpr int kPieces = kDnCols / 8;
+  constexpr bool kStaged = 32 * MB * kEp * 2 <= down_lds_bytes<BITS, MB>();
+  if (!kStaged || a.out_f32 || !a.out_vec) {
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
+    for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = mb * 32 + acc_row(r, h);
-      if (row < ti.m) {
-        const size_t o = size_t(s_ord[row]) * a.out_cols;
-        if (a.out_f32)
-          static_cast<float*>(a.out)[o + col] = acc[mb][r];
-        else
-          static_cast<uint16_t*>(a.out)[o + col] = f2bf(acc[mb][r]);
+      for (int r = 0; r < 16; ++r) {
+        const int row = mb * 32 + acc_row(r, h);
+        if (row < ti.m) {
+          const size_t o = size_t(s_ord[row]) * a.out_cols;
+          if (a.out_f32)
+            static_cast<float*>(a.out)[o + col] = acc[mb][r];
+          else
+            static_cast<uint16_t*>(a.out)[o + col] = f2bf(acc[mb][r]);
+        }
       }
     }
+    return;
+  }
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+    if (mb < nmb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        lds[(mb * 32 + acc_row(r, h)) * kEp + wave * 32 + (lane & 31)] = f2bf(acc[mb][r]);
+  __syncthreads();
+  uint16_t* out = static_cast<uint16_t*>(a.out) + cb * kDnCols;
+  for (int q = threadIdx.x; q < ti.m * kPieces; q += kThreads) {
+    const int row = q / kPieces, pc = q - row * kPieces;
+    *reinterpret_cast<uint4*>(out + size_t(s_ord[row]) * a.out_cols + 8 * pc) =
+        *reinterpret_cast<const uint4*>(lds + row * kEp + 8 * pc);
   }
 }
 
@@ -965,6 +995,7 @@ int prefill_experts(const pmoe_geom* g, const uint8_t* slab, const uint16_t* x, 
   a.out_cols = g->hidden;
   a.out = y;
   a.out_f32 = y_f32;
+  a.out_vec = (reinterpret_cast<uintptr_t>(y) & 15) == 0;
   {
     const int items = g->hidden / kDnCols * max_tiles;
     dim3 grid((items + 7) / 8 * 8);

@@ -99,6 +99,40 @@ def test_prefill_switch_glu_seam_and_nonresident():
     check_close(y[mask], ref[mask], "prefill seam")
 
 
+def test_prefill_switch_glu_unaligned_output_matches_aligned():
+    """The down GEMM writes bf16 rows through LDS as 16-byte pieces when the
+    output is 16-byte aligned and element by element otherwise: y at a
+    2-byte offset (the element-wise path) equals the aligned result bit for
+    bit, at 128-row tiles."""
+    import ctypes
+    from pagedmoe_amd import kernels as KM
+    from pagedmoe_amd._lib import check, lib
+    K = _k()
+    spec = O.LayerSpec(1024, 16, 512, 4)
+    gw, experts, _, _, _ = O.make_layer(spec, seed=32)
+    rng = np.random.default_rng(33)
+    n, k = 320, 4
+    xb = _x(rng, n, spec.hidden)
+    inds = torch.from_numpy(np.stack([rng.choice(spec.experts, k, replace=False)
+                                      for _ in range(n)]).astype(np.int32)).to(DEV)
+    assert _tile_rows(n, k, spec.experts) == 128
+    g, slab = _slab(spec, experts)
+    table = torch.arange(spec.experts, dtype=torch.int32, device=DEV)
+    x = bits_to_bf16_tensor(xb, DEV)
+    y_al = K.switch_glu(g, slab.buf, table, spec.experts, x, inds)
+    big = torch.full((n * k * spec.hidden + 8,), float("nan"), dtype=torch.bfloat16, device=DEV)
+    y_un = big[1:1 + n * k * spec.hidden]
+    assert y_un.data_ptr() % 16 == 2
+    ws = KM.moe_workspace(g, n, k, 0, spec.experts, x.device)
+    check(lib().pmoe_switch_glu(ctypes.byref(g), KM._ptr(slab.buf), KM._table_ptr(table),
+                                spec.experts, KM._ptr(x), KM._ptr(inds), n, k,
+                                ctypes.c_void_p(y_un.data_ptr()), KM._ptr(ws), ws.numel(),
+                                KM._stream()), "pmoe_switch_glu")
+    torch.cuda.synchronize()
+    assert torch.equal(y_al.reshape(-1).view(torch.int16), y_un.view(torch.int16))
+    assert torch.isnan(big[0]) and torch.isnan(big[-7:]).all()
+
+
 def test_prefill_sigmoid_shared_vs_oracle():
     """DeepSeek-style routing (sigmoid + bias, 8 groups / top-4, top-6,
     scale 2.5) with a shared expert: 384 tokens x 7 columns."""
